@@ -1,0 +1,151 @@
+/* slm_hip.h — the C ABI of the MI355X (gfx950) backend for SLM.use's token loop.
+ *
+ * One entry point per method of the reference's operator trait `Ops` (src/ops.rs:68-228).
+ * The reference's model (src/model.rs) drives that trait; a Rust `impl Ops for Hip`
+ * binds these functions one to one the way src/cuda.rs binds its
+ * CUDA kernels, so model.rs, the loop-count logic, the sampler, the CLI and the server
+ * run unchanged above it.
+ *
+ * Conventions, all from src/ops.rs:1-9 and the trait signatures:
+ *   - Every buffer is flat fp32 in device memory, allocated by slm_hip_alloc/upload.
+ *   - An `At { buf, offset }` view (ops.rs:13-17) is passed as `buf + offset`.
+ *   - Outputs never alias inputs, except the in/out state of gla (`s`) and store
+ *     (`cache`), as the trait's `&mut` signatures guarantee.
+ *   - Sizes are element counts. The caller sizes every output; the library checks each
+ *     pointer range against its own allocation table and returns SLM_E_BOUNDS, touching
+ *     nothing, when a range falls outside one live allocation.
+ *   - Work is queued on one stream per context; slm_hip_read waits for it (ops.rs:88).
+ *   - Every function returns SLM_OK (0) or a negative SLM_E_* code; the message is kept
+ *     in the context (slm_hip_last_error), as src/cuda.rs:138 names the failing op.
+ *   - One context is used from one thread at a time (src/serve.rs:1-3).
+ */
+#ifndef SLM_HIP_H
+#define SLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SLM_OK = 0,
+    SLM_NO_DEVICE = 1,        /* slm_hip_open only: no usable GPU; not an error (cuda.rs:72-83) */
+    SLM_E_INVALID = -1,       /* bad argument (null pointer, zero size where one is needed) */
+    SLM_E_HIP = -2,           /* the HIP runtime failed */
+    SLM_E_UNSUPPORTED = -3,   /* a shape the kernels do not handle, e.g. head size > 256 */
+    SLM_E_MEMORY = -4,        /* device allocation failed */
+    SLM_E_BOUNDS = -5         /* a pointer range is outside every live allocation */
+};
+
+typedef struct slm_hip slm_hip;
+
+/* src/ops.rs:34-46. `reach` may be SIZE_MAX (global layers, model.rs:530). */
+typedef struct slm_attn {
+    size_t pos, m, reach, gap, cap, heads, key_heads, dh;
+    float scale;
+} slm_attn;
+
+/* ---- context: replaces Cuda::probe (src/cuda.rs:72-120) and Ops::name (ops.rs:71) ---- */
+
+/* Opens `device`, loads the embedded gfx950 code object with hipModuleLoadData. Returns
+ * SLM_NO_DEVICE (and *out = NULL) on a machine without a usable GPU. */
+int slm_hip_open(int device, slm_hip** out);
+void slm_hip_close(slm_hip* ctx);
+/* The last error message of this context ("" if none). NULL ctx: the last open failure. */
+const char* slm_hip_last_error(const slm_hip* ctx);
+/* Ops::name (ops.rs:71): writes e.g. "hip (AMD Instinct MI355X, gfx950)" into out[n]. */
+int slm_hip_name(slm_hip* ctx, char* out, size_t n);
+
+/* ---- buffers: Ops::zeros / zeros_cache / upload / upload_cache / read / flush
+ *      (ops.rs:72-91; cuda.rs:152-169) ---- */
+
+/* A zeroed buffer of max(n, 1) floats (ops.rs:72, cuda.rs:152-154). */
+int slm_hip_alloc(slm_hip* ctx, size_t n, float** out);
+int slm_hip_free(slm_hip* ctx, float* buf);
+/* Copies n host floats into dst (Ops::upload, ops.rs:77). */
+int slm_hip_upload(slm_hip* ctx, float* dst, const float* src, size_t n);
+/* Waits for pending work and copies n floats to the host (Ops::read, ops.rs:88-89). */
+int slm_hip_read(slm_hip* ctx, float* host, const float* dev, size_t n);
+/* Ops::flush (ops.rs:90-91): called once at the end of every advance with every buffer
+ * that outlives it. With step graphs on it ends the step (see slm_hip_set_graphs). */
+int slm_hip_flush(slm_hip* ctx, const float* const* keep, size_t nkeep);
+
+/* ---- the operations (ops.rs:93-227; cpu.rs:66-403 define the arithmetic) ---- */
+
+/* y[i] = w[ids[i]], rows of d (ops.rs:93-94). `ids` is host memory. */
+int slm_hip_gather(slm_hip* ctx, float* y, const float* w, const uint32_t* ids, size_t m,
+                   size_t d);
+/* y = x (ops.rs:95). */
+int slm_hip_copy(slm_hip* ctx, float* y, const float* x, size_t n);
+/* y[0] = first, y[i] = x[i-1], rows of d (ops.rs:96-104). */
+int slm_hip_shift(slm_hip* ctx, float* y, const float* first, const float* x, size_t m,
+                  size_t d);
+/* y[i] = x[i][off .. off+len], rows of `stride` (ops.rs:105-115). */
+int slm_hip_columns(slm_hip* ctx, float* y, const float* x, size_t m, size_t stride,
+                    size_t off, size_t len);
+/* y[i] = w·x[i], w of rows × cols (ops.rs:116-126). */
+int slm_hip_linear(slm_hip* ctx, float* y, const float* w, size_t rows, size_t cols,
+                   const float* x, size_t m);
+/* y = a + b (ops.rs:127). */
+int slm_hip_add(slm_hip* ctx, float* y, const float* a, const float* b, size_t n);
+/* y[i] = x[i] + row (ops.rs:128-136). */
+int slm_hip_add_row(slm_hip* ctx, float* y, const float* x, const float* row, size_t m,
+                    size_t d);
+/* y[i] = f[i]·x[i], m = number of factors; `f` is host memory (ops.rs:137-138). */
+int slm_hip_scale_rows(slm_hip* ctx, float* y, const float* x, const float* f, size_t m,
+                       size_t d);
+/* y = a + t·(b − a) (ops.rs:139-147). */
+int slm_hip_mix(slm_hip* ctx, float* y, const float* a, const float* b, size_t n, float t);
+/* RMSNorm over `groups` runs of `size`, shared weight w (ops.rs:148-158). */
+int slm_hip_rms(slm_hip* ctx, float* y, const float* x, const float* w, size_t groups,
+                size_t size, float eps);
+/* y = silu(g)·u (ops.rs:159-166). */
+int slm_hip_silu_mul(slm_hip* ctx, float* y, const float* g, const float* u, size_t n);
+/* [m][half] cos/sin tables for positions pos.. (ops.rs:167-177). The first call of
+ * every advance (model.rs:566); with step graphs on it begins the step. */
+int slm_hip_rope_table(slm_hip* ctx, float* cos, float* sin, const float* inv, size_t pos,
+                       size_t m, size_t half);
+/* Half-split rotary embedding (ops.rs:178-188). */
+int slm_hip_rope(slm_hip* ctx, float* y, const float* x, const float* cos, const float* sin,
+                 size_t m, size_t heads, size_t dh);
+/* L2-normalises `heads` runs of dh (ops.rs:189-190). */
+int slm_hip_l2norm(slm_hip* ctx, float* y, const float* x, size_t heads, size_t dh);
+/* Gated linear attention over m tokens in order, state s in/out (ops.rs:191-205). */
+int slm_hip_gla(slm_hip* ctx, float* y, float* s, const float* q, const float* k,
+                const float* v, const float* decay, const float* bias, size_t m,
+                size_t heads, size_t dh);
+/* Writes m [heads][dh] rows into ring slots (pos+i) % cap of cache [heads][cap][dh]
+ * (ops.rs:206-217). */
+int slm_hip_store(slm_hip* ctx, float* cache, const float* src, size_t pos, size_t m,
+                  size_t cap, size_t heads, size_t dh);
+/* Softmax attention of m queries over the ring (ops.rs:218-227). `scores` is the trait's
+ * scratch; this backend keeps its own workspace and ignores it (it may be NULL). `k` and
+ * `v` are [key_heads][cap][dh]. */
+int slm_hip_attend(slm_hip* ctx, float* y, float* scores, const float* q, const float* k,
+                   const float* v, const slm_attn* a);
+
+/* ---- step graphs (no trait counterpart; a backend setting like cuda.rs's one stream) ----
+ * When on (the default), the operations of one advance — from rope_table to flush — are
+ * recorded instead of launched; flush replays a cached hipGraph when the step matches a
+ * recorded one (same operations, buffers and sizes; positions, ids and factors may
+ * differ) and captures a new one otherwise. A read, free or upload inside a step runs
+ * what was recorded so far and finishes the step eagerly. Results are identical either
+ * way: the graph runs the same kernels. */
+int slm_hip_set_graphs(slm_hip* ctx, int on);
+/* Counters for tests and benchmarks: graphs launched, graphs captured, eager steps. */
+int slm_hip_graph_stats(slm_hip* ctx, uint64_t* launched, uint64_t* captured,
+                        uint64_t* eager);
+
+/* ---- diagnostics (no trait counterpart) ----
+ * One v_mfma_f32_16x16x4f32 on one wave: lane l supplies a[l] and b[l] (device, 64 floats
+ * each) and writes the four result elements it holds to out[4l .. 4l+3] (256 floats).
+ * Tests use it to pin the lane layout the kernels assume. */
+int slm_hip_probe_mfma(slm_hip* ctx, float* out, const float* a, const float* b);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLM_HIP_H */

@@ -1,0 +1,31 @@
+"""Shared helpers for the GPU tests."""
+
+import os
+import sys
+import tempfile
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT / "slm.use_amd"))
+
+import synth  # noqa: E402
+
+
+def model_dir(name: str, seed: int) -> Path:
+    """A synthetic model folder (cached under the temp dir for the process's lifetime)."""
+    base = Path(os.environ.get("SLM_MODEL_CACHE", tempfile.gettempdir())) / "slm_models"
+    return synth.write_model(base / f"{name}-{seed}", name, seed)
+
+
+def rel(a, b) -> float:
+    """||a - b||_inf / ||b||_inf."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def greedy(logits) -> int:
+    """src/sample.rs:179-184: the first maximum wins."""
+    return int(np.argmax(logits))

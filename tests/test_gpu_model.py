@@ -1,0 +1,192 @@
+"""The token loop on the GPU: the model twin (src/model.rs restated over the C ABI) against
+the reference's PyTorch fixture and against the oracle (src/cpu.rs + src/model.rs
+restated), on the reference's own fixture and on seeded synthetic models.
+
+Bars (the north star's): per-position logits within 1e-4 relative (‖g − c‖∞ / ‖c‖∞) of the
+CPU path, identical greedy token ids, and identical ring state (every buffer the model
+keeps across steps, model.rs:626-638) after a chunked prompt and after the same prompt
+token by token.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import greedy, model_dir, rel, synth
+from verify import check_parity
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def hip(pkg):
+    h = pkg.Hip(0)
+    print("device:", h.name(), flush=True)
+    yield h
+    h.close()
+
+
+@pytest.fixture(scope="module")
+def tiny_hip(pkg, hip, tiny_dir):
+    return pkg.Model(hip, tiny_dir)
+
+
+def test_reference_fixture_split_matrix(tiny_hip, tiny_dir):
+    """tests/parity.rs:15-46 on the GPU, at the reference's own tolerance (1e-4 abs)."""
+    reports = check_parity(tiny_hip, tiny_dir)
+    worst = max(r.max_diff for r in reports)
+    print(f"max |diff| vs PyTorch fixture: {worst:.3g}; max rel {max(r.max_rel for r in reports):.3g}")
+    assert max(r.max_rel for r in reports) < TOL
+
+
+def _both(pkg, hip, folder, loops, global_cap=None):
+    g = pkg.Model(hip, folder, global_cap=global_cap)
+    c = O.Model(folder, global_cap=global_cap)
+    return g, c
+
+
+def test_c1_tiny_random_greedy(pkg, hip):
+    """Tiny shape, seeded N(0, 0.02) weights, a 32-token prompt, R = 2, 16 greedy tokens:
+    logits at all 48 positions and the greedy ids against the oracle."""
+    folder = model_dir("tiny", 1)
+    g, c = _both(pkg, hip, folder, 2)
+    prompt = synth.tokens(32, 97, seed=11)
+    gs, cs = g.session(2), c.session(2)
+    worst = 0.0
+    for t in prompt:  # every prompt position, token by token
+        gs.step(int(t))
+        cs.step(int(t))
+        worst = max(worst, rel(gs.logits(), cs.logits()))
+    ids_g, ids_c = [], []
+    for _ in range(16):
+        lg, lc = gs.logits(), cs.logits()
+        worst = max(worst, rel(lg, lc))
+        ids_g.append(greedy(lg))
+        ids_c.append(greedy(lc))
+        gs.step(ids_g[-1])
+        cs.step(ids_c[-1])
+    print(f"C1: max rel {worst:.3g}; ids {ids_g}")
+    assert worst < TOL
+    assert ids_g == ids_c
+    # the C++ decode loop (main.rs:207-223) picks the same ids
+    gs2 = g.session(2)
+    gs2.feed(prompt, 256)
+    assert gs2.decode_greedy(16).tolist() == ids_c
+
+
+def _kept_equal(a, b):
+    ka, kb = a.kept(), b.kept()
+    assert len(ka) == len(kb)
+    for i, (x, y) in enumerate(zip(ka, kb)):
+        assert x.shape == y.shape, i
+        assert np.array_equal(x, y), (i, float(np.abs(x - y).max()))
+
+
+@pytest.mark.parametrize("chunk", [7, 256])
+def test_chunked_equals_step_bitwise(tiny_hip, chunk):
+    toks = synth.tokens(300, 97, seed=5)  # past cap = 264: the rings wrap
+    a, b = tiny_hip.session(3), tiny_hip.session(3)
+    a.feed(toks, 1)
+    b.feed(toks, chunk)
+    assert np.array_equal(a.logits(), b.logits())
+    _kept_equal(a, b)
+
+
+def test_ring_overwrite_against_oracle(pkg, hip):
+    folder = model_dir("tiny", 2)
+    g, c = _both(pkg, hip, folder, 3)
+    toks = synth.tokens(700, 97, seed=6)
+    gs, cs = g.session(3), c.session(3)
+    gs.feed(toks, 256)
+    cs.feed(toks, 256)
+    assert rel(gs.logits(), cs.logits()) < TOL
+    for t in synth.tokens(20, 97, seed=7):
+        gs.step(int(t))
+        cs.step(int(t))
+        assert rel(gs.logits(), cs.logits()) < TOL
+        assert greedy(gs.logits()) == greedy(cs.logits())
+
+
+def test_global_grow(pkg, hip):
+    """Caches that start at 16 slots and double (model.rs:383-398) give the same bits as
+    caches that never grow, and match the oracle."""
+    folder = model_dir("tiny", 3)
+    small = pkg.Model(hip, folder, global_cap=16)
+    big = pkg.Model(hip, folder)
+    c = O.Model(folder)
+    toks = synth.tokens(90, 97, seed=8)
+    a, b, o = small.session(2), big.session(2), c.session(2)
+    for s in (a, b, o):
+        s.feed(toks, 13)
+    assert np.array_equal(a.logits(), b.logits())
+    assert rel(a.logits(), o.logits()) < TOL
+    for t in (1, 2, 3):
+        a.step(t)
+        b.step(t)
+        o.step(t)
+        assert np.array_equal(a.logits(), b.logits())
+        assert rel(a.logits(), o.logits()) < TOL
+
+
+def test_graphs_match_eager(pkg, hip, tiny_dir):
+    """Step graphs replay the same kernels: results are bit-identical to eager launches."""
+    m = pkg.Model(hip, tiny_dir)
+    toks = synth.tokens(40, 97, seed=9)
+    hip.set_graphs(False)
+    e = m.session(3)
+    e.feed(toks[:20], 8)
+    le = []
+    for t in toks[20:]:
+        e.step(int(t))
+        le.append(e.logits())
+    hip.set_graphs(True)
+    before = hip.graph_stats()
+    g = m.session(3)
+    g.feed(toks[:20], 8)
+    lg = []
+    for t in toks[20:]:
+        g.step(int(t))
+        lg.append(g.logits())
+    after = hip.graph_stats()
+    for x, y in zip(le, lg):
+        assert np.array_equal(x, y)
+    _kept_equal(e, g)
+    assert after["launched"] - before["launched"] >= 10
+    print("graph stats:", after)
+
+
+def test_a86_short_prompt_against_oracle(pkg, hip):
+    """The 86M shape (d 768, 12 x 64, FFN 4x, vocab 32000, window 4096) at R = 4: a 300-token
+    prompt in chunks of 256 + 44, then 6 greedy steps."""
+    folder = model_dir("a86", 2)
+    g, c = _both(pkg, hip, folder, 4)
+    toks = synth.tokens(300, 32000, seed=3)
+    gs, cs = g.session(4), c.session(4)
+    gs.feed(toks, 256)
+    cs.feed(toks, 256)
+    worst = rel(gs.logits(), cs.logits())
+    ids = []
+    for _ in range(6):
+        lg, lc = gs.logits(), cs.logits()
+        worst = max(worst, rel(lg, lc))
+        assert greedy(lg) == greedy(lc)
+        ids.append(greedy(lg))
+        gs.step(ids[-1])
+        cs.step(ids[-1])
+    print(f"a86: max rel {worst:.3g}; ids {ids}")
+    assert worst < TOL
+
+
+def test_a86_chunked_ring_state_equals_step(pkg, hip):
+    """Config 3's check at full size: a 4096-token prompt in 256-token chunks leaves the
+    same ring state, bit for bit, as the same prompt token by token (R = 4)."""
+    folder = model_dir("a86", 2)
+    g = pkg.Model(hip, folder)
+    toks = synth.tokens(4096, 32000, seed=4)
+    a, b = g.session(4), g.session(4)
+    a.feed(toks, 256)
+    b.feed(toks, 1)
+    assert np.array_equal(a.logits(), b.logits())
+    _kept_equal(a, b)

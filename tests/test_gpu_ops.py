@@ -1,0 +1,248 @@
+"""Every operation of the C ABI on the GPU against the oracle (the restatement of
+src/cpu.rs), on seeded inputs, plus the property the token loop depends on: each output is
+computed the same way whatever the number of tokens in the call, so m = 1 and m = 256
+give the same bits.
+
+Tolerances: bit-exact where the kernel follows the reference's order exactly (data
+movement, rms, l2norm, rope, rope_table); otherwise 2e-6 relative to the largest output
+(linear, attend, gla: MFMA / tree reassociation; silu: device expf).
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import rel
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(7)
+
+
+@pytest.fixture(scope="module")
+def hip(pkg):
+    h = pkg.Hip(0)
+    print("device:", h.name(), flush=True)
+    yield h
+    h.close()
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def test_mfma_lane_layout(hip):
+    """v_mfma_f32_16x16x4f32: lane l holds A[l%16][l/16], B[l/16][l%16] and
+    D[4(l/16)+r][l%16] — the layout every linear and attention kernel assumes."""
+    a = np.arange(64, dtype=np.float32)
+    b = (np.arange(64, dtype=np.float32) % 7) - 3
+    A = np.zeros((16, 4))
+    B = np.zeros((4, 16))
+    for l in range(64):
+        A[l % 16, l // 16] = a[l]
+        B[l // 16, l % 16] = b[l]
+    D = A @ B
+    out = hip.alloc(256)
+    da, db = hip.upload(a), hip.upload(b)
+    hip.probe_mfma(out.ptr, da.ptr, db.ptr)
+    got = out.read().reshape(64, 4)
+    for l in range(64):
+        for r in range(4):
+            assert got[l, r] == D[4 * (l // 16) + r, l % 16]
+
+
+LINEAR_SHAPES = [(96, 32, 1), (2304, 768, 1), (768, 3072, 1), (32000, 768, 1), (768, 768, 5),
+                 (13, 37, 3), (768, 768, 16), (768, 768, 17), (2304, 768, 256),
+                 (6144, 768, 256), (768, 3072, 256), (12, 768, 256), (50, 21, 70)]
+
+
+@pytest.mark.parametrize("rows,cols,m", LINEAR_SHAPES)
+def test_linear(hip, rows, cols, m):
+    w = rnd(rows, cols, scale=0.02)
+    x = rnd(m, cols)
+    dw, dx, dy = hip.upload(w), hip.upload(x), hip.alloc(m * rows)
+    hip.linear(dy.ptr, dw.ptr, rows, cols, dx.ptr, m)
+    got = dy.read(m * rows)
+    want = O.linear(w, x, rows, cols, m)
+    assert rel(got, want) < 2e-6, (rows, cols, m)
+
+
+@pytest.mark.parametrize("rows,cols", [(768, 768), (6144, 768), (768, 3072), (97, 32), (40, 52)])
+def test_linear_same_bits_for_any_m(hip, rows, cols):
+    """The decode kernel (m <= 16) and the prompt kernel (m > 16) run one MFMA chain."""
+    m = 256
+    w = rnd(rows, cols, scale=0.02)
+    x = rnd(m, cols)
+    dw, dx = hip.upload(w), hip.upload(x)
+    full = hip.alloc(m * rows)
+    hip.linear(full.ptr, dw.ptr, rows, cols, dx.ptr, m)
+    ref = full.read(m * rows).reshape(m, rows)
+    one = hip.alloc(rows)
+    for i in [0, 1, 17, 100, 255]:
+        hip.linear(one.ptr, dw.ptr, rows, cols, dx.at(i * cols), 1)
+        assert np.array_equal(one.read(rows), ref[i]), i
+    some = hip.alloc(16 * rows)
+    hip.linear(some.ptr, dw.ptr, rows, cols, dx.at(32 * cols), 16)
+    assert np.array_equal(some.read(16 * rows).reshape(16, rows), ref[32:48])
+    odd = hip.alloc(33 * rows)
+    hip.linear(odd.ptr, dw.ptr, rows, cols, dx.at(7 * cols), 33)
+    assert np.array_equal(odd.read(33 * rows).reshape(33, rows), ref[7:40])
+
+
+@pytest.mark.parametrize("groups,size", [(1, 768), (256, 768), (3072, 64), (4, 8), (5, 37)])
+def test_rms_bit_exact(hip, groups, size):
+    x = rnd(groups, size)
+    w = rnd(size)
+    dx, dw, dy = hip.upload(x), hip.upload(w), hip.alloc(groups * size)
+    hip.rms(dy.ptr, dx.ptr, dw.ptr, groups, size, 1e-6)
+    assert np.array_equal(dy.read(), O.rms(x, w, groups, size, 1e-6))
+
+
+@pytest.mark.parametrize("heads,dh", [(12, 64), (3072, 64), (4, 8), (3, 20)])
+def test_l2norm_bit_exact(hip, heads, dh):
+    x = rnd(heads, dh)
+    x[0] = 0.0  # max(norm, 1e-12)
+    dx, dy = hip.upload(x), hip.alloc(heads * dh)
+    hip.l2norm(dy.ptr, dx.ptr, heads, dh)
+    assert np.array_equal(dy.read(), O.l2norm(x, heads, dh))
+
+
+def test_silu_mul(hip):
+    n = 256 * 3072
+    g, u = rnd(n, scale=3.0), rnd(n)
+    dg, du, dy = hip.upload(g), hip.upload(u), hip.alloc(n)
+    hip.silu_mul(dy.ptr, dg.ptr, du.ptr, n)
+    got, want = dy.read(), O.silu_mul(g, u)
+    assert np.abs(got - want).max() <= 2e-6 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("pos,m", [(0, 1), (4095, 1), (100, 256), (20000, 3)])
+def test_rope_table_and_rope_bit_exact(hip, pos, m):
+    dh, heads = 64, 12
+    half = dh // 2
+    inv = (1.0 / np.power(np.float32(10000.0),
+                          (2 * np.arange(half)).astype(np.float32) / np.float32(dh))).astype(np.float32)
+    dinv = hip.upload(inv)
+    dc, ds = hip.alloc(m * half), hip.alloc(m * half)
+    hip.set_graphs(False)
+    hip.rope_table(dc.ptr, ds.ptr, dinv.ptr, pos, m, half)
+    wc, ws = O.rope_table(inv, pos, m, half)
+    assert np.array_equal(dc.read(), wc) and np.array_equal(ds.read(), ws)
+    x = rnd(m, heads, dh)
+    dx, dy = hip.upload(x), hip.alloc(m * heads * dh)
+    hip.rope(dy.ptr, dx.ptr, dc.ptr, ds.ptr, m, heads, dh)
+    assert np.array_equal(dy.read(), O.rope(x, wc, ws, m, heads, dh))
+    hip.set_graphs(True)
+
+
+def test_data_movement_bit_exact(hip):
+    m, d = 7, 40
+    x, a, b = rnd(m, d), rnd(m, d), rnd(m, d)
+    row, first = rnd(d), rnd(d)
+    dx, da, db, drow, dfirst = (hip.upload(t) for t in (x, a, b, row, first))
+    dy = hip.alloc(m * d)
+    hip.copy(dy.ptr, dx.ptr, m * d)
+    assert np.array_equal(dy.read(), x.reshape(-1))
+    hip.add(dy.ptr, da.ptr, db.ptr, m * d)
+    assert np.array_equal(dy.read(), (a + b).reshape(-1))
+    hip.add_row(dy.ptr, dx.ptr, drow.ptr, m, d)
+    assert np.array_equal(dy.read(), (x + row).reshape(-1))
+    hip.mix(dy.ptr, da.ptr, db.ptr, m * d, np.float32(0.3))
+    assert np.array_equal(dy.read(), (a + np.float32(0.3) * (b - a)).reshape(-1))
+    hip.shift(dy.ptr, dfirst.ptr, dx.ptr, m, d)
+    assert np.array_equal(dy.read(), np.concatenate([first[None], x[:-1]]).reshape(-1))
+    f = rnd(m)
+    hip.scale_rows(dy.ptr, dx.ptr, f, d)
+    assert np.array_equal(dy.read(), (x * f[:, None]).reshape(-1))
+    hip.scale_rows(dy.ptr, dx.ptr, f[:1], d)
+    assert np.array_equal(dy.read(d), x[0] * f[0])
+    dc = hip.alloc(m * 10)
+    hip.columns(dc.ptr, dx.ptr, m, d, 13, 10)
+    assert np.array_equal(dc.read(), x[:, 13:23].reshape(-1))
+    w = rnd(50, d)
+    dw = hip.upload(w)
+    ids = np.array([3, 49, 0, 3, 7, 7, 1], dtype=np.uint32)
+    hip.gather(dy.ptr, dw.ptr, ids, d)
+    assert np.array_equal(dy.read(), w[ids].reshape(-1))
+
+
+def test_store_wraps_the_ring(hip):
+    heads, dh, cap = 3, 8, 20
+    cache = np.zeros((heads, cap, dh), np.float32)
+    dcache = hip.upload(cache)
+    for pos, m in [(0, 5), (5, 20), (25, 1), (37, 9)]:
+        src = rnd(m, heads, dh)
+        dsrc = hip.upload(src)
+        hip.store(dcache.ptr, dsrc.ptr, pos, m, cap, heads, dh)
+        cache = O.store(cache, src, pos, m, cap, heads, dh).reshape(heads, cap, dh)
+        assert np.array_equal(dcache.read(), cache.reshape(-1))
+
+
+def test_bounds_are_checked_before_launch(hip, pkg):
+    dy, dx = hip.alloc(10), hip.alloc(10)
+    with pytest.raises(pkg.SlmError) as e:
+        hip.copy(dy.ptr, dx.ptr, 11)
+    assert e.value.code == -5
+    dw = hip.alloc(4 * 8)
+    with pytest.raises(pkg.SlmError):
+        hip.gather(dy.ptr, dw.ptr, np.array([4], np.uint32), 2)  # id past the rows
+    with pytest.raises(pkg.SlmError):
+        hip.linear(dy.ptr, dw.ptr, 10, 4, dx.ptr, 3)  # x too short
+
+
+@pytest.mark.parametrize("m,heads,dh", [(1, 12, 64), (256, 12, 64), (37, 4, 8), (5, 2, 16)])
+def test_gla(hip, m, heads, dh):
+    q, k, v = rnd(m, heads, dh), rnd(m, heads, dh), rnd(m, heads, dh)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    dec = rnd(m, heads)
+    bias = rnd(heads) - 3
+    s0 = rnd(heads, dh, dh, scale=0.1)
+    bufs = [hip.upload(t) for t in (q, k, v, dec, bias, s0)]
+    dq, dk, dv, dd, db, ds = bufs
+    dy = hip.alloc(m * heads * dh)
+    hip.gla(dy.ptr, ds.ptr, dq.ptr, dk.ptr, dv.ptr, dd.ptr, db.ptr, m, heads, dh)
+    wy, wst = O.gla(s0, q, k, v, dec, bias, m, heads, dh)
+    assert rel(dy.read(), wy) < 2e-6
+    assert rel(ds.read(), wst) < 2e-6
+    # token by token leaves the same bits
+    ds2 = hip.upload(s0)
+    dy1 = hip.alloc(heads * dh)
+    ys = []
+    for i in range(m):
+        hip.gla(dy1.ptr, ds2.ptr, dq.at(i * heads * dh), dk.at(i * heads * dh),
+                dv.at(i * heads * dh), dd.at(i * heads), db.ptr, 1, heads, dh)
+        ys.append(dy1.read())
+    assert np.array_equal(np.concatenate(ys), dy.read())
+    assert np.array_equal(ds2.read(), ds.read())
+
+
+ATTN_CASES = [
+    dict(pos=0, m=1, reach=8, gap=0, cap=24, heads=4, key_heads=4, dh=8),
+    dict(pos=30, m=7, reach=8, gap=0, cap=24, heads=4, key_heads=4, dh=8),
+    dict(pos=50, m=9, reach=O.USIZE_MAX, gap=8, cap=64, heads=4, key_heads=2, dh=8),
+    dict(pos=2, m=3, reach=O.USIZE_MAX, gap=8, cap=64, heads=4, key_heads=1, dh=8),
+    dict(pos=4100, m=1, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
+    dict(pos=5000, m=256, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
+    dict(pos=9000, m=40, reach=O.USIZE_MAX, gap=4096, cap=16384, heads=12, key_heads=4, dh=64),
+    dict(pos=600, m=33, reach=200, gap=0, cap=456, heads=6, key_heads=3, dh=32),
+]
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"p{c['pos']}m{c['m']}kh{c['key_heads']}")
+def test_attend(hip, case):
+    a = dict(case, scale=float(1 / np.sqrt(case["dh"])))
+    m, heads, kh, dh, cap = a["m"], a["heads"], a["key_heads"], a["dh"], a["cap"]
+    q = rnd(m, heads, dh)
+    k = rnd(kh, cap, dh)
+    v = rnd(kh, cap, dh)
+    dq, dk, dv, dy = hip.upload(q), hip.upload(k), hip.upload(v), hip.alloc(m * heads * dh)
+    hip.attend(dy.ptr, dq.ptr, dk.ptr, dv.ptr, **a)
+    got = dy.read()
+    want = O.attend(q, k, v, **a)
+    assert rel(got, want) < 2e-6
+    # each query alone (m = 1 at its own position) gives the same bits
+    d1 = hip.alloc(heads * dh)
+    for i in sorted({0, m // 2, m - 1}):
+        hip.attend(d1.ptr, dq.at(i * heads * dh), dk.ptr, dv.ptr, **dict(a, pos=a["pos"] + i, m=1))
+        assert np.array_equal(d1.read(), got[i * heads * dh:(i + 1) * heads * dh]), i
