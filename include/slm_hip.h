@@ -143,6 +143,8 @@ int slm_hip_graph_stats(slm_hip* ctx, uint64_t* launched, uint64_t* captured,
  * each) and writes the four result elements it holds to out[4l .. 4l+3] (256 floats).
  * Tests use it to pin the lane layout the kernels assume. */
 int slm_hip_probe_mfma(slm_hip* ctx, float* out, const float* a, const float* b);
+/* The context's hipStream_t, so a caller can time its work with HIP events. */
+int slm_hip_stream(slm_hip* ctx, void** out);
 
 #ifdef __cplusplus
 }

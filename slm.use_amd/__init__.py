@@ -90,6 +90,7 @@ _SIGS = {
     "slm_hip_graph_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                  C.POINTER(C.c_uint64)]),
     "slm_hip_probe_mfma": (_i, [_p, _p, _p, _p]),
+    "slm_hip_stream": (_i, [_p, C.POINTER(_p)]),
     "slm_model_load": (_i, [_p, C.c_char_p, C.POINTER(_p)]),
     "slm_model_free": (None, [_p]),
     "slm_model_error": (C.c_char_p, [_p]),
@@ -262,6 +263,11 @@ class Hip:
     def attend(self, y, q, k, v, **a):
         args = Attn(**a)
         self.check(lib.slm_hip_attend(self.ctx, y, None, q, k, v, C.byref(args)))
+
+    def stream(self) -> int:
+        s = _p()
+        self.check(lib.slm_hip_stream(self.ctx, C.byref(s)))
+        return s.value or 0
 
     def probe_mfma(self, out, a, b):
         self.check(lib.slm_hip_probe_mfma(self.ctx, out, a, b))

@@ -427,7 +427,8 @@ int slm_hip_open(int device, slm_hip** out) {
     OPEN_HIP(hipSetDevice(device));
     hipDeviceProp_t prop;
     OPEN_HIP(hipGetDeviceProperties(&prop, device));
-    snprintf(c->name, sizeof c->name, "hip (%s, %s)", prop.name, prop.gcnArchName);
+    snprintf(c->name, sizeof c->name, "hip (%s, %s)", prop.name[0] ? prop.name : "AMD GPU",
+             prop.gcnArchName);
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return bail(fail(c, SLM_E_UNSUPPORTED, "device %d is %s; this build is for gfx950",
                          device, prop.gcnArchName));
@@ -914,6 +915,12 @@ int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const fl
 }
 
 // ---- diagnostics ----
+
+int slm_hip_stream(slm_hip* c, void** out) {
+    if (!c || !out) return SLM_E_INVALID;
+    *out = (void*)c->stream;
+    return SLM_OK;
+}
 
 // Runs one 16x16x4 f32 MFMA on lane inputs a[64], b[64] (device) into out[256].
 int slm_hip_probe_mfma(slm_hip* c, float* out, const float* a, const float* b) {

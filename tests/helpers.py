@@ -29,3 +29,23 @@ def rel(a, b) -> float:
 def greedy(logits) -> int:
     """src/sample.rs:179-184: the first maximum wins."""
     return int(np.argmax(logits))
+
+
+def attend64(q, k, v, pos, m, reach, gap, cap, heads, key_heads, dh, scale):
+    """Softmax attention in float64 over positions picked by number (ops.rs:48-66)."""
+    out = np.zeros((m, heads, dh))
+    group = heads // key_heads
+    kk = np.asarray(k, np.float64).reshape(key_heads, cap, dh)
+    vv = np.asarray(v, np.float64).reshape(key_heads, cap, dh)
+    q = np.asarray(q, np.float64).reshape(m, heads, dh)
+    for i in range(m):
+        p = pos + i
+        lo, hi = max(0, p - reach + 1), max(0, p + 1 - gap)
+        if hi <= lo:
+            continue
+        slots = np.arange(lo, hi) % cap
+        for h in range(heads):
+            s = kk[h // group, slots] @ q[i, h] * scale
+            e = np.exp(s - s.max())
+            out[i, h] = (e / e.sum()) @ vv[h // group, slots]
+    return out.reshape(-1)

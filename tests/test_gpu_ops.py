@@ -5,14 +5,15 @@ give the same bits.
 
 Tolerances: bit-exact where the kernel follows the reference's order exactly (data
 movement, rms, l2norm, rope, rope_table); otherwise 2e-6 relative to the largest output
-(linear, attend, gla: MFMA / tree reassociation; silu: device expf).
+(linear, gla: MFMA / tree reassociation; silu: device expf), and for attention 1e-5
+relative plus an error against float64 no larger than twice the oracle's own.
 """
 
 import numpy as np
 import pytest
 
 import oracle as O
-from helpers import rel
+from helpers import attend64, rel
 
 pytestmark = pytest.mark.gpu
 
@@ -183,9 +184,10 @@ def test_bounds_are_checked_before_launch(hip, pkg):
     with pytest.raises(pkg.SlmError) as e:
         hip.copy(dy.ptr, dx.ptr, 11)
     assert e.value.code == -5
-    dw = hip.alloc(4 * 8)
+    dw = hip.alloc(4 * 8)  # 16 rows of 2
+    hip.gather(dy.ptr, dw.ptr, np.array([15], np.uint32), 2)
     with pytest.raises(pkg.SlmError):
-        hip.gather(dy.ptr, dw.ptr, np.array([4], np.uint32), 2)  # id past the rows
+        hip.gather(dy.ptr, dw.ptr, np.array([16], np.uint32), 2)  # id past the rows
     with pytest.raises(pkg.SlmError):
         hip.linear(dy.ptr, dw.ptr, 10, 4, dx.ptr, 3)  # x too short
 
@@ -240,7 +242,11 @@ def test_attend(hip, case):
     hip.attend(dy.ptr, dq.ptr, dk.ptr, dv.ptr, **a)
     got = dy.read()
     want = O.attend(q, k, v, **a)
-    assert rel(got, want) < 2e-6
+    exact = attend64(q, k, v, **a)
+    # both are fp32 sums over up to thousands of keys in different orders: the GPU is
+    # judged against float64 no worse than the reference's own order is
+    assert rel(got, want) < 1e-5
+    assert rel(got, exact) <= 2 * rel(want, exact) + 1e-7
     # each query alone (m = 1 at its own position) gives the same bits
     d1 = hip.alloc(heads * dh)
     for i in sorted({0, m // 2, m - 1}):
