@@ -1,0 +1,327 @@
+"""Token-loop benchmark on one MI355X: the reference's `slm bench` sequence
+(src/main.rs:285-315) on the 86M-class synthetic model.
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--loops 4] [--no-cpu]
+
+Workload (one GPU): model "a86" (d 768, 12 x 64 heads, FFN 4x, vocab 32000, window 4096,
+prelude SS / core LS / coda SS, seeded N(0, 0.02) fp32 weights), R loops. A session reads
+16 warm-up tokens, then a 4096-token uniform-random prompt in 256-token chunks (timed:
+prefill tok/s, including the final logits read, main.rs:200-205) — which fills the
+sliding window — then decodes greedily, reading the logits back every token
+(main.rs:207-223): `--warmup` untimed tokens, then `--steps` timed ones. A "step" is one
+decoded token.
+
+Printed: one JSON line. `value` is decode tok/s. `roofline` is the dominant decode kernel
+(the m = 1 GEMV, slm_linear_small_v) against HBM, timed with HIP events on the backend's
+stream over one decode step's exact sequence of GEMV shapes; `decode_roofline` is the whole
+step against HBM (algorithmic bytes per token); `prefill_roofline` is prefill against fp32
+MFMA peak. `cpu_baseline` times the oracle (a C++ restatement of src/cpu.rs +
+src/model.rs, OpenMP over the host's cores) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK = 8.0e12            # bytes/s, MI355X
+FP32_MFMA_PEAK = 157.3e12    # flop/s, MI355X dense fp32 matrix
+
+
+def package():
+    spec = importlib.util.spec_from_file_location(
+        "slm_use_amd", ROOT / "slm.use_amd" / "__init__.py",
+        submodule_search_locations=[str(ROOT / "slm.use_amd")])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["slm_use_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------------------
+# algorithmic work of the token loop
+# ---------------------------------------------------------------------------------------
+
+def block_linears(cfg, kind, pos_plus_m_over_far=True):
+    d, H = cfg["d_model"], cfg["n_heads"]
+    dh = d // H
+    hid = int(round(cfg.get("mlp_mult", 4.0) * d))
+    kd = cfg["global_kv_heads"] * dh
+    if kind == "S":
+        mix = [(3 * d, d), (d, d)]
+    elif kind == "L":
+        mix = [(4 * d, d), (H, d), (d, d)]
+    else:
+        mix = [(d, d), (2 * kd, d)] + ([(2 * kd, d)] if cfg["global_kshift"] else [])
+        mix += [(d, d)] if pos_plus_m_over_far else []
+    return mix + [(2 * hid, d), (d, hid)]
+
+
+def step_linears(cfg, loops):
+    """(rows, cols) of every linear of one m = 1 advance, in call order (model.rs:563-624)."""
+    out = []
+    for k in cfg["prelude"]:
+        out += block_linears(cfg, k)
+    if cfg["core"]:
+        out.append((cfg["d_model"], cfg["d_model"]))
+        for _ in range(loops):
+            for k in cfg["core"]:
+                out += block_linears(cfg, k)
+    for k in cfg["coda"]:
+        out += block_linears(cfg, k)
+    out.append((cfg["vocab_size"], cfg["d_model"]))
+    return out
+
+
+def instances(cfg, loops):
+    kinds = cfg["prelude"] + cfg["core"] * loops + cfg["coda"]
+    return {k: kinds.count(k) for k in "SLG"}
+
+
+def decode_bytes(cfg, loops, pos):
+    """Algorithmic HBM bytes of one decoded token at position `pos`: every weight read as
+    executed, the K/V window read and the new K/V written, GLA state read + written."""
+    d, H, W = cfg["d_model"], cfg["n_heads"], cfg["window"]
+    dh = d // H
+    n = instances(cfg, loops)
+    w = sum(r * c for r, c in step_linears(cfg, loops))
+    keys = min(pos + 1, W)
+    far = W if cfg.get("global_far") else 0
+    gkeys = max(pos + 1 - far, 0)
+    kd = cfg["global_kv_heads"] * dh
+    return 4 * (w + n["S"] * (2 * keys * d + 2 * d) + n["L"] * 2 * H * dh * dh
+                + n["G"] * (2 * gkeys * kd + 2 * kd))
+
+
+def prefill_flops(cfg, loops, start, count):
+    """Algorithmic flops of reading `count` prompt tokens from position `start`."""
+    d, H, W = cfg["d_model"], cfg["n_heads"], cfg["window"]
+    dh = d // H
+    n = instances(cfg, loops)
+    lin = 2 * sum(r * c for r, c in step_linears(cfg, loops)[:-1])  # no logits per token
+    p = np.arange(start, start + count)
+    keys = np.minimum(p + 1, W).sum()
+    far = W if cfg.get("global_far") else 0
+    gkeys = np.maximum(p + 1 - far, 0).sum()
+    return (lin * count + n["S"] * 4 * d * keys + n["G"] * 4 * d * gkeys
+            + n["L"] * 4 * H * dh * dh * count)
+
+
+# ---------------------------------------------------------------------------------------
+# HIP events on the backend's stream
+# ---------------------------------------------------------------------------------------
+
+class Events:
+    def __init__(self, stream: int):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.stream = C.c_void_p(stream)
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+
+    def new(self):
+        e = C.c_void_p()
+        assert self.hip.hipEventCreate(C.byref(e)) == 0
+        return e
+
+    def record(self, e):
+        assert self.hip.hipEventRecord(e, self.stream) == 0
+
+    def sync(self, e):
+        assert self.hip.hipEventSynchronize(e) == 0
+
+    def ms(self, a, b) -> float:
+        out = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(out), a, b) == 0
+        return out.value
+
+
+def time_gemv_sequence(pkg, hip, shapes, reps=20):
+    """Average duration of one launch of the decode GEMV over one decode step's exact
+    sequence of shapes, each launch bracketed by its own pair of HIP events on the
+    backend's stream; and the algorithmic bytes per launch (weights + input + output)."""
+    rng = np.random.default_rng(0)
+    uniq = sorted(set(shapes))
+    w = {s: hip.upload(rng.standard_normal(s[0] * s[1], dtype=np.float32) * np.float32(0.02))
+         for s in uniq}
+    x = hip.upload(rng.standard_normal(max(c for _, c in uniq), dtype=np.float32))
+    y = hip.alloc(max(r for r, _ in uniq))
+    ev = Events(hip.stream())
+    pairs = [(ev.new(), ev.new()) for _ in shapes]
+    hip.set_graphs(False)
+    for _ in range(3):  # warm
+        for r, c in shapes:
+            hip.linear(y.ptr, w[(r, c)].ptr, r, c, x.ptr, 1)
+    total = 0.0
+    for _ in range(reps):
+        for (a, b), (r, c) in zip(pairs, shapes):
+            ev.record(a)
+            hip.linear(y.ptr, w[(r, c)].ptr, r, c, x.ptr, 1)
+            ev.record(b)
+        ev.sync(pairs[-1][1])
+        total += sum(ev.ms(a, b) for a, b in pairs)
+    hip.set_graphs(True)
+    for b in list(w.values()) + [x, y]:
+        b.free()
+    per_launch_s = total / 1e3 / (reps * len(shapes))
+    bytes_per_launch = sum(4 * (r * c + c + r) for r, c in shapes) / len(shapes)
+    return per_launch_s, bytes_per_launch
+
+
+# ---------------------------------------------------------------------------------------
+# the CPU baseline: the oracle on the host cores
+# ---------------------------------------------------------------------------------------
+
+def cpu_baseline(folder, cfg, loops, prompt, decode_tokens):
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    cores = os.cpu_count() or 1
+    omp = int(os.environ.get("OMP_NUM_THREADS", cores))
+    m = O.Model(folder)
+    se = m.session(loops)
+    se.feed(prompt[:16], 256)
+    t = time.perf_counter()
+    se.feed(prompt, 256)
+    se.logits()
+    fill_s = time.perf_counter() - t
+    ids = []
+    t = time.perf_counter()
+    for _ in range(decode_tokens):
+        ids.append(O.pick(se.logits()))
+        se.step(ids[-1])
+    dec_s = time.perf_counter() - t
+    return dict(value=round(decode_tokens / dec_s, 2), unit="tok/s", cores=omp, kind="port",
+                sample=(f"oracle (C++ restatement of src/cpu.rs + src/model.rs, OpenMP) on the "
+                        f"same model and prompt: 16 + {len(prompt)} prompt tokens in 256-chunks, "
+                        f"then {decode_tokens} greedy decode steps timed (of the GPU run's "
+                        f"steps); {omp} threads of {cores} visible cores"),
+                prefill_tok_s=round(len(prompt) / fill_s, 1), ids=ids)
+
+
+# ---------------------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--loops", type=int, default=4)
+    ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-steps", type=int, default=32)
+    ap.add_argument("--no-graphs", action="store_true")
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py runs on one GPU: --gpus {a.gpus} (WORLD_SIZE {world}) is not "
+              "supported; the token loop has no multi-GPU path in this build", file=sys.stderr)
+        sys.exit(2)
+
+    pkg = package()
+    sys.path.insert(0, str(ROOT / "slm.use_amd"))
+    import synth
+
+    cache = Path(os.environ.get("SLM_MODEL_CACHE", "/tmp")) / "slm_models"
+    folder = synth.write_model(cache / "a86-2", "a86", 2)
+    cfg = synth.A86
+    prompt = synth.tokens(a.prompt, cfg["vocab_size"], seed=3)
+
+    hip = pkg.Hip(0)
+    if a.no_graphs:
+        hip.set_graphs(False)
+    log("device:", hip.name())
+    model = pkg.Model(hip, folder)
+    se = model.session(a.loops)
+    se.feed(prompt[:16], 256)  # main.rs:309
+    se.logits()
+    t = time.perf_counter()
+    se.feed(prompt, 256)
+    se.logits()
+    fill_s = time.perf_counter() - t
+    prefill = len(prompt) / fill_s
+    log(f"prefill: {prefill:.1f} tok/s ({len(prompt)} tokens, R={a.loops})")
+    warm_ids = se.decode_greedy(a.warmup).tolist() if a.warmup else []
+    se.logits()
+    pos0 = se.pos
+    t = time.perf_counter()
+    ids = se.decode_greedy(a.steps)
+    se.logits()  # waits for the last step
+    dec_s = time.perf_counter() - t
+    tok_s = a.steps / dec_s
+    log(f"decode: {tok_s:.1f} tok/s over {a.steps} steps at pos {pos0}..{se.pos - 1}")
+    stats = hip.graph_stats()
+
+    # whole-step roofline (decode) and MFMA utilisation (prefill)
+    bpt = np.mean([decode_bytes(cfg, a.loops, p) for p in range(pos0, pos0 + a.steps)])
+    fl = prefill_flops(cfg, a.loops, 16, len(prompt))
+    # dominant kernel: the decode GEMV over one step's shapes, timed live with events
+    shapes = step_linears(cfg, a.loops)
+    per_launch, bpl = time_gemv_sequence(pkg, hip, shapes)
+    gemv_bw = bpl / per_launch
+    log(f"decode GEMV: {per_launch * 1e6:.2f} us/launch avg over {len(shapes)} shapes, "
+        f"{gemv_bw / 1e9:.0f} GB/s")
+
+    cpu = None
+    if not a.no_cpu:
+        n = min(a.cpu_steps, a.steps)
+        log(f"CPU baseline: oracle prefill {len(prompt)} + decode {n} ...")
+        cpu = cpu_baseline(folder, cfg, a.loops, prompt, n)
+        same = cpu.pop("ids") == (warm_ids + ids.tolist())[:n]
+        cpu["same_greedy_ids_as_gpu"] = bool(same)
+        log(f"CPU: prefill {cpu['prefill_tok_s']} tok/s, decode {cpu['value']} tok/s, "
+            f"same ids: {same}")
+
+    line = {
+        "metric": f"decode tok/s @R={a.loops}, full {cfg['window']} window (86M fp32)",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(1e3 * dec_s / a.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded N(0,0.02) fp32 weights, uniform random token ids",
+        "config": {"workload": "a86 decode after a 4096-token prompt (window full), greedy, "
+                               "logits read back every token",
+                   "loops": a.loops, "d_model": 768, "heads": 12, "head_dim": 64,
+                   "ffn": 3072, "vocab": 32000, "window": 4096, "layers": "SS|LS|SS",
+                   "prompt_tokens": len(prompt), "decode_from_pos": pos0},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_bw / 1e9, 1), "peak": 8000.0,
+                     "unit": "GB/s", "frac": round(gemv_bw / HBM_PEAK, 4), "traffic": None,
+                     "kernel": "slm_linear_small_v",
+                     "bytes_per_launch": round(bpl), "us_per_launch": round(per_launch * 1e6, 3)},
+        "decode_roofline": {"bound": "hbm", "bytes_per_token": round(bpt),
+                            "achieved": round(bpt * tok_s / 1e9, 1), "peak": 8000.0,
+                            "unit": "GB/s", "frac": round(bpt * tok_s / HBM_PEAK, 4)},
+        "prefill": {"value": round(prefill, 1), "unit": "tok/s", "prompt_tokens": len(prompt),
+                    "flops_per_token": round(fl / len(prompt)),
+                    "achieved_tflops": round(fl / fill_s / 1e12, 2),
+                    "peak_tflops": FP32_MFMA_PEAK / 1e12,
+                    "frac": round(fl / fill_s / FP32_MFMA_PEAK, 4)},
+        "graphs": stats,
+        "cpu_baseline": cpu,
+        "reference_published": {"decode_tok_s_r4_rtx5080": 209, "prefill_tok_s_r4_rtx5080": 2819,
+                                "note": "README.md:143-147; different GPU and model dims"},
+    }
+    print(json.dumps(line), flush=True)
+    del se, model
+    hip.close()
+
+
+if __name__ == "__main__":
+    main()

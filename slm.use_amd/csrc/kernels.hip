@@ -142,41 +142,52 @@ KERNEL void slm_rope_table(float* __restrict__ cs, float* __restrict__ sn,
 
 // Sum of squares of in[0..size) in the reference's order: lane j keeps the running sum of
 // elements j, j+16, ...; the 16 sums are added left to right from -0.0, then the tail.
-__device__ __forceinline__ float dot16_self(const float* in, long long size, int l) {
-    long long chunks = size / 16;
+// `in` may be global or LDS memory.
+__device__ __forceinline__ float dot16_self(const float* in, int size, int l) {
+    int chunks = size / 16;
     float acc = 0.0f;
-    for (long long c = 0; c < chunks; c++) {
+    for (int c = 0; c < chunks; c++) {
         float v = in[c * 16 + l];
         acc = acc + v * v;
     }
     float s = -0.0f;
     for (int t = 0; t < 16; t++) s = s + __shfl(acc, t, 16);
     float tail = -0.0f;
-    for (long long j = chunks * 16; j < size; j++) tail = tail + in[j] * in[j];
+    for (int j = chunks * 16; j < size; j++) tail = tail + in[j] * in[j];
     return s + tail;
 }
 
-// cpu.rs:187-207: r = 1/sqrt(dot/size + eps); y = x·r·w.
-KERNEL void __launch_bounds__(256) slm_rms(float* __restrict__ y, const float* __restrict__ x,
-                                           const float* __restrict__ w, long long groups,
-                                           long long size, float eps) {
-    long long grp = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
-    int l = threadIdx.x & 15;
-    if (grp >= groups) return;  // the 16 lanes of a group leave together
-    const float* in = x + grp * size;
-    float r = 1.0f / sqrtf(dot16_self(in, size, l) / (float)size + eps);
-    for (long long j = l; j < size; j += 16) y[grp * size + j] = in[j] * r * w[j];
+// Up to 16 groups per workgroup: the groups are staged in LDS with coalesced loads (rows
+// padded to an odd stride against bank conflicts), then 16 lanes per group run the
+// reference's sums. mode 0: rms (cpu.rs:187-207), r = 1/sqrt(dot/size + eps), y = x·r·w;
+// mode 1: l2norm (cpu.rs:270-282), r = 1/max(sqrt(dot), 1e-12), y = x·r.
+template <int MODE>
+__device__ void norm_body(float* __restrict__ y, const float* __restrict__ x,
+                          const float* __restrict__ w, int groups, int size, float eps, int G) {
+    extern __shared__ float buf[];
+    int stride = size | 1;
+    long long g0 = (long long)blockIdx.x * G;
+    int ng = (int)min((long long)G, groups - g0);
+    const float* src = x + g0 * size;
+    for (int i = threadIdx.x; i < ng * size; i += blockDim.x) buf[(i / size) * stride + i % size] = src[i];
+    __syncthreads();
+    int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+    if (grp >= ng) return;  // the 16 lanes of a group leave together
+    const float* in = buf + grp * stride;
+    float d = dot16_self(in, size, l);
+    float r = MODE == 0 ? 1.0f / sqrtf(d / (float)size + eps) : 1.0f / fmaxf(sqrtf(d), 1e-12f);
+    float* out = y + (g0 + grp) * size;
+    for (int j = l; j < size; j += 16) out[j] = MODE == 0 ? in[j] * r * w[j] : in[j] * r;
 }
 
-// cpu.rs:270-282: r = 1/max(sqrt(dot), 1e-12); y = x·r.
-KERNEL void __launch_bounds__(256) slm_l2norm(float* __restrict__ y, const float* __restrict__ x,
-                                              long long groups, long long size) {
-    long long grp = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
-    int l = threadIdx.x & 15;
-    if (grp >= groups) return;
-    const float* in = x + grp * size;
-    float r = 1.0f / fmaxf(sqrtf(dot16_self(in, size, l)), 1e-12f);
-    for (long long j = l; j < size; j += 16) y[grp * size + j] = in[j] * r;
+KERNEL void __launch_bounds__(256) slm_rms(float* y, const float* x, const float* w, int groups,
+                                           int size, float eps, int G) {
+    norm_body<0>(y, x, w, groups, size, eps, G);
+}
+
+KERNEL void __launch_bounds__(256) slm_l2norm(float* y, const float* x, int groups, int size,
+                                              int G) {
+    norm_body<1>(y, x, nullptr, groups, size, 0.0f, G);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -274,7 +285,9 @@ __device__ __forceinline__ f4 ld4(const float* __restrict__ p, long long row, lo
 }
 
 // m <= 16: one workgroup per 16 rows, one wave per slice (waves take slices w, w+W, ...),
-// slice partials meet in LDS and one pass adds them in order.
+// slice partials meet in LDS and one pass adds them in order. A wave loads its whole
+// slice (16 rows x 256 columns of w, and the tokens' columns) before the chain starts, so
+// one memory latency covers it.
 template <bool VEC>
 __device__ void linear_small_body(float* __restrict__ y, const float* __restrict__ w,
                                   const float* __restrict__ x, int rows, int cols, int m) {
@@ -284,17 +297,27 @@ __device__ void linear_small_body(float* __restrict__ y, const float* __restrict
     long long r0 = (long long)blockIdx.x * 16;
     int kblocks = (cols + 15) >> 4, nsl = (kblocks + 15) >> 4;
     for (int s = wave; s < nsl; s += waves) {
+        int nkb = min(16, kblocks - s * 16);
+        f4 wa[16], xb[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            long long c = (long long)(s * 16 + u) * 16 + g * 4;
+            wa[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            xb[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (u < nkb) {
+                wa[u] = ld4<VEC>(w, r0 + i, rows, cols, c);
+                xb[u] = ld4<VEC>(x, i, m, cols, c);
+            }
+        }
         f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        int kb1 = min(s * 16 + 16, kblocks);
-#pragma unroll 4
-        for (int kb = s * 16; kb < kb1; kb++) {
-            long long c = (long long)kb * 16 + g * 4;
-            f4 a = ld4<VEC>(w, r0 + i, rows, cols, c);
-            f4 b = ld4<VEC>(x, i, m, cols, c);
-            acc = mfma4(a.x, b.x, acc);
-            acc = mfma4(a.y, b.y, acc);
-            acc = mfma4(a.z, b.z, acc);
-            acc = mfma4(a.w, b.w, acc);
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            if (u < nkb) {
+                acc = mfma4(wa[u].x, xb[u].x, acc);
+                acc = mfma4(wa[u].y, xb[u].y, acc);
+                acc = mfma4(wa[u].z, xb[u].z, acc);
+                acc = mfma4(wa[u].w, xb[u].w, acc);
+            }
         }
         float* p = part + s * 256;
 #pragma unroll
@@ -431,7 +454,8 @@ __device__ __forceinline__ Col column(int c, long long qtile, long long pos, int
 }
 
 // One 64-key segment for the wave's 16 columns. The lane keeps its column's (m, l) and
-// o for dims 16dt + 4g + r.
+// o for dims 16dt + 4g + r. The keys and values of every tile some column sees are loaded
+// before any arithmetic (one memory latency per segment).
 template <int DT>
 __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __restrict__ kb,
                              const float* __restrict__ vb, long long seg_lo, long long cap,
@@ -442,23 +466,47 @@ __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __
     lo = 0.0f;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    bool need[4];
+    f4 kr[4][DT];
+    float vr[4][4][DT];
+#pragma unroll
     for (int st = 0; st < 4; st++) {
         long long b0 = seg_lo + 16 * st;
         bool sees = col.valid && col.lo < b0 + 16 && col.hi > b0;
-        if (__ballot(sees) == 0) continue;
+        need[st] = __ballot(sees) != 0;
+        if (need[st]) {
+            // A operand of the scores: key b0 + i, dims 16t + 4g .. +3
+            const float* krow = kb + ((b0 + i) % cap) * dh;
+#pragma unroll
+            for (int t = 0; t < DT; t++) {
+                int c = 16 * t + 4 * g;
+                kr[st][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (c < dh) kr[st][t] = *(const f4*)(krow + c);
+            }
+            // A operand of P·V for MFMA r: value of key b0 + 4g + r, dim 16dt + i
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float* vrow = vb + ((b0 + 4 * g + r) % cap) * dh;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    int dim = 16 * dt + i;
+                    vr[st][r][dt] = dim < dh ? vrow[dim] : 0.0f;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+        if (!need[st]) continue;
+        long long b0 = seg_lo + 16 * st;
         // scores: lane holds S[key b0 + 4g + r][column i]
-        long long kslot = (b0 + i) % cap;
-        const float* krow = kb + kslot * dh;
         f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < DT; t++) {
-            int c = 16 * t + 4 * g;
-            f4 a = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (c < dh) a = *(const f4*)(krow + c);
-            s = mfma4(a.x, qv[t].x, s);
-            s = mfma4(a.y, qv[t].y, s);
-            s = mfma4(a.z, qv[t].z, s);
-            s = mfma4(a.w, qv[t].w, s);
+            s = mfma4(kr[st][t].x, qv[t].x, s);
+            s = mfma4(kr[st][t].y, qv[t].y, s);
+            s = mfma4(kr[st][t].z, qv[t].z, s);
+            s = mfma4(kr[st][t].w, qv[t].w, s);
         }
         float sv[4];
         bool any = false;
@@ -488,16 +536,9 @@ __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) on[dt] = o[dt] * alpha;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            long long kp = b0 + 4 * g + r;
-            const float* vrow = vb + (kp % cap) * dh;
+        for (int r = 0; r < 4; r++)
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                int dim = 16 * dt + i;
-                float a = dim < dh ? vrow[dim] : 0.0f;
-                on[dt] = mfma4(a, p[r], on[dt]);
-            }
-        }
+            for (int dt = 0; dt < DT; dt++) on[dt] = mfma4(vr[st][r][dt], p[r], on[dt]);
         if (anyi) {
             lo = lo * alpha + rs;
             mo = mnew;

@@ -788,6 +788,19 @@ int slm_hip_rope_table(slm_hip* c, float* cs, float* sn, const float* inv, size_
 
 // ---- normalisation ----
 
+static int norm_launch(slm_hip* c, hipFunction_t f, float* y, const float* x, const float* w,
+                size_t groups, size_t size, float eps, bool rms) {
+    if (!fits_int(groups) || !fits_int(size) || groups * size > (size_t)INT_MAX)
+        return fail(c, SLM_E_UNSUPPORTED, "%s: %zu groups of %zu", rms ? "rms" : "l2norm", groups, size);
+    size_t stride = size | 1;
+    size_t G = std::min<size_t>(16, std::max<size_t>(1, 16384 / stride));
+    if (G * stride * 4 > 65536) return fail(c, SLM_E_UNSUPPORTED, "norm: size %zu is above 16383", size);
+    uint32_t blocks = (uint32_t)((groups + G - 1) / G);
+    uint32_t shmem = (uint32_t)(G * stride * 4);
+    if (rms) return go(c, f, blocks, 1, 1, 256, shmem, y, x, w, (int)groups, (int)size, eps, (int)G);
+    return go(c, f, blocks, 1, 1, 256, shmem, y, x, (int)groups, (int)size, (int)G);
+}
+
 int slm_hip_rms(slm_hip* c, float* y, const float* x, const float* w, size_t groups, size_t size,
                 float eps) {
     if (!c) return SLM_E_INVALID;
@@ -795,8 +808,7 @@ int slm_hip_rms(slm_hip* c, float* y, const float* x, const float* w, size_t gro
     NEED(c, "rms", x, groups * size);
     NEED(c, "rms", w, size);
     if (!groups || !size) return SLM_OK;
-    return go(c, c->k.rms, blocks_for(groups, 16, UINT32_MAX), 1, 1, 256, 0, y, x, w,
-              (long long)groups, (long long)size, eps);
+    return norm_launch(c, c->k.rms, y, x, w, groups, size, eps, true);
 }
 
 int slm_hip_l2norm(slm_hip* c, float* y, const float* x, size_t heads, size_t dh) {
@@ -804,8 +816,7 @@ int slm_hip_l2norm(slm_hip* c, float* y, const float* x, size_t heads, size_t dh
     NEED(c, "l2norm", y, heads * dh);
     NEED(c, "l2norm", x, heads * dh);
     if (!heads || !dh) return SLM_OK;
-    return go(c, c->k.l2norm, blocks_for(heads, 16, UINT32_MAX), 1, 1, 256, 0, y, x,
-              (long long)heads, (long long)dh);
+    return norm_launch(c, c->k.l2norm, y, x, nullptr, heads, dh, 0.0f, false);
 }
 
 // ---- linear ----
