@@ -126,17 +126,25 @@ int slm_hip_store(slm_hip* ctx, float* cache, const float* src, size_t pos, size
 int slm_hip_attend(slm_hip* ctx, float* y, float* scores, const float* q, const float* k,
                    const float* v, const slm_attn* a);
 
-/* ---- step graphs (no trait counterpart; a backend setting like cuda.rs's one stream) ----
- * When on (the default), the operations of one advance — from rope_table to flush — are
- * recorded instead of launched; flush replays a cached hipGraph when the step matches a
- * recorded one (same operations, buffers and sizes; positions, ids and factors may
- * differ) and captures a new one otherwise. A read, free or upload inside a step runs
- * what was recorded so far and finishes the step eagerly. Results are identical either
- * way: the graph runs the same kernels. */
+/* ---- steps (no trait counterpart; backend settings like cuda.rs's one stream) ----
+ * With step graphs or fusion on (both are by default), the operations of one advance —
+ * from rope_table to flush — are recorded instead of launched. At flush the planner
+ * lowers the step (fusing one-token runs when fusion is on); with graphs on, flush
+ * replays a cached hipGraph when the step matches a recorded one (same operations,
+ * buffers and sizes; positions, ids and factors may differ) and captures a new one
+ * otherwise, and with graphs off it launches the planned kernels directly. A read, free
+ * or upload inside a step runs what was recorded so far and finishes the step eagerly.
+ * Results are identical in every mode: the same arithmetic runs. */
 int slm_hip_set_graphs(slm_hip* ctx, int on);
+/* Fusion (on by default): the planner lowers a recorded one-token step into fused
+ * kernels (prologue vector ops + GEMV + epilogue) that compute the same values with the
+ * same arithmetic as the per-op kernels. Off: one launch per operation. */
+int slm_hip_set_fusion(slm_hip* ctx, int on);
 /* Counters for tests and benchmarks: graphs launched, graphs captured, eager steps. */
 int slm_hip_graph_stats(slm_hip* ctx, uint64_t* launched, uint64_t* captured,
                         uint64_t* eager);
+/* Operations recorded and kernel launches planned for the last step that was lowered. */
+int slm_hip_last_plan(slm_hip* ctx, uint64_t* ops, uint64_t* kernels);
 
 /* ---- diagnostics (no trait counterpart) ----
  * One v_mfma_f32_16x16x4f32 on one wave: lane l supplies a[l] and b[l] (device, 64 floats

@@ -87,8 +87,10 @@ _SIGS = {
     "slm_hip_store": (_i, [_p, _p, _p, _sz, _sz, _sz, _sz, _sz]),
     "slm_hip_attend": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_set_graphs": (_i, [_p, _i]),
+    "slm_hip_set_fusion": (_i, [_p, _i]),
     "slm_hip_graph_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                  C.POINTER(C.c_uint64)]),
+    "slm_hip_last_plan": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "slm_hip_probe_mfma": (_i, [_p, _p, _p, _p]),
     "slm_hip_stream": (_i, [_p, C.POINTER(_p)]),
     "slm_model_load": (_i, [_p, C.c_char_p, C.POINTER(_p)]),
@@ -199,6 +201,14 @@ class Hip:
 
     def set_graphs(self, on: bool):
         self.check(lib.slm_hip_set_graphs(self.ctx, int(on)))
+
+    def last_plan(self):
+        a, b = C.c_uint64(), C.c_uint64()
+        self.check(lib.slm_hip_last_plan(self.ctx, C.byref(a), C.byref(b)))
+        return dict(ops=a.value, kernels=b.value)
+
+    def set_fusion(self, on: bool):
+        self.check(lib.slm_hip_set_fusion(self.ctx, int(on)))
 
     def graph_stats(self):
         a, b, c = C.c_uint64(), C.c_uint64(), C.c_uint64()

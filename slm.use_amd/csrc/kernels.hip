@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fusion.h"
+
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 #define KERNEL extern "C" __global__
@@ -146,7 +148,15 @@ KERNEL void slm_rope_table(float* __restrict__ cs, float* __restrict__ sn,
 __device__ __forceinline__ float dot16_self(const float* in, int size, int l) {
     int chunks = size / 16;
     float acc = 0.0f;
-    for (int c = 0; c < chunks; c++) {
+    int c = 0;
+    for (; c + 8 <= chunks; c += 8) {  // eight reads in flight, then the sums in order
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = in[(c + u) * 16 + l];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = acc + v[u] * v[u];
+    }
+    for (; c < chunks; c++) {
         float v = in[c * 16 + l];
         acc = acc + v * v;
     }
@@ -258,14 +268,14 @@ GLA(64)
 // linear: y[i][r] = Σ_c w[r][c]·x[i][c] (ops.rs:116-126)
 // ---------------------------------------------------------------------------------------
 //
-// The canonical chain, shared by both kernels below. For v_mfma_f32_16x16x4f32 lane l
-// holds A[l%16][l/16], B[l/16][l%16] and D[4(l/16)+r][l%16] in element r. Rows of w are
-// A's rows, tokens are B's columns. Columns go in blocks of 16: lane group g = l/16 loads
-// the four columns 16kb+4g .. 16kb+4g+3 of its row (of w) and of its token (of x), and
-// MFMA e (e = 0..3) takes element e of both, so MFMA e of block kb sums the columns
-// {16kb + 4g + e : g = 0..3}. Blocks are chained in order within a slice of 16 blocks
-// (256 columns) starting from zero, and the slice sums are added in order:
-// y = ((P0 + P1) + P2) + ...   Columns past `cols` load as zero.
+// The canonical chain, shared by every linear kernel (and the fused one). For
+// v_mfma_f32_16x16x4f32 lane l holds A[l%16][l/16], B[l/16][l%16] and D[4(l/16)+r][l%16]
+// in element r. Rows of w are A's rows, tokens are B's columns. Columns go in blocks of
+// 16: lane group g = l/16 loads the four columns 16kb+4g .. 16kb+4g+3 of its row (of w)
+// and of its token (of x), and MFMA e (e = 0..3) takes element e of both, so MFMA e of
+// block kb sums the columns {16kb + 4g + e : g = 0..3}. Blocks are chained in order
+// within a slice of SLM_KS = 4 blocks (64 columns) starting from zero, and the slice
+// sums are added in order: y = ((P0 + P1) + P2) + ...   Columns past `cols` load as zero.
 
 template <bool VEC>
 __device__ __forceinline__ f4 ld4(const float* __restrict__ p, long long row, long long nrows,
@@ -284,10 +294,9 @@ __device__ __forceinline__ f4 ld4(const float* __restrict__ p, long long row, lo
     return r;
 }
 
-// m <= 16: one workgroup per 16 rows, one wave per slice (waves take slices w, w+W, ...),
-// slice partials meet in LDS and one pass adds them in order. A wave loads its whole
-// slice (16 rows x 256 columns of w, and the tokens' columns) before the chain starts, so
-// one memory latency covers it.
+// m <= 16: one workgroup per 16 rows; wave w takes slices w, w+W, w+2W, ... four at a
+// time, loading them before their chains start (four independent chains interleave);
+// slice partials meet in LDS and one pass adds them in order.
 template <bool VEC>
 __device__ void linear_small_body(float* __restrict__ y, const float* __restrict__ w,
                                   const float* __restrict__ x, int rows, int cols, int m) {
@@ -295,33 +304,44 @@ __device__ void linear_small_body(float* __restrict__ y, const float* __restrict
     int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     int i = lane & 15, g = lane >> 4;
     long long r0 = (long long)blockIdx.x * 16;
-    int kblocks = (cols + 15) >> 4, nsl = (kblocks + 15) >> 4;
-    for (int s = wave; s < nsl; s += waves) {
-        int nkb = min(16, kblocks - s * 16);
-        f4 wa[16], xb[16];
+    int kblocks = (cols + 15) >> 4, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
+    for (int s0 = wave; s0 < nsl; s0 += 4 * waves) {
+        f4 wa[4][SLM_KS], xb[4][SLM_KS];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            long long c = (long long)(s * 16 + u) * 16 + g * 4;
-            wa[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            xb[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (u < nkb) {
-                wa[u] = ld4<VEC>(w, r0 + i, rows, cols, c);
-                xb[u] = ld4<VEC>(x, i, m, cols, c);
+        for (int j = 0; j < 4; j++) {
+            int s = s0 + j * waves;
+#pragma unroll
+            for (int u = 0; u < SLM_KS; u++) {
+                int kb = s * SLM_KS + u;
+                wa[j][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                xb[j][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (s < nsl && kb < kblocks) {
+                    long long c = (long long)kb * 16 + g * 4;
+                    wa[j][u] = ld4<VEC>(w, r0 + i, rows, cols, c);
+                    xb[j][u] = ld4<VEC>(x, i, m, cols, c);
+                }
             }
         }
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        f4 acc[4];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            if (u < nkb) {
-                acc = mfma4(wa[u].x, xb[u].x, acc);
-                acc = mfma4(wa[u].y, xb[u].y, acc);
-                acc = mfma4(wa[u].z, xb[u].z, acc);
-                acc = mfma4(wa[u].w, xb[u].w, acc);
+        for (int j = 0; j < 4; j++) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < SLM_KS; u++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    int s = s0 + j * waves;
+                    if (s < nsl && s * SLM_KS + u < kblocks) acc[j] = mfma4(wa[j][u][e], xb[j][u][e], acc[j]);
+                }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int s = s0 + j * waves;
+            if (s < nsl) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) part[s * 256 + (4 * g + r) * 16 + i] = acc[j][r];
             }
         }
-        float* p = part + s * 256;
-#pragma unroll
-        for (int r = 0; r < 4; r++) p[(4 * g + r) * 16 + i] = acc[r];
     }
     __syncthreads();
     for (int t = threadIdx.x; t < 256; t += blockDim.x) {
@@ -349,7 +369,7 @@ __device__ void linear_big_body(float* __restrict__ y, const float* __restrict__
     int i = lane & 15, g = lane >> 4;
     long long rb = (long long)blockIdx.x * 64 + (wave & 1) * 32;
     long long tb = (long long)blockIdx.y * 64 + (wave >> 1) * 32;
-    int kblocks = (cols + 15) >> 4, nsl = (kblocks + 15) >> 4;
+    int kblocks = (cols + 15) >> 4, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
     f4 tot[2][2];
     for (int s = 0; s < nsl; s++) {
         f4 acc[2][2];
@@ -357,8 +377,8 @@ __device__ void linear_big_body(float* __restrict__ y, const float* __restrict__
         for (int u = 0; u < 2; u++)
 #pragma unroll
             for (int v = 0; v < 2; v++) acc[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        int kb1 = min(s * 16 + 16, kblocks);
-        for (int kb = s * 16; kb < kb1; kb++) {
+        int kb1 = min(s * SLM_KS + SLM_KS, kblocks);
+        for (int kb = s * SLM_KS; kb < kb1; kb++) {
             long long c = (long long)kb * 16 + g * 4;
             f4 a[2], b[2];
 #pragma unroll
@@ -675,3 +695,316 @@ KERNEL void slm_probe_mfma(float* out, const float* a, const float* b) {
     f4 d = mfma4(a[l], b[l], f4{0.0f, 0.0f, 0.0f, 0.0f});
     for (int r = 0; r < 4; r++) out[4 * l + r] = d[r];
 }
+
+// ---------------------------------------------------------------------------------------
+// fused decode kernels (one token), driven by the descriptors of fusion.h
+// ---------------------------------------------------------------------------------------
+
+// One prologue operation on LDS vectors. Every thread of the workgroup calls it; it ends
+// on a barrier. `misc` is a few floats of LDS for reduction results.
+__device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0) {
+    int tid = threadIdx.x, nt = blockDim.x, n = o.n;
+    const float* a = lds + o.in0;
+    const float* b = o.in1 >= 0 ? lds + o.in1 : nullptr;
+    float* out = o.out >= 0 ? lds + o.out : nullptr;
+    float* gout = wg0 ? o.gout : nullptr;
+    switch (o.kind) {
+        case VP_RMS: {  // rms (cpu.rs:187-207) of one group; a and out may not alias
+            if (tid < 16) {
+                float d = dot16_self(a, n, tid);
+                if (tid == 0) misc[0] = 1.0f / sqrtf(d / (float)n + o.f);
+            }
+            __syncthreads();
+            float r = misc[0];
+            const float* wt = lds + o.w;
+            for (int c = tid; c < n; c += nt) {
+                float v = a[c] * r * wt[c];
+                out[c] = v;
+                if (gout) gout[c] = v;
+            }
+            break;
+        }
+        case VP_COMBINE: {  // slm_attn_combine for one query
+            const float* part = o.w >= 0 ? (const float*)(lds + o.w) : o.part;
+            for (int c = tid; c < n; c += nt) {
+                int h = c / o.dh, e = c % o.dh;
+                float M = NEG_INF, L = 0.0f, O = 0.0f;
+                for (int z = 0; z < o.nsb; z++) {
+                    const float* P = part + ((long long)z * o.heads + h) * (o.dp + 2);
+                    fold(M, L, O, P[0], P[1], P[2 + e]);
+                }
+                float v = L > 0.0f ? O / L : 0.0f;
+                if (out) out[c] = v;
+                if (gout) gout[c] = v;
+            }
+            break;
+        }
+        default: {
+            float factor = o.f;
+            if (o.kind == VP_SCALE && o.dyn) factor = *(const float*)o.dyn;
+            for (int c = tid; c < n; c += nt) {
+                float v;
+                switch (o.kind) {
+                    case VP_COPY: v = a[c]; break;
+                    case VP_ADD: v = a[c] + b[c]; break;
+                    case VP_MIX: v = a[c] + factor * (b[c] - a[c]); break;
+                    case VP_SCALE: v = a[c] * factor; break;
+                    default: {  // VP_SILU
+                        float gg = a[c];
+                        v = b[c] * gg / (1.0f + expf(-gg));
+                    }
+                }
+                if (out) out[c] = v;
+                if (gout) gout[c] = v;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// The tile a wave's rows come from: workgroup `local` of segment `sg`, tile t of T.
+__device__ __forceinline__ int fg_tile(const FgSeg& sg, int local, int t) {
+    if (sg.epi == EPI_SILU) return t == 0 ? local : local + sg.hid / 16;
+    return local * sg.T + t;
+}
+
+KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
+    extern __shared__ float lds[];
+    float* misc = lds + d.lds_vp;          // 32 floats
+    float* foldb = lds + d.fold_off;       // [T][slices][16]
+    float* val = lds + d.epi_off;          // [T·16] row values, then per-head norms
+    int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
+    int i = lane & 15, g = lane >> 4;
+    int sgi = 0;
+    for (int k = 1; k < d.nseg; k++)
+        if ((int)blockIdx.x >= d.seg[k].wg_first) sgi = k;
+    const FgSeg& sg = d.seg[sgi];
+    int local = blockIdx.x - sg.wg_first;
+    int Wt = d.Wt, nsl = d.nsl, kblocks = d.cols >> 4;
+    int t = wave / Wt, wl = wave % Wt;
+    int tile = fg_tile(sg, local, t);
+    bool live = t < sg.T && tile < sg.tiles;
+    long long row = (long long)tile * 16 + i;
+    long long first_row = (long long)local * sg.T * 16;
+    // 1. this wave's weights (slices wl, wl + Wt, ...), issued first
+    f4 wa[SLM_FG_SLICES][SLM_KS];
+#pragma unroll
+    for (int j = 0; j < SLM_FG_SLICES; j++) {
+        int s = wl + j * Wt;
+#pragma unroll
+        for (int u = 0; u < SLM_KS; u++) {
+            int kb = s * SLM_KS + u;
+            wa[j][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (live && s < nsl && kb < kblocks && row < sg.rows)
+                wa[j][u] = *(const f4*)(sg.w + row * d.cols + kb * 16 + 4 * g);
+        }
+    }
+    // 2. every global vector the prologue and epilogue read, into LDS, loads first
+    {
+        long long base[SLM_PF_MAX];
+#pragma unroll
+        for (int j = 0; j < SLM_PF_MAX; j++) {
+            base[j] = 0;
+            if (j < d.npf) {
+                if (d.pf[j].dyn) base[j] = d.pf[j].dyn[0] * d.pf[j].stride;
+                if (d.pf[j].wgrow) base[j] += first_row;
+            }
+        }
+        float v[SLM_PF_PER_THREAD];
+        int dst[SLM_PF_PER_THREAD];
+#pragma unroll
+        for (int q = 0; q < SLM_PF_PER_THREAD; q++) {
+            int f = tid + q * nt, acc = 0, j = 0;
+            dst[q] = -1;
+            for (; j < d.npf; j++) {
+                if (f < acc + d.pf[j].n) break;
+                acc += d.pf[j].n;
+            }
+            if (j < d.npf) {
+                int c = f - acc;
+                const PfOp& p = d.pf[j];
+                bool ok = !p.wgrow || first_row + c < p.limit;
+                if (ok) {
+                    v[q] = p.src[base[j] + c];
+                    dst[q] = p.lds + c;
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < SLM_PF_PER_THREAD; q++)
+            if (dst[q] >= 0) lds[dst[q]] = v[q];
+    }
+    __syncthreads();
+    // 3. the prologue
+    bool first = blockIdx.x == 0;
+    for (int k = 0; k < d.nvp; k++) {
+        const VpOp& o = d.vp[k];
+        if (o.wg0 && !first) continue;
+        vp_run(o, lds, misc, first);
+    }
+    // 4. the canonical chains (token 0 is column 0 of B), several slices interleaved
+    const float* xin = d.xin >= 0 ? (const float*)(lds + d.xin) : d.x;
+    f4 acc[SLM_FG_SLICES];
+#pragma unroll
+    for (int j = 0; j < SLM_FG_SLICES; j++) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < SLM_KS; u++) {
+        f4 xb[SLM_FG_SLICES];
+#pragma unroll
+        for (int j = 0; j < SLM_FG_SLICES; j++) {
+            int kb = (wl + j * Wt) * SLM_KS + u;
+            xb[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (i == 0 && wl + j * Wt < nsl && kb < kblocks) xb[j] = *(const f4*)(xin + kb * 16 + 4 * g);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int j = 0; j < SLM_FG_SLICES; j++) {
+                int s = wl + j * Wt;
+                if (s < nsl && s * SLM_KS + u < kblocks) acc[j] = mfma4(wa[j][u][e], xb[j][e], acc[j]);
+            }
+    }
+    if (live && i == 0) {
+#pragma unroll
+        for (int j = 0; j < SLM_FG_SLICES; j++) {
+            int s = wl + j * Wt;
+            if (s < nsl) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) foldb[(t * nsl + s) * 16 + 4 * g + r] = acc[j][r];
+            }
+        }
+    }
+    __syncthreads();
+    int T = sg.T, nrow = T * 16;
+    if (tid < nrow) {
+        int tt = tid >> 4, rr = tid & 15;
+        float tot = foldb[(tt * nsl) * 16 + rr];
+        for (int q = 1; q < nsl; q++) tot = tot + foldb[(tt * nsl + q) * 16 + rr];
+        val[tid] = tot;
+    }
+    __syncthreads();
+    // 5. the epilogue: one thread per row
+    if (sg.epi == EPI_L2) {  // per-head norms of the q and k parts first
+        int nh = nrow / sg.dh;
+        int hq = tid >> 4;
+        if (hq < nh) {
+            float dsum = dot16_self(val + hq * sg.dh, sg.dh, tid & 15);
+            if ((tid & 15) == 0) val[nrow + hq] = 1.0f / fmaxf(sqrtf(dsum), 1e-12f);
+        }
+        __syncthreads();
+    }
+    if (tid < nrow) {
+        int tt = tid >> 4, rr = tid & 15;
+        int tl = fg_tile(sg, local, tt);
+        long long R = (long long)tl * 16 + rr;
+        float v = val[tid];
+        if (tl < sg.tiles && R < sg.rows) {
+            sg.y[R] = v;
+            switch (sg.epi) {
+                case EPI_RESID:
+                    sg.o1[R] = lds[sg.res_lds + tid] + v;
+                    break;
+                case EPI_SILU:
+                    if (tt == 0) {
+                        float amp = val[16 + rr];
+                        sg.o1[R] = amp * v / (1.0f + expf(-v));
+                    }
+                    break;
+                case EPI_ROPE: {
+                    int part = (int)(R / sg.d), j = (int)(R % sg.d);
+                    int e = j % sg.dh, half = sg.dh / 2, head = j / sg.dh;
+                    if (part < 2) {
+                        int ie = e < half ? e : e - half;
+                        float cs = lds[sg.cs_lds + ie], sn = lds[sg.sn_lds + ie];
+                        float p = val[e < half ? tid + half : tid - half];
+                        float o = e < half ? v * cs - p * sn : p * sn + v * cs;
+                        if (part == 0) {
+                            sg.o1[j] = o;
+                        } else {
+                            long long slot = (sg.dyn ? sg.dyn[0] : sg.imm) % sg.cap;
+                            sg.o2[j] = o;
+                            sg.o3[((long long)head * sg.cap + slot) * sg.dh + e] = o;
+                        }
+                    } else {
+                        long long slot = (sg.dyn2 ? sg.dyn2[0] : sg.imm2) % sg.cap;
+                        sg.o4[((long long)head * sg.cap + slot) * sg.dh + e] = v;
+                    }
+                    break;
+                }
+                case EPI_L2: {
+                    int part = (int)(R / sg.d), j = (int)(R % sg.d);
+                    if (part < 2) {
+                        float o = v * val[nrow + tid / sg.dh];
+                        if (part == 0) sg.o1[j] = o;
+                        else sg.o2[j] = o;
+                    }
+                    break;
+                }
+                default:
+                    break;
+            }
+        }
+    }
+}
+
+// One token of gated linear attention per head (the m = 1 case of gla_body), then, when
+// fused, the head RMSNorm and the SiLU gate of model.rs:483-484, in the same expressions
+// as slm_rms and slm_silu_mul.
+template <int RPL>
+__device__ void gla1_body(const GlaDesc& g) {
+    extern __shared__ float lds[];
+    int h = blockIdx.x, tid = threadIdx.x, dh = g.dh;
+    int b = tid >> 2, j = tid & 3;
+    bool live = b < dh;
+    float* Sh = g.s + (long long)h * dh * dh;
+    long long at = (long long)h * dh;
+    float st[RPL];
+#pragma unroll
+    for (int rr = 0; rr < RPL; rr++) {
+        int a = j * RPL + rr;
+        st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
+    }
+    float dc = 1.0f / (1.0f + expf(g.decay[h] + g.bias[h]));
+    float vb = live ? g.v[at + b] : 0.0f;
+    float part = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPL; rr++) {
+        int a = j * RPL + rr;
+        if (live && a < dh) {
+            st[rr] = dc * st[rr] + g.k[at + a] * vb;
+            part = part + g.q[at + a] * st[rr];
+        }
+    }
+    float t1 = part + __shfl_xor(part, 1);
+    float t2 = t1 + __shfl_xor(t1, 2);
+#pragma unroll
+    for (int rr = 0; rr < RPL; rr++) {
+        int a = j * RPL + rr;
+        if (live && a < dh) Sh[(long long)a * dh + b] = st[rr];
+    }
+    if (live && j == 0) g.y[at + b] = t2;
+    if (!g.fuse) return;
+    if (live && j == 0) lds[b] = t2;
+    __syncthreads();
+    if (tid < 16) {
+        float d = dot16_self(lds, dh, tid);
+        if (tid == 0) lds[dh] = 1.0f / sqrtf(d / (float)dh + g.eps);
+    }
+    __syncthreads();
+    if (live && j == 0) {
+        float y2 = lds[b] * lds[dh] * g.hn[b];
+        g.y2[at + b] = y2;
+        float gt = g.gate[at + b];
+        g.out[at + b] = y2 * gt / (1.0f + expf(-gt));
+    }
+}
+
+#define GLA1(R)                                                                   \
+    KERNEL void __launch_bounds__(1024) slm_gla1_##R(const GlaDesc g) { gla1_body<R>(g); }
+GLA1(1)
+GLA1(2)
+GLA1(4)
+GLA1(8)
+GLA1(16)
+GLA1(32)
+GLA1(64)

@@ -3,8 +3,15 @@
 // One context = one device, one stream (default priority), the gfx950 code object loaded
 // with hipModuleLoadData, a table of live allocations that every operation checks its
 // pointer ranges against before anything is queued, a workspace for attention partials,
-// and the step-graph cache. Kernels live in kernels.hip; this file only validates, sizes
-// launches and queues them.
+// and the step-graph cache.
+//
+// Every entry point validates its arguments and turns the call into an `Op`. Outside a
+// step an Op is lowered to its kernels and launched at once. Inside a step (rope_table
+// .. flush, with graphs on) Ops are recorded; at flush the planner lowers the whole step —
+// fusing runs of one-token ops into the fused kernels of fusion.h — and the launches are
+// captured into a hipGraph, which later steps with the same ops replay. Positions, token
+// ids and factors live in a per-step block of device memory that is refreshed before
+// each replay, so a step's ops compare equal from one token to the next.
 
 #include <hip/hip_runtime.h>
 
@@ -18,6 +25,7 @@
 #include <string>
 #include <vector>
 
+#include "fusion.h"
 #include "slm_hip.h"
 
 extern "C" const unsigned char slm_code_object[];
@@ -28,21 +36,40 @@ namespace {
 std::string g_open_error;
 
 constexpr int MAX_ARGS = 16;
-constexpr size_t DYN_CAP = 1 << 20;          // bytes of per-step dynamic values
-constexpr size_t STAGE_CAP = 4 << 20;        // bytes of eager staging
-constexpr size_t BOUNCE_CAP = 4 << 20;       // pinned bounce buffer for reads
+constexpr size_t BLOB = 2048;             // bytes of kernel arguments per launch
+constexpr size_t DYN_CAP = 1 << 20;       // bytes of per-step dynamic values
+constexpr size_t STAGE_CAP = 4 << 20;     // bytes of eager staging
+constexpr size_t BOUNCE_CAP = 4 << 20;    // pinned bounce buffer for reads
 constexpr size_t MAX_GRAPHS = 8;
+constexpr int VP_LEN_MAX = 4096;          // longest vector a fused prologue holds
+constexpr int LDS_MAX = 65536;
 
-// One queued kernel launch: everything hipModuleLaunchKernel needs, by value, so a step
-// can be compared with a cached one byte for byte.
+enum OpKind : uint32_t {
+    OP_GATHER = 1, OP_COPY, OP_SHIFT, OP_COLUMNS, OP_LINEAR, OP_ADD, OP_ADD_ROW, OP_SCALE_ROWS,
+    OP_MIX, OP_RMS, OP_SILU_MUL, OP_ROPE_TABLE, OP_ROPE, OP_L2NORM, OP_GLA, OP_STORE, OP_ATTEND
+};
+
+// One operation, by value. p[] are device pointers (outputs first), n[] sizes, f[]
+// scalars, dyn the device copy of its per-step values (position, ids, factors) or null.
+struct Op {
+    uint32_t kind, pad;
+    const float* p[8];
+    int64_t n[10];
+    float f[2];
+    const void* dyn;
+};
+
+// One kernel launch: the function, its grid, and its arguments by value. Scalar-argument
+// kernels use 8-byte slots (values little-endian in the low bytes); descriptor kernels
+// take one struct, `bytes` long.
 struct Rec {
     hipFunction_t f;
-    uint32_t gx, gy, gz, bx, shmem, nargs;
-    uint64_t args[MAX_ARGS];
+    uint32_t gx, gy, gz, bx, shmem, nargs, bytes;
+    alignas(16) unsigned char blob[BLOB];
 };
 
 struct Graph {
-    std::vector<Rec> recs;
+    std::vector<Op> ops;
     size_t ndyn = 0;
     hipGraphExec_t exec = nullptr;
     uint64_t used = 0;
@@ -57,9 +84,9 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 
 struct Kernels {
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
-        store, rope, rope_table, rms, l2norm, fill, combine, probe;
+        store, rope, rope_table, rms, l2norm, fill, combine, probe, fg;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
-    hipFunction_t gla[7];                    // rows per lane 1, 2, 4, .., 64
+    hipFunction_t gla[7], gla1[7];           // rows per lane 1, 2, 4, .., 64
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
 };
 
@@ -72,30 +99,25 @@ struct slm_hip {
     Kernels k{};
     std::string err;
     char name[256] = {0};
-    // live allocations: start -> bytes
-    std::map<uintptr_t, size_t> allocs;
-    // attention partials
-    float* ws = nullptr;
+    std::map<uintptr_t, size_t> allocs;  // live allocations: start -> bytes
+    float* ws = nullptr;                 // attention partials
     size_t ws_bytes = 0;
-    // eager staging: pinned host ring copied into a device ring
-    unsigned char* stage_host = nullptr;
+    unsigned char* stage_host = nullptr; // eager staging: pinned ring copied into a device ring
     unsigned char* stage_dev = nullptr;
     size_t stage_head = 0;
-    // step dynamic values: host copy (this step), two pinned uploads, one device area
-    unsigned char* dyn_pin[2] = {nullptr, nullptr};
+    unsigned char* dyn_pin[2] = {nullptr, nullptr};  // step values: two pinned uploads
     hipEvent_t dyn_ev[2] = {nullptr, nullptr};
     int dyn_flip = 0;
     unsigned char* dyn_dev = nullptr;
     float* bounce = nullptr;
     std::map<uintptr_t, Table> tables;
-    // step graphs
-    bool graphs_on = true;
-    bool recording = false;
-    bool tainted = false;
-    std::vector<Rec> recs;
+    bool graphs_on = true, fusion_on = true;
+    bool recording = false, tainted = false;
+    std::vector<Op> ops;                 // the step being recorded
     std::vector<unsigned char> dyn;
     std::vector<Graph> cache;
     uint64_t clock = 0, n_launched = 0, n_captured = 0, n_eager = 0;
+    uint64_t last_ops = 0, last_kernels = 0;  // of the last step the planner lowered
 };
 
 namespace {
@@ -115,6 +137,12 @@ int fail(slm_hip* c, int code, const char* fmt, ...) {
         hipError_t e_ = (call);                                                      \
         if (e_ != hipSuccess)                                                        \
             return fail(c, SLM_E_HIP, "%s: %s", #call, hipGetErrorString(e_));      \
+    } while (0)
+
+#define TRY(expr)                \
+    do {                         \
+        int rc_ = (expr);        \
+        if (rc_) return rc_;     \
     } while (0)
 
 // Is [p, p + bytes) inside one live allocation?
@@ -146,12 +174,16 @@ size_t room(const slm_hip* c, const void* p) {
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
 
+// ---------------------------------------------------------------------------------------
+// launch records
+// ---------------------------------------------------------------------------------------
+
 template <typename T>
 void put(Rec& r, T v) {
     static_assert(sizeof(T) <= 8, "argument too large");
     uint64_t s = 0;
     std::memcpy(&s, &v, sizeof(T));
-    r.args[r.nargs++] = s;
+    std::memcpy(r.blob + 8 * r.nargs++, &s, 8);
 }
 
 void pack(Rec&) {}
@@ -161,15 +193,58 @@ void pack(Rec& r, T v, A... rest) {
     pack(r, rest...);
 }
 
-// Argument sizes per kernel, needed to hand hipModuleLaunchKernel pointers into the
-// 8-byte slots: values are stored little-endian in the low bytes, so a pointer to the
-// slot serves every argument type up to 8 bytes.
+Rec rec(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t shmem) {
+    Rec r;
+    r.f = f;
+    r.gx = gx;
+    r.gy = gy;
+    r.gz = gz;
+    r.bx = bx;
+    r.shmem = shmem;
+    r.nargs = 0;
+    r.bytes = 0;
+    return r;
+}
+
+template <typename... A>
+Rec mk(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t shmem,
+       A... args) {
+    Rec r = rec(f, gx, gy, gz, bx, shmem);
+    std::memset(r.blob, 0, 8 * MAX_ARGS);
+    pack(r, args...);
+    return r;
+}
+
+template <typename D>
+Rec mk_desc(hipFunction_t f, uint32_t gx, uint32_t bx, uint32_t shmem, const D& d) {
+    static_assert(sizeof(D) <= BLOB, "descriptor too large");
+    Rec r = rec(f, gx, 1, 1, bx, shmem);
+    std::memcpy(r.blob, &d, sizeof(D));
+    r.bytes = sizeof(D);
+    return r;
+}
+
 int launch_now(slm_hip* c, const Rec& r) {
     void* ptrs[MAX_ARGS];
-    for (uint32_t i = 0; i < r.nargs; i++) ptrs[i] = (void*)&r.args[i];
+    if (r.bytes) {
+        ptrs[0] = (void*)r.blob;
+    } else {
+        for (uint32_t i = 0; i < r.nargs; i++) ptrs[i] = (void*)(r.blob + 8 * i);
+    }
     HIPC(c, hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream, ptrs,
                                   nullptr));
     return SLM_OK;
+}
+
+uint32_t blocks_for(size_t n, size_t per = 256, size_t cap = 4096) {
+    size_t b = (n + per - 1) / per;
+    return (uint32_t)std::max<size_t>(1, std::min(b, cap));
+}
+
+int pow2_index(size_t need, int maxi) {  // smallest i with 2^i >= need
+    int i = 0;
+    while (i < maxi && ((size_t)1 << i) < need) i++;
+    return i;
 }
 
 void drop_graphs(slm_hip* c) {
@@ -179,6 +254,743 @@ void drop_graphs(slm_hip* c) {
         if (g.exec) hipGraphExecDestroy(g.exec);
     c->cache.clear();
 }
+
+// ---------------------------------------------------------------------------------------
+// per-op lowering (the unfused kernels)
+// ---------------------------------------------------------------------------------------
+
+int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
+    const Kernels& k = c->k;
+    const float* const* p = o.p;
+    const int64_t* n = o.n;
+    switch (o.kind) {
+        case OP_GATHER:  // p0 y, p1 w; n0 m, n1 d; dyn ids
+            out.push_back(mk(k.gather, blocks_for(n[0] * n[1]), 1, 1, 256, 0, p[0], p[1],
+                             (const long long*)o.dyn, (long long)(n[0] * n[1]), (long long)n[1]));
+            return SLM_OK;
+        case OP_COPY:
+            out.push_back(mk(k.copy, blocks_for(n[0]), 1, 1, 256, 0, p[0], p[1], (long long)n[0]));
+            return SLM_OK;
+        case OP_SHIFT:  // p0 y, p1 first, p2 x; n0 m, n1 d
+            out.push_back(mk(k.shift, blocks_for(n[0] * n[1]), 1, 1, 256, 0, p[0], p[1], p[2],
+                             (long long)(n[0] * n[1]), (long long)n[1]));
+            return SLM_OK;
+        case OP_COLUMNS:  // p0 y, p1 x; n0 m, n1 stride, n2 off, n3 len
+            out.push_back(mk(k.columns, blocks_for(n[0] * n[3]), 1, 1, 256, 0, p[0], p[1],
+                             (long long)(n[0] * n[3]), (long long)n[1], (long long)n[2],
+                             (long long)n[3]));
+            return SLM_OK;
+        case OP_LINEAR: {  // p0 y, p1 w, p2 x; n0 rows, n1 cols, n2 m
+            int64_t rows = n[0], cols = n[1], m = n[2];
+            if (cols == 0) {
+                out.push_back(mk(k.fill, blocks_for(m * rows), 1, 1, 256, 0, p[0],
+                                 (long long)(m * rows), 0.0f));
+                return SLM_OK;
+            }
+            int vec = (cols % 4 == 0 && aligned16(p[1]) && aligned16(p[2])) ? 1 : 0;
+            int64_t kblocks = (cols + 15) / 16, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
+            if (m <= 16 && nsl <= 64) {
+                uint32_t waves = (uint32_t)std::min<int64_t>(nsl, 8);
+                out.push_back(mk(k.lin_small[vec], (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
+                                 (uint32_t)(nsl * 1024), p[0], p[1], p[2], (int)rows, (int)cols,
+                                 (int)m));
+            } else {
+                out.push_back(mk(k.lin_big[vec], (uint32_t)((rows + 63) / 64),
+                                 (uint32_t)((m + 63) / 64), 1, 256, 0, p[0], p[1], p[2],
+                                 (int)rows, (int)cols, (int)m));
+            }
+            return SLM_OK;
+        }
+        case OP_ADD:
+            out.push_back(mk(k.add, blocks_for(n[0]), 1, 1, 256, 0, p[0], p[1], p[2], (long long)n[0]));
+            return SLM_OK;
+        case OP_ADD_ROW:  // p0 y, p1 x, p2 row; n0 m, n1 d
+            out.push_back(mk(k.add_row, blocks_for(n[0] * n[1]), 1, 1, 256, 0, p[0], p[1], p[2],
+                             (long long)(n[0] * n[1]), (long long)n[1]));
+            return SLM_OK;
+        case OP_SCALE_ROWS:  // p0 y, p1 x; n0 m, n1 d; dyn factors or f0
+            out.push_back(mk(k.scale_rows, blocks_for(n[0] * n[1]), 1, 1, 256, 0, p[0], p[1],
+                             (const float*)o.dyn, o.f[0], (long long)(n[0] * n[1]), (long long)n[1]));
+            return SLM_OK;
+        case OP_MIX:
+            out.push_back(mk(k.mix, blocks_for(n[0]), 1, 1, 256, 0, p[0], p[1], p[2], (long long)n[0],
+                             o.f[0]));
+            return SLM_OK;
+        case OP_RMS:
+        case OP_L2NORM: {  // p0 y, p1 x, p2 w; n0 groups, n1 size; f0 eps
+            int64_t groups = n[0], size = n[1];
+            int64_t stride = size | 1;
+            int64_t G = std::min<int64_t>(16, std::max<int64_t>(1, 16384 / stride));
+            uint32_t blocks = (uint32_t)((groups + G - 1) / G);
+            uint32_t shmem = (uint32_t)(G * stride * 4);
+            if (o.kind == OP_RMS)
+                out.push_back(mk(k.rms, blocks, 1, 1, 256, shmem, p[0], p[1], p[2], (int)groups,
+                                 (int)size, o.f[0], (int)G));
+            else
+                out.push_back(mk(k.l2norm, blocks, 1, 1, 256, shmem, p[0], p[1], (int)groups,
+                                 (int)size, (int)G));
+            return SLM_OK;
+        }
+        case OP_SILU_MUL:
+            out.push_back(mk(k.silu_mul, blocks_for(n[0]), 1, 1, 256, 0, p[0], p[1], p[2],
+                             (long long)n[0]));
+            return SLM_OK;
+        case OP_ROPE_TABLE:  // p0 cos, p1 sin, p2 table cos, p3 table sin; n0 m, n1 half, n2 pos
+            out.push_back(mk(k.rope_table, blocks_for(n[0] * n[1]), 1, 1, 256, 0, p[0], p[1], p[2],
+                             p[3], (const long long*)o.dyn, (long long)n[2],
+                             (long long)(n[0] * n[1]), (long long)n[1]));
+            return SLM_OK;
+        case OP_ROPE:  // p0 y, p1 x, p2 cos, p3 sin; n0 m, n1 heads, n2 dh
+            out.push_back(mk(k.rope, blocks_for(n[0] * n[1] * n[2] / 2), 1, 1, 256, 0, p[0], p[1],
+                             p[2], p[3], (long long)n[0], (long long)n[1], (long long)n[2]));
+            return SLM_OK;
+        case OP_GLA: {  // p0 y, p1 s, p2 q, p3 k, p4 v, p5 decay, p6 bias; n0 m, n1 heads, n2 dh
+            int i = pow2_index((n[2] + 3) / 4, 6);
+            size_t threads = (size_t)(n[1] * n[2] * 4);
+            out.push_back(mk(k.gla[i], (uint32_t)((threads + 255) / 256), 1, 1, 256, 0, p[0], p[1],
+                             p[2], p[3], p[4], p[5], p[6], (int)n[0], (int)n[1], (int)n[2]));
+            return SLM_OK;
+        }
+        case OP_STORE:  // p0 cache, p1 src; n0 m, n1 cap, n2 heads, n3 dh, n4 pos
+            out.push_back(mk(k.store, blocks_for(n[0] * n[2] * n[3]), 1, 1, 256, 0, p[0], p[1],
+                             (const long long*)o.dyn, (long long)n[4], (long long)(n[0] * n[2] * n[3]),
+                             (long long)n[1], (long long)n[2], (long long)n[3]));
+            return SLM_OK;
+        case OP_ATTEND: {
+            // p0 y, p1 q, p2 k, p3 v; n0 pos, n1 m, n2 reach, n3 gap, n4 cap, n5 heads,
+            // n6 key_heads, n7 dh, n8 nsb; f0 scale
+            int64_t m = n[1], heads = n[5], kh = n[6], dh = n[7], nsb = n[8];
+            int dti = pow2_index((dh + 15) / 16, 4);
+            int64_t dp = (int64_t)16 << dti;
+            int64_t wpp = 8;
+            while (wpp > 1 && wpp * 16 * (dp + 2) * 4 > 65536) wpp /= 2;
+            int64_t qpt = 16 / (heads / kh);
+            out.push_back(mk(k.attn[dti], (uint32_t)((m + qpt - 1) / qpt), (uint32_t)kh, (uint32_t)nsb,
+                             512, (uint32_t)(wpp * 16 * (dp + 2) * 4), c->ws, p[1], p[2], p[3],
+                             (const long long*)o.dyn, (long long)n[0], (int)m, (long long)n[2],
+                             (long long)n[3], (long long)n[4], (int)heads, (int)kh, (int)dh, o.f[0],
+                             (int)wpp));
+            out.push_back(mk(k.combine, blocks_for(m * heads * dh), 1, 1, 256, 0, p[0],
+                             (const float*)c->ws, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
+            return SLM_OK;
+        }
+    }
+    return fail(c, SLM_E_INVALID, "unknown op %u", o.kind);
+}
+
+// ---------------------------------------------------------------------------------------
+// the fusion planner (one-token steps)
+// ---------------------------------------------------------------------------------------
+
+struct Range {
+    uintptr_t a, b;  // [a, b) bytes
+};
+Range rng(const float* p, int64_t n) { return Range{(uintptr_t)p, (uintptr_t)(p + n)}; }
+bool overlap(const Range& x, const Range& y) { return x.a < y.b && y.a < x.b; }
+
+// An element-wise one-token op as prologue material: what it reads and writes.
+enum { SRC_COPY = 1, SRC_ADD, SRC_MIX, SRC_SCALE, SRC_GATHER, SRC_RMS, SRC_ROPE_TABLE, SRC_SILU,
+       SRC_COMBINE };
+struct VpSrc {
+    int kind = 0;
+    int n = 0;
+    const float* in[2] = {nullptr, nullptr};
+    const float* out[2] = {nullptr, nullptr};
+    const Op* op = nullptr;
+};
+
+// Can this op run inside a fused prologue? (one token, one row, a short vector)
+bool vp_of(const Op& o, VpSrc* v) {
+    const int64_t* n = o.n;
+    v->op = &o;
+    switch (o.kind) {
+        case OP_COPY:
+            v->kind = SRC_COPY; v->n = (int)n[0]; v->in[0] = o.p[1]; v->out[0] = o.p[0];
+            break;
+        case OP_ADD:
+            v->kind = SRC_ADD; v->n = (int)n[0]; v->in[0] = o.p[1]; v->in[1] = o.p[2]; v->out[0] = o.p[0];
+            break;
+        case OP_ADD_ROW:
+            if (n[0] != 1) return false;
+            v->kind = SRC_ADD; v->n = (int)n[1]; v->in[0] = o.p[1]; v->in[1] = o.p[2]; v->out[0] = o.p[0];
+            break;
+        case OP_MIX:
+            v->kind = SRC_MIX; v->n = (int)n[0]; v->in[0] = o.p[1]; v->in[1] = o.p[2]; v->out[0] = o.p[0];
+            break;
+        case OP_SCALE_ROWS:
+            if (n[0] != 1) return false;
+            v->kind = SRC_SCALE; v->n = (int)n[1]; v->in[0] = o.p[1]; v->out[0] = o.p[0];
+            break;
+        case OP_GATHER:
+            if (n[0] != 1) return false;
+            v->kind = SRC_GATHER; v->n = (int)n[1]; v->out[0] = o.p[0];
+            break;
+        case OP_RMS:
+            if (n[0] != 1) return false;
+            v->kind = SRC_RMS; v->n = (int)n[1]; v->in[0] = o.p[1]; v->out[0] = o.p[0];
+            break;
+        case OP_ROPE_TABLE:
+            if (n[0] != 1) return false;
+            v->kind = SRC_ROPE_TABLE; v->n = (int)n[1]; v->out[0] = o.p[0]; v->out[1] = o.p[1];
+            break;
+        case OP_SILU_MUL:
+            v->kind = SRC_SILU; v->n = (int)n[0]; v->in[0] = o.p[1]; v->in[1] = o.p[2]; v->out[0] = o.p[0];
+            break;
+        case OP_COLUMNS:
+            if (n[0] != 1) return false;
+            v->kind = SRC_COPY; v->n = (int)n[3]; v->in[0] = o.p[1] + n[2]; v->out[0] = o.p[0];
+            break;
+        default:
+            return false;
+    }
+    return v->n > 0 && v->n <= VP_LEN_MAX && v->n % 4 == 0;
+}
+
+int combine_dp(int64_t dh) { return 16 << pow2_index((dh + 15) / 16, 4); }
+
+// Builds one slm_fg launch: LDS slots, prefetches, prologue ops, segments.
+struct FgBuild {
+    FgDesc d;
+    int lds = 0;  // floats of LDS handed out so far
+    struct Slot {  // an LDS vector holding what global [g, g + n) holds at this point
+        const float* g;
+        int n, off;
+    };
+    std::vector<Slot> slots;     // produced by prologue ops, in order
+    std::vector<int> slot_op;    // the prologue op (index into d.vp) that made each slot, -1: a prefetch
+    std::vector<Range> reads, writes;
+    int pf_floats = 0;
+
+    FgBuild() { std::memset(&d, 0, sizeof d); }
+    int alloc(int n) {
+        int off = lds;
+        lds += (n + 3) & ~3;
+        return off;
+    }
+    // LDS offset of [p, p + len) if a slot produced so far covers it; -1 none; -2 partial
+    int find(const float* p, int64_t len, size_t upto) const {
+        for (size_t k = std::min(upto, slots.size()); k-- > 0;) {
+            const Slot& s = slots[k];
+            if (p >= s.g && p + len <= s.g + s.n) return s.off + (int)(p - s.g);
+            if (overlap(rng(p, len), rng(s.g, s.n))) return -2;
+        }
+        return -1;
+    }
+    bool prefetch(const float* src, int n, const long long* dyn, int stride, int wgrow, int limit,
+                  int* off) {
+        if (d.npf >= SLM_PF_MAX) return false;
+        PfOp& p = d.pf[d.npf++];
+        p.src = src;
+        p.dyn = dyn;
+        p.n = n;
+        p.stride = stride;
+        p.wgrow = wgrow;
+        p.limit = limit;
+        p.lds = alloc(n);
+        pf_floats += n;
+        *off = p.lds;
+        return true;
+    }
+    // An input vector: a slot if one holds it, else a prefetch of global memory.
+    bool input(const float* p, int n, int* off) {
+        int r = find(p, n, slots.size());
+        if (r == -2) return false;
+        if (r >= 0) {
+            *off = r;
+            return true;
+        }
+        reads.push_back(rng(p, n));
+        return prefetch(p, n, nullptr, 0, 0, 0, off);
+    }
+};
+
+struct Planner {
+    slm_hip* c;
+    const std::vector<Op>& ops;
+    std::vector<Rec>& out;
+    std::vector<VpSrc> pend;
+
+    int flush_pending() {
+        for (auto& v : pend) {
+            if (v.kind == SRC_COMBINE) {
+                const Op& o = *v.op;
+                int64_t heads = o.n[5], dh = o.n[7], nsb = o.n[8];
+                out.push_back(mk(c->k.combine, blocks_for(heads * dh), 1, 1, 256, 0, o.p[0],
+                                 (const float*)c->ws, 1, (int)heads, (int)dh, combine_dp(dh),
+                                 (int)nsb));
+            } else {
+                TRY(lower_one(c, *v.op, out));
+            }
+        }
+        pend.clear();
+        return SLM_OK;
+    }
+
+    // Adds one prologue op; false when it cannot be fused.
+    bool add_vp(FgBuild& b, const VpSrc& v, bool side) {
+        const Op& so = *v.op;
+        if (b.d.nvp >= SLM_VP_MAX) return false;
+        int k = b.d.nvp;
+        VpOp& o = b.d.vp[k];
+        std::memset(&o, 0, sizeof o);
+        o.n = v.n;
+        o.in1 = -1;
+        o.w = -1;
+        o.wg0 = side ? 1 : 0;
+        o.out = -1;
+        auto emit_slot = [&](const float* g, int off) {
+            b.slots.push_back({g, v.n, off});
+            b.slot_op.push_back(k);
+        };
+        switch (v.kind) {
+            case SRC_GATHER: {  // the row is prefetched straight into its slot
+                int off;
+                if (!b.prefetch(so.p[1], v.n, (const long long*)so.dyn, v.n, 0, 0, &off)) return false;
+                b.reads.push_back(rng(so.p[1], 1));  // the embedding table is only read
+                o.kind = VP_COPY;
+                o.in0 = off;
+                o.gout = (float*)v.out[0];
+                b.d.nvp++;
+                emit_slot(v.out[0], off);
+                b.writes.push_back(rng(v.out[0], v.n));
+                return true;
+            }
+            case SRC_ROPE_TABLE: {  // two rows of the resident tables at the step's position
+                int oc, os;
+                if (!b.prefetch(so.p[2], v.n, (const long long*)so.dyn, v.n, 0, 0, &oc)) return false;
+                if (!b.prefetch(so.p[3], v.n, (const long long*)so.dyn, v.n, 0, 0, &os)) return false;
+                if (b.d.nvp + 2 > SLM_VP_MAX) return false;
+                o.kind = VP_COPY;
+                o.in0 = oc;
+                o.gout = (float*)v.out[0];
+                emit_slot(v.out[0], oc);
+                b.d.nvp++;
+                VpOp& o2 = b.d.vp[b.d.nvp];
+                std::memset(&o2, 0, sizeof o2);
+                o2.kind = VP_COPY;
+                o2.n = v.n;
+                o2.in0 = os;
+                o2.in1 = -1;
+                o2.w = -1;
+                o2.out = -1;
+                o2.wg0 = o.wg0;
+                o2.gout = (float*)v.out[1];
+                b.slots.push_back({v.out[1], v.n, os});
+                b.slot_op.push_back(b.d.nvp);
+                b.d.nvp++;
+                b.writes.push_back(rng(v.out[0], v.n));
+                b.writes.push_back(rng(v.out[1], v.n));
+                return true;
+            }
+            case SRC_COMBINE: {
+                int64_t heads = so.n[5], dh = so.n[7], nsb = so.n[8];
+                int dp = combine_dp(dh);
+                int64_t pn = nsb * heads * (dp + 2);
+                o.kind = VP_COMBINE;
+                o.heads = (int32_t)heads;
+                o.dh = (int32_t)dh;
+                o.dp = dp;
+                o.nsb = (int32_t)nsb;
+                o.part = c->ws;
+                if (pn <= 8192) {
+                    int off;
+                    if (!b.prefetch(c->ws, (int)pn, nullptr, 0, 0, 0, &off)) return false;
+                    o.w = off;
+                }
+                break;
+            }
+            default: {
+                o.kind = v.kind == SRC_COPY ? VP_COPY : v.kind == SRC_ADD ? VP_ADD : v.kind == SRC_MIX ? VP_MIX
+                       : v.kind == SRC_SCALE ? VP_SCALE : v.kind == SRC_RMS ? VP_RMS : VP_SILU;
+                if (!b.input(v.in[0], v.n, &o.in0)) return false;
+                if (v.in[1] && !b.input(v.in[1], v.n, &o.in1)) return false;
+                if (v.kind == SRC_RMS) {
+                    b.reads.push_back(rng(so.p[2], v.n));
+                    if (!b.prefetch(so.p[2], v.n, nullptr, 0, 0, 0, &o.w)) return false;
+                    o.f = so.f[0];
+                } else if (v.kind == SRC_SCALE) {
+                    o.dyn = (const long long*)so.dyn;
+                    o.f = so.f[0];
+                } else if (v.kind == SRC_MIX) {
+                    o.f = so.f[0];
+                }
+            }
+        }
+        o.out = b.alloc(v.n);
+        o.gout = (float*)v.out[0];
+        b.writes.push_back(rng(v.out[0], v.n));
+        emit_slot(v.out[0], o.out);
+        b.d.nvp++;
+        return true;
+    }
+
+    // Tries to fuse pend + ops[i] (a one-token linear) + what follows. Returns the number of
+    // ops of `ops` consumed from i (0: no fusion).
+    size_t try_fg(size_t i) {
+        const Op& L = ops[i];
+        int64_t rows = L.n[0], cols = L.n[1];
+        if (L.n[2] != 1 || cols % 16 || cols > VP_LEN_MAX || !aligned16(L.p[1]) || rows < 1)
+            return 0;
+        const float* x = L.p[2];
+        FgBuild b;
+        for (auto& v : pend)
+            if (!add_vp(b, v, false)) return 0;
+        size_t nproduced = b.slots.size();  // slots the linear may read
+        // epilogue pattern
+        int epi = EPI_PLAIN;
+        size_t used = 1;
+        FgSeg seg[SLM_SEG_MAX];
+        std::memset(seg, 0, sizeof seg);
+        int nseg = 1;
+        auto is = [&](size_t j, uint32_t kind) { return j < ops.size() && ops[j].kind == kind; };
+        const float* y = L.p[0];
+        FgSeg& s0 = seg[0];
+        s0.w = L.p[1];
+        s0.y = (float*)y;
+        s0.rows = (int32_t)rows;
+        s0.tiles = (int32_t)((rows + 15) / 16);
+        s0.T = 1;
+        const float *cs = nullptr, *sn = nullptr, *res = nullptr;
+        // S block: rope q, rope k, store k, store v (model.rs:430-438)
+        if (is(i + 1, OP_ROPE) && is(i + 2, OP_ROPE) && is(i + 3, OP_STORE) && is(i + 4, OP_STORE)) {
+            const Op &rq = ops[i + 1], &rk = ops[i + 2], &sk = ops[i + 3], &sv = ops[i + 4];
+            int64_t heads = rq.n[1], dh = rq.n[2], dd = heads * dh;
+            bool ok = rq.n[0] == 1 && rk.n[0] == 1 && rk.n[1] == heads && rk.n[2] == dh &&
+                      rows == 3 * dd && rq.p[1] == y && rk.p[1] == y + dd && rq.p[2] == rk.p[2] &&
+                      rq.p[3] == rk.p[3] && sk.n[0] == 1 && sv.n[0] == 1 && sk.p[1] == rk.p[0] &&
+                      sv.p[1] == y + 2 * dd && sk.n[1] == sv.n[1] && sk.n[2] == heads &&
+                      sv.n[2] == heads && sk.n[3] == dh && sv.n[3] == dh && dh % 2 == 0;
+            int64_t T = 1;
+            while ((16 * T) % dh) T++;
+            ok = ok && T <= 4 && dd % (16 * T) == 0;
+            if (ok) {
+                epi = EPI_ROPE;
+                used = 5;
+                s0.T = (int32_t)T;
+                s0.d = (int32_t)dd;
+                s0.dh = (int32_t)dh;
+                s0.o1 = (float*)rq.p[0];
+                s0.o2 = (float*)rk.p[0];
+                s0.o3 = (float*)sk.p[0];
+                s0.o4 = (float*)sv.p[0];
+                cs = rq.p[2];
+                sn = rq.p[3];
+                s0.cap = sk.n[1];
+                s0.dyn = (const long long*)sk.dyn;
+                s0.imm = sk.n[4];
+                s0.dyn2 = (const long long*)sv.dyn;
+                s0.imm2 = sv.n[4];
+            }
+        }
+        // L block: l2norm q, l2norm k, then the decay linear on the same input
+        // (model.rs:463-470)
+        if (epi == EPI_PLAIN && is(i + 1, OP_L2NORM) && is(i + 2, OP_L2NORM)) {
+            const Op &lq = ops[i + 1], &lk = ops[i + 2];
+            int64_t heads = lq.n[0], dh = lq.n[1], dd = heads * dh;
+            bool ok = lk.n[0] == heads && lk.n[1] == dh && rows == 4 * dd && lq.p[1] == y &&
+                      lk.p[1] == y + dd;
+            int64_t T = 1;
+            while ((16 * T) % dh) T++;
+            ok = ok && T <= 4 && dd % (16 * T) == 0;
+            if (ok) {
+                epi = EPI_L2;
+                used = 3;
+                s0.T = (int32_t)T;
+                s0.d = (int32_t)dd;
+                s0.dh = (int32_t)dh;
+                s0.o1 = (float*)lq.p[0];
+                s0.o2 = (float*)lk.p[0];
+                if (is(i + 3, OP_LINEAR) && ops[i + 3].n[2] == 1 && ops[i + 3].p[2] == x &&
+                    ops[i + 3].n[1] == cols && aligned16(ops[i + 3].p[1])) {
+                    const Op& D = ops[i + 3];
+                    FgSeg& s1 = seg[1];
+                    s1.w = D.p[1];
+                    s1.y = (float*)D.p[0];
+                    s1.rows = (int32_t)D.n[0];
+                    s1.tiles = (int32_t)((D.n[0] + 15) / 16);
+                    s1.T = 1;
+                    s1.epi = EPI_PLAIN;
+                    nseg = 2;
+                    used = 4;
+                }
+            }
+        }
+        // MLP up: SiLU of the gate half times the amp half (model.rs:552-555)
+        if (epi == EPI_PLAIN && is(i + 1, OP_SILU_MUL)) {
+            const Op& sm = ops[i + 1];
+            int64_t hid = rows / 2;
+            if (rows % 32 == 0 && sm.n[0] == hid && sm.p[1] == y && sm.p[2] == y + hid) {
+                epi = EPI_SILU;
+                used = 2;
+                s0.T = 2;
+                s0.hid = (int32_t)hid;
+                s0.o1 = (float*)sm.p[0];
+            }
+        }
+        // residual add after the linear (model.rs:547, 557)
+        if (epi == EPI_PLAIN && is(i + 1, OP_ADD) && ops[i + 1].n[0] == rows &&
+            (ops[i + 1].p[1] == y || ops[i + 1].p[2] == y)) {
+            const Op& a = ops[i + 1];
+            const float* r = a.p[1] == y ? a.p[2] : a.p[1];
+            if (!overlap(rng(r, rows), rng(y, rows))) {
+                epi = EPI_RESID;
+                used = 2;
+                s0.o1 = (float*)a.p[0];
+                res = r;
+            }
+        }
+        s0.epi = epi;
+        int nsl = (int)((cols / 16 + SLM_KS - 1) / SLM_KS);
+        // a big linear takes more tiles per workgroup (fewer copies of the prologue)
+        if ((epi == EPI_PLAIN || epi == EPI_RESID) && nseg == 1 && rows >= 4096) s0.T = 4;
+        auto fits = [&](int T) {
+            int Wt = std::min(16 / T, nsl);
+            return (nsl + Wt - 1) / Wt <= SLM_FG_SLICES;
+        };
+        if (epi == EPI_PLAIN || epi == EPI_RESID)
+            while (s0.T > 1 && !fits(s0.T)) s0.T /= 2;
+        int maxT = 1;
+        for (int k = 0; k < nseg; k++) maxT = std::max(maxT, (int)seg[k].T);
+        if (!fits(maxT)) return 0;
+        int Wt = std::min(16 / maxT, nsl);
+        // what the segments read and write
+        for (int k = 0; k < nseg; k++) {
+            const FgSeg& s = seg[k];
+            b.reads.push_back(rng(s.w, (int64_t)s.rows * cols));
+            b.writes.push_back(rng(s.y, s.rows));
+            switch (s.epi) {
+                case EPI_RESID: b.writes.push_back(rng(s.o1, s.rows)); break;
+                case EPI_SILU: b.writes.push_back(rng(s.o1, s.hid)); break;
+                case EPI_L2:
+                    b.writes.push_back(rng(s.o1, s.d));
+                    b.writes.push_back(rng(s.o2, s.d));
+                    break;
+                case EPI_ROPE: {
+                    int64_t heads = s.d / s.dh;
+                    b.writes.push_back(rng(s.o1, s.d));
+                    b.writes.push_back(rng(s.o2, s.d));
+                    b.writes.push_back(rng(s.o3, heads * s.cap * s.dh));
+                    b.writes.push_back(rng(s.o4, heads * s.cap * s.dh));
+                    break;
+                }
+            }
+        }
+        // the GEMV input and the epilogue inputs
+        int xin = b.find(x, cols, nproduced);
+        if (xin == -2) return 0;
+        if (xin < 0) {
+            if (!aligned16(x)) return 0;
+            b.reads.push_back(rng(x, cols));
+        }
+        std::vector<int> want;
+        if (xin >= 0) want.push_back(xin);
+        if (epi == EPI_ROPE) {
+            int half = s0.dh / 2;
+            int r1 = b.find(cs, half, nproduced), r2 = b.find(sn, half, nproduced);
+            if (r1 == -2 || r2 == -2) return 0;
+            if (r1 < 0) {
+                b.reads.push_back(rng(cs, half));
+                if (!b.prefetch(cs, half, nullptr, 0, 0, 0, &r1)) return 0;
+            } else {
+                want.push_back(r1);
+            }
+            if (r2 < 0) {
+                b.reads.push_back(rng(sn, half));
+                if (!b.prefetch(sn, half, nullptr, 0, 0, 0, &r2)) return 0;
+            } else {
+                want.push_back(r2);
+            }
+            s0.cs_lds = r1;
+            s0.sn_lds = r2;
+        }
+        if (epi == EPI_RESID) {
+            if (b.find(res, rows, b.slots.size()) != -1) return 0;  // must be in memory already
+            b.reads.push_back(rng(res, rows));
+            if (!b.prefetch(res, s0.T * 16, nullptr, 0, 1, (int)rows, &s0.res_lds)) return 0;
+        }
+        // element-wise ops right after the group that neither read its results nor touch
+        // what it reads run in workgroup 0 (e.g. the copy s <- x after the inject linear,
+        // model.rs:580-581)
+        for (size_t j = i + used; j < ops.size(); j++) {
+            VpSrc v;
+            if (!vp_of(ops[j], &v) || (v.kind != SRC_COPY && v.kind != SRC_ADD && v.kind != SRC_MIX))
+                break;
+            bool clash = false;
+            for (int q = 0; q < 2; q++) {
+                if (v.in[q])
+                    for (auto& w : b.writes) clash |= overlap(rng(v.in[q], v.n), w);
+                if (v.out[q]) {
+                    for (auto& w : b.writes) clash |= overlap(rng(v.out[q], v.n), w);
+                    for (auto& r : b.reads) clash |= overlap(rng(v.out[q], v.n), r);
+                }
+            }
+            if (clash) break;
+            FgBuild save = b;
+            if (!add_vp(b, v, true)) {
+                b = save;
+                break;
+            }
+            used++;
+        }
+        // prologue ops every workgroup needs: those the GEMV input and the epilogue read
+        std::vector<bool> need(b.d.nvp, false);
+        for (size_t k = b.slots.size(); k-- > 0;) {
+            const auto& sl = b.slots[k];
+            int opk = b.slot_op[k];
+            bool hit = false;
+            for (int w : want) hit |= w >= sl.off && w < sl.off + sl.n;
+            if (!hit || opk < 0 || need[opk]) continue;
+            need[opk] = true;
+            const VpOp& o = b.d.vp[opk];
+            want.push_back(o.in0);
+            if (o.in1 >= 0) want.push_back(o.in1);
+            // the slot's op may read slots made earlier: resolve them on later passes
+            k = b.slots.size();
+        }
+        for (int k = 0; k < b.d.nvp; k++) b.d.vp[k].wg0 = need[k] ? 0 : 1;
+        // hazards: no global write of this kernel may meet a global read or another write
+        for (auto& w : b.writes)
+            for (auto& r : b.reads)
+                if (overlap(w, r)) return 0;
+        for (size_t a = 0; a < b.writes.size(); a++)
+            for (size_t q = a + 1; q < b.writes.size(); q++)
+                if (overlap(b.writes[a], b.writes[q])) return 0;
+        // workgroups and LDS
+        int wg = 0;
+        for (int k = 0; k < nseg; k++) {
+            FgSeg& s = seg[k];
+            if (s.epi == EPI_SILU) {
+                if (s.tiles % 2) return 0;
+                s.wgs = s.tiles / 2;
+            } else {
+                s.wgs = (s.tiles + s.T - 1) / s.T;
+            }
+            s.wg_first = wg;
+            wg += s.wgs;
+        }
+        int threads = 64 * maxT * Wt;
+        if (b.pf_floats > SLM_PF_PER_THREAD * threads) return 0;
+        FgDesc& d = b.d;
+        d.cols = (int32_t)cols;
+        d.nsl = nsl;
+        d.Wt = Wt;
+        d.xin = xin;
+        d.x = x;
+        d.nseg = nseg;
+        d.lds_vp = (b.lds + 3) & ~3;
+        d.fold_off = d.lds_vp + 32;
+        d.epi_off = d.fold_off + maxT * nsl * 16;
+        int total = d.epi_off + maxT * 16 + 16;
+        if (total * 4 > LDS_MAX) return 0;
+        for (int k = 0; k < nseg; k++) d.seg[k] = seg[k];
+        out.push_back(mk_desc(c->k.fg, (uint32_t)wg, (uint32_t)threads, (uint32_t)(total * 4), d));
+        return used;
+    }
+
+    // gla (one token) + rms(head_norm) + silu_mul(gate): model.rs:471-484
+    size_t try_gla(size_t i) {
+        const Op& g = ops[i];
+        if (g.n[0] != 1) return 0;
+        int64_t heads = g.n[1], dh = g.n[2];
+        if (dh * 4 > 1024) return 0;
+        GlaDesc d;
+        std::memset(&d, 0, sizeof d);
+        d.y = (float*)g.p[0];
+        d.s = (float*)g.p[1];
+        d.q = g.p[2];
+        d.k = g.p[3];
+        d.v = g.p[4];
+        d.decay = g.p[5];
+        d.bias = g.p[6];
+        d.heads = (int32_t)heads;
+        d.dh = (int32_t)dh;
+        size_t used = 1;
+        if (i + 2 < ops.size() && ops[i + 1].kind == OP_RMS && ops[i + 2].kind == OP_SILU_MUL) {
+            const Op &r = ops[i + 1], &sm = ops[i + 2];
+            int64_t n = heads * dh;
+            bool ok = r.n[0] == heads && r.n[1] == dh && r.p[1] == g.p[0] && sm.n[0] == n &&
+                      sm.p[2] == r.p[0];
+            // the gate is read while y, y2 and the output are written by other workgroups
+            ok = ok && !overlap(rng(sm.p[1], n), rng(g.p[0], n)) &&
+                 !overlap(rng(sm.p[1], n), rng(r.p[0], n)) && !overlap(rng(sm.p[1], n), rng(sm.p[0], n)) &&
+                 !overlap(rng(r.p[0], n), rng(g.p[0], n));
+            if (ok) {
+                d.fuse = 1;
+                d.y2 = (float*)r.p[0];
+                d.hn = r.p[2];
+                d.eps = r.f[0];
+                d.gate = sm.p[1];
+                d.out = (float*)sm.p[0];
+                used = 3;
+            }
+        }
+        int ri = pow2_index((dh + 3) / 4, 6);
+        out.push_back(mk_desc(c->k.gla1[ri], (uint32_t)heads, (uint32_t)((dh * 4 + 63) / 64 * 64),
+                              (uint32_t)((dh + 1) * 4), d));
+        return used;
+    }
+
+    int run(bool fuse) {
+        size_t i = 0;
+        while (i < ops.size()) {
+            const Op& o = ops[i];
+            VpSrc v;
+            if (fuse && pend.size() < SLM_VP_MAX && vp_of(o, &v)) {
+                pend.push_back(v);
+                i++;
+                continue;
+            }
+            if (fuse && o.kind == OP_LINEAR && o.n[2] == 1) {
+                size_t used = try_fg(i);
+                if (used) {
+                    pend.clear();
+                    i += used;
+                    continue;
+                }
+            }
+            TRY(flush_pending());
+            if (fuse && o.kind == OP_ATTEND && o.n[1] == 1) {
+                std::vector<Rec> two;
+                TRY(lower_one(c, o, two));
+                out.push_back(two[0]);  // the partials; the combine waits for the next linear
+                VpSrc cv;
+                cv.kind = SRC_COMBINE;
+                cv.n = (int)(o.n[5] * o.n[7]);
+                cv.out[0] = o.p[0];
+                cv.op = &o;
+                if (cv.n % 4 == 0 && cv.n <= VP_LEN_MAX)
+                    pend.push_back(cv);
+                else
+                    out.push_back(two[1]);
+                i++;
+                continue;
+            }
+            if (fuse && o.kind == OP_GLA) {
+                size_t used = try_gla(i);
+                if (used) {
+                    i += used;
+                    continue;
+                }
+            }
+            TRY(lower_one(c, o, out));
+            i++;
+        }
+        return flush_pending();
+    }
+};
+
+int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fuse) {
+    Planner p{c, ops, out, {}};
+    size_t before = out.size();
+    TRY(p.run(fuse));
+    c->last_ops = ops.size();
+    c->last_kernels = out.size() - before;
+    return SLM_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// dynamic values, recording, graphs
+// ---------------------------------------------------------------------------------------
 
 int upload_dyn(slm_hip* c) {
     if (c->dyn.empty()) return SLM_OK;
@@ -191,53 +1003,48 @@ int upload_dyn(slm_hip* c) {
     return SLM_OK;
 }
 
+int launch_all(slm_hip* c, const std::vector<Rec>& recs) {
+    for (auto& r : recs) TRY(launch_now(c, r));
+    return SLM_OK;
+}
+
 // Leaves recording for the rest of this step: what was recorded runs now.
 int taint(slm_hip* c) {
     if (!c->recording || c->tainted) return SLM_OK;
     c->tainted = true;
     c->n_eager++;
-    int rc = upload_dyn(c);
-    if (rc) return rc;
-    for (auto& r : c->recs)
-        if ((rc = launch_now(c, r))) return rc;
-    c->recs.clear();
-    return SLM_OK;
+    TRY(upload_dyn(c));
+    std::vector<Rec> recs;
+    TRY(plan(c, c->ops, recs, c->fusion_on));
+    c->ops.clear();
+    return launch_all(c, recs);
 }
 
-int emit(slm_hip* c, const Rec& r) {
-    if (c->recording && !c->tainted) {
-        c->recs.push_back(r);
+bool recording(const slm_hip* c) { return c->recording && !c->tainted; }
+
+// Queues an op: recorded inside a step, lowered and launched otherwise.
+int submit(slm_hip* c, const Op& o) {
+    if (recording(c)) {
+        c->ops.push_back(o);
         return SLM_OK;
     }
-    return launch_now(c, r);
+    std::vector<Rec> recs;
+    TRY(lower_one(c, o, recs));
+    return launch_all(c, recs);
 }
 
-template <typename... A>
-int go(slm_hip* c, hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx,
-       uint32_t shmem, A... args) {
-    Rec r;
-    r.f = f;
-    r.gx = gx;
-    r.gy = gy;
-    r.gz = gz;
-    r.bx = bx;
-    r.shmem = shmem;
-    r.nargs = 0;
-    std::memset(r.args, 0, sizeof r.args);
-    pack(r, args...);
-    return emit(c, r);
-}
-
-uint32_t blocks_for(size_t n, size_t per = 256, size_t cap = 4096) {
-    size_t b = (n + per - 1) / per;
-    return (uint32_t)std::max<size_t>(1, std::min(b, cap));
+Op op(uint32_t kind) {
+    Op o;
+    std::memset(&o, 0, sizeof o);
+    o.kind = kind;
+    return o;
 }
 
 // Dynamic values (positions, token ids, factors): returns a device pointer to a copy of
 // `bytes` bytes of `src`, valid for kernels queued after it on the stream.
 int stage(slm_hip* c, const void* src, size_t bytes, const void** out) {
     size_t need = (bytes + 7) & ~(size_t)7;
-    if (c->recording && !c->tainted) {
+    if (recording(c)) {
         size_t off = c->dyn.size();
         if (off + need <= DYN_CAP) {
             c->dyn.resize(off + need);
@@ -245,8 +1052,7 @@ int stage(slm_hip* c, const void* src, size_t bytes, const void** out) {
             *out = c->dyn_dev + off;
             return SLM_OK;
         }
-        int rc = taint(c);
-        if (rc) return rc;
+        TRY(taint(c));
     }
     if (need > STAGE_CAP) return fail(c, SLM_E_UNSUPPORTED, "stage: %zu bytes at once", bytes);
     if (c->stage_head + need > STAGE_CAP) {
@@ -261,11 +1067,23 @@ int stage(slm_hip* c, const void* src, size_t bytes, const void** out) {
     return SLM_OK;
 }
 
+// A position: staged inside a step (so the op is the same every token), immediate outside.
+int stage_pos(slm_hip* c, size_t pos, Op& o, int slot) {
+    long long p = (long long)pos;
+    if (recording(c)) {
+        TRY(stage(c, &p, 8, &o.dyn));
+        o.n[slot] = 0;
+    } else {
+        o.dyn = nullptr;
+        o.n[slot] = p;
+    }
+    return SLM_OK;
+}
+
 // Reallocations of internal buffers happen between launches only: recorded work that
 // may point at the old buffer runs first, and graphs that do are dropped.
 int internal_realloc(slm_hip* c, void** p, size_t bytes) {
-    int rc = taint(c);
-    if (rc) return rc;
+    TRY(taint(c));
     drop_graphs(c);
     HIPC(c, hipStreamSynchronize(c->stream));
     if (*p) HIPC(c, hipFree(*p));
@@ -277,92 +1095,37 @@ int internal_realloc(slm_hip* c, void** p, size_t bytes) {
 int need_ws(slm_hip* c, size_t bytes) {
     if (bytes <= c->ws_bytes) return SLM_OK;
     size_t nb = std::max(bytes, c->ws_bytes * 2);
-    int rc = internal_realloc(c, (void**)&c->ws, nb);
-    if (rc) return rc;
+    TRY(internal_realloc(c, (void**)&c->ws, nb));
     c->ws_bytes = nb;
     return SLM_OK;
 }
 
-int get_fn(slm_hip* c, hipFunction_t* f, const char* name) {
-    hipError_t e = hipModuleGetFunction(f, c->mod, name);
-    if (e != hipSuccess) return fail(c, SLM_E_HIP, "kernel %s: %s", name, hipGetErrorString(e));
-    return SLM_OK;
-}
-
-int load_kernels(slm_hip* c) {
-    Kernels& k = c->k;
-    struct {
-        hipFunction_t* f;
-        const char* n;
-    } fns[] = {{&k.copy, "slm_copy"},
-               {&k.add, "slm_add"},
-               {&k.add_row, "slm_add_row"},
-               {&k.mix, "slm_mix"},
-               {&k.silu_mul, "slm_silu_mul"},
-               {&k.scale_rows, "slm_scale_rows"},
-               {&k.shift, "slm_shift"},
-               {&k.columns, "slm_columns"},
-               {&k.gather, "slm_gather"},
-               {&k.store, "slm_store"},
-               {&k.rope, "slm_rope"},
-               {&k.rope_table, "slm_rope_table"},
-               {&k.rms, "slm_rms"},
-               {&k.l2norm, "slm_l2norm"},
-               {&k.fill, "slm_fill"},
-               {&k.combine, "slm_attn_combine"},
-               {&k.probe, "slm_probe_mfma"},
-               {&k.lin_small[0], "slm_linear_small_s"},
-               {&k.lin_small[1], "slm_linear_small_v"},
-               {&k.lin_big[0], "slm_linear_big_s"},
-               {&k.lin_big[1], "slm_linear_big_v"},
-               {&k.gla[0], "slm_gla_1"},
-               {&k.gla[1], "slm_gla_2"},
-               {&k.gla[2], "slm_gla_4"},
-               {&k.gla[3], "slm_gla_8"},
-               {&k.gla[4], "slm_gla_16"},
-               {&k.gla[5], "slm_gla_32"},
-               {&k.gla[6], "slm_gla_64"},
-               {&k.attn[0], "slm_attn_part_1"},
-               {&k.attn[1], "slm_attn_part_2"},
-               {&k.attn[2], "slm_attn_part_4"},
-               {&k.attn[3], "slm_attn_part_8"},
-               {&k.attn[4], "slm_attn_part_16"}};
-    for (auto& f : fns) {
-        int rc = get_fn(c, f.f, f.n);
-        if (rc) return rc;
-    }
-    return SLM_OK;
-}
-
-int fill(slm_hip* c, float* y, size_t n, float v) {
-    return go(c, c->k.fill, blocks_for(n), 1, 1, 256, 0, y, (long long)n, v);
-}
-
-int pow2_index(size_t need, int maxi) {  // smallest i with 2^i >= need
-    int i = 0;
-    while (i < maxi && ((size_t)1 << i) < need) i++;
-    return i;
-}
-
-// Captures the recorded step into a graph, or finds one that matches it.
+// Captures the recorded step into a graph, or finds one that matches it; with graphs
+// off, plans the step and launches it directly.
 int finish_step(slm_hip* c) {
     c->recording = false;
     if (c->tainted) {
         c->tainted = false;
         return SLM_OK;
     }
-    int rc = upload_dyn(c);
-    if (rc) return rc;
+    TRY(upload_dyn(c));
+    if (!c->graphs_on) {
+        std::vector<Rec> recs;
+        TRY(plan(c, c->ops, recs, c->fusion_on));
+        return launch_all(c, recs);
+    }
     c->clock++;
     for (auto& g : c->cache) {
-        if (g.recs.size() == c->recs.size() && g.ndyn == c->dyn.size() &&
-            std::memcmp(g.recs.data(), c->recs.data(), c->recs.size() * sizeof(Rec)) == 0) {
+        if (g.ops.size() == c->ops.size() && g.ndyn == c->dyn.size() &&
+            std::memcmp(g.ops.data(), c->ops.data(), c->ops.size() * sizeof(Op)) == 0) {
             g.used = c->clock;
             HIPC(c, hipGraphLaunch(g.exec, c->stream));
             c->n_launched++;
             return SLM_OK;
         }
     }
+    std::vector<Rec> recs;
+    TRY(plan(c, c->ops, recs, c->fusion_on));
     if (c->cache.size() >= MAX_GRAPHS) {
         auto old = std::min_element(c->cache.begin(), c->cache.end(),
                                     [](const Graph& a, const Graph& b) { return a.used < b.used; });
@@ -371,13 +1134,13 @@ int finish_step(slm_hip* c) {
         c->cache.erase(old);
     }
     Graph g;
-    g.recs = c->recs;
+    g.ops = c->ops;
     g.ndyn = c->dyn.size();
     g.used = c->clock;
     hipGraph_t graph = nullptr;
     HIPC(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    for (auto& r : g.recs) {
-        rc = launch_now(c, r);
+    for (auto& r : recs) {
+        int rc = launch_now(c, r);
         if (rc) {
             hipStreamEndCapture(c->stream, &graph);
             if (graph) hipGraphDestroy(graph);
@@ -392,6 +1155,41 @@ int finish_step(slm_hip* c) {
     c->n_captured++;
     c->n_launched++;
     c->cache.push_back(std::move(g));
+    return SLM_OK;
+}
+
+int get_fn(slm_hip* c, hipFunction_t* f, const char* name) {
+    hipError_t e = hipModuleGetFunction(f, c->mod, name);
+    if (e != hipSuccess) return fail(c, SLM_E_HIP, "kernel %s: %s", name, hipGetErrorString(e));
+    return SLM_OK;
+}
+
+int load_kernels(slm_hip* c) {
+    Kernels& k = c->k;
+    struct {
+        hipFunction_t* f;
+        const char* n;
+    } fns[] = {{&k.copy, "slm_copy"},           {&k.add, "slm_add"},
+               {&k.add_row, "slm_add_row"},     {&k.mix, "slm_mix"},
+               {&k.silu_mul, "slm_silu_mul"},   {&k.scale_rows, "slm_scale_rows"},
+               {&k.shift, "slm_shift"},         {&k.columns, "slm_columns"},
+               {&k.gather, "slm_gather"},       {&k.store, "slm_store"},
+               {&k.rope, "slm_rope"},           {&k.rope_table, "slm_rope_table"},
+               {&k.rms, "slm_rms"},             {&k.l2norm, "slm_l2norm"},
+               {&k.fill, "slm_fill"},           {&k.combine, "slm_attn_combine"},
+               {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
+               {&k.lin_small[0], "slm_linear_small_s"}, {&k.lin_small[1], "slm_linear_small_v"},
+               {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
+               {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
+               {&k.gla[3], "slm_gla_8"},   {&k.gla[4], "slm_gla_16"},  {&k.gla[5], "slm_gla_32"},
+               {&k.gla[6], "slm_gla_64"},
+               {&k.gla1[0], "slm_gla1_1"}, {&k.gla1[1], "slm_gla1_2"}, {&k.gla1[2], "slm_gla1_4"},
+               {&k.gla1[3], "slm_gla1_8"}, {&k.gla1[4], "slm_gla1_16"}, {&k.gla1[5], "slm_gla1_32"},
+               {&k.gla1[6], "slm_gla1_64"},
+               {&k.attn[0], "slm_attn_part_1"}, {&k.attn[1], "slm_attn_part_2"},
+               {&k.attn[2], "slm_attn_part_4"}, {&k.attn[3], "slm_attn_part_8"},
+               {&k.attn[4], "slm_attn_part_16"}};
+    for (auto& f : fns) TRY(get_fn(c, f.f, f.n));
     return SLM_OK;
 }
 
@@ -447,9 +1245,11 @@ int slm_hip_open(int device, slm_hip** out) {
     c->ws_bytes = 1 << 20;
     OPEN_HIP(hipMalloc((void**)&c->ws, c->ws_bytes));
     c->dyn.reserve(DYN_CAP);
-    c->recs.reserve(4096);
+    c->ops.reserve(4096);
     const char* env = getenv("SLM_HIP_GRAPHS");
     if (env && env[0] == '0') c->graphs_on = false;
+    env = getenv("SLM_HIP_FUSION");
+    if (env && env[0] == '0') c->fusion_on = false;
 #undef OPEN_HIP
     *out = c;
     return SLM_OK;
@@ -497,16 +1297,8 @@ int slm_hip_alloc(slm_hip* c, size_t n, float** out) {
     if (e != hipSuccess) return fail(c, SLM_E_MEMORY, "alloc %zu floats: %s", n, hipGetErrorString(e));
     // zeroed on the stream now, ordered before any later use of the buffer (also before
     // the launches of a step being recorded, which run at flush)
-    Rec r;
-    r.f = c->k.fill;
-    r.gx = blocks_for(bytes / 4);
-    r.gy = r.gz = 1;
-    r.bx = 256;
-    r.shmem = 0;
-    r.nargs = 0;
-    std::memset(r.args, 0, sizeof r.args);
-    pack(r, p, (long long)(bytes / 4), 0.0f);
-    int rc = launch_now(c, r);
+    int rc = launch_now(c, mk(c->k.fill, blocks_for(bytes / 4), 1, 1, 256, 0, p,
+                              (long long)(bytes / 4), 0.0f));
     if (rc) {
         hipFree(p);
         return rc;
@@ -521,8 +1313,7 @@ int slm_hip_free(slm_hip* c, float* p) {
     if (!p) return SLM_OK;
     auto it = c->allocs.find((uintptr_t)p);
     if (it == c->allocs.end()) return fail(c, SLM_E_BOUNDS, "free: %p was not allocated here", (void*)p);
-    int rc = taint(c);
-    if (rc) return rc;
+    TRY(taint(c));
     drop_graphs(c);
     c->allocs.erase(it);
     HIPC(c, hipStreamSynchronize(c->stream));
@@ -534,11 +1325,11 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
     if (!c || (n && !src)) return SLM_E_INVALID;
     NEED(c, "upload", dst, n);
     if (n == 0) return SLM_OK;
-    int rc = taint(c);
-    if (rc) return rc;
+    TRY(taint(c));
     for (auto it = c->tables.begin(); it != c->tables.end();) {  // inv_freq rewritten
         if (it->first >= (uintptr_t)dst && it->first < (uintptr_t)(dst + n)) {
             drop_graphs(c);
+            hipStreamSynchronize(c->stream);
             hipFree(it->second.cos);
             hipFree(it->second.sin);
             it = c->tables.erase(it);
@@ -554,8 +1345,7 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
 int slm_hip_read(slm_hip* c, float* host, const float* dev, size_t n) {
     if (!c || (n && !host)) return SLM_E_INVALID;
     NEED(c, "read", dev, n);
-    int rc = taint(c);
-    if (rc) return rc;
+    TRY(taint(c));
     size_t done = 0;
     while (done < n) {
         size_t part = std::min(n - done, BOUNCE_CAP / 4);
@@ -578,11 +1368,17 @@ int slm_hip_flush(slm_hip* c, const float* const* keep, size_t nkeep) {
 
 int slm_hip_set_graphs(slm_hip* c, int on) {
     if (!c) return SLM_E_INVALID;
-    if (c->recording) {
-        int rc = finish_step(c);
-        if (rc) return rc;
-    }
+    if (c->recording) TRY(finish_step(c));
+    if (!on) drop_graphs(c);
     c->graphs_on = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_set_fusion(slm_hip* c, int on) {
+    if (!c) return SLM_E_INVALID;
+    if (c->recording) TRY(finish_step(c));
+    if (c->fusion_on != (on != 0)) drop_graphs(c);
+    c->fusion_on = on != 0;
     return SLM_OK;
 }
 
@@ -594,6 +1390,13 @@ int slm_hip_graph_stats(slm_hip* c, uint64_t* launched, uint64_t* captured, uint
     return SLM_OK;
 }
 
+int slm_hip_last_plan(slm_hip* c, uint64_t* ops, uint64_t* kernels) {
+    if (!c) return SLM_E_INVALID;
+    if (ops) *ops = c->last_ops;
+    if (kernels) *kernels = c->last_kernels;
+    return SLM_OK;
+}
+
 // ---- element-wise operations ----
 
 int slm_hip_copy(slm_hip* c, float* y, const float* x, size_t n) {
@@ -601,7 +1404,11 @@ int slm_hip_copy(slm_hip* c, float* y, const float* x, size_t n) {
     NEED(c, "copy", y, n);
     NEED(c, "copy", x, n);
     if (!n) return SLM_OK;
-    return go(c, c->k.copy, blocks_for(n), 1, 1, 256, 0, y, x, (long long)n);
+    Op o = op(OP_COPY);
+    o.p[0] = y;
+    o.p[1] = x;
+    o.n[0] = (int64_t)n;
+    return submit(c, o);
 }
 
 int slm_hip_add(slm_hip* c, float* y, const float* a, const float* b, size_t n) {
@@ -610,7 +1417,12 @@ int slm_hip_add(slm_hip* c, float* y, const float* a, const float* b, size_t n) 
     NEED(c, "add", a, n);
     NEED(c, "add", b, n);
     if (!n) return SLM_OK;
-    return go(c, c->k.add, blocks_for(n), 1, 1, 256, 0, y, a, b, (long long)n);
+    Op o = op(OP_ADD);
+    o.p[0] = y;
+    o.p[1] = a;
+    o.p[2] = b;
+    o.n[0] = (int64_t)n;
+    return submit(c, o);
 }
 
 int slm_hip_add_row(slm_hip* c, float* y, const float* x, const float* row, size_t m, size_t d) {
@@ -619,8 +1431,13 @@ int slm_hip_add_row(slm_hip* c, float* y, const float* x, const float* row, size
     NEED(c, "add_row", x, m * d);
     NEED(c, "add_row", row, d);
     if (!m || !d) return SLM_OK;
-    return go(c, c->k.add_row, blocks_for(m * d), 1, 1, 256, 0, y, x, row, (long long)(m * d),
-              (long long)d);
+    Op o = op(OP_ADD_ROW);
+    o.p[0] = y;
+    o.p[1] = x;
+    o.p[2] = row;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)d;
+    return submit(c, o);
 }
 
 int slm_hip_mix(slm_hip* c, float* y, const float* a, const float* b, size_t n, float t) {
@@ -629,7 +1446,13 @@ int slm_hip_mix(slm_hip* c, float* y, const float* a, const float* b, size_t n, 
     NEED(c, "mix", a, n);
     NEED(c, "mix", b, n);
     if (!n) return SLM_OK;
-    return go(c, c->k.mix, blocks_for(n), 1, 1, 256, 0, y, a, b, (long long)n, t);
+    Op o = op(OP_MIX);
+    o.p[0] = y;
+    o.p[1] = a;
+    o.p[2] = b;
+    o.n[0] = (int64_t)n;
+    o.f[0] = t;
+    return submit(c, o);
 }
 
 int slm_hip_silu_mul(slm_hip* c, float* y, const float* g, const float* u, size_t n) {
@@ -638,7 +1461,12 @@ int slm_hip_silu_mul(slm_hip* c, float* y, const float* g, const float* u, size_
     NEED(c, "silu_mul", g, n);
     NEED(c, "silu_mul", u, n);
     if (!n) return SLM_OK;
-    return go(c, c->k.silu_mul, blocks_for(n), 1, 1, 256, 0, y, g, u, (long long)n);
+    Op o = op(OP_SILU_MUL);
+    o.p[0] = y;
+    o.p[1] = g;
+    o.p[2] = u;
+    o.n[0] = (int64_t)n;
+    return submit(c, o);
 }
 
 int slm_hip_scale_rows(slm_hip* c, float* y, const float* x, const float* f, size_t m, size_t d) {
@@ -646,16 +1474,17 @@ int slm_hip_scale_rows(slm_hip* c, float* y, const float* x, const float* f, siz
     NEED(c, "scale_rows", y, m * d);
     NEED(c, "scale_rows", x, m * d);
     if (!m || !d) return SLM_OK;
-    const void* fd = nullptr;
-    float f0 = 0.0f;
-    if (m == 1 && !(c->recording && !c->tainted)) {
-        f0 = f[0];
+    Op o = op(OP_SCALE_ROWS);
+    o.p[0] = y;
+    o.p[1] = x;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)d;
+    if (m == 1 && !recording(c)) {
+        o.f[0] = f[0];
     } else {
-        int rc = stage(c, f, m * 4, &fd);
-        if (rc) return rc;
+        TRY(stage(c, f, m * 4, &o.dyn));
     }
-    return go(c, c->k.scale_rows, blocks_for(m * d), 1, 1, 256, 0, y, x, (const float*)fd, f0,
-              (long long)(m * d), (long long)d);
+    return submit(c, o);
 }
 
 int slm_hip_shift(slm_hip* c, float* y, const float* first, const float* x, size_t m, size_t d) {
@@ -665,8 +1494,13 @@ int slm_hip_shift(slm_hip* c, float* y, const float* first, const float* x, size
     NEED(c, "shift", first, d);
     NEED(c, "shift", x, (m - 1) * d);
     if (!d) return SLM_OK;
-    return go(c, c->k.shift, blocks_for(m * d), 1, 1, 256, 0, y, first, x, (long long)(m * d),
-              (long long)d);
+    Op o = op(OP_SHIFT);
+    o.p[0] = y;
+    o.p[1] = first;
+    o.p[2] = x;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)d;
+    return submit(c, o);
 }
 
 int slm_hip_columns(slm_hip* c, float* y, const float* x, size_t m, size_t stride, size_t off,
@@ -676,8 +1510,14 @@ int slm_hip_columns(slm_hip* c, float* y, const float* x, size_t m, size_t strid
     if (off + len > stride) return fail(c, SLM_E_INVALID, "columns: off + len > stride");
     NEED(c, "columns", y, m * len);
     NEED(c, "columns", x, (m - 1) * stride + off + len);
-    return go(c, c->k.columns, blocks_for(m * len), 1, 1, 256, 0, y, x, (long long)(m * len),
-              (long long)stride, (long long)off, (long long)len);
+    Op o = op(OP_COLUMNS);
+    o.p[0] = y;
+    o.p[1] = x;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)stride;
+    o.n[2] = (int64_t)off;
+    o.n[3] = (int64_t)len;
+    return submit(c, o);
 }
 
 int slm_hip_gather(slm_hip* c, float* y, const float* w, const uint32_t* ids, size_t m, size_t d) {
@@ -691,11 +1531,13 @@ int slm_hip_gather(slm_hip* c, float* y, const float* w, const uint32_t* ids, si
             return fail(c, SLM_E_BOUNDS, "gather: id %u is past the %zu rows of w", ids[i], rows);
         v[i] = ids[i];
     }
-    const void* dv = nullptr;
-    int rc = stage(c, v.data(), m * 8, &dv);
-    if (rc) return rc;
-    return go(c, c->k.gather, blocks_for(m * d), 1, 1, 256, 0, y, w, (const long long*)dv,
-              (long long)(m * d), (long long)d);
+    Op o = op(OP_GATHER);
+    o.p[0] = y;
+    o.p[1] = w;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)d;
+    TRY(stage(c, v.data(), m * 8, &o.dyn));
+    return submit(c, o);
 }
 
 int slm_hip_store(slm_hip* c, float* cache, const float* src, size_t pos, size_t m, size_t cap,
@@ -705,15 +1547,15 @@ int slm_hip_store(slm_hip* c, float* cache, const float* src, size_t pos, size_t
     if (!cap) return fail(c, SLM_E_INVALID, "store: cap is 0");
     NEED(c, "store", cache, heads * cap * dh);
     NEED(c, "store", src, m * heads * dh);
-    const void* dp = nullptr;
-    long long p = (long long)pos;
-    if (c->recording && !c->tainted) {
-        int rc = stage(c, &p, 8, &dp);
-        if (rc) return rc;
-    }
-    return go(c, c->k.store, blocks_for(m * heads * dh), 1, 1, 256, 0, cache, src,
-              (const long long*)dp, dp ? 0LL : p, (long long)(m * heads * dh), (long long)cap,
-              (long long)heads, (long long)dh);
+    Op o = op(OP_STORE);
+    o.p[0] = cache;
+    o.p[1] = src;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)cap;
+    o.n[2] = (int64_t)heads;
+    o.n[3] = (int64_t)dh;
+    TRY(stage_pos(c, pos, o, 4));
+    return submit(c, o);
 }
 
 int slm_hip_rope(slm_hip* c, float* y, const float* x, const float* cs, const float* sn,
@@ -725,8 +1567,15 @@ int slm_hip_rope(slm_hip* c, float* y, const float* x, const float* cs, const fl
     NEED(c, "rope", cs, m * dh / 2);
     NEED(c, "rope", sn, m * dh / 2);
     if (!m || !heads || !dh) return SLM_OK;
-    return go(c, c->k.rope, blocks_for(m * heads * dh / 2), 1, 1, 256, 0, y, x, cs, sn,
-              (long long)m, (long long)heads, (long long)dh);
+    Op o = op(OP_ROPE);
+    o.p[0] = y;
+    o.p[1] = x;
+    o.p[2] = cs;
+    o.p[3] = sn;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)heads;
+    o.n[2] = (int64_t)dh;
+    return submit(c, o);
 }
 
 int slm_hip_rope_table(slm_hip* c, float* cs, float* sn, const float* inv, size_t pos, size_t m,
@@ -735,28 +1584,17 @@ int slm_hip_rope_table(slm_hip* c, float* cs, float* sn, const float* inv, size_
     NEED(c, "rope_table", cs, m * half);
     NEED(c, "rope_table", sn, m * half);
     NEED(c, "rope_table", inv, half);
-    // the first call of every advance (model.rs:566) begins a step
-    if (c->graphs_on) {
-        if (c->recording) {
-            int rc = finish_step(c);
-            if (rc) return rc;
-        }
-        c->recording = true;
-        c->tainted = false;
-        c->recs.clear();
-        c->dyn.clear();
-    }
-    if (!m || !half) return SLM_OK;
+    // the first call of every advance (model.rs:566) ends the previous step, makes sure the
+    // resident table covers this one, then begins it
+    if (c->recording) TRY(finish_step(c));
     Table& t = c->tables[(uintptr_t)inv];
-    if (t.inv.size() != half) {  // first sight of this inv_freq buffer
-        int rc = taint(c);
-        if (rc) return rc;
+    if (half && t.inv.size() != half) {  // first sight of this inv_freq buffer
         t.inv.assign(half, 0.0f);
         HIPC(c, hipStreamSynchronize(c->stream));
         HIPC(c, hipMemcpy(t.inv.data(), inv, half * 4, hipMemcpyDeviceToHost));
         t.rows = 0;
     }
-    if (pos + m > t.rows) {
+    if (half && pos + m > t.rows) {
         size_t rows = std::max<size_t>({pos + m, t.rows * 2, 8192});
         // cpu.rs:228-236: angle (pos + i) as f32 times inv[j], then libm cos/sin
         std::vector<float> hc(rows * half), hs(rows * half);
@@ -768,37 +1606,45 @@ int slm_hip_rope_table(slm_hip* c, float* cs, float* sn, const float* inv, size_
                 hs[p * half + j] = sinf(a);
             }
         }
-        int rc = internal_realloc(c, (void**)&t.cos, rows * half * 4);
-        if (!rc) rc = internal_realloc(c, (void**)&t.sin, rows * half * 4);
-        if (rc) return rc;
+        TRY(internal_realloc(c, (void**)&t.cos, rows * half * 4));
+        TRY(internal_realloc(c, (void**)&t.sin, rows * half * 4));
         HIPC(c, hipMemcpy(t.cos, hc.data(), rows * half * 4, hipMemcpyHostToDevice));
         HIPC(c, hipMemcpy(t.sin, hs.data(), rows * half * 4, hipMemcpyHostToDevice));
         t.rows = rows;
     }
-    const void* dp = nullptr;
-    long long p = (long long)pos;
-    if (c->recording && !c->tainted) {
-        int rc = stage(c, &p, 8, &dp);
-        if (rc) return rc;
+    if (c->graphs_on || c->fusion_on) {
+        c->recording = true;
+        c->tainted = false;
+        c->ops.clear();
+        c->dyn.clear();
     }
-    return go(c, c->k.rope_table, blocks_for(m * half), 1, 1, 256, 0, cs, sn,
-              (const float*)t.cos, (const float*)t.sin, (const long long*)dp, dp ? 0LL : p,
-              (long long)(m * half), (long long)half);
+    if (!m || !half) return SLM_OK;
+    Op o = op(OP_ROPE_TABLE);
+    o.p[0] = cs;
+    o.p[1] = sn;
+    o.p[2] = t.cos;
+    o.p[3] = t.sin;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)half;
+    TRY(stage_pos(c, pos, o, 2));
+    return submit(c, o);
 }
 
 // ---- normalisation ----
 
-static int norm_launch(slm_hip* c, hipFunction_t f, float* y, const float* x, const float* w,
-                size_t groups, size_t size, float eps, bool rms) {
+static int norm_op(slm_hip* c, uint32_t kind, float* y, const float* x, const float* w,
+                   size_t groups, size_t size, float eps) {
     if (!fits_int(groups) || !fits_int(size) || groups * size > (size_t)INT_MAX)
-        return fail(c, SLM_E_UNSUPPORTED, "%s: %zu groups of %zu", rms ? "rms" : "l2norm", groups, size);
-    size_t stride = size | 1;
-    size_t G = std::min<size_t>(16, std::max<size_t>(1, 16384 / stride));
-    if (G * stride * 4 > 65536) return fail(c, SLM_E_UNSUPPORTED, "norm: size %zu is above 16383", size);
-    uint32_t blocks = (uint32_t)((groups + G - 1) / G);
-    uint32_t shmem = (uint32_t)(G * stride * 4);
-    if (rms) return go(c, f, blocks, 1, 1, 256, shmem, y, x, w, (int)groups, (int)size, eps, (int)G);
-    return go(c, f, blocks, 1, 1, 256, shmem, y, x, (int)groups, (int)size, (int)G);
+        return fail(c, SLM_E_UNSUPPORTED, "norm: %zu groups of %zu", groups, size);
+    if ((size | 1) * 4 > 65536) return fail(c, SLM_E_UNSUPPORTED, "norm: size %zu is above 16383", size);
+    Op o = op(kind);
+    o.p[0] = y;
+    o.p[1] = x;
+    o.p[2] = w;
+    o.n[0] = (int64_t)groups;
+    o.n[1] = (int64_t)size;
+    o.f[0] = eps;
+    return submit(c, o);
 }
 
 int slm_hip_rms(slm_hip* c, float* y, const float* x, const float* w, size_t groups, size_t size,
@@ -808,7 +1654,7 @@ int slm_hip_rms(slm_hip* c, float* y, const float* x, const float* w, size_t gro
     NEED(c, "rms", x, groups * size);
     NEED(c, "rms", w, size);
     if (!groups || !size) return SLM_OK;
-    return norm_launch(c, c->k.rms, y, x, w, groups, size, eps, true);
+    return norm_op(c, OP_RMS, y, x, w, groups, size, eps);
 }
 
 int slm_hip_l2norm(slm_hip* c, float* y, const float* x, size_t heads, size_t dh) {
@@ -816,7 +1662,7 @@ int slm_hip_l2norm(slm_hip* c, float* y, const float* x, size_t heads, size_t dh
     NEED(c, "l2norm", y, heads * dh);
     NEED(c, "l2norm", x, heads * dh);
     if (!heads || !dh) return SLM_OK;
-    return norm_launch(c, c->k.l2norm, y, x, nullptr, heads, dh, 0.0f, false);
+    return norm_op(c, OP_L2NORM, y, x, nullptr, heads, dh, 0.0f);
 }
 
 // ---- linear ----
@@ -828,18 +1674,16 @@ int slm_hip_linear(slm_hip* c, float* y, const float* w, size_t rows, size_t col
     NEED(c, "linear", w, rows * cols);
     NEED(c, "linear", x, m * cols);
     if (!m || !rows) return SLM_OK;
-    if (!cols) return fill(c, y, m * rows, 0.0f);
     if (!fits_int(rows) || !fits_int(cols) || !fits_int(m))
         return fail(c, SLM_E_UNSUPPORTED, "linear: %zu x %zu x %zu", rows, cols, m);
-    int vec = (cols % 4 == 0 && aligned16(w) && aligned16(x)) ? 1 : 0;
-    size_t kblocks = (cols + 15) / 16, nsl = (kblocks + 15) / 16;
-    if (m <= 16 && nsl <= 64) {
-        uint32_t waves = (uint32_t)std::min<size_t>(nsl, 8);
-        return go(c, c->k.lin_small[vec], (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
-                  (uint32_t)(nsl * 1024), y, w, x, (int)rows, (int)cols, (int)m);
-    }
-    return go(c, c->k.lin_big[vec], (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64), 1,
-              256, 0, y, w, x, (int)rows, (int)cols, (int)m);
+    Op o = op(OP_LINEAR);
+    o.p[0] = y;
+    o.p[1] = w;
+    o.p[2] = x;
+    o.n[0] = (int64_t)rows;
+    o.n[1] = (int64_t)cols;
+    o.n[2] = (int64_t)m;
+    return submit(c, o);
 }
 
 // ---- gated linear attention ----
@@ -859,10 +1703,18 @@ int slm_hip_gla(slm_hip* c, float* y, float* s, const float* q, const float* k, 
     if (dh > 256) return fail(c, SLM_E_UNSUPPORTED, "gla: head size %zu is above 256", dh);
     if (!fits_int(m) || !fits_int(heads * dh * 4))
         return fail(c, SLM_E_UNSUPPORTED, "gla: %zu tokens x %zu heads", m, heads);
-    int i = pow2_index((dh + 3) / 4, 6);
-    size_t threads = heads * dh * 4;
-    return go(c, c->k.gla[i], (uint32_t)((threads + 255) / 256), 1, 1, 256, 0, y, s, q, k, v,
-              decay, bias, (int)m, (int)heads, (int)dh);
+    Op o = op(OP_GLA);
+    o.p[0] = y;
+    o.p[1] = s;
+    o.p[2] = q;
+    o.p[3] = k;
+    o.p[4] = v;
+    o.p[5] = decay;
+    o.p[6] = bias;
+    o.n[0] = (int64_t)m;
+    o.n[1] = (int64_t)heads;
+    o.n[2] = (int64_t)dh;
+    return submit(c, o);
 }
 
 // ---- attention ----
@@ -900,29 +1752,28 @@ int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const fl
         long long last = pos + (long long)m - 1 - gap;
         nsb = last >= first ? (size_t)(last / 512 - first / 512 + 1) : 1;
     }
-    int dti = pow2_index((dh + 15) / 16, 4);
-    size_t dp = (size_t)16 << dti;
-    size_t wpp = 8;
-    while (wpp > 1 && wpp * 16 * (dp + 2) * 4 > 65536) wpp /= 2;
     size_t qpt = 16 / group;
     size_t qtiles = (m + qpt - 1) / qpt;
-    size_t part_floats = nsb * m * heads * (dp + 2);
-    int rc = need_ws(c, part_floats * 4);
-    if (rc) return rc;
-    const void* dpos = nullptr;
-    if (c->recording && !c->tainted) {
-        rc = stage(c, &pos, 8, &dpos);
-        if (rc) return rc;
-    }
     if (qtiles > UINT32_MAX || nsb > 65535)
         return fail(c, SLM_E_UNSUPPORTED, "attend: %zu query tiles x %zu superblocks", qtiles, nsb);
-    rc = go(c, c->k.attn[dti], (uint32_t)qtiles, (uint32_t)kh, (uint32_t)nsb, 512,
-            (uint32_t)(wpp * 16 * (dp + 2) * 4), c->ws, q, k, v, (const long long*)dpos,
-            dpos ? 0LL : pos, (int)m, reach, gap, (long long)cap, (int)heads, (int)kh, (int)dh,
-            a->scale, (int)wpp);
-    if (rc) return rc;
-    return go(c, c->k.combine, blocks_for(m * heads * dh), 1, 1, 256, 0, y, (const float*)c->ws,
-              (int)m, (int)heads, (int)dh, (int)dp, (int)nsb);
+    size_t dp = (size_t)16 << pow2_index((dh + 15) / 16, 4);
+    TRY(need_ws(c, nsb * m * heads * (dp + 2) * 4));
+    Op o = op(OP_ATTEND);
+    o.p[0] = y;
+    o.p[1] = q;
+    o.p[2] = k;
+    o.p[3] = v;
+    o.n[1] = (int64_t)m;
+    o.n[2] = reach;
+    o.n[3] = gap;
+    o.n[4] = (int64_t)cap;
+    o.n[5] = (int64_t)heads;
+    o.n[6] = (int64_t)kh;
+    o.n[7] = (int64_t)dh;
+    o.n[8] = (int64_t)nsb;
+    o.f[0] = a->scale;
+    TRY(stage_pos(c, a->pos, o, 0));
+    return submit(c, o);
 }
 
 // ---- diagnostics ----
@@ -939,7 +1790,8 @@ int slm_hip_probe_mfma(slm_hip* c, float* out, const float* a, const float* b) {
     NEED(c, "probe", out, 256);
     NEED(c, "probe", a, 64);
     NEED(c, "probe", b, 64);
-    return go(c, c->k.probe, 1, 1, 1, 64, 0, out, a, b);
+    TRY(taint(c));
+    return launch_now(c, mk(c->k.probe, 1, 1, 1, 64, 0, out, a, b));
 }
 
 }  // extern "C"

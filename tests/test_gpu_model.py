@@ -190,3 +190,30 @@ def test_a86_chunked_ring_state_equals_step(pkg, hip):
     b.feed(toks, 1)
     assert np.array_equal(a.logits(), b.logits())
     _kept_equal(a, b)
+
+
+@pytest.mark.parametrize("name", ["tiny", "a86"])
+def test_fused_steps_match_per_op_kernels(pkg, hip, tiny_dir, name):
+    """The planner's fused one-token kernels give the same bits as one launch per op."""
+    folder = tiny_dir if name == "tiny" else model_dir("a86", 2)
+    m = pkg.Model(hip, folder)
+    vocab = m.cfg.vocab_size
+    toks = synth.tokens(300, vocab, seed=12)
+    runs = []
+    for fuse in (False, True):
+        hip.set_fusion(fuse)
+        s = m.session(3 if name == "tiny" else 4)
+        s.feed(toks[:260], 256)
+        logits = []
+        for t in toks[260:]:
+            s.step(int(t))
+            logits.append(s.logits())
+        runs.append((s, logits, hip.last_plan()))
+    hip.set_fusion(True)
+    (a, la, pa), (b, lb, pb) = runs
+    print(f"{name}: one-token step = {pb['ops']} ops -> {pa['kernels']} kernels unfused, "
+          f"{pb['kernels']} fused")
+    assert pb["kernels"] < pa["kernels"]
+    for x, y in zip(la, lb):
+        assert np.array_equal(x, y)
+    _kept_equal(a, b)

@@ -252,3 +252,91 @@ def test_attend(hip, case):
     for i in sorted({0, m // 2, m - 1}):
         hip.attend(d1.ptr, dq.at(i * heads * dh), dk.ptr, dv.ptr, **dict(a, pos=a["pos"] + i, m=1))
         assert np.array_equal(d1.read(), got[i * heads * dh:(i + 1) * heads * dh]), i
+
+
+# ---------------------------------------------------------------------------------------
+# fused one-token kernels: each pattern the planner fuses, against one launch per op
+# ---------------------------------------------------------------------------------------
+
+def _step(hip, body, inv, cs, sn, fuse):
+    """Records one step (rope_table .. flush) and runs it fused or unfused."""
+    hip.set_fusion(fuse)
+    hip.rope_table(cs.ptr, sn.ptr, inv.ptr, 7, 1, 32)
+    body()
+    hip.flush()
+    plan = hip.last_plan()
+    hip.set_fusion(True)
+    return plan
+
+
+FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "combine", "side_copy"]
+
+
+@pytest.mark.parametrize("case", FUSION_CASES)
+def test_fusion_pattern(hip, case):
+    d, heads, dh, hid, cap = 768, 12, 64, 3072, 4352
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(32), hip.alloc(32)
+    wsq = hip.upload(rnd(d, d, scale=0.02))
+    wqkv = hip.upload(rnd(3 * d, d, scale=0.02))
+    wqkvg = hip.upload(rnd(4 * d, d, scale=0.02))
+    wdec = hip.upload(rnd(heads, d, scale=0.02))
+    wup = hip.upload(rnd(2 * hid, d, scale=0.02))
+    x = hip.upload(rnd(d))
+    res = hip.upload(rnd(d))
+    nw = hip.upload(rnd(d))
+    kring = hip.upload(rnd(heads, cap, dh))
+    vring = hip.upload(rnd(heads, cap, dh))
+    q = hip.upload(rnd(heads, dh))
+
+    def outs():
+        return {k: hip.alloc(n) for k, n in
+                dict(n=d, y=4 * d, q=d, k=d, t=d, up=2 * hid, g=hid, dd=heads, s=d,
+                     kr=heads * cap * dh, vr=heads * cap * dh, att=d).items()}
+
+    def body(o):
+        if case == "plain":
+            hip.linear(o["y"].ptr, wsq.ptr, d, d, x.ptr, 1)
+        elif case == "rms":
+            hip.rms(o["n"].ptr, x.ptr, nw.ptr, 1, d, 1e-6)
+            hip.linear(o["y"].ptr, wsq.ptr, d, d, o["n"].ptr, 1)
+        elif case == "resid":
+            hip.linear(o["y"].ptr, wsq.ptr, d, d, x.ptr, 1)
+            hip.add(o["t"].ptr, res.ptr, o["y"].ptr, d)
+        elif case == "silu":
+            hip.linear(o["up"].ptr, wup.ptr, 2 * hid, d, x.ptr, 1)
+            hip.silu_mul(o["g"].ptr, o["up"].ptr, o["up"].at(hid), hid)
+        elif case == "rope_store":
+            hip.rms(o["n"].ptr, x.ptr, nw.ptr, 1, d, 1e-6)
+            hip.linear(o["y"].ptr, wqkv.ptr, 3 * d, d, o["n"].ptr, 1)
+            hip.rope(o["q"].ptr, o["y"].ptr, cs.ptr, sn.ptr, 1, heads, dh)
+            hip.rope(o["k"].ptr, o["y"].at(d), cs.ptr, sn.ptr, 1, heads, dh)
+            hip.store(o["kr"].ptr, o["k"].ptr, 4100, 1, cap, heads, dh)
+            hip.store(o["vr"].ptr, o["y"].at(2 * d), 4100, 1, cap, heads, dh)
+        elif case == "l2_decay":
+            hip.linear(o["y"].ptr, wqkvg.ptr, 4 * d, d, x.ptr, 1)
+            hip.l2norm(o["q"].ptr, o["y"].ptr, heads, dh)
+            hip.l2norm(o["k"].ptr, o["y"].at(d), heads, dh)
+            hip.linear(o["dd"].ptr, wdec.ptr, heads, d, x.ptr, 1)
+        elif case == "combine":
+            hip.attend(o["att"].ptr, q.ptr, kring.ptr, vring.ptr, pos=5000, m=1, reach=4096,
+                       gap=0, cap=cap, heads=heads, key_heads=heads, dh=dh, scale=0.125)
+            hip.linear(o["y"].ptr, wsq.ptr, d, d, o["att"].ptr, 1)
+            hip.add(o["t"].ptr, res.ptr, o["y"].ptr, d)
+        elif case == "side_copy":
+            hip.linear(o["y"].ptr, wsq.ptr, d, d, x.ptr, 1)
+            hip.copy(o["s"].ptr, x.ptr, d)
+            hip.add(o["t"].ptr, o["s"].ptr, o["y"].ptr, d)
+
+    got = []
+    for fuse in (False, True):
+        o = outs()
+        plan = _step(hip, lambda: body(o), inv, cs, sn, fuse)
+        got.append(({k: b.read() for k, b in o.items()}, plan))
+    (a, pa), (b, pb) = got
+    print(case, "unfused", pa, "fused", pb)
+    assert pb["kernels"] <= pa["kernels"]
+    if case != "plain":
+        assert pb["kernels"] < pa["kernels"]
+    for k in a:
+        assert np.array_equal(a[k], b[k]), (case, k, float(np.abs(a[k] - b[k]).max()))
