@@ -2,26 +2,30 @@
 // the device code (kernels.hip): plain C layouts of fixed-width fields, passed by value
 // as the single kernel argument.
 //
-// A fused GEMV (slm_fg) runs, for one token (m = 1):
-//   1. a prologue of small vector operations (the step's element-wise ops, rms, the
-//      attention combine, rope-table rows, the embedding row) that produce the GEMV's
-//      input: every workgroup computes them into LDS, workgroup 0 also writes them out;
-//   2. one to three weight matrices applied to that input (the canonical MFMA chain);
-//   3. an epilogue on each matrix's outputs (rope + ring store, l2norm, SiLU of the
-//      gate/amp pair, residual add).
-// Every value is computed with the same expression, in the same order, as the per-op
-// kernels, so fused and unfused runs give the same bits.
+// A fused GEMV (slm_fg) runs, for one token (m = 1), in a workgroup of two kinds of waves:
+//   - GEMV waves, one per 64-column slice of a split: each issues the weight loads of its
+//     first unit at once, then runs the canonical MFMA chain of its slice for every unit
+//     of the workgroup, the loads of the next unit in flight while one unit computes;
+//   - prologue/epilogue waves: they load every global vector the kernel reads into LDS,
+//     run the prologue (the step's element-wise ops, rms, the attention combine, the
+//     fold of a split linear's partials, rope-table rows, the embedding row) that makes
+//     the GEMV input, then, per unit, add the slice partials in order and run the
+//     epilogue (residual add, rope + ring store, SiLU of the gate/amp pair).
+// A unit is one 16-row tile of one split of one weight matrix; units go round-robin over
+// the grid. Every value is computed with the same expression, in the same order, as the
+// per-op kernels, so fused and unfused runs give the same bits.
 #ifndef SLM_FUSION_H
 #define SLM_FUSION_H
 
 #include <stdint.h>
 
-#define SLM_VP_MAX 10
+#define SLM_VP_MAX 12
 #define SLM_SEG_MAX 3
 #define SLM_PF_MAX 12
-#define SLM_PF_PER_THREAD 12   // prefetched floats per thread (flat over all PfOps)
 #define SLM_KS 4               // 16-column blocks per canonical slice (64 columns)
-#define SLM_FG_SLICES 3        // most slices one wave of slm_fg holds
+#define SLM_SPLIT 12           // slices per canonical split (768 columns)
+#define SLM_FG_EPI_WAVES 4     // prologue/epilogue waves of slm_fg
+#define SLM_FG_MISC (32 + 4 * SLM_PF_MAX)  // LDS floats of slm_fg's scalars and prefetch table
 
 enum {
     VP_COPY = 1,    // out = in0
@@ -31,29 +35,28 @@ enum {
     VP_RMS,         // out = rms(in0) · lds[w], eps f
     VP_COMBINE,     // out = attention combine of the partials (lds[w], or `part`), heads × dh
     VP_SILU,        // out = in1 · in0 / (1 + e^−in0)   (silu_mul with g = in0, u = in1)
+    VP_FOLD,        // out = ((P0 + P1) + P2) + ...: the splits of a linear, lds[w] [nsb][n]
 };
 
 enum {
-    EPI_PLAIN = 0,  // y
-    EPI_RESID = 1,  // y; o1 = residual + y                    (add after the linear)
+    EPI_PLAIN = 0,  // y (or the split's partial)
+    EPI_RESID = 1,  // y; o1 = res + y                       (add after the linear)
     EPI_ROPE = 2,   // y = [q|k|v]; o1 = rope(q), o2 = rope(k), o3[ring] = o2, o4[ring] = v
-    EPI_L2 = 3,     // y = [q|k|v|g]; o1 = l2norm(q), o2 = l2norm(k)
-    EPI_SILU = 4,   // y = [gate|amp]; o1 = amp · gate / (1 + e^−gate)
+    EPI_SILU = 3,   // y = [gate|amp]; o1 = amp · gate / (1 + e^−gate)
 };
 
-// A global vector copied into LDS before anything else runs, so the kernel waits for
-// memory once: src + dyn[0]·stride (when dyn) + the workgroup's first row (when wgrow).
+// A global vector copied into LDS by the prologue waves: src + dyn[0]·stride (when dyn).
+// n is a multiple of 4 and the source 16-byte aligned.
 typedef struct {
     const float* src;
     const long long* dyn;
-    int32_t n, lds, stride, wgrow;
-    int32_t limit, pad;     // wgrow: rows past `limit` are not read
+    int32_t n, lds, stride, first4;  // first4: running count of float4s before this one
 } PfOp;
 
 typedef struct {
     int32_t kind, n, wg0;   // length; wg0: only workgroup 0 runs it (a side effect)
     int32_t out, in0, in1;  // LDS float offsets
-    int32_t w;              // LDS offset of the rms weight / combine partials (-1: `part`)
+    int32_t w;              // LDS offset of the rms weight / combine / fold partials (-1: `part`)
     int32_t heads, dh, dp, nsb;
     int32_t pad;
     float* gout;            // global output, written by workgroup 0 (null: none)
@@ -63,21 +66,24 @@ typedef struct {
     float pad2;
 } VpOp;
 
+// One weight matrix of a fused GEMV. Its rows are grouped into 16-row tiles: the first
+// pair_rows rows (a multiple of 16) in tiles of 8 (row, row + half) pairs, pair P at row
+// (P / half)·2·half + P % half (the rope halves of a head, or the gate and amp rows of a
+// SiLU pair), the rest in consecutive rows.
 typedef struct {
     const float* w;         // weights [rows][cols]
     float* y;               // the linear's output
-    int32_t rows, tiles;    // tiles = ceil(rows / 16)
-    int32_t T;              // tiles per workgroup
-    int32_t wgs;            // workgroups of this segment
-    int32_t wg_first;       // index of its first workgroup
+    float* part;            // nsplit > 1: the split partials [nsplit][rows]
+    int32_t rows, tiles, nsplit, units, unit_first;
+    int32_t pair_rows, half;
     int32_t epi;
-    int32_t d, dh, hid;     // part width, head size, hidden width (SiLU pairs)
-    int32_t res_lds;        // RESID: LDS offset of this workgroup's residual rows
+    int32_t d, dh;          // ROPE: part width, head size
     int32_t cs_lds, sn_lds; // ROPE: LDS offsets of the cos / sin row
     float* o1;
     float* o2;
     float* o3;
     float* o4;
+    const float* res;       // RESID: the residual
     long long cap;          // ring slots (ROPE)
     const long long* dyn;   // ring position of the k store (ROPE), else imm
     long long imm;
@@ -86,17 +92,17 @@ typedef struct {
 } FgSeg;
 
 typedef struct {
-    int32_t npf, nvp, cols, nsl;  // nsl: canonical slices of `cols`
-    int32_t Wt, xin, nseg, lds_vp;  // Wt: waves per tile; xin: LDS offset of the input (-1: x)
-    int32_t fold_off, epi_off, pad0, pad1;
-    const float* x;
+    int32_t npf, nvp, cols, nsl;    // nsl: canonical slices of `cols`
+    int32_t W, xin, nseg, units;    // W: GEMV waves (slices per split); xin: LDS offset of x
+    int32_t lds_vp, fold_off, pf4, pad;  // pf4: float4s the prologue loads
     PfOp pf[SLM_PF_MAX];
     VpOp vp[SLM_VP_MAX];
     FgSeg seg[SLM_SEG_MAX];
 } FgDesc;
 
-// Gated linear attention for one token with the head RMSNorm and SiLU gate that follow it
-// in an L block (model.rs:471-484): y = gla(...); y2 = rms(y, head_norm); out = silu(gate)·y2.
+// Gated linear attention for one token with the ops around it in an L block
+// (model.rs:463-484): optionally q, k = l2norm(q_raw), l2norm(k_raw) first; then
+// y = gla(...); when fused further y2 = rms(y, head_norm) and out = silu(gate)·y2.
 typedef struct {
     float* s;
     const float* q;
@@ -104,13 +110,16 @@ typedef struct {
     const float* v;
     const float* decay;
     const float* bias;
-    float* y;        // the gla output when not fused further
+    float* y;        // the gla output
     float* y2;       // rms output
     float* out;      // silu_mul output
     const float* hn; // head_norm weight
     const float* gate;
-    int32_t heads, dh, fuse;
+    float* qn;       // l2: the normalised q and k, written out
+    float* kn;
+    int32_t heads, dh, fuse, l2;
     float eps;
+    float pad;
 } GlaDesc;
 
 #endif

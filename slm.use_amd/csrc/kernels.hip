@@ -6,8 +6,9 @@
 // many tokens a call carries (m = 1 decode or an m = 256 prompt chunk), so a prompt read
 // in chunks leaves bit-identical state to one read token by token:
 //   - linear: one fixed MFMA chain per output (v_mfma_f32_16x16x4f32 over 16-column
-//     blocks, columns split into 256-wide slices whose partial sums are added in order);
-//     the m <= 16 kernel and the m > 16 kernel run the same chain;
+//     blocks, chained from zero within 64-column slices; slice sums added in order within
+//     768-column splits, split sums added in order); the m <= 16 kernel, the m > 16
+//     kernel and the fused one-token kernel run the same chain;
 //   - attend: keys are grouped by absolute position into 16-key tiles, 64-key segments
 //     and 512-key superblocks; a segment is an online softmax over its tiles, segments
 //     fold into superblocks in order and superblocks into the result in order;
@@ -274,8 +275,10 @@ GLA(64)
 // 16: lane group g = l/16 loads the four columns 16kb+4g .. 16kb+4g+3 of its row (of w)
 // and of its token (of x), and MFMA e (e = 0..3) takes element e of both, so MFMA e of
 // block kb sums the columns {16kb + 4g + e : g = 0..3}. Blocks are chained in order
-// within a slice of SLM_KS = 4 blocks (64 columns) starting from zero, and the slice
-// sums are added in order: y = ((P0 + P1) + P2) + ...   Columns past `cols` load as zero.
+// within a slice of SLM_KS = 4 blocks (64 columns) starting from zero; the slice sums of
+// a split of SLM_SPLIT = 12 slices (768 columns) are added in order, Q = ((P0 + P1) + P2)
+// + ..., and the split sums are added in order: y = ((Q0 + Q1) + Q2) + ...  Columns past
+// `cols` load as zero.
 
 template <bool VEC>
 __device__ __forceinline__ f4 ld4(const float* __restrict__ p, long long row, long long nrows,
@@ -346,8 +349,13 @@ __device__ void linear_small_body(float* __restrict__ y, const float* __restrict
     __syncthreads();
     for (int t = threadIdx.x; t < 256; t += blockDim.x) {
         int rr = t >> 4, tt = t & 15;
-        float tot = part[t];
-        for (int s = 1; s < nsl; s++) tot = tot + part[s * 256 + t];
+        float tot = 0.0f;
+        for (int s0 = 0; s0 < nsl; s0 += SLM_SPLIT) {
+            float q = part[s0 * 256 + t];
+            int s1 = min(s0 + SLM_SPLIT, nsl);
+            for (int s = s0 + 1; s < s1; s++) q = q + part[s * 256 + t];
+            tot = s0 == 0 ? q : tot + q;
+        }
         if (r0 + rr < rows && tt < m) y[(long long)tt * rows + r0 + rr] = tot;
     }
 }
@@ -370,7 +378,7 @@ __device__ void linear_big_body(float* __restrict__ y, const float* __restrict__
     long long rb = (long long)blockIdx.x * 64 + (wave & 1) * 32;
     long long tb = (long long)blockIdx.y * 64 + (wave >> 1) * 32;
     int kblocks = (cols + 15) >> 4, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
-    f4 tot[2][2];
+    f4 tot[2][2], sp[2][2];
     for (int s = 0; s < nsl; s++) {
         f4 acc[2][2];
 #pragma unroll
@@ -392,10 +400,14 @@ __device__ void linear_big_body(float* __restrict__ y, const float* __restrict__
 #pragma unroll
                     for (int v = 0; v < 2; v++) acc[u][v] = mfma4(a[u][e], b[v][e], acc[u][v]);
         }
+        bool open = s % SLM_SPLIT == 0, close = s % SLM_SPLIT == SLM_SPLIT - 1 || s == nsl - 1;
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
-            for (int v = 0; v < 2; v++) tot[u][v] = s == 0 ? acc[u][v] : tot[u][v] + acc[u][v];
+            for (int v = 0; v < 2; v++) {
+                sp[u][v] = open ? acc[u][v] : sp[u][v] + acc[u][v];
+                if (close) tot[u][v] = s < SLM_SPLIT ? sp[u][v] : tot[u][v] + sp[u][v];
+            }
     }
 #pragma unroll
     for (int u = 0; u < 2; u++)
@@ -700,24 +712,25 @@ KERNEL void slm_probe_mfma(float* out, const float* a, const float* b) {
 // fused decode kernels (one token), driven by the descriptors of fusion.h
 // ---------------------------------------------------------------------------------------
 
-// One prologue operation on LDS vectors. Every thread of the workgroup calls it; it ends
-// on a barrier. `misc` is a few floats of LDS for reduction results.
-__device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0) {
-    int tid = threadIdx.x, nt = blockDim.x, n = o.n;
+// One prologue operation on LDS vectors, run by the `pnt` prologue threads (ptid = 0..)
+// of the workgroup. It ends on a barrier that every wave of the workgroup meets (the
+// GEMV waves count them with vp_barriers). `misc` is a few floats of LDS.
+__device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0, int ptid, int pnt) {
+    int n = o.n;
     const float* a = lds + o.in0;
     const float* b = o.in1 >= 0 ? lds + o.in1 : nullptr;
     float* out = o.out >= 0 ? lds + o.out : nullptr;
     float* gout = wg0 ? o.gout : nullptr;
     switch (o.kind) {
         case VP_RMS: {  // rms (cpu.rs:187-207) of one group; a and out may not alias
-            if (tid < 16) {
-                float d = dot16_self(a, n, tid);
-                if (tid == 0) misc[0] = 1.0f / sqrtf(d / (float)n + o.f);
+            if (ptid < 16) {
+                float d = dot16_self(a, n, ptid);
+                if (ptid == 0) misc[0] = 1.0f / sqrtf(d / (float)n + o.f);
             }
             __syncthreads();
             float r = misc[0];
             const float* wt = lds + o.w;
-            for (int c = tid; c < n; c += nt) {
+            for (int c = ptid; c < n; c += pnt) {
                 float v = a[c] * r * wt[c];
                 out[c] = v;
                 if (gout) gout[c] = v;
@@ -726,7 +739,7 @@ __device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0) {
         }
         case VP_COMBINE: {  // slm_attn_combine for one query
             const float* part = o.w >= 0 ? (const float*)(lds + o.w) : o.part;
-            for (int c = tid; c < n; c += nt) {
+            for (int c = ptid; c < n; c += pnt) {
                 int h = c / o.dh, e = c % o.dh;
                 float M = NEG_INF, L = 0.0f, O = 0.0f;
                 for (int z = 0; z < o.nsb; z++) {
@@ -739,10 +752,20 @@ __device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0) {
             }
             break;
         }
+        case VP_FOLD: {  // slm_fold: the splits of a linear added in order
+            const float* part = lds + o.w;
+            for (int c = ptid; c < n; c += pnt) {
+                float v = part[c];
+                for (int z = 1; z < o.nsb; z++) v = v + part[z * n + c];
+                if (out) out[c] = v;
+                if (gout) gout[c] = v;
+            }
+            break;
+        }
         default: {
             float factor = o.f;
             if (o.kind == VP_SCALE && o.dyn) factor = *(const float*)o.dyn;
-            for (int c = tid; c < n; c += nt) {
+            for (int c = ptid; c < n; c += pnt) {
                 float v;
                 switch (o.kind) {
                     case VP_COPY: v = a[c]; break;
@@ -762,153 +785,201 @@ __device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0) {
     __syncthreads();
 }
 
-// The tile a wave's rows come from: workgroup `local` of segment `sg`, tile t of T.
-__device__ __forceinline__ int fg_tile(const FgSeg& sg, int local, int t) {
-    if (sg.epi == EPI_SILU) return t == 0 ? local : local + sg.hid / 16;
-    return local * sg.T + t;
+// Barriers of the prologue: two for the loads, then each op's.
+__device__ __forceinline__ int vp_barriers(const FgDesc& d, bool first) {
+    int n = 2;
+    for (int k = 0; k < d.nvp; k++)
+        if (first || !d.vp[k].wg0) n += d.vp[k].kind == VP_RMS ? 2 : 1;
+    return n;
+}
+
+struct FgUnit {
+    int seg, tile, split;
+};
+
+__device__ __forceinline__ FgUnit fg_unit(const FgDesc& d, int u) {
+    int k = 0;
+    for (int q = 1; q < d.nseg; q++)
+        if (u >= d.seg[q].unit_first) k = q;
+    const FgSeg& s = d.seg[k];
+    int local = u - s.unit_first;
+    return FgUnit{k, local % s.tiles, local / s.tiles};
+}
+
+// Row of lane row i (0..15) of tile t.
+__device__ __forceinline__ long long fg_row(const FgSeg& s, int t, int i) {
+    if (t * 16 < s.pair_rows) {
+        int P = t * 8 + (i & 7);
+        return (long long)(P / s.half) * 2 * s.half + P % s.half + ((i & 8) ? s.half : 0);
+    }
+    return (long long)t * 16 + i;
+}
+
+// Sixteen zero bytes: what a lane past the end of a weight matrix loads.
+__device__ __attribute__((aligned(16))) float slm_zero16[4];
+
+// The weights of slice `sl` of one unit for this lane: four float4s. Lanes past the matrix
+// load zeros from slm_zero16, so the loads are always four and their results are used
+// as they arrive, without a select that would wait for them.
+__device__ __forceinline__ void fg_load(const FgDesc& d, int u, int wave, int i, int g, f4 (&wa)[SLM_KS]) {
+    int kblocks = d.cols >> 4;
+    bool live = u < d.units;
+    FgUnit un = fg_unit(d, live ? u : 0);
+    const FgSeg& s = d.seg[un.seg];
+    int sl = un.split * SLM_SPLIT + wave;
+    long long row = fg_row(s, un.tile, i);
+    bool ok = live && sl < d.nsl && row < s.rows;
+    const float* base = s.w + (ok ? row : 0) * d.cols + 4 * g;
+#pragma unroll
+    for (int q = 0; q < SLM_KS; q++) {
+        int kb = sl * SLM_KS + q;
+        const float* src = ok && kb < kblocks ? base + kb * 16 : slm_zero16;
+        wa[q] = *(const f4*)src;
+    }
+}
+
+// The canonical chain of slice `wave` of unit u; lanes of row 0 of B hold the token.
+__device__ __forceinline__ void fg_chain(const FgDesc& d, int u, int wave, int i, int g,
+                                         const f4 (&wa)[SLM_KS], const float* xin, float* out) {
+    int kblocks = d.cols >> 4;
+    FgUnit cur = fg_unit(d, u);
+    int sl = cur.split * SLM_SPLIT + wave;
+    if (sl >= d.nsl) return;
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < SLM_KS; q++) {
+        int kb = sl * SLM_KS + q;
+        if (kb < kblocks) {
+            f4 xb = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (i == 0) xb = *(const f4*)(xin + kb * 16 + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc = mfma4(wa[q][e], xb[e], acc);
+        }
+    }
+    if (i == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) out[4 * g + r] = acc[r];
+    }
 }
 
 KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
     extern __shared__ float lds[];
-    float* misc = lds + d.lds_vp;          // 32 floats
-    float* foldb = lds + d.fold_off;       // [T][slices][16]
-    float* val = lds + d.epi_off;          // [T·16] row values, then per-head norms
-    int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
-    int i = lane & 15, g = lane >> 4;
-    int sgi = 0;
-    for (int k = 1; k < d.nseg; k++)
-        if ((int)blockIdx.x >= d.seg[k].wg_first) sgi = k;
-    const FgSeg& sg = d.seg[sgi];
-    int local = blockIdx.x - sg.wg_first;
-    int Wt = d.Wt, nsl = d.nsl, kblocks = d.cols >> 4;
-    int t = wave / Wt, wl = wave % Wt;
-    int tile = fg_tile(sg, local, t);
-    bool live = t < sg.T && tile < sg.tiles;
-    long long row = (long long)tile * 16 + i;
-    long long first_row = (long long)local * sg.T * 16;
-    // 1. this wave's weights (slices wl, wl + Wt, ...), issued first
-    f4 wa[SLM_FG_SLICES][SLM_KS];
-#pragma unroll
-    for (int j = 0; j < SLM_FG_SLICES; j++) {
-        int s = wl + j * Wt;
-#pragma unroll
-        for (int u = 0; u < SLM_KS; u++) {
-            int kb = s * SLM_KS + u;
-            wa[j][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (live && s < nsl && kb < kblocks && row < sg.rows)
-                wa[j][u] = *(const f4*)(sg.w + row * d.cols + kb * 16 + 4 * g);
+    float* misc = lds + d.lds_vp;   // 32 floats, then the prefetch table (SLM_FG_MISC)
+    float* foldb = lds + d.fold_off;  // [2 rounds][2 units][W][16]
+    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int W = d.W;
+    bool first = blockIdx.x == 0;
+    int nbar = vp_barriers(d, first);
+    if (wave < W) {
+        // GEMV wave: slice `wave` of the split of every unit of this workgroup, two units
+        // (u and u + grid) per round, eight loads in flight
+        int i = lane & 15, g = lane >> 4, G = gridDim.x;
+        f4 wa[SLM_KS], wb[SLM_KS];
+        int u = blockIdx.x;
+        fg_load(d, u, wave, i, g, wa);
+        fg_load(d, u + G, wave, i, g, wb);
+        for (int k = 0; k < nbar; k++) __syncthreads();
+        const float* xin = lds + d.xin;
+        for (int par = 0;; par ^= 1) {  // rounds alternate between two halves of foldb
+            float* fb = foldb + par * 2 * W * 16;
+            fg_chain(d, u, wave, i, g, wa, xin, fb + wave * 16);
+            if (u + G < d.units) fg_chain(d, u + G, wave, i, g, wb, xin, fb + (W + wave) * 16);
+            __syncthreads();
+            u += 2 * G;
+            if (u >= d.units) break;
+            fg_load(d, u, wave, i, g, wa);
+            fg_load(d, u + G, wave, i, g, wb);
         }
+        return;
     }
-    // 2. every global vector the prologue and epilogue read, into LDS, loads first
-    {
-        long long base[SLM_PF_MAX];
-#pragma unroll
-        for (int j = 0; j < SLM_PF_MAX; j++) {
-            base[j] = 0;
-            if (j < d.npf) {
-                if (d.pf[j].dyn) base[j] = d.pf[j].dyn[0] * d.pf[j].stride;
-                if (d.pf[j].wgrow) base[j] += first_row;
-            }
-        }
-        float v[SLM_PF_PER_THREAD];
-        int dst[SLM_PF_PER_THREAD];
-#pragma unroll
-        for (int q = 0; q < SLM_PF_PER_THREAD; q++) {
-            int f = tid + q * nt, acc = 0, j = 0;
-            dst[q] = -1;
-            for (; j < d.npf; j++) {
-                if (f < acc + d.pf[j].n) break;
-                acc += d.pf[j].n;
-            }
-            if (j < d.npf) {
-                int c = f - acc;
-                const PfOp& p = d.pf[j];
-                bool ok = !p.wgrow || first_row + c < p.limit;
-                if (ok) {
-                    v[q] = p.src[base[j] + c];
-                    dst[q] = p.lds + c;
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < SLM_PF_PER_THREAD; q++)
-            if (dst[q] >= 0) lds[dst[q]] = v[q];
+    // prologue / epilogue waves: where each prefetch comes from, then the loads, many in
+    // flight per thread
+    int ptid = tid - 64 * W, pnt = (int)blockDim.x - 64 * W;
+    const float** pf_src = (const float**)(misc + 32);  // [SLM_PF_MAX]
+    int* pf_tab = (int*)(misc + 32 + 2 * SLM_PF_MAX);   // [SLM_PF_MAX][2]: lds, first4
+    if (ptid < d.npf) {
+        const PfOp& p = d.pf[ptid];
+        pf_src[ptid] = p.src + (p.dyn ? p.dyn[0] * p.stride : 0);
+        pf_tab[2 * ptid] = p.lds;
+        pf_tab[2 * ptid + 1] = p.first4;
     }
     __syncthreads();
-    // 3. the prologue
-    bool first = blockIdx.x == 0;
+    for (int base = ptid; base < d.pf4; base += 8 * pnt) {
+        f4 v[8];
+        int dst[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            int f = base + q * pnt;
+            dst[q] = -1;
+            if (f < d.pf4) {
+                int j = 0;
+                for (int t = 1; t < d.npf; t++)
+                    if (f >= pf_tab[2 * t + 1]) j = t;
+                int c4 = f - pf_tab[2 * j + 1];
+                v[q] = *(const f4*)(pf_src[j] + 4 * c4);
+                dst[q] = pf_tab[2 * j] + 4 * c4;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (dst[q] >= 0) *(f4*)(lds + dst[q]) = v[q];
+    }
+    __syncthreads();
     for (int k = 0; k < d.nvp; k++) {
         const VpOp& o = d.vp[k];
         if (o.wg0 && !first) continue;
-        vp_run(o, lds, misc, first);
+        vp_run(o, lds, misc, first, ptid, pnt);
     }
-    // 4. the canonical chains (token 0 is column 0 of B), several slices interleaved
-    const float* xin = d.xin >= 0 ? (const float*)(lds + d.xin) : d.x;
-    f4 acc[SLM_FG_SLICES];
+    for (int u0 = blockIdx.x, par = 0; u0 < d.units; u0 += 2 * gridDim.x, par ^= 1) {
+        // the GEMV waves write the next round's partials into the other half of foldb
+        // while this round's are read here
+        const float* fb = foldb + par * 2 * W * 16;
+        // epilogue inputs of both units go out before the wait for the partials
+        float res[2] = {0.0f, 0.0f};
+        long long slot[2] = {0, 0};
+        int r = ptid & 15;  // row r of the tile (lanes 0..15 of the first epilogue wave)
 #pragma unroll
-    for (int j = 0; j < SLM_FG_SLICES; j++) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int u = 0; u < SLM_KS; u++) {
-        f4 xb[SLM_FG_SLICES];
-#pragma unroll
-        for (int j = 0; j < SLM_FG_SLICES; j++) {
-            int kb = (wl + j * Wt) * SLM_KS + u;
-            xb[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (i == 0 && wl + j * Wt < nsl && kb < kblocks) xb[j] = *(const f4*)(xin + kb * 16 + 4 * g);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-#pragma unroll
-            for (int j = 0; j < SLM_FG_SLICES; j++) {
-                int s = wl + j * Wt;
-                if (s < nsl && s * SLM_KS + u < kblocks) acc[j] = mfma4(wa[j][u][e], xb[j][e], acc[j]);
+        for (int h = 0; h < 2; h++) {
+            int u = u0 + h * gridDim.x;
+            if (ptid >= 16 || u >= d.units) continue;
+            FgUnit cur = fg_unit(d, u);
+            const FgSeg& sg = d.seg[cur.seg];
+            long long R = fg_row(sg, cur.tile, r);
+            if (R >= sg.rows || sg.nsplit > 1) continue;
+            if (sg.epi == EPI_RESID) res[h] = sg.res[R];
+            if (sg.epi == EPI_ROPE) {
+                int part = (int)(R / sg.d);
+                if (part == 1) slot[h] = (sg.dyn ? sg.dyn[0] : sg.imm) % sg.cap;
+                if (part == 2) slot[h] = (sg.dyn2 ? sg.dyn2[0] : sg.imm2) % sg.cap;
             }
-    }
-    if (live && i == 0) {
-#pragma unroll
-        for (int j = 0; j < SLM_FG_SLICES; j++) {
-            int s = wl + j * Wt;
-            if (s < nsl) {
-#pragma unroll
-                for (int r = 0; r < 4; r++) foldb[(t * nsl + s) * 16 + 4 * g + r] = acc[j][r];
-            }
-        }
-    }
-    __syncthreads();
-    int T = sg.T, nrow = T * 16;
-    if (tid < nrow) {
-        int tt = tid >> 4, rr = tid & 15;
-        float tot = foldb[(tt * nsl) * 16 + rr];
-        for (int q = 1; q < nsl; q++) tot = tot + foldb[(tt * nsl + q) * 16 + rr];
-        val[tid] = tot;
-    }
-    __syncthreads();
-    // 5. the epilogue: one thread per row
-    if (sg.epi == EPI_L2) {  // per-head norms of the q and k parts first
-        int nh = nrow / sg.dh;
-        int hq = tid >> 4;
-        if (hq < nh) {
-            float dsum = dot16_self(val + hq * sg.dh, sg.dh, tid & 15);
-            if ((tid & 15) == 0) val[nrow + hq] = 1.0f / fmaxf(sqrtf(dsum), 1e-12f);
         }
         __syncthreads();
-    }
-    if (tid < nrow) {
-        int tt = tid >> 4, rr = tid & 15;
-        int tl = fg_tile(sg, local, tt);
-        long long R = (long long)tl * 16 + rr;
-        float v = val[tid];
-        if (tl < sg.tiles && R < sg.rows) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int u = u0 + h * gridDim.x;
+            if (u >= d.units) break;
+            FgUnit cur = fg_unit(d, u);
+            const FgSeg& sg = d.seg[cur.seg];
+            float v = 0.0f;
+            if (ptid < 16) {
+                int nsl = min(SLM_SPLIT, d.nsl - cur.split * SLM_SPLIT);
+                v = fb[(h * W) * 16 + r];
+                for (int s = 1; s < nsl; s++) v = v + fb[(h * W + s) * 16 + r];
+            }
+            float partner = __shfl_xor(v, 8);
+            long long R = fg_row(sg, cur.tile, r);
+            if (ptid >= 16 || R >= sg.rows) continue;
+            if (sg.nsplit > 1) {
+                sg.part[(long long)cur.split * sg.rows + R] = v;
+                continue;
+            }
             sg.y[R] = v;
             switch (sg.epi) {
                 case EPI_RESID:
-                    sg.o1[R] = lds[sg.res_lds + tid] + v;
+                    sg.o1[R] = res[h] + v;
                     break;
                 case EPI_SILU:
-                    if (tt == 0) {
-                        float amp = val[16 + rr];
-                        sg.o1[R] = amp * v / (1.0f + expf(-v));
-                    }
+                    if (r < 8) sg.o1[cur.tile * 8 + r] = partner * v / (1.0f + expf(-v));
                     break;
                 case EPI_ROPE: {
                     int part = (int)(R / sg.d), j = (int)(R % sg.d);
@@ -916,27 +987,15 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
                     if (part < 2) {
                         int ie = e < half ? e : e - half;
                         float cs = lds[sg.cs_lds + ie], sn = lds[sg.sn_lds + ie];
-                        float p = val[e < half ? tid + half : tid - half];
-                        float o = e < half ? v * cs - p * sn : p * sn + v * cs;
+                        float o = e < half ? v * cs - partner * sn : partner * sn + v * cs;
                         if (part == 0) {
                             sg.o1[j] = o;
                         } else {
-                            long long slot = (sg.dyn ? sg.dyn[0] : sg.imm) % sg.cap;
                             sg.o2[j] = o;
-                            sg.o3[((long long)head * sg.cap + slot) * sg.dh + e] = o;
+                            sg.o3[((long long)head * sg.cap + slot[h]) * sg.dh + e] = o;
                         }
                     } else {
-                        long long slot = (sg.dyn2 ? sg.dyn2[0] : sg.imm2) % sg.cap;
-                        sg.o4[((long long)head * sg.cap + slot) * sg.dh + e] = v;
-                    }
-                    break;
-                }
-                case EPI_L2: {
-                    int part = (int)(R / sg.d), j = (int)(R % sg.d);
-                    if (part < 2) {
-                        float o = v * val[nrow + tid / sg.dh];
-                        if (part == 0) sg.o1[j] = o;
-                        else sg.o2[j] = o;
+                        sg.o4[((long long)head * sg.cap + slot[h]) * sg.dh + e] = v;
                     }
                     break;
                 }
@@ -947,12 +1006,22 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
     }
 }
 
-// One token of gated linear attention per head (the m = 1 case of gla_body), then, when
-// fused, the head RMSNorm and the SiLU gate of model.rs:483-484, in the same expressions
-// as slm_rms and slm_silu_mul.
+// The splits of a linear added in order: y[c] = ((P0[c] + P1[c]) + P2[c]) + ...
+KERNEL void slm_fold(float* __restrict__ y, const float* __restrict__ part, long long n, int nsplit) {
+    GRID_LOOP(c, n) {
+        float v = part[c];
+        for (int z = 1; z < nsplit; z++) v = v + part[z * n + c];
+        y[c] = v;
+    }
+}
+
+// One token of gated linear attention per head (the m = 1 case of gla_body). When `l2`,
+// q and k are first l2-normalised per head (model.rs:465-467, the expressions of
+// slm_l2norm); when `fuse`, the head RMSNorm and the SiLU gate of model.rs:483-484
+// follow, in the expressions of slm_rms and slm_silu_mul.
 template <int RPL>
 __device__ void gla1_body(const GlaDesc& g) {
-    extern __shared__ float lds[];
+    extern __shared__ float lds[];  // [dh + 4] rms, [dh] q, [dh] k, 4 norms
     int h = blockIdx.x, tid = threadIdx.x, dh = g.dh;
     int b = tid >> 2, j = tid & 3;
     bool live = b < dh;
@@ -964,6 +1033,34 @@ __device__ void gla1_body(const GlaDesc& g) {
         int a = j * RPL + rr;
         st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
     }
+    const float* q = g.q + at;
+    const float* k = g.k + at;
+    if (g.l2) {
+        float* lq = lds + dh + 4;
+        float* lk = lq + dh;
+        float* nr = lk + dh;
+        for (int c = tid; c < dh; c += blockDim.x) {
+            lq[c] = q[c];
+            lk[c] = k[c];
+        }
+        __syncthreads();
+        if (tid < 32) {
+            float d = dot16_self(tid < 16 ? lq : lk, dh, tid & 15);
+            if ((tid & 15) == 0) nr[tid >> 4] = 1.0f / fmaxf(sqrtf(d), 1e-12f);
+        }
+        __syncthreads();
+        float rq = nr[0], rk = nr[1];
+        for (int c = tid; c < dh; c += blockDim.x) {
+            float a = lq[c] * rq, bb = lk[c] * rk;
+            g.qn[at + c] = a;
+            g.kn[at + c] = bb;
+            lq[c] = a;
+            lk[c] = bb;
+        }
+        __syncthreads();
+        q = lq;
+        k = lk;
+    }
     float dc = 1.0f / (1.0f + expf(g.decay[h] + g.bias[h]));
     float vb = live ? g.v[at + b] : 0.0f;
     float part = 0.0f;
@@ -971,8 +1068,8 @@ __device__ void gla1_body(const GlaDesc& g) {
     for (int rr = 0; rr < RPL; rr++) {
         int a = j * RPL + rr;
         if (live && a < dh) {
-            st[rr] = dc * st[rr] + g.k[at + a] * vb;
-            part = part + g.q[at + a] * st[rr];
+            st[rr] = dc * st[rr] + k[a] * vb;
+            part = part + q[a] * st[rr];
         }
     }
     float t1 = part + __shfl_xor(part, 1);

@@ -43,6 +43,7 @@ constexpr size_t BOUNCE_CAP = 4 << 20;    // pinned bounce buffer for reads
 constexpr size_t MAX_GRAPHS = 8;
 constexpr int VP_LEN_MAX = 4096;          // longest vector a fused prologue holds
 constexpr int LDS_MAX = 65536;
+constexpr int FG_GRID_MAX = 256;          // workgroups of a fused GEMV: one per compute unit
 
 enum OpKind : uint32_t {
     OP_GATHER = 1, OP_COPY, OP_SHIFT, OP_COLUMNS, OP_LINEAR, OP_ADD, OP_ADD_ROW, OP_SCALE_ROWS,
@@ -84,7 +85,7 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 
 struct Kernels {
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
-        store, rope, rope_table, rms, l2norm, fill, combine, probe, fg;
+        store, rope, rope_table, rms, l2norm, fill, combine, probe, fg, fold;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[7], gla1[7];           // rows per lane 1, 2, 4, .., 64
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
@@ -102,6 +103,8 @@ struct slm_hip {
     std::map<uintptr_t, size_t> allocs;  // live allocations: start -> bytes
     float* ws = nullptr;                 // attention partials
     size_t ws_bytes = 0;
+    float* part = nullptr;               // split partials of fused one-token linears (two halves)
+    size_t part_bytes = 0;
     unsigned char* stage_host = nullptr; // eager staging: pinned ring copied into a device ring
     unsigned char* stage_dev = nullptr;
     size_t stage_head = 0;
@@ -111,7 +114,7 @@ struct slm_hip {
     unsigned char* dyn_dev = nullptr;
     float* bounce = nullptr;
     std::map<uintptr_t, Table> tables;
-    bool graphs_on = true, fusion_on = true;
+    bool graphs_on = true, fusion_on = true, plan_trace = false;
     bool recording = false, tainted = false;
     std::vector<Op> ops;                 // the step being recorded
     std::vector<unsigned char> dyn;
@@ -384,16 +387,19 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
 
 struct Range {
     uintptr_t a, b;  // [a, b) bytes
+    bool wg0 = false;  // written by workgroup 0 alone, in program order (a prologue output)
 };
 Range rng(const float* p, int64_t n) { return Range{(uintptr_t)p, (uintptr_t)(p + n)}; }
+Range rng0(const float* p, int64_t n) { return Range{(uintptr_t)p, (uintptr_t)(p + n), true}; }
 bool overlap(const Range& x, const Range& y) { return x.a < y.b && y.a < x.b; }
 
 // An element-wise one-token op as prologue material: what it reads and writes.
 enum { SRC_COPY = 1, SRC_ADD, SRC_MIX, SRC_SCALE, SRC_GATHER, SRC_RMS, SRC_ROPE_TABLE, SRC_SILU,
-       SRC_COMBINE };
+       SRC_COMBINE, SRC_FOLD };
 struct VpSrc {
     int kind = 0;
     int n = 0;
+    int nsplit = 0;  // SRC_FOLD: partials [nsplit][n] at in[0]
     const float* in[2] = {nullptr, nullptr};
     const float* out[2] = {nullptr, nullptr};
     const Op* op = nullptr;
@@ -448,6 +454,92 @@ bool vp_of(const Op& o, VpSrc* v) {
 
 int combine_dp(int64_t dh) { return 16 << pow2_index((dh + 15) / 16, 4); }
 
+// What an op reads and writes, in bytes of device memory (ring and state updates count as
+// both). The embedding table and the rope tables are only ever read.
+void op_ranges(const Op& o, std::vector<Range>& rd, std::vector<Range>& wr) {
+    const float* const* p = o.p;
+    const int64_t* n = o.n;
+    switch (o.kind) {
+        case OP_GATHER: wr.push_back(rng(p[0], n[0] * n[1])); rd.push_back(rng(p[1], 1)); break;
+        case OP_COPY: wr.push_back(rng(p[0], n[0])); rd.push_back(rng(p[1], n[0])); break;
+        case OP_SHIFT:
+            wr.push_back(rng(p[0], n[0] * n[1]));
+            rd.push_back(rng(p[1], n[1]));
+            rd.push_back(rng(p[2], n[0] * n[1]));
+            break;
+        case OP_COLUMNS: wr.push_back(rng(p[0], n[0] * n[3])); rd.push_back(rng(p[1], n[0] * n[1])); break;
+        case OP_LINEAR:
+            wr.push_back(rng(p[0], n[2] * n[0]));
+            rd.push_back(rng(p[1], n[0] * n[1]));
+            rd.push_back(rng(p[2], n[2] * n[1]));
+            break;
+        case OP_ADD:
+        case OP_MIX:
+        case OP_SILU_MUL:
+            wr.push_back(rng(p[0], n[0]));
+            rd.push_back(rng(p[1], n[0]));
+            rd.push_back(rng(p[2], n[0]));
+            break;
+        case OP_ADD_ROW:
+            wr.push_back(rng(p[0], n[0] * n[1]));
+            rd.push_back(rng(p[1], n[0] * n[1]));
+            rd.push_back(rng(p[2], n[1]));
+            break;
+        case OP_SCALE_ROWS: wr.push_back(rng(p[0], n[0] * n[1])); rd.push_back(rng(p[1], n[0] * n[1])); break;
+        case OP_RMS:
+            wr.push_back(rng(p[0], n[0] * n[1]));
+            rd.push_back(rng(p[1], n[0] * n[1]));
+            rd.push_back(rng(p[2], n[1]));
+            break;
+        case OP_L2NORM: wr.push_back(rng(p[0], n[0] * n[1])); rd.push_back(rng(p[1], n[0] * n[1])); break;
+        case OP_ROPE_TABLE: wr.push_back(rng(p[0], n[0] * n[1])); wr.push_back(rng(p[1], n[0] * n[1])); break;
+        case OP_ROPE:
+            wr.push_back(rng(p[0], n[0] * n[1] * n[2]));
+            rd.push_back(rng(p[1], n[0] * n[1] * n[2]));
+            rd.push_back(rng(p[2], n[0] * (n[2] / 2)));
+            rd.push_back(rng(p[3], n[0] * (n[2] / 2)));
+            break;
+        case OP_GLA: {
+            int64_t t = n[0] * n[1] * n[2];
+            wr.push_back(rng(p[0], t));
+            wr.push_back(rng(p[1], n[1] * n[2] * n[2]));
+            rd.push_back(rng(p[1], n[1] * n[2] * n[2]));
+            for (int q = 2; q < 5; q++) rd.push_back(rng(p[q], t));
+            rd.push_back(rng(p[5], n[0] * n[1]));
+            rd.push_back(rng(p[6], n[1]));
+            break;
+        }
+        case OP_STORE:
+            wr.push_back(rng(p[0], n[2] * n[1] * n[3]));
+            rd.push_back(rng(p[0], n[2] * n[1] * n[3]));
+            rd.push_back(rng(p[1], n[0] * n[2] * n[3]));
+            break;
+        case OP_ATTEND:
+            wr.push_back(rng(p[0], n[1] * n[5] * n[7]));
+            rd.push_back(rng(p[1], n[1] * n[5] * n[7]));
+            rd.push_back(rng(p[2], n[6] * n[4] * n[7]));
+            rd.push_back(rng(p[3], n[6] * n[4] * n[7]));
+            break;
+    }
+}
+
+// Is what [r) holds after op `from - 1` never read again? True when a later op overwrites
+// all of it before any op reads it; false when it is read or the step ends first (the
+// caller may read it after the step).
+bool dead_after(const std::vector<Op>& ops, size_t from, const Range& r) {
+    std::vector<Range> rd, wr;
+    for (size_t j = from; j < ops.size(); j++) {
+        rd.clear();
+        wr.clear();
+        op_ranges(ops[j], rd, wr);
+        for (auto& x : rd)
+            if (overlap(x, r)) return false;
+        for (auto& x : wr)
+            if (x.a <= r.a && r.b <= x.b) return true;
+    }
+    return false;
+}
+
 // Builds one slm_fg launch: LDS slots, prefetches, prologue ops, segments.
 struct FgBuild {
     FgDesc d;
@@ -459,7 +551,7 @@ struct FgBuild {
     std::vector<Slot> slots;     // produced by prologue ops, in order
     std::vector<int> slot_op;    // the prologue op (index into d.vp) that made each slot, -1: a prefetch
     std::vector<Range> reads, writes;
-    int pf_floats = 0;
+    int pf4 = 0;
 
     FgBuild() { std::memset(&d, 0, sizeof d); }
     int alloc(int n) {
@@ -476,18 +568,19 @@ struct FgBuild {
         }
         return -1;
     }
-    bool prefetch(const float* src, int n, const long long* dyn, int stride, int wgrow, int limit,
-                  int* off) {
-        if (d.npf >= SLM_PF_MAX) return false;
+    // n floats from src (+ dyn[0]·stride) into LDS; n is rounded up to whole float4s, so the
+    // source must be 16-byte aligned and readable that far
+    bool prefetch(const float* src, int n, const long long* dyn, int stride, int* off) {
+        if (d.npf >= SLM_PF_MAX || !aligned16(src) || (dyn && stride % 4)) return false;
         PfOp& p = d.pf[d.npf++];
+        int n4 = (n + 3) / 4;
         p.src = src;
         p.dyn = dyn;
-        p.n = n;
+        p.n = 4 * n4;
         p.stride = stride;
-        p.wgrow = wgrow;
-        p.limit = limit;
-        p.lds = alloc(n);
-        pf_floats += n;
+        p.lds = alloc(4 * n4);
+        p.first4 = pf4;
+        pf4 += n4;
         *off = p.lds;
         return true;
     }
@@ -499,16 +592,42 @@ struct FgBuild {
             *off = r;
             return true;
         }
+        if (n % 4) return false;
         reads.push_back(rng(p, n));
-        return prefetch(p, n, nullptr, 0, 0, 0, off);
+        return prefetch(p, n, nullptr, 0, off);
     }
 };
+
+// Split partials of the one-token linears whose columns span several splits: two
+// alternating halves of c->part, so one kernel can read the last linear's partials while
+// it writes its own.
+int64_t nsplit_of(int64_t cols) {
+    int64_t nsl = (cols / 16 + SLM_KS - 1) / SLM_KS;
+    return (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
+}
 
 struct Planner {
     slm_hip* c;
     const std::vector<Op>& ops;
     std::vector<Rec>& out;
     std::vector<VpSrc> pend;
+    int part_flip = 0;
+    std::vector<VpSrc> next_pend;  // what a fused kernel leaves pending (a split's fold)
+    const Op* l2q = nullptr;  // l2norm ops held back for the GLA kernel that reads them
+    const Op* l2k = nullptr;
+
+    // Why a one-token linear runs unfused: printed when SLM_HIP_PLAN_TRACE is set.
+    size_t nofuse(size_t i, const char* why) {
+        if (c->plan_trace) fprintf(stderr, "slm plan: linear op %zu runs alone: %s\n", i, why);
+        return 0;
+    }
+
+    int flush_l2() {
+        if (l2q) TRY(lower_one(c, *l2q, out));
+        if (l2k) TRY(lower_one(c, *l2k, out));
+        l2q = l2k = nullptr;
+        return SLM_OK;
+    }
 
     int flush_pending() {
         for (auto& v : pend) {
@@ -518,6 +637,9 @@ struct Planner {
                 out.push_back(mk(c->k.combine, blocks_for(heads * dh), 1, 1, 256, 0, o.p[0],
                                  (const float*)c->ws, 1, (int)heads, (int)dh, combine_dp(dh),
                                  (int)nsb));
+            } else if (v.kind == SRC_FOLD) {
+                out.push_back(mk(c->k.fold, blocks_for(v.n), 1, 1, 256, 0, v.out[0], v.in[0],
+                                 (long long)v.n, v.nsplit));
             } else {
                 TRY(lower_one(c, *v.op, out));
             }
@@ -545,21 +667,21 @@ struct Planner {
         switch (v.kind) {
             case SRC_GATHER: {  // the row is prefetched straight into its slot
                 int off;
-                if (!b.prefetch(so.p[1], v.n, (const long long*)so.dyn, v.n, 0, 0, &off)) return false;
+                if (!b.prefetch(so.p[1], v.n, (const long long*)so.dyn, v.n, &off)) return false;
                 b.reads.push_back(rng(so.p[1], 1));  // the embedding table is only read
                 o.kind = VP_COPY;
                 o.in0 = off;
                 o.gout = (float*)v.out[0];
                 b.d.nvp++;
                 emit_slot(v.out[0], off);
-                b.writes.push_back(rng(v.out[0], v.n));
+                b.writes.push_back(rng0(v.out[0], v.n));
                 return true;
             }
             case SRC_ROPE_TABLE: {  // two rows of the resident tables at the step's position
                 int oc, os;
-                if (!b.prefetch(so.p[2], v.n, (const long long*)so.dyn, v.n, 0, 0, &oc)) return false;
-                if (!b.prefetch(so.p[3], v.n, (const long long*)so.dyn, v.n, 0, 0, &os)) return false;
                 if (b.d.nvp + 2 > SLM_VP_MAX) return false;
+                if (!b.prefetch(so.p[2], v.n, (const long long*)so.dyn, v.n, &oc)) return false;
+                if (!b.prefetch(so.p[3], v.n, (const long long*)so.dyn, v.n, &os)) return false;
                 o.kind = VP_COPY;
                 o.in0 = oc;
                 o.gout = (float*)v.out[0];
@@ -578,8 +700,8 @@ struct Planner {
                 b.slots.push_back({v.out[1], v.n, os});
                 b.slot_op.push_back(b.d.nvp);
                 b.d.nvp++;
-                b.writes.push_back(rng(v.out[0], v.n));
-                b.writes.push_back(rng(v.out[1], v.n));
+                b.writes.push_back(rng0(v.out[0], v.n));
+                b.writes.push_back(rng0(v.out[1], v.n));
                 return true;
             }
             case SRC_COMBINE: {
@@ -592,11 +714,19 @@ struct Planner {
                 o.dp = dp;
                 o.nsb = (int32_t)nsb;
                 o.part = c->ws;
-                if (pn <= 8192) {
+                b.reads.push_back(rng(c->ws, pn));
+                if (pn <= 12288) {
                     int off;
-                    if (!b.prefetch(c->ws, (int)pn, nullptr, 0, 0, 0, &off)) return false;
+                    if (!b.prefetch(c->ws, (int)pn, nullptr, 0, &off)) return false;
                     o.w = off;
                 }
+                break;
+            }
+            case SRC_FOLD: {
+                o.kind = VP_FOLD;
+                o.nsb = v.nsplit;
+                b.reads.push_back(rng(v.in[0], (int64_t)v.nsplit * v.n));
+                if (!b.prefetch(v.in[0], v.nsplit * v.n, nullptr, 0, &o.w)) return false;
                 break;
             }
             default: {
@@ -606,7 +736,7 @@ struct Planner {
                 if (v.in[1] && !b.input(v.in[1], v.n, &o.in1)) return false;
                 if (v.kind == SRC_RMS) {
                     b.reads.push_back(rng(so.p[2], v.n));
-                    if (!b.prefetch(so.p[2], v.n, nullptr, 0, 0, 0, &o.w)) return false;
+                    if (!b.prefetch(so.p[2], v.n, nullptr, 0, &o.w)) return false;
                     o.f = so.f[0];
                 } else if (v.kind == SRC_SCALE) {
                     o.dyn = (const long long*)so.dyn;
@@ -618,10 +748,19 @@ struct Planner {
         }
         o.out = b.alloc(v.n);
         o.gout = (float*)v.out[0];
-        b.writes.push_back(rng(v.out[0], v.n));
+        b.writes.push_back(rng0(v.out[0], v.n));
         emit_slot(v.out[0], o.out);
         b.d.nvp++;
         return true;
+    }
+
+    static void seg_init(FgSeg& s, const Op& L) {
+        s.w = L.p[1];
+        s.y = (float*)L.p[0];
+        s.rows = (int32_t)L.n[0];
+        s.tiles = (int32_t)((L.n[0] + 15) / 16);
+        s.nsplit = 1;
+        s.epi = EPI_PLAIN;
     }
 
     // Tries to fuse pend + ops[i] (a one-token linear) + what follows. Returns the number of
@@ -629,15 +768,15 @@ struct Planner {
     size_t try_fg(size_t i) {
         const Op& L = ops[i];
         int64_t rows = L.n[0], cols = L.n[1];
-        if (L.n[2] != 1 || cols % 16 || cols > VP_LEN_MAX || !aligned16(L.p[1]) || rows < 1)
-            return 0;
+        if (L.n[2] != 1 || cols % 16 || cols > VP_LEN_MAX || !aligned16(L.p[1]) || rows < 1 ||
+            rows > (int64_t)1 << 26)
+            return nofuse(i, "shape");
         const float* x = L.p[2];
         FgBuild b;
         for (auto& v : pend)
-            if (!add_vp(b, v, false)) return 0;
+            if (!add_vp(b, v, false)) return nofuse(i, "a pending op does not fit the prologue");
         size_t nproduced = b.slots.size();  // slots the linear may read
-        // epilogue pattern
-        int epi = EPI_PLAIN;
+        int64_t nsplit = nsplit_of(cols);
         size_t used = 1;
         FgSeg seg[SLM_SEG_MAX];
         std::memset(seg, 0, sizeof seg);
@@ -645,28 +784,31 @@ struct Planner {
         auto is = [&](size_t j, uint32_t kind) { return j < ops.size() && ops[j].kind == kind; };
         const float* y = L.p[0];
         FgSeg& s0 = seg[0];
-        s0.w = L.p[1];
-        s0.y = (float*)y;
-        s0.rows = (int32_t)rows;
-        s0.tiles = (int32_t)((rows + 15) / 16);
-        s0.T = 1;
-        const float *cs = nullptr, *sn = nullptr, *res = nullptr;
+        seg_init(s0, L);
+        const float *cs = nullptr, *sn = nullptr;
+        const Op *hold_q = nullptr, *hold_k = nullptr;
+        if (nsplit > 1) {
+            // the partials go out; the fold waits for the next kernel's prologue
+            if ((int64_t)c->part_bytes < 2 * nsplit * rows * 4) return nofuse(i, "no room for split partials");
+            s0.nsplit = (int32_t)nsplit;
+            s0.part = c->part + (size_t)part_flip * (c->part_bytes / 8);
+        }
         // S block: rope q, rope k, store k, store v (model.rs:430-438)
-        if (is(i + 1, OP_ROPE) && is(i + 2, OP_ROPE) && is(i + 3, OP_STORE) && is(i + 4, OP_STORE)) {
+        if (nsplit == 1 && is(i + 1, OP_ROPE) && is(i + 2, OP_ROPE) && is(i + 3, OP_STORE) &&
+            is(i + 4, OP_STORE)) {
             const Op &rq = ops[i + 1], &rk = ops[i + 2], &sk = ops[i + 3], &sv = ops[i + 4];
             int64_t heads = rq.n[1], dh = rq.n[2], dd = heads * dh;
             bool ok = rq.n[0] == 1 && rk.n[0] == 1 && rk.n[1] == heads && rk.n[2] == dh &&
                       rows == 3 * dd && rq.p[1] == y && rk.p[1] == y + dd && rq.p[2] == rk.p[2] &&
                       rq.p[3] == rk.p[3] && sk.n[0] == 1 && sv.n[0] == 1 && sk.p[1] == rk.p[0] &&
                       sv.p[1] == y + 2 * dd && sk.n[1] == sv.n[1] && sk.n[2] == heads &&
-                      sv.n[2] == heads && sk.n[3] == dh && sv.n[3] == dh && dh % 2 == 0;
-            int64_t T = 1;
-            while ((16 * T) % dh) T++;
-            ok = ok && T <= 4 && dd % (16 * T) == 0;
+                      sv.n[2] == heads && sk.n[3] == dh && sv.n[3] == dh && dh % 2 == 0 &&
+                      dd % 16 == 0;
             if (ok) {
-                epi = EPI_ROPE;
                 used = 5;
-                s0.T = (int32_t)T;
+                s0.epi = EPI_ROPE;
+                s0.pair_rows = (int32_t)(2 * dd);
+                s0.half = (int32_t)(dh / 2);
                 s0.d = (int32_t)dd;
                 s0.dh = (int32_t)dh;
                 s0.o1 = (float*)rq.p[0];
@@ -682,89 +824,73 @@ struct Planner {
                 s0.imm2 = sv.n[4];
             }
         }
-        // L block: l2norm q, l2norm k, then the decay linear on the same input
-        // (model.rs:463-470)
-        if (epi == EPI_PLAIN && is(i + 1, OP_L2NORM) && is(i + 2, OP_L2NORM)) {
-            const Op &lq = ops[i + 1], &lk = ops[i + 2];
+        // L block: the two l2norms wait for the GLA kernel; the decay linear on the same
+        // input joins as a second matrix (model.rs:463-470)
+        if (s0.epi == EPI_PLAIN && nsplit == 1 && is(i + 1, OP_L2NORM) && is(i + 2, OP_L2NORM) &&
+            is(i + 3, OP_LINEAR)) {
+            const Op &lq = ops[i + 1], &lk = ops[i + 2], &D = ops[i + 3];
             int64_t heads = lq.n[0], dh = lq.n[1], dd = heads * dh;
             bool ok = lk.n[0] == heads && lk.n[1] == dh && rows == 4 * dd && lq.p[1] == y &&
-                      lk.p[1] == y + dd;
-            int64_t T = 1;
-            while ((16 * T) % dh) T++;
-            ok = ok && T <= 4 && dd % (16 * T) == 0;
+                      lk.p[1] == y + dd && D.n[2] == 1 && D.p[2] == x && D.n[1] == cols &&
+                      aligned16(D.p[1]);
+            // the l2norm outputs are untouched until the GLA kernel writes them
+            ok = ok && !overlap(rng(lq.p[0], dd), rng(D.p[0], D.n[0])) &&
+                 !overlap(rng(lk.p[0], dd), rng(D.p[0], D.n[0])) &&
+                 !overlap(rng(lq.p[0], dd), rng(y, rows)) && !overlap(rng(lk.p[0], dd), rng(y, rows)) &&
+                 !overlap(rng(lq.p[0], dd), rng(x, cols)) && !overlap(rng(lk.p[0], dd), rng(x, cols)) &&
+                 !overlap(rng(D.p[0], D.n[0]), rng(y, rows));
             if (ok) {
-                epi = EPI_L2;
-                used = 3;
-                s0.T = (int32_t)T;
-                s0.d = (int32_t)dd;
-                s0.dh = (int32_t)dh;
-                s0.o1 = (float*)lq.p[0];
-                s0.o2 = (float*)lk.p[0];
-                if (is(i + 3, OP_LINEAR) && ops[i + 3].n[2] == 1 && ops[i + 3].p[2] == x &&
-                    ops[i + 3].n[1] == cols && aligned16(ops[i + 3].p[1])) {
-                    const Op& D = ops[i + 3];
-                    FgSeg& s1 = seg[1];
-                    s1.w = D.p[1];
-                    s1.y = (float*)D.p[0];
-                    s1.rows = (int32_t)D.n[0];
-                    s1.tiles = (int32_t)((D.n[0] + 15) / 16);
-                    s1.T = 1;
-                    s1.epi = EPI_PLAIN;
-                    nseg = 2;
-                    used = 4;
-                }
+                seg_init(seg[1], D);
+                nseg = 2;
+                used = 4;
+                hold_q = &lq;
+                hold_k = &lk;
             }
         }
         // MLP up: SiLU of the gate half times the amp half (model.rs:552-555)
-        if (epi == EPI_PLAIN && is(i + 1, OP_SILU_MUL)) {
+        if (s0.epi == EPI_PLAIN && nseg == 1 && nsplit == 1 && is(i + 1, OP_SILU_MUL)) {
             const Op& sm = ops[i + 1];
             int64_t hid = rows / 2;
-            if (rows % 32 == 0 && sm.n[0] == hid && sm.p[1] == y && sm.p[2] == y + hid) {
-                epi = EPI_SILU;
+            if (rows % 16 == 0 && sm.n[0] == hid && sm.p[1] == y && sm.p[2] == y + hid &&
+                !overlap(rng(sm.p[0], hid), rng(y, rows))) {
                 used = 2;
-                s0.T = 2;
-                s0.hid = (int32_t)hid;
+                s0.epi = EPI_SILU;
+                s0.pair_rows = (int32_t)rows;
+                s0.half = (int32_t)hid;
                 s0.o1 = (float*)sm.p[0];
             }
         }
         // residual add after the linear (model.rs:547, 557)
-        if (epi == EPI_PLAIN && is(i + 1, OP_ADD) && ops[i + 1].n[0] == rows &&
-            (ops[i + 1].p[1] == y || ops[i + 1].p[2] == y)) {
+        if (s0.epi == EPI_PLAIN && nseg == 1 && nsplit == 1 && is(i + 1, OP_ADD) &&
+            ops[i + 1].n[0] == rows && (ops[i + 1].p[1] == y || ops[i + 1].p[2] == y)) {
             const Op& a = ops[i + 1];
             const float* r = a.p[1] == y ? a.p[2] : a.p[1];
-            if (!overlap(rng(r, rows), rng(y, rows))) {
-                epi = EPI_RESID;
+            if (!overlap(rng(r, rows), rng(y, rows)) && b.find(r, rows, b.slots.size()) == -1) {
                 used = 2;
+                s0.epi = EPI_RESID;
                 s0.o1 = (float*)a.p[0];
-                res = r;
+                s0.res = r;
+                b.reads.push_back(rng(r, rows));
             }
         }
-        s0.epi = epi;
-        int nsl = (int)((cols / 16 + SLM_KS - 1) / SLM_KS);
-        // a big linear takes more tiles per workgroup (fewer copies of the prologue)
-        if ((epi == EPI_PLAIN || epi == EPI_RESID) && nseg == 1 && rows >= 4096) s0.T = 4;
-        auto fits = [&](int T) {
-            int Wt = std::min(16 / T, nsl);
-            return (nsl + Wt - 1) / Wt <= SLM_FG_SLICES;
-        };
-        if (epi == EPI_PLAIN || epi == EPI_RESID)
-            while (s0.T > 1 && !fits(s0.T)) s0.T /= 2;
-        int maxT = 1;
-        for (int k = 0; k < nseg; k++) maxT = std::max(maxT, (int)seg[k].T);
-        if (!fits(maxT)) return 0;
-        int Wt = std::min(16 / maxT, nsl);
+        int64_t nsl = (cols / 16 + SLM_KS - 1) / SLM_KS;
+        int W = (int)std::min<int64_t>(nsl, SLM_SPLIT);
         // what the segments read and write
+        int units = 0;
         for (int k = 0; k < nseg; k++) {
-            const FgSeg& s = seg[k];
+            FgSeg& s = seg[k];
+            s.units = s.tiles * s.nsplit;
+            s.unit_first = units;
+            units += s.units;
             b.reads.push_back(rng(s.w, (int64_t)s.rows * cols));
+            if (s.nsplit > 1) {
+                b.writes.push_back(rng(s.part, (int64_t)s.nsplit * s.rows));
+                continue;
+            }
             b.writes.push_back(rng(s.y, s.rows));
             switch (s.epi) {
                 case EPI_RESID: b.writes.push_back(rng(s.o1, s.rows)); break;
-                case EPI_SILU: b.writes.push_back(rng(s.o1, s.hid)); break;
-                case EPI_L2:
-                    b.writes.push_back(rng(s.o1, s.d));
-                    b.writes.push_back(rng(s.o2, s.d));
-                    break;
+                case EPI_SILU: b.writes.push_back(rng(s.o1, s.half)); break;
                 case EPI_ROPE: {
                     int64_t heads = s.d / s.dh;
                     b.writes.push_back(rng(s.o1, s.d));
@@ -776,51 +902,51 @@ struct Planner {
             }
         }
         // the GEMV input and the epilogue inputs
-        int xin = b.find(x, cols, nproduced);
-        if (xin == -2) return 0;
-        if (xin < 0) {
-            if (!aligned16(x)) return 0;
-            b.reads.push_back(rng(x, cols));
-        }
         std::vector<int> want;
-        if (xin >= 0) want.push_back(xin);
-        if (epi == EPI_ROPE) {
+        int xin = b.find(x, cols, nproduced);
+        if (xin == -2) return nofuse(i, "input partly produced by the prologue");
+        if (xin >= 0) {
+            want.push_back(xin);
+        } else {
+            b.reads.push_back(rng(x, cols));
+            if (!b.prefetch(x, (int)cols, nullptr, 0, &xin)) return nofuse(i, "input cannot be prefetched");
+        }
+        if (s0.epi == EPI_ROPE) {
             int half = s0.dh / 2;
             int r1 = b.find(cs, half, nproduced), r2 = b.find(sn, half, nproduced);
-            if (r1 == -2 || r2 == -2) return 0;
+            if (r1 == -2 || r2 == -2) return nofuse(i, "rope table partly produced by the prologue");
             if (r1 < 0) {
+                if (half % 4) return nofuse(i, "rope table rows not whole float4s");
                 b.reads.push_back(rng(cs, half));
-                if (!b.prefetch(cs, half, nullptr, 0, 0, 0, &r1)) return 0;
+                if (!b.prefetch(cs, half, nullptr, 0, &r1)) return nofuse(i, "rope table cannot be prefetched");
             } else {
                 want.push_back(r1);
             }
             if (r2 < 0) {
+                if (half % 4) return nofuse(i, "rope table rows not whole float4s");
                 b.reads.push_back(rng(sn, half));
-                if (!b.prefetch(sn, half, nullptr, 0, 0, 0, &r2)) return 0;
+                if (!b.prefetch(sn, half, nullptr, 0, &r2)) return nofuse(i, "rope table cannot be prefetched");
             } else {
                 want.push_back(r2);
             }
             s0.cs_lds = r1;
             s0.sn_lds = r2;
         }
-        if (epi == EPI_RESID) {
-            if (b.find(res, rows, b.slots.size()) != -1) return 0;  // must be in memory already
-            b.reads.push_back(rng(res, rows));
-            if (!b.prefetch(res, s0.T * 16, nullptr, 0, 1, (int)rows, &s0.res_lds)) return 0;
-        }
         // element-wise ops right after the group that neither read its results nor touch
         // what it reads run in workgroup 0 (e.g. the copy s <- x after the inject linear,
         // model.rs:580-581)
-        for (size_t j = i + used; j < ops.size(); j++) {
+        for (size_t j = i + used; j < ops.size() && nsplit == 1; j++) {
             VpSrc v;
             if (!vp_of(ops[j], &v) || (v.kind != SRC_COPY && v.kind != SRC_ADD && v.kind != SRC_MIX))
                 break;
+            // (prologue outputs are in LDS slots by then, and workgroup 0 writes its own
+            // outputs in order; what every workgroup writes is out of reach)
             bool clash = false;
             for (int q = 0; q < 2; q++) {
                 if (v.in[q])
-                    for (auto& w : b.writes) clash |= overlap(rng(v.in[q], v.n), w);
+                    for (auto& w : b.writes) clash |= !w.wg0 && overlap(rng(v.in[q], v.n), w);
                 if (v.out[q]) {
-                    for (auto& w : b.writes) clash |= overlap(rng(v.out[q], v.n), w);
+                    for (auto& w : b.writes) clash |= !w.wg0 && overlap(rng(v.out[q], v.n), w);
                     for (auto& r : b.reads) clash |= overlap(rng(v.out[q], v.n), r);
                 }
             }
@@ -848,46 +974,80 @@ struct Planner {
             k = b.slots.size();
         }
         for (int k = 0; k < b.d.nvp; k++) b.d.vp[k].wg0 = need[k] ? 0 : 1;
+        // prologue outputs that no later op reads are not written out (their LDS copies
+        // still serve this kernel); a side op that writes nothing else is dropped from
+        // workgroup 0's work
+        {
+            std::vector<Range> kept;
+            for (auto& w : b.writes)
+                if (!w.wg0) kept.push_back(w);
+            for (int k = 0; k < b.d.nvp; k++) {
+                VpOp& o = b.d.vp[k];
+                if (!o.gout) continue;
+                if (dead_after(ops, i + used, rng(o.gout, o.n)))
+                    o.gout = nullptr;
+                else
+                    kept.push_back(rng0(o.gout, o.n));
+            }
+            b.writes.swap(kept);
+        }
         // hazards: no global write of this kernel may meet a global read or another write
         for (auto& w : b.writes)
             for (auto& r : b.reads)
-                if (overlap(w, r)) return 0;
+                if (overlap(w, r)) {
+                    if (c->plan_trace) {
+                        fprintf(stderr, "slm plan: write [%#zx, %#zx) meets read [%#zx, %#zx)\n",
+                                (size_t)w.a, (size_t)w.b, (size_t)r.a, (size_t)r.b);
+                        for (auto& v : pend)
+                            fprintf(stderr, "  pending kind %d n %d in %p %p out %p\n", v.kind, v.n,
+                                    (const void*)v.in[0], (const void*)v.in[1], (const void*)v.out[0]);
+                        for (size_t j = i; j < i + used; j++)
+                            fprintf(stderr, "  op %zu kind %u p %p %p %p\n", j, ops[j].kind,
+                                    (const void*)ops[j].p[0], (const void*)ops[j].p[1], (const void*)ops[j].p[2]);
+                    }
+                    return nofuse(i, "a write meets a read");
+                }
+        // (prologue outputs may meet each other: workgroup 0 writes them one after another)
         for (size_t a = 0; a < b.writes.size(); a++)
             for (size_t q = a + 1; q < b.writes.size(); q++)
-                if (overlap(b.writes[a], b.writes[q])) return 0;
-        // workgroups and LDS
-        int wg = 0;
-        for (int k = 0; k < nseg; k++) {
-            FgSeg& s = seg[k];
-            if (s.epi == EPI_SILU) {
-                if (s.tiles % 2) return 0;
-                s.wgs = s.tiles / 2;
-            } else {
-                s.wgs = (s.tiles + s.T - 1) / s.T;
-            }
-            s.wg_first = wg;
-            wg += s.wgs;
-        }
-        int threads = 64 * maxT * Wt;
-        if (b.pf_floats > SLM_PF_PER_THREAD * threads) return 0;
+                if (overlap(b.writes[a], b.writes[q]) && !(b.writes[a].wg0 && b.writes[q].wg0))
+                    return nofuse(i, "two writes meet");
         FgDesc& d = b.d;
         d.cols = (int32_t)cols;
-        d.nsl = nsl;
-        d.Wt = Wt;
+        d.nsl = (int32_t)nsl;
+        d.W = W;
         d.xin = xin;
-        d.x = x;
         d.nseg = nseg;
+        d.units = units;
+        d.pf4 = b.pf4;
         d.lds_vp = (b.lds + 3) & ~3;
-        d.fold_off = d.lds_vp + 32;
-        d.epi_off = d.fold_off + maxT * nsl * 16;
-        int total = d.epi_off + maxT * 16 + 16;
-        if (total * 4 > LDS_MAX) return 0;
+        d.fold_off = d.lds_vp + SLM_FG_MISC;
+        int total = d.fold_off + 4 * W * 16;
+        if (total * 4 > LDS_MAX) return nofuse(i, "LDS");
         for (int k = 0; k < nseg; k++) d.seg[k] = seg[k];
-        out.push_back(mk_desc(c->k.fg, (uint32_t)wg, (uint32_t)threads, (uint32_t)(total * 4), d));
+        int threads = 64 * (W + SLM_FG_EPI_WAVES);
+        uint32_t grid = (uint32_t)std::min(units, FG_GRID_MAX);
+        out.push_back(mk_desc(c->k.fg, grid, (uint32_t)threads, (uint32_t)(total * 4), d));
+        if (nsplit > 1) {
+            part_flip ^= 1;
+            VpSrc f;
+            f.kind = SRC_FOLD;
+            f.n = (int)rows;
+            f.nsplit = (int)nsplit;
+            f.in[0] = s0.part;
+            f.out[0] = y;
+            f.op = &L;
+            next_pend.push_back(f);
+        }
+        if (hold_q) {
+            l2q = hold_q;
+            l2k = hold_k;
+        }
         return used;
     }
 
-    // gla (one token) + rms(head_norm) + silu_mul(gate): model.rs:471-484
+    // [l2norm q, l2norm k] + gla (one token) + rms(head_norm) + silu_mul(gate):
+    // model.rs:465-484
     size_t try_gla(size_t i) {
         const Op& g = ops[i];
         if (g.n[0] != 1) return 0;
@@ -904,16 +1064,46 @@ struct Planner {
         d.bias = g.p[6];
         d.heads = (int32_t)heads;
         d.dh = (int32_t)dh;
+        int64_t n = heads * dh;
+        if (l2q && l2q->p[0] == g.p[2] && l2k->p[0] == g.p[3] && l2q->n[0] == heads &&
+            l2q->n[1] == dh && l2k->n[0] == heads && l2k->n[1] == dh) {
+            // each workgroup normalises its own head before it reads q and k; the raw
+            // vectors are not written, and the normalised ones (possibly in place of the
+            // raw ones) meet nothing else the kernel reads or writes
+            std::vector<Range> wr = {rng(g.p[0], n), rng(g.p[1], heads * dh * dh)};
+            if (i + 2 < ops.size() && ops[i + 1].kind == OP_RMS && ops[i + 2].kind == OP_SILU_MUL) {
+                wr.push_back(rng(ops[i + 1].p[0], n));
+                wr.push_back(rng(ops[i + 2].p[0], n));
+            }
+            std::vector<Range> rd = {rng(g.p[4], n), rng(g.p[5], heads), rng(g.p[6], heads)};
+            Range rq = rng(l2q->p[1], n), rk = rng(l2k->p[1], n);
+            Range nq = rng(l2q->p[0], n), nk = rng(l2k->p[0], n);
+            bool ok = !overlap(nq, nk) && !overlap(rq, nk) && !overlap(rk, nq);
+            for (auto& w : wr) ok = ok && !overlap(w, rq) && !overlap(w, rk) && !overlap(w, nq) && !overlap(w, nk);
+            for (auto& r : rd) ok = ok && !overlap(r, nq) && !overlap(r, nk);
+            if (ok) {
+                d.l2 = 1;
+                d.q = l2q->p[1];
+                d.k = l2k->p[1];
+                d.qn = (float*)l2q->p[0];
+                d.kn = (float*)l2k->p[0];
+                l2q = l2k = nullptr;
+            }
+        }
+        if (l2q) return 0;  // held l2norms this kernel cannot take: run them first
         size_t used = 1;
         if (i + 2 < ops.size() && ops[i + 1].kind == OP_RMS && ops[i + 2].kind == OP_SILU_MUL) {
             const Op &r = ops[i + 1], &sm = ops[i + 2];
-            int64_t n = heads * dh;
             bool ok = r.n[0] == heads && r.n[1] == dh && r.p[1] == g.p[0] && sm.n[0] == n &&
                       sm.p[2] == r.p[0];
             // the gate is read while y, y2 and the output are written by other workgroups
             ok = ok && !overlap(rng(sm.p[1], n), rng(g.p[0], n)) &&
                  !overlap(rng(sm.p[1], n), rng(r.p[0], n)) && !overlap(rng(sm.p[1], n), rng(sm.p[0], n)) &&
                  !overlap(rng(r.p[0], n), rng(g.p[0], n));
+            if (d.l2)
+                ok = ok && !overlap(rng(sm.p[1], n), rng(d.qn, n)) && !overlap(rng(sm.p[1], n), rng(d.kn, n)) &&
+                     !overlap(rng(r.p[0], n), rng(d.qn, n)) && !overlap(rng(r.p[0], n), rng(d.kn, n)) &&
+                     !overlap(rng(sm.p[0], n), rng(d.qn, n)) && !overlap(rng(sm.p[0], n), rng(d.kn, n));
             if (ok) {
                 d.fuse = 1;
                 d.y2 = (float*)r.p[0];
@@ -926,7 +1116,7 @@ struct Planner {
         }
         int ri = pow2_index((dh + 3) / 4, 6);
         out.push_back(mk_desc(c->k.gla1[ri], (uint32_t)heads, (uint32_t)((dh * 4 + 63) / 64 * 64),
-                              (uint32_t)((dh + 1) * 4), d));
+                              (uint32_t)((4 * dh + 16) * 4), d));
         return used;
     }
 
@@ -936,19 +1126,40 @@ struct Planner {
             const Op& o = ops[i];
             VpSrc v;
             if (fuse && pend.size() < SLM_VP_MAX && vp_of(o, &v)) {
+                // a held l2norm's output may not be touched before the GLA kernel
+                bool clash = false;
+                for (const Op* h : {l2q, l2k})
+                    if (h)
+                        for (int q = 0; q < 2; q++) {
+                            if (v.in[q]) clash |= overlap(rng(v.in[q], v.n), rng(h->p[0], h->n[0] * h->n[1]));
+                            if (v.out[q]) clash |= overlap(rng(v.out[q], v.n), rng(h->p[0], h->n[0] * h->n[1])) ||
+                                                   overlap(rng(v.out[q], v.n), rng(h->p[1], h->n[0] * h->n[1]));
+                        }
+                if (clash) TRY(flush_l2());
                 pend.push_back(v);
                 i++;
                 continue;
             }
-            if (fuse && o.kind == OP_LINEAR && o.n[2] == 1) {
+            if (fuse && o.kind == OP_LINEAR && o.n[2] == 1 && !l2q) {
+                next_pend.clear();
                 size_t used = try_fg(i);
                 if (used) {
-                    pend.clear();
+                    // the prologue took every pending op; a split linear leaves its fold
+                    pend.swap(next_pend);
+                    next_pend.clear();
                     i += used;
                     continue;
                 }
             }
             TRY(flush_pending());
+            if (fuse && o.kind == OP_GLA) {
+                size_t used = try_gla(i);
+                if (used) {
+                    i += used;
+                    continue;
+                }
+            }
+            TRY(flush_l2());
             if (fuse && o.kind == OP_ATTEND && o.n[1] == 1) {
                 std::vector<Rec> two;
                 TRY(lower_one(c, o, two));
@@ -965,17 +1176,11 @@ struct Planner {
                 i++;
                 continue;
             }
-            if (fuse && o.kind == OP_GLA) {
-                size_t used = try_gla(i);
-                if (used) {
-                    i += used;
-                    continue;
-                }
-            }
             TRY(lower_one(c, o, out));
             i++;
         }
-        return flush_pending();
+        TRY(flush_pending());
+        return flush_l2();
     }
 };
 
@@ -1092,7 +1297,17 @@ int internal_realloc(slm_hip* c, void** p, size_t bytes) {
     return SLM_OK;
 }
 
+int need_part(slm_hip* c, size_t bytes) {
+    bytes += 64;  // fused prologues read whole float4s past an odd-sized end
+    if (bytes <= c->part_bytes) return SLM_OK;
+    size_t nb = std::max(bytes, c->part_bytes * 2);
+    TRY(internal_realloc(c, (void**)&c->part, nb));
+    c->part_bytes = nb;
+    return SLM_OK;
+}
+
 int need_ws(slm_hip* c, size_t bytes) {
+    bytes += 64;  // fused prologues read whole float4s past an odd-sized end
     if (bytes <= c->ws_bytes) return SLM_OK;
     size_t nb = std::max(bytes, c->ws_bytes * 2);
     TRY(internal_realloc(c, (void**)&c->ws, nb));
@@ -1178,6 +1393,7 @@ int load_kernels(slm_hip* c) {
                {&k.rms, "slm_rms"},             {&k.l2norm, "slm_l2norm"},
                {&k.fill, "slm_fill"},           {&k.combine, "slm_attn_combine"},
                {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
+               {&k.fold, "slm_fold"},
                {&k.lin_small[0], "slm_linear_small_s"}, {&k.lin_small[1], "slm_linear_small_v"},
                {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
                {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
@@ -1246,6 +1462,7 @@ int slm_hip_open(int device, slm_hip** out) {
     OPEN_HIP(hipMalloc((void**)&c->ws, c->ws_bytes));
     c->dyn.reserve(DYN_CAP);
     c->ops.reserve(4096);
+    c->plan_trace = getenv("SLM_HIP_PLAN_TRACE") != nullptr;
     const char* env = getenv("SLM_HIP_GRAPHS");
     if (env && env[0] == '0') c->graphs_on = false;
     env = getenv("SLM_HIP_FUSION");
@@ -1266,6 +1483,7 @@ void slm_hip_close(slm_hip* c) {
     }
     for (auto& a : c->allocs) hipFree((void*)a.first);
     if (c->ws) hipFree(c->ws);
+    if (c->part) hipFree(c->part);
     if (c->stage_dev) hipFree(c->stage_dev);
     if (c->dyn_dev) hipFree(c->dyn_dev);
     if (c->stage_host) hipHostFree(c->stage_host);
@@ -1676,6 +1894,10 @@ int slm_hip_linear(slm_hip* c, float* y, const float* w, size_t rows, size_t col
     if (!m || !rows) return SLM_OK;
     if (!fits_int(rows) || !fits_int(cols) || !fits_int(m))
         return fail(c, SLM_E_UNSUPPORTED, "linear: %zu x %zu x %zu", rows, cols, m);
+    if (m == 1 && c->fusion_on && cols <= (size_t)VP_LEN_MAX) {
+        int64_t ns = nsplit_of((int64_t)cols);
+        if (ns > 1) TRY(need_part(c, (size_t)(2 * ns) * rows * 4));
+    }
     Op o = op(OP_LINEAR);
     o.p[0] = y;
     o.p[1] = w;

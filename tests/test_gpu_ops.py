@@ -68,7 +68,8 @@ def test_linear(hip, rows, cols, m):
     assert rel(got, want) < 2e-6, (rows, cols, m)
 
 
-@pytest.mark.parametrize("rows,cols", [(768, 768), (6144, 768), (768, 3072), (97, 32), (40, 52)])
+@pytest.mark.parametrize("rows,cols", [(768, 768), (6144, 768), (768, 3072), (97, 32), (40, 52),
+                                       (64, 1600)])
 def test_linear_same_bits_for_any_m(hip, rows, cols):
     """The decode kernel (m <= 16) and the prompt kernel (m > 16) run one MFMA chain."""
     m = 256
@@ -269,7 +270,8 @@ def _step(hip, body, inv, cs, sn, fuse):
     return plan
 
 
-FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "combine", "side_copy"]
+FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "combine", "side_copy",
+                "split_fold", "split_flush", "gla_l2", "rounds"]
 
 
 @pytest.mark.parametrize("case", FUSION_CASES)
@@ -282,6 +284,12 @@ def test_fusion_pattern(hip, case):
     wqkvg = hip.upload(rnd(4 * d, d, scale=0.02))
     wdec = hip.upload(rnd(heads, d, scale=0.02))
     wup = hip.upload(rnd(2 * hid, d, scale=0.02))
+    wdown = hip.upload(rnd(d, hid, scale=0.02))
+    whead = hip.upload(rnd(32000, d, scale=0.02))
+    xh = hip.upload(rnd(hid))
+    bias = hip.upload(rnd(heads))
+    hn = hip.upload(rnd(dh))
+    s0 = rnd(heads, dh, dh, scale=0.1)
     x = hip.upload(rnd(d))
     res = hip.upload(rnd(d))
     nw = hip.upload(rnd(d))
@@ -292,7 +300,8 @@ def test_fusion_pattern(hip, case):
     def outs():
         return {k: hip.alloc(n) for k, n in
                 dict(n=d, y=4 * d, q=d, k=d, t=d, up=2 * hid, g=hid, dd=heads, s=d,
-                     kr=heads * cap * dh, vr=heads * cap * dh, att=d).items()}
+                     kr=heads * cap * dh, vr=heads * cap * dh, att=d, h=d, z=d, y2=d,
+                     S=heads * dh * dh, lg=32000).items()}
 
     def body(o):
         if case == "plain":
@@ -327,16 +336,37 @@ def test_fusion_pattern(hip, case):
             hip.linear(o["y"].ptr, wsq.ptr, d, d, x.ptr, 1)
             hip.copy(o["s"].ptr, x.ptr, d)
             hip.add(o["t"].ptr, o["s"].ptr, o["y"].ptr, d)
+        elif case == "split_fold":  # a 3072-column linear's splits fold in the next prologue
+            hip.linear(o["h"].ptr, wdown.ptr, d, hid, xh.ptr, 1)
+            hip.add(o["t"].ptr, res.ptr, o["h"].ptr, d)
+            hip.rms(o["n"].ptr, o["t"].ptr, nw.ptr, 1, d, 1e-6)
+            hip.linear(o["y"].ptr, wsq.ptr, d, d, o["n"].ptr, 1)
+        elif case == "split_flush":  # ... or in a kernel of their own
+            hip.linear(o["h"].ptr, wdown.ptr, d, hid, xh.ptr, 1)
+            hip.add(o["t"].ptr, res.ptr, o["h"].ptr, d)
+        elif case == "rounds":  # 2000 tiles: each workgroup takes several rounds of two
+            hip.rms(o["n"].ptr, x.ptr, nw.ptr, 1, d, 1e-6)
+            hip.linear(o["lg"].ptr, whead.ptr, 32000, d, o["n"].ptr, 1)
+        elif case == "gla_l2":  # the L mixer: the l2norms move into the GLA kernel
+            hip.linear(o["y"].ptr, wqkvg.ptr, 4 * d, d, x.ptr, 1)
+            hip.l2norm(o["q"].ptr, o["y"].ptr, heads, dh)
+            hip.l2norm(o["k"].ptr, o["y"].at(d), heads, dh)
+            hip.linear(o["dd"].ptr, wdec.ptr, heads, d, x.ptr, 1)
+            hip.gla(o["z"].ptr, o["S"].ptr, o["q"].ptr, o["k"].ptr, o["y"].at(2 * d), o["dd"].ptr,
+                    bias.ptr, 1, heads, dh)
+            hip.rms(o["y2"].ptr, o["z"].ptr, hn.ptr, heads, dh, 1e-6)
+            hip.silu_mul(o["z"].ptr, o["y"].at(3 * d), o["y2"].ptr, d)
 
     got = []
     for fuse in (False, True):
         o = outs()
+        hip.write(o["S"], s0)
         plan = _step(hip, lambda: body(o), inv, cs, sn, fuse)
         got.append(({k: b.read() for k, b in o.items()}, plan))
     (a, pa), (b, pb) = got
     print(case, "unfused", pa, "fused", pb)
     assert pb["kernels"] <= pa["kernels"]
-    if case != "plain":
+    if case not in ("plain", "split_flush"):  # a fold with no kernel to join runs alone
         assert pb["kernels"] < pa["kernels"]
     for k in a:
         assert np.array_equal(a[k], b[k]), (case, k, float(np.abs(a[k] - b[k]).max()))
