@@ -25,6 +25,8 @@
 #define SLM_KS 4               // 16-column blocks per canonical slice (64 columns)
 #define SLM_SPLIT 12           // slices per canonical split (768 columns)
 #define SLM_FG_EPI_WAVES 4     // prologue/epilogue waves of slm_fg
+#define SLM_SB_SEGS 4          // 64-key attention segments per superblock
+#define SLM_SB_KEYS (64 * SLM_SB_SEGS)
 #define SLM_FG_MISC (32 + 4 * SLM_PF_MAX)  // LDS floats of slm_fg's scalars and prefetch table
 
 enum {
@@ -91,7 +93,7 @@ typedef struct {
     long long imm2;
 } FgSeg;
 
-typedef struct {
+typedef struct __attribute__((aligned(16))) {
     int32_t npf, nvp, cols, nsl;    // nsl: canonical slices of `cols`
     int32_t W, xin, nseg, units;    // W: GEMV waves (slices per split); xin: LDS offset of x
     int32_t lds_vp, fold_off, pf4, pad;  // pf4: float4s the prologue loads

@@ -10,7 +10,7 @@
 //     768-column splits, split sums added in order); the m <= 16 kernel, the m > 16
 //     kernel and the fused one-token kernel run the same chain;
 //   - attend: keys are grouped by absolute position into 16-key tiles, 64-key segments
-//     and 512-key superblocks; a segment is an online softmax over its tiles, segments
+//     and 256-key superblocks; a segment is an online softmax over its tiles, segments
 //     fold into superblocks in order and superblocks into the result in order;
 //   - gla: one kernel for every m, tokens in order;
 //   - rms / l2norm: the 16-accumulator dot of the reference CPU backend (src/cpu.rs:9-21),
@@ -34,6 +34,18 @@ static constexpr float NEG_INF = -__builtin_inff();
 
 __device__ __forceinline__ long long dyn_or(const long long* dyn, long long imm) {
     return dyn ? dyn[0] : imm;
+}
+
+// Loads and stores through pointers the compiler cannot see are global (for instance
+// pointers read from LDS), as global rather than flat memory instructions.
+#define GAS __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ T gld(const T* p) {
+    return *(const GAS T*)p;
+}
+template <typename T>
+__device__ __forceinline__ void gst(T* p, T v) {
+    *(GAS T*)p = v;
 }
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
@@ -438,8 +450,8 @@ KERNEL void __launch_bounds__(256) slm_linear_big_s(float* y, const float* w, co
 // 16 / group). The query at position p sees [lo, hi) = [max(0, p-reach+1),
 // max(0, p+1-gap)), stored at slots p % cap.
 //
-// Keys are grouped by absolute position: 16-key tiles, 64-key segments (4 tiles), 512-key
-// superblocks (8 segments). A segment's partial (max m, sum l, o = Σ p·v) is an online
+// Keys are grouped by absolute position: 16-key tiles, 64-key segments (4 tiles), 256-key
+// superblocks (4 segments). A segment's partial (max m, sum l, o = Σ p·v) is an online
 // softmax over its tiles in order; a tile with no visible key for a column leaves that
 // column's partial unchanged. Partials fold in order: segments into a superblock (inside
 // one workgroup, one wave per segment), superblocks into the result (slm_attn_combine).
@@ -487,11 +499,14 @@ __device__ __forceinline__ Col column(int c, long long qtile, long long pos, int
 
 // One 64-key segment for the wave's 16 columns. The lane keeps its column's (m, l) and
 // o for dims 16dt + 4g + r. The keys and values of every tile some column sees are loaded
-// before any arithmetic (one memory latency per segment).
+// before any arithmetic (one memory latency per segment), both as float4 rows; each tile
+// of values then goes through this wave's LDS tile `vt` ([16 keys][16·DT + 4]) into the
+// layout the P·V MFMA takes.
 template <int DT>
 __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __restrict__ kb,
                              const float* __restrict__ vb, long long seg_lo, long long cap,
-                             int dh, float scale, float& mo, float& lo, f4 (&o)[DT]) {
+                             int dh, float scale, float& mo, float& lo, f4 (&o)[DT], float* vt) {
+    constexpr int VS = 16 * DT + 4;
     int lane = threadIdx.x & 63;
     int i = lane & 15, g = lane >> 4;
     mo = NEG_INF;
@@ -499,30 +514,25 @@ __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     bool need[4];
-    f4 kr[4][DT];
-    float vr[4][4][DT];
+    f4 kr[4][DT], vq[4][DT];
 #pragma unroll
     for (int st = 0; st < 4; st++) {
         long long b0 = seg_lo + 16 * st;
         bool sees = col.valid && col.lo < b0 + 16 && col.hi > b0;
         need[st] = __ballot(sees) != 0;
         if (need[st]) {
-            // A operand of the scores: key b0 + i, dims 16t + 4g .. +3
-            const float* krow = kb + ((b0 + i) % cap) * dh;
+            // key and value b0 + i, dims 16t + 4g .. +3 (the scores' A operand for keys)
+            long long slot = (b0 + i) % cap;
+            const float* krow = kb + slot * dh;
+            const float* vrow = vb + slot * dh;
 #pragma unroll
             for (int t = 0; t < DT; t++) {
                 int c = 16 * t + 4 * g;
                 kr[st][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (c < dh) kr[st][t] = *(const f4*)(krow + c);
-            }
-            // A operand of P·V for MFMA r: value of key b0 + 4g + r, dim 16dt + i
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float* vrow = vb + ((b0 + 4 * g + r) % cap) * dh;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++) {
-                    int dim = 16 * dt + i;
-                    vr[st][r][dt] = dim < dh ? vrow[dim] : 0.0f;
+                vq[st][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (c < dh) {
+                    kr[st][t] = *(const f4*)(krow + c);
+                    vq[st][t] = *(const f4*)(vrow + c);
                 }
             }
         }
@@ -540,6 +550,14 @@ __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __
             s = mfma4(kr[st][t].z, qv[t].z, s);
             s = mfma4(kr[st][t].w, qv[t].w, s);
         }
+        // values: A operand of P·V for MFMA r is value of key b0 + 4g + r, dim 16dt + i
+#pragma unroll
+        for (int t = 0; t < DT; t++) *(f4*)(vt + i * VS + 16 * t + 4 * g) = vq[st][t];
+        float vr[4][DT];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vr[r][dt] = vt[(4 * g + r) * VS + 16 * dt + i];
         float sv[4];
         bool any = false;
 #pragma unroll
@@ -570,7 +588,7 @@ __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __
 #pragma unroll
         for (int r = 0; r < 4; r++)
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) on[dt] = mfma4(vr[st][r][dt], p[r], on[dt]);
+            for (int dt = 0; dt < DT; dt++) on[dt] = mfma4(vr[r][dt], p[r], on[dt]);
         if (anyi) {
             lo = lo * alpha + rs;
             mo = mnew;
@@ -580,9 +598,9 @@ __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __
     }
 }
 
-// Superblock partials. Grid (query tiles, key heads, superblock slots); 8 waves, wave w
-// takes segment 8·sb + w, where sb = floor(first visible position / 512) + blockIdx.z.
-// Output part[z][qidx][head][2 + DP]: m, l, o.
+// Superblock partials. Grid (query tiles, key heads, superblock slots); SLM_SB_SEGS waves,
+// wave w takes segment SLM_SB_SEGS·sb + w, where sb = floor(first visible position /
+// SLM_SB_KEYS) + blockIdx.z. Output part[z][qidx][head][2 + DP]: m, l, o.
 template <int DT>
 __device__ void attn_part_body(float* __restrict__ part, const float* __restrict__ q,
                                const float* __restrict__ kc, const float* __restrict__ vc,
@@ -590,14 +608,15 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
                                long long reach, long long gap, long long cap, int heads,
                                int key_heads, int dh, float scale, int wpp) {
     constexpr int DP = 16 * DT;
-    extern __shared__ float lds[];  // [wpp][16][DP + 2]
+    constexpr int NT = 64 * SLM_SB_SEGS;
+    extern __shared__ float lds[];  // [wpp][16][DP + 2] folds, then [waves][16][DP + 4] values
     long long pos = dyn_or(dyn, pos_imm);
     int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int i = lane & 15, g = lane >> 4;
     int group = heads / key_heads, qpt = 16 / group;
     int kvh = blockIdx.y;
     long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
-    long long sb = first / 512 + blockIdx.z;
+    long long sb = first / SLM_SB_KEYS + blockIdx.z;
     Col col = column(i, blockIdx.x, pos, m, reach, gap, group, qpt, kvh);
     // this lane's share of its column's query: B[k = g][j = i] for each 16-dim block
     f4 qv[DT];
@@ -610,10 +629,11 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
     }
     float mo, lo;
     f4 o[DT];
+    float* vt = lds + wpp * 16 * (DP + 2) + wave * 16 * (DP + 4);
     attn_segment<DT>(col, qv, kc + (long long)kvh * cap * dh, vc + (long long)kvh * cap * dh,
-                     (sb * 8 + wave) * 64, cap, dh, scale, mo, lo, o);
-    // fold the 8 segments in order, wpp at a time through LDS
-    constexpr int PER = (16 * DP + 511) / 512;  // (column, dim) pairs per thread
+                     (sb * SLM_SB_SEGS + wave) * 64, cap, dh, scale, mo, lo, o, vt);
+    // fold the segments in order, wpp at a time through LDS
+    constexpr int PER = (16 * DP + NT - 1) / NT;  // (column, dim) pairs per thread
     float FM[PER], FL[PER], FO[PER];
 #pragma unroll
     for (int u = 0; u < PER; u++) {
@@ -621,7 +641,7 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
         FL[u] = 0.0f;
         FO[u] = 0.0f;
     }
-    for (int ph = 0; ph < 8; ph += wpp) {
+    for (int ph = 0; ph < SLM_SB_SEGS; ph += wpp) {
         if (wave >= ph && wave < ph + wpp) {
             float* L = lds + ((wave - ph) * 16 + i) * (DP + 2);
 #pragma unroll
@@ -636,7 +656,7 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < PER; u++) {
-            int t = threadIdx.x + 512 * u;
+            int t = threadIdx.x + NT * u;
             if (t < 16 * DP) {
                 int cc = t / DP, dd = t % DP;
                 for (int w = 0; w < wpp; w++) {
@@ -649,7 +669,7 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
     }
 #pragma unroll
     for (int u = 0; u < PER; u++) {
-        int t = threadIdx.x + 512 * u;
+        int t = threadIdx.x + NT * u;
         if (t < 16 * DP) {
             int cc = t / DP, dd = t % DP;
             Col c2 = column(cc, blockIdx.x, pos, m, reach, gap, group, qpt, kvh);
@@ -667,7 +687,7 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
 }
 
 #define ATTN_PART(DT)                                                                    \
-    KERNEL void __launch_bounds__(512) slm_attn_part_##DT(                               \
+    KERNEL void __launch_bounds__(64 * SLM_SB_SEGS) slm_attn_part_##DT(                               \
         float* part, const float* q, const float* kc, const float* vc,                   \
         const long long* dyn, long long pos_imm, int m, long long reach, long long gap,  \
         long long cap, int heads, int key_heads, int dh, float scale, int wpp) {         \
@@ -680,18 +700,30 @@ ATTN_PART(4)
 ATTN_PART(8)
 ATTN_PART(16)
 
-// y[qidx][head][dim] = O / L after folding the nsb superblock partials in order (0 when
-// the query sees nothing, cpu.rs:378-382).
+// y[qidx][head][dim] from the nsb superblock partials: with M the largest m of the
+// superblocks that saw a key, w_z = e^(m_z − M), L = Σ l_z·w_z and O = Σ o_z·w_z (both in
+// superblock order), y = O / L (0 when the query sees nothing, cpu.rs:378-382). The fused
+// decode prologue (VP_COMBINE) computes the same expressions.
 KERNEL void slm_attn_combine(float* __restrict__ y, const float* __restrict__ part, int m,
                              int heads, int dh, int dp, int nsb) {
     long long n = (long long)m * heads * dh;
+    long long stride = (long long)m * heads * (dp + 2);
     GRID_LOOP(t, n) {
         long long row = t / dh;
         int dd = (int)(t % dh);
-        float M = NEG_INF, L = 0.0f, O = 0.0f;
+        const float* P = part + row * (dp + 2);
+        float M = NEG_INF;
+        for (int z = 0; z < nsb; z++)
+            if (P[z * stride + 1] > 0.0f) M = fmaxf(M, P[z * stride]);
+        float L = 0.0f, O = 0.0f;
         for (int z = 0; z < nsb; z++) {
-            const float* P = part + ((long long)z * m * heads + row) * (dp + 2);
-            fold(M, L, O, P[0], P[1], P[2 + dd]);
+            const float* Q = P + z * stride;
+            float l = Q[1];
+            if (l > 0.0f) {
+                float w = expf(Q[0] - M);
+                L = L + l * w;
+                O = O + Q[2 + dd] * w;
+            }
         }
         y[t] = L > 0.0f ? O / L : 0.0f;
     }
@@ -712,60 +744,148 @@ KERNEL void slm_probe_mfma(float* out, const float* a, const float* b) {
 // fused decode kernels (one token), driven by the descriptors of fusion.h
 // ---------------------------------------------------------------------------------------
 
-// One prologue operation on LDS vectors, run by the `pnt` prologue threads (ptid = 0..)
-// of the workgroup. It ends on a barrier that every wave of the workgroup meets (the
-// GEMV waves count them with vp_barriers). `misc` is a few floats of LDS.
-__device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0, int ptid, int pnt) {
+// The prologue waves' own barrier: a counter in LDS that each of the `nw` waves bumps once
+// per barrier, then waits for (the GEMV waves meanwhile wait for their weights, not for
+// this). Only LDS is ordered by it. The wait gives up after about a second, so a mistake
+// cannot hang the GPU.
+__device__ __forceinline__ void esync(int* ctr, int& target, int nw) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    target += nw;
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int it = 0; it < (1 << 24); it++) {
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+struct ESync {
+    int* ctr;
+    int target, nw;
+    __device__ __forceinline__ void operator()() { esync(ctr, target, nw); }
+};
+
+// Sum of squares of in[0..size) in the order of dot16_self, run by lanes 0..15 of one
+// wave: each lane's 16 partial sums in registers, the lane totals added left to right
+// through readlane.
+__device__ __forceinline__ float dot16_lanes0(const float* in, int size, int l) {
+    int chunks = size / 16;
+    float acc = 0.0f;
+    int c = 0;
+    for (; c + 16 <= chunks; c += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = in[(c + u) * 16 + l];
+#pragma unroll
+        for (int u = 0; u < 16; u++) acc = acc + v[u] * v[u];
+    }
+    for (; c < chunks; c++) {
+        float v = in[c * 16 + l];
+        acc = acc + v * v;
+    }
+    float s = -0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; t++)
+        s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), t));
+    float tail = -0.0f;
+    for (int j = chunks * 16; j < size; j++) tail = tail + in[j] * in[j];
+    return s + tail;
+}
+
+// One prologue operation on LDS vectors, run by every thread of the workgroup (the GEMV
+// waves' weights are in flight meanwhile; nothing here touches global memory, so their
+// loads never hold it up). Element c of every element-wise op is computed by the same
+// thread, so such ops follow each other without a barrier; rms and the combine wait for
+// the other threads where they need their results. misc[0]: the rms factor; misc[4 + k]:
+// the dynamic factor of op k.
+__device__ void vp_run(const VpOp& o, float* lds, const float* misc, int k, int tid, int nt) {
     int n = o.n;
     const float* a = lds + o.in0;
     const float* b = o.in1 >= 0 ? lds + o.in1 : nullptr;
     float* out = o.out >= 0 ? lds + o.out : nullptr;
-    float* gout = wg0 ? o.gout : nullptr;
     switch (o.kind) {
         case VP_RMS: {  // rms (cpu.rs:187-207) of one group; a and out may not alias
-            if (ptid < 16) {
-                float d = dot16_self(a, n, ptid);
-                if (ptid == 0) misc[0] = 1.0f / sqrtf(d / (float)n + o.f);
+            __syncthreads();  // the input may come from other threads
+            if (tid < 64) {
+                float d = dot16_lanes0(a, n, tid & 15);
+                if (tid == 0) ((float*)misc)[0] = 1.0f / sqrtf(d / (float)n + o.f);
             }
             __syncthreads();
             float r = misc[0];
             const float* wt = lds + o.w;
-            for (int c = ptid; c < n; c += pnt) {
-                float v = a[c] * r * wt[c];
-                out[c] = v;
-                if (gout) gout[c] = v;
-            }
+            for (int c = tid; c < n; c += nt) out[c] = a[c] * r * wt[c];
             break;
         }
-        case VP_COMBINE: {  // slm_attn_combine for one query
-            const float* part = o.w >= 0 ? (const float*)(lds + o.w) : o.part;
-            for (int c = ptid; c < n; c += pnt) {
-                int h = c / o.dh, e = c % o.dh;
-                float M = NEG_INF, L = 0.0f, O = 0.0f;
-                for (int z = 0; z < o.nsb; z++) {
-                    const float* P = part + ((long long)z * o.heads + h) * (o.dp + 2);
-                    fold(M, L, O, P[0], P[1], P[2 + e]);
+        case VP_COMBINE: {  // slm_attn_combine for one query; lds[in1]: [heads][nsb] weights
+            int rec = o.dp + 2, stride = rec * o.heads;
+            const float* P = lds + o.w;
+            float* wz = lds + o.in1;
+            for (int t = tid; t < o.heads * o.nsb; t += nt) {  // w_z of each head
+                int h = t / o.nsb, z = t % o.nsb;
+                float M = NEG_INF;
+                int q = 0;
+                for (; q + 4 <= o.nsb; q += 4) {
+                    float l4[4], m4[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        l4[u] = P[(q + u) * stride + h * rec + 1];
+                        m4[u] = P[(q + u) * stride + h * rec];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        if (l4[u] > 0.0f) M = fmaxf(M, m4[u]);
                 }
-                float v = L > 0.0f ? O / L : 0.0f;
-                if (out) out[c] = v;
-                if (gout) gout[c] = v;
+                for (; q < o.nsb; q++)
+                    if (P[q * stride + h * rec + 1] > 0.0f) M = fmaxf(M, P[q * stride + h * rec]);
+                wz[t] = expf(P[z * stride + h * rec] - M);
+            }
+            __syncthreads();
+            for (int c = tid; c < n; c += nt) {
+                int h = c / o.dh, e = c % o.dh;
+                float L = 0.0f, O = 0.0f;
+                int z = 0;
+                for (; z + 4 <= o.nsb; z += 4) {
+                    float l4[4], w4[4], o4[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        int at = (z + u) * stride + h * rec;
+                        l4[u] = P[at + 1];
+                        w4[u] = wz[h * o.nsb + z + u];
+                        o4[u] = P[at + 2 + e];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        if (l4[u] > 0.0f) {
+                            L = L + l4[u] * w4[u];
+                            O = O + o4[u] * w4[u];
+                        }
+                }
+                for (; z < o.nsb; z++) {
+                    int at = z * stride + h * rec;
+                    float l = P[at + 1];
+                    if (l > 0.0f) {
+                        float w = wz[h * o.nsb + z];
+                        L = L + l * w;
+                        O = O + P[at + 2 + e] * w;
+                    }
+                }
+                out[c] = L > 0.0f ? O / L : 0.0f;
             }
             break;
         }
         case VP_FOLD: {  // slm_fold: the splits of a linear added in order
             const float* part = lds + o.w;
-            for (int c = ptid; c < n; c += pnt) {
+            for (int c = tid; c < n; c += nt) {
                 float v = part[c];
                 for (int z = 1; z < o.nsb; z++) v = v + part[z * n + c];
-                if (out) out[c] = v;
-                if (gout) gout[c] = v;
+                out[c] = v;
             }
             break;
         }
         default: {
-            float factor = o.f;
-            if (o.kind == VP_SCALE && o.dyn) factor = *(const float*)o.dyn;
-            for (int c = ptid; c < n; c += pnt) {
+            float factor = o.kind == VP_SCALE && o.dyn ? misc[4 + k] : o.f;
+            if (!out) break;  // a copy whose source slot is written out as it is
+            for (int c = tid; c < n; c += nt) {
                 float v;
                 switch (o.kind) {
                     case VP_COPY: v = a[c]; break;
@@ -777,20 +897,10 @@ __device__ void vp_run(const VpOp& o, float* lds, float* misc, bool wg0, int pti
                         v = b[c] * gg / (1.0f + expf(-gg));
                     }
                 }
-                if (out) out[c] = v;
-                if (gout) gout[c] = v;
+                out[c] = v;
             }
         }
     }
-    __syncthreads();
-}
-
-// Barriers of the prologue: two for the loads, then each op's.
-__device__ __forceinline__ int vp_barriers(const FgDesc& d, bool first) {
-    int n = 2;
-    for (int k = 0; k < d.nvp; k++)
-        if (first || !d.vp[k].wg0) n += d.vp[k].kind == VP_RMS ? 2 : 1;
-    return n;
 }
 
 struct FgUnit {
@@ -834,7 +944,7 @@ __device__ __forceinline__ void fg_load(const FgDesc& d, int u, int wave, int i,
     for (int q = 0; q < SLM_KS; q++) {
         int kb = sl * SLM_KS + q;
         const float* src = ok && kb < kblocks ? base + kb * 16 : slm_zero16;
-        wa[q] = *(const f4*)src;
+        wa[q] = gld((const f4*)src);
     }
 }
 
@@ -862,23 +972,43 @@ __device__ __forceinline__ void fg_chain(const FgDesc& d, int u, int wave, int i
     }
 }
 
-KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
+KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
+    // The descriptor is copied into LDS with one wide load per thread, so the many fields
+    // the kernel reads (some at indices only known per lane) cost one memory round trip.
+    __shared__ FgDesc d;
     extern __shared__ float lds[];
+    static_assert(sizeof(FgDesc) % 16 == 0, "descriptor copy in float4s");
+    for (int q = threadIdx.x; q < (int)(sizeof(FgDesc) / 16); q += blockDim.x)
+        ((f4*)&d)[q] = ((const f4*)&dk)[q];
+    if (threadIdx.x < 2) ((int*)(lds + dk.lds_vp + 28))[threadIdx.x] = 0;
+    __syncthreads();
     float* misc = lds + d.lds_vp;   // 32 floats, then the prefetch table (SLM_FG_MISC)
     float* foldb = lds + d.fold_off;  // [2 rounds][2 units][W][16]
+    int* sync_ctr = (int*)(misc + 28);  // the prologue waves' barrier; misc + 29: loads issued
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int W = d.W;
     bool first = blockIdx.x == 0;
-    int nbar = vp_barriers(d, first);
     if (wave < W) {
         // GEMV wave: slice `wave` of the split of every unit of this workgroup, two units
-        // (u and u + grid) per round, eight loads in flight
+        // (u and u + grid) per round, eight loads in flight. The prologue's loads go out
+        // first, so they do not queue behind the weights.
         int i = lane & 15, g = lane >> 4, G = gridDim.x;
+        if (d.pf4 > 0) {
+            for (int it = 0; it < (1 << 24); it++) {
+                if (__hip_atomic_load(sync_ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >=
+                    SLM_FG_EPI_WAVES)
+                    break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
         f4 wa[SLM_KS], wb[SLM_KS];
         int u = blockIdx.x;
         fg_load(d, u, wave, i, g, wa);
         fg_load(d, u + G, wave, i, g, wb);
-        for (int k = 0; k < nbar; k++) __syncthreads();
+        __syncthreads();  // the prologue's vectors are in LDS
+        for (int k = 0; k < d.nvp; k++)
+            if (first || !d.vp[k].wg0) vp_run(d.vp[k], lds, misc, k, tid, (int)blockDim.x);
+        __syncthreads();  // the prologue is done: x is in LDS
         const float* xin = lds + d.xin;
         for (int par = 0;; par ^= 1) {  // rounds alternate between two halves of foldb
             float* fb = foldb + par * 2 * W * 16;
@@ -895,15 +1025,19 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
     // prologue / epilogue waves: where each prefetch comes from, then the loads, many in
     // flight per thread
     int ptid = tid - 64 * W, pnt = (int)blockDim.x - 64 * W;
+    ESync sync{sync_ctr, 0, SLM_FG_EPI_WAVES};
     const float** pf_src = (const float**)(misc + 32);  // [SLM_PF_MAX]
     int* pf_tab = (int*)(misc + 32 + 2 * SLM_PF_MAX);   // [SLM_PF_MAX][2]: lds, first4
+    float sf = 0.0f;  // a dynamic scale factor, loaded with the table, stored after the loads
     if (ptid < d.npf) {
         const PfOp& p = d.pf[ptid];
-        pf_src[ptid] = p.src + (p.dyn ? p.dyn[0] * p.stride : 0);
+        pf_src[ptid] = p.src + (p.dyn ? gld(p.dyn) * p.stride : 0);
         pf_tab[2 * ptid] = p.lds;
         pf_tab[2 * ptid + 1] = p.first4;
     }
-    __syncthreads();
+    bool has_sf = ptid < d.nvp && d.vp[ptid].kind == VP_SCALE && d.vp[ptid].dyn;
+    if (has_sf) sf = gld((const float*)d.vp[ptid].dyn);
+    sync();
     for (int base = ptid; base < d.pf4; base += 8 * pnt) {
         f4 v[8];
         int dst[8];
@@ -916,19 +1050,30 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
                 for (int t = 1; t < d.npf; t++)
                     if (f >= pf_tab[2 * t + 1]) j = t;
                 int c4 = f - pf_tab[2 * j + 1];
-                v[q] = *(const f4*)(pf_src[j] + 4 * c4);
+                v[q] = gld((const f4*)(pf_src[j] + 4 * c4));
                 dst[q] = pf_tab[2 * j] + 4 * c4;
             }
         }
+        if (base == ptid && lane == 0)  // this wave's first loads are out: the weights may go
+            __hip_atomic_fetch_add(sync_ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #pragma unroll
         for (int q = 0; q < 8; q++)
             if (dst[q] >= 0) *(f4*)(lds + dst[q]) = v[q];
     }
-    __syncthreads();
-    for (int k = 0; k < d.nvp; k++) {
-        const VpOp& o = d.vp[k];
-        if (o.wg0 && !first) continue;
-        vp_run(o, lds, misc, first, ptid, pnt);
+    if (d.pf4 > 0 && ptid >= d.pf4 && lane == 0)  // a wave with no loads of its own
+        __hip_atomic_fetch_add(sync_ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (has_sf) misc[4 + ptid] = sf;
+    __syncthreads();  // the prologue's vectors are in LDS
+    for (int k = 0; k < d.nvp; k++)
+        if (first || !d.vp[k].wg0) vp_run(d.vp[k], lds, misc, k, tid, (int)blockDim.x);
+    __syncthreads();  // x is ready for the GEMV waves
+    if (first) {  // workgroup 0 writes out what the prologue made that later ops read
+        for (int k = 0; k < d.nvp; k++) {
+            const VpOp& o = d.vp[k];
+            if (!o.gout) continue;
+            const float* src = lds + (o.out >= 0 ? o.out : o.in0);
+            for (int c = ptid; c < o.n; c += pnt) gst(o.gout + c, src[c]);
+        }
     }
     for (int u0 = blockIdx.x, par = 0; u0 < d.units; u0 += 2 * gridDim.x, par ^= 1) {
         // the GEMV waves write the next round's partials into the other half of foldb
@@ -946,11 +1091,11 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
             const FgSeg& sg = d.seg[cur.seg];
             long long R = fg_row(sg, cur.tile, r);
             if (R >= sg.rows || sg.nsplit > 1) continue;
-            if (sg.epi == EPI_RESID) res[h] = sg.res[R];
+            if (sg.epi == EPI_RESID) res[h] = gld(sg.res + R);
             if (sg.epi == EPI_ROPE) {
                 int part = (int)(R / sg.d);
-                if (part == 1) slot[h] = (sg.dyn ? sg.dyn[0] : sg.imm) % sg.cap;
-                if (part == 2) slot[h] = (sg.dyn2 ? sg.dyn2[0] : sg.imm2) % sg.cap;
+                if (part == 1) slot[h] = (sg.dyn ? gld(sg.dyn) : sg.imm) % sg.cap;
+                if (part == 2) slot[h] = (sg.dyn2 ? gld(sg.dyn2) : sg.imm2) % sg.cap;
             }
         }
         __syncthreads();
@@ -961,25 +1106,30 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
             FgUnit cur = fg_unit(d, u);
             const FgSeg& sg = d.seg[cur.seg];
             float v = 0.0f;
-            if (ptid < 16) {
+            if (ptid < 16) {  // the split's slice partials, read at once, added in order
                 int nsl = min(SLM_SPLIT, d.nsl - cur.split * SLM_SPLIT);
-                v = fb[(h * W) * 16 + r];
-                for (int s = 1; s < nsl; s++) v = v + fb[(h * W + s) * 16 + r];
+                float pv[SLM_SPLIT];
+#pragma unroll
+                for (int s = 0; s < SLM_SPLIT; s++) pv[s] = s < nsl ? fb[(h * W + s) * 16 + r] : 0.0f;
+                v = pv[0];
+#pragma unroll
+                for (int s = 1; s < SLM_SPLIT; s++)
+                    if (s < nsl) v = v + pv[s];
             }
             float partner = __shfl_xor(v, 8);
             long long R = fg_row(sg, cur.tile, r);
             if (ptid >= 16 || R >= sg.rows) continue;
             if (sg.nsplit > 1) {
-                sg.part[(long long)cur.split * sg.rows + R] = v;
+                gst(sg.part + (long long)cur.split * sg.rows + R, v);
                 continue;
             }
-            sg.y[R] = v;
+            gst(sg.y + R, v);
             switch (sg.epi) {
                 case EPI_RESID:
-                    sg.o1[R] = res[h] + v;
+                    gst(sg.o1 + R, res[h] + v);
                     break;
                 case EPI_SILU:
-                    if (r < 8) sg.o1[cur.tile * 8 + r] = partner * v / (1.0f + expf(-v));
+                    if (r < 8) gst(sg.o1 + cur.tile * 8 + r, partner * v / (1.0f + expf(-v)));
                     break;
                 case EPI_ROPE: {
                     int part = (int)(R / sg.d), j = (int)(R % sg.d);
@@ -989,13 +1139,13 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc d) {
                         float cs = lds[sg.cs_lds + ie], sn = lds[sg.sn_lds + ie];
                         float o = e < half ? v * cs - partner * sn : partner * sn + v * cs;
                         if (part == 0) {
-                            sg.o1[j] = o;
+                            gst(sg.o1 + j, o);
                         } else {
-                            sg.o2[j] = o;
-                            sg.o3[((long long)head * sg.cap + slot[h]) * sg.dh + e] = o;
+                            gst(sg.o2 + j, o);
+                            gst(sg.o3 + ((long long)head * sg.cap + slot[h]) * sg.dh + e, o);
                         }
                     } else {
-                        sg.o4[((long long)head * sg.cap + slot[h]) * sg.dh + e] = v;
+                        gst(sg.o4 + ((long long)head * sg.cap + slot[h]) * sg.dh + e, v);
                     }
                     break;
                 }

@@ -42,8 +42,10 @@ constexpr size_t STAGE_CAP = 4 << 20;     // bytes of eager staging
 constexpr size_t BOUNCE_CAP = 4 << 20;    // pinned bounce buffer for reads
 constexpr size_t MAX_GRAPHS = 8;
 constexpr int VP_LEN_MAX = 4096;          // longest vector a fused prologue holds
-constexpr int LDS_MAX = 65536;
-constexpr int FG_GRID_MAX = 256;          // workgroups of a fused GEMV: one per compute unit
+constexpr int LDS_MAX = 163840;            // gfx950: 160 KB of LDS per workgroup
+constexpr int FG_GRID_MAX = 256;           // workgroups of a fused GEMV: one per compute unit
+constexpr int64_t COMBINE_LDS_MAX = 24576; // attention partials a fused prologue holds in LDS
+constexpr int ATTN_LDS_MAX = LDS_MAX;
 
 enum OpKind : uint32_t {
     OP_GATHER = 1, OP_COPY, OP_SHIFT, OP_COLUMNS, OP_LINEAR, OP_ADD, OP_ADD_ROW, OP_SCALE_ROWS,
@@ -365,11 +367,13 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int64_t m = n[1], heads = n[5], kh = n[6], dh = n[7], nsb = n[8];
             int dti = pow2_index((dh + 15) / 16, 4);
             int64_t dp = (int64_t)16 << dti;
-            int64_t wpp = 8;
-            while (wpp > 1 && wpp * 16 * (dp + 2) * 4 > 65536) wpp /= 2;
+            // LDS: wpp segment partials being folded, then each wave's tile of values
+            auto shm = [&](int64_t w) { return (w * 16 * (dp + 2) + SLM_SB_SEGS * 16 * (dp + 4)) * 4; };
+            int64_t wpp = SLM_SB_SEGS;
+            while (wpp > 1 && shm(wpp) > ATTN_LDS_MAX) wpp /= 2;
             int64_t qpt = 16 / (heads / kh);
             out.push_back(mk(k.attn[dti], (uint32_t)((m + qpt - 1) / qpt), (uint32_t)kh, (uint32_t)nsb,
-                             512, (uint32_t)(wpp * 16 * (dp + 2) * 4), c->ws, p[1], p[2], p[3],
+                             64 * SLM_SB_SEGS, (uint32_t)shm(wpp), c->ws, p[1], p[2], p[3],
                              (const long long*)o.dyn, (long long)n[0], (int)m, (long long)n[2],
                              (long long)n[3], (long long)n[4], (int)heads, (int)kh, (int)dh, o.f[0],
                              (int)wpp));
@@ -713,13 +717,11 @@ struct Planner {
                 o.dh = (int32_t)dh;
                 o.dp = dp;
                 o.nsb = (int32_t)nsb;
+                if (pn > COMBINE_LDS_MAX) return false;
                 o.part = c->ws;
+                o.in1 = b.alloc((int)(heads * nsb));  // the superblock weights
                 b.reads.push_back(rng(c->ws, pn));
-                if (pn <= 12288) {
-                    int off;
-                    if (!b.prefetch(c->ws, (int)pn, nullptr, 0, &off)) return false;
-                    o.w = off;
-                }
+                if (!b.prefetch(c->ws, (int)pn, nullptr, 0, &o.w)) return false;
                 break;
             }
             case SRC_FOLD: {
@@ -1169,7 +1171,8 @@ struct Planner {
                 cv.n = (int)(o.n[5] * o.n[7]);
                 cv.out[0] = o.p[0];
                 cv.op = &o;
-                if (cv.n % 4 == 0 && cv.n <= VP_LEN_MAX)
+                int64_t pn = o.n[8] * o.n[5] * (combine_dp(o.n[7]) + 2);
+                if (cv.n % 4 == 0 && cv.n <= VP_LEN_MAX && pn <= COMBINE_LDS_MAX)
                     pend.push_back(cv);
                 else
                     out.push_back(two[1]);
@@ -1968,11 +1971,11 @@ int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const fl
     // superblock slots: a fixed count for a window, else the current span
     size_t nsb;
     if (reach < BIG / 2) {
-        nsb = (size_t)((reach + (long long)m - 2) / 512 + 2);
+        nsb = (size_t)((reach + (long long)m - 2) / SLM_SB_KEYS + 2);
     } else {
         long long first = reach - 1 > pos ? 0 : pos - (reach - 1);
         long long last = pos + (long long)m - 1 - gap;
-        nsb = last >= first ? (size_t)(last / 512 - first / 512 + 1) : 1;
+        nsb = last >= first ? (size_t)(last / SLM_SB_KEYS - first / SLM_SB_KEYS + 1) : 1;
     }
     size_t qpt = 16 / group;
     size_t qtiles = (m + qpt - 1) / qpt;

@@ -229,6 +229,8 @@ ATTN_CASES = [
     dict(pos=5000, m=256, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
     dict(pos=9000, m=40, reach=O.USIZE_MAX, gap=4096, cap=16384, heads=12, key_heads=4, dh=64),
     dict(pos=600, m=33, reach=200, gap=0, cap=456, heads=6, key_heads=3, dh=32),
+    dict(pos=700, m=20, reach=512, gap=0, cap=600, heads=4, key_heads=2, dh=128),
+    dict(pos=300, m=5, reach=O.USIZE_MAX, gap=0, cap=320, heads=2, key_heads=2, dh=256),
 ]
 
 
