@@ -27,6 +27,7 @@
 #define SLM_FG_EPI_WAVES 4     // prologue/epilogue waves of slm_fg
 #define SLM_SB_SEGS 4          // 64-key attention segments per superblock
 #define SLM_SB_KEYS (64 * SLM_SB_SEGS)
+#define SLM_GLA_T 32           // tokens per LDS stage of the prompt GLA kernel
 #define SLM_FG_MISC (32 + 4 * SLM_PF_MAX)  // LDS floats of slm_fg's scalars and prefetch table
 
 enum {

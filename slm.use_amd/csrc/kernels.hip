@@ -217,20 +217,21 @@ KERNEL void __launch_bounds__(256) slm_l2norm(float* y, const float* x, int grou
 // gated linear attention (ops.rs:191-205, cpu.rs:284-329)
 // ---------------------------------------------------------------------------------------
 //
-// Four lanes per state column (head h, column b); lane j owns rows j·RPL .. j·RPL+RPL-1
-// of S[h][:, b] in registers. Tokens run in order: d = 1/(1 + e^(decay + bias)),
-// S[a][b] = d·S[a][b] + k[a]·v[b], y[b] = Σ_a q[a]·S[a][b], where each lane sums its rows
-// in order and the four partial sums are added as (P0 + P1) + (P2 + P3).
+// One workgroup per head, four lanes per state column b; lane j owns rows j·RPL ..
+// j·RPL+RPL-1 of S[h][:, b] in registers. Tokens run in order: d = 1/(1 + e^(decay +
+// bias)), S[a][b] = d·S[a][b] + k[a]·v[b], y[b] = Σ_a q[a]·S[a][b], where each lane sums
+// its rows in order and the four partial sums are added as (P0 + P1) + (P2 + P3). The
+// head's q, k and v for SLM_GLA_T tokens at a time are staged in LDS with coalesced loads.
 template <int RPL>
 __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                          const float* __restrict__ q, const float* __restrict__ k,
                          const float* __restrict__ v, const float* __restrict__ decay,
-                         const float* __restrict__ bias, int m, int heads, int dh) {
-    long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    long long col = t >> 2;
-    int j = (int)(t & 3);
-    bool live = col < (long long)heads * dh;
-    int h = live ? (int)(col / dh) : 0, b = live ? (int)(col % dh) : 0;
+                         const float* __restrict__ bias, int m, int heads, int dh, int vec) {
+    extern __shared__ float lds[];  // [SLM_GLA_T][q | k | v] rows, then [SLM_GLA_T] decay factors
+    int h = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+    int b = tid >> 2, j = tid & 3;
+    bool live = b < dh;
+    bool full = live && (j + 1) * RPL <= dh;  // every row of this lane is a row of S
     float* Sh = S + (long long)h * dh * dh;
     float st[RPL];
 #pragma unroll
@@ -238,23 +239,53 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
         int a = j * RPL + rr;
         st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
     }
-    float bh = live ? bias[h] : 0.0f;
-    for (int i = 0; i < m; i++) {
-        long long at = ((long long)i * heads + h) * dh;
-        float dc = live ? 1.0f / (1.0f + expf(decay[(long long)i * heads + h] + bh)) : 0.0f;
-        float vb = live ? v[at + b] : 0.0f;
-        float part = 0.0f;
-#pragma unroll
-        for (int rr = 0; rr < RPL; rr++) {
-            int a = j * RPL + rr;
-            if (live && a < dh) {
-                st[rr] = dc * st[rr] + k[at + a] * vb;
-                part = part + q[at + a] * st[rr];
-            }
+    float bh = bias[h];
+    int row3 = 3 * dh;
+    float* dcs = lds + SLM_GLA_T * row3;
+    // the staging loads: thread tid takes piece pc of tokens tt0, tt0 + tpar, ...
+    int lpt = row3 / vec, tpar = max(1, nt / lpt);
+    int tt0 = tid / lpt, pc = (tid % lpt) * vec;
+    int part = pc / dh, col = pc % dh;
+    const float* src0 = (part == 0 ? q : part == 1 ? k : v) + (long long)h * dh + col;
+    bool loader = tid < tpar * lpt;
+    for (int i0 = 0; i0 < m; i0 += SLM_GLA_T) {
+        int nt_tok = min(SLM_GLA_T, m - i0);
+        for (int tt = tt0; loader && tt < nt_tok; tt += tpar) {
+            const float* src = src0 + (long long)(i0 + tt) * heads * dh;
+            float* dst = lds + tt * row3 + pc;
+            if (vec == 4) *(f4*)dst = *(const f4*)src;
+            else *dst = *src;
         }
-        float t1 = part + __shfl_xor(part, 1);
-        float t2 = t1 + __shfl_xor(t1, 2);
-        if (live && j == 0) y[at + b] = t2;
+        for (int tt = tid; tt < nt_tok; tt += nt)
+            dcs[tt] = 1.0f / (1.0f + expf(decay[(long long)(i0 + tt) * heads + h] + bh));
+        __syncthreads();
+        for (int tt = 0; tt < nt_tok; tt++) {
+            const float* row = lds + tt * row3;
+            float dc = dcs[tt];
+            float vb = live ? row[2 * dh + b] : 0.0f;
+            float part_sum = 0.0f;
+            if (full) {
+#pragma unroll
+                for (int rr = 0; rr < RPL; rr++) {
+                    int a = j * RPL + rr;
+                    st[rr] = dc * st[rr] + row[dh + a] * vb;
+                    part_sum = part_sum + row[a] * st[rr];
+                }
+            } else if (live) {
+#pragma unroll
+                for (int rr = 0; rr < RPL; rr++) {
+                    int a = j * RPL + rr;
+                    if (a < dh) {
+                        st[rr] = dc * st[rr] + row[dh + a] * vb;
+                        part_sum = part_sum + row[a] * st[rr];
+                    }
+                }
+            }
+            float t1 = part_sum + __shfl_xor(part_sum, 1);
+            float t2 = t1 + __shfl_xor(t1, 2);
+            if (live && j == 0) y[((long long)(i0 + tt) * heads + h) * dh + b] = t2;
+        }
+        __syncthreads();
     }
 #pragma unroll
     for (int rr = 0; rr < RPL; rr++) {
@@ -264,10 +295,11 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
 }
 
 #define GLA(R)                                                                          \
-    KERNEL void __launch_bounds__(256)                                                  \
+    KERNEL void __launch_bounds__(1024)                                                 \
         slm_gla_##R(float* y, float* S, const float* q, const float* k, const float* v, \
-                    const float* decay, const float* bias, int m, int heads, int dh) {  \
-        gla_body<R>(y, S, q, k, v, decay, bias, m, heads, dh);                          \
+                    const float* decay, const float* bias, int m, int heads, int dh,    \
+                    int vec) {                                                          \
+        gla_body<R>(y, S, q, k, v, decay, bias, m, heads, dh, vec);                     \
     }
 GLA(1)
 GLA(2)
@@ -439,6 +471,113 @@ KERNEL void __launch_bounds__(256) slm_linear_big_v(float* y, const float* w, co
 KERNEL void __launch_bounds__(256) slm_linear_big_s(float* y, const float* w, const float* x,
                                                     int rows, int cols, int m) {
     linear_big_body<false>(y, w, x, rows, cols, m);
+}
+
+// m > 16, columns a multiple of 4, 16-byte aligned rows: the prompt GEMM. A 64-row × 64-token
+// tile per workgroup, 32 × 32 per wave; the weights and tokens of one slice (64 columns)
+// at a time are staged in LDS (row stride 68 floats), the next slice's loads in flight
+// while one computes. blockIdx.z is the split: with several splits each workgroup adds
+// one split's slices and writes its partial to part[split][token][row] (added in order by
+// slm_fold); with one it writes y. Same chain and sums as linear_big_body.
+#define GEMM_LS 68
+KERNEL void __launch_bounds__(256) slm_gemm(float* __restrict__ y, float* __restrict__ part,
+                                            const float* __restrict__ w,
+                                            const float* __restrict__ x, int rows, int cols,
+                                            int m) {
+    __shared__ float sw[2][64 * GEMM_LS];
+    __shared__ float sx[2][64 * GEMM_LS];
+    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int i = lane & 15, g = lane >> 4;
+    int wr = (wave & 1) * 32, wt = (wave >> 1) * 32;
+    long long r0 = (long long)blockIdx.x * 64, t0 = (long long)blockIdx.y * 64;
+    int kblocks = (cols + 15) >> 4, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
+    int s_first = blockIdx.z * SLM_SPLIT, s_end = min(nsl, s_first + SLM_SPLIT);
+    // staging: f4 number fi = tid + 256q of a 64 x 64 tile: row fi / 16, column 4 (fi % 16)
+    f4 rw[4], rx[4];
+    auto fetch = [&](int s) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            int fi = tid + 256 * q, row = fi >> 4, c = s * 64 + 4 * (fi & 15);
+            bool cin = c < cols;
+            rw[q] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            rx[q] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (cin && r0 + row < rows) rw[q] = *(const f4*)(w + (r0 + row) * cols + c);
+            if (cin && t0 + row < m) rx[q] = *(const f4*)(x + (t0 + row) * cols + c);
+        }
+    };
+    auto stash = [&](int b) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            int fi = tid + 256 * q, row = fi >> 4, c = 4 * (fi & 15);
+            *(f4*)(&sw[b][row * GEMM_LS + c]) = rw[q];
+            *(f4*)(&sx[b][row * GEMM_LS + c]) = rx[q];
+        }
+    };
+    f4 tot[2][2], sp[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int v = 0; v < 2; v++) {
+            tot[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            sp[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    fetch(s_first);
+    stash(0);
+    __syncthreads();
+    for (int s = s_first; s < s_end; s++) {
+        int b = (s - s_first) & 1;
+        if (s + 1 < s_end) fetch(s + 1);
+        f4 acc[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int v = 0; v < 2; v++) acc[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < SLM_KS; q++) {
+            if (s * SLM_KS + q >= kblocks) break;
+            f4 a[2], bb[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) a[u] = *(const f4*)(&sw[b][(wr + 16 * u + i) * GEMM_LS + 16 * q + 4 * g]);
+#pragma unroll
+            for (int v = 0; v < 2; v++) bb[v] = *(const f4*)(&sx[b][(wt + 16 * v + i) * GEMM_LS + 16 * q + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int v = 0; v < 2; v++) acc[u][v] = mfma4(a[u][e], bb[v][e], acc[u][v]);
+        }
+        // slice sums in order within the split, split sums in order (one split here)
+        bool open = (s - s_first) == 0;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int v = 0; v < 2; v++) sp[u][v] = open ? acc[u][v] : sp[u][v] + acc[u][v];
+        if (s + 1 < s_end) {
+            stash(b ^ 1);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int v = 0; v < 2; v++) tot[u][v] = sp[u][v];
+    // out: D[4g + r][i] is row wr + 16u + 4g + r, token wt + 16v + i; through LDS so the
+    // stores run along rows
+    __syncthreads();
+    float* so = &sw[0][0];  // [64 tokens][65]
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int v = 0; v < 2; v++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * 65 + wr + 16 * u + 4 * g + r] = tot[u][v][r];
+    __syncthreads();
+    float* out = gridDim.z > 1 ? part + (long long)blockIdx.z * m * rows : y;
+    for (int e = tid; e < 64 * 64; e += 256) {
+        int tok = e >> 6, row = e & 63;
+        if (t0 + tok < m && r0 + row < rows) out[(t0 + tok) * rows + r0 + row] = so[tok * 65 + row];
+    }
 }
 
 // ---------------------------------------------------------------------------------------

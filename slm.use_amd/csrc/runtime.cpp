@@ -87,7 +87,7 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 
 struct Kernels {
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
-        store, rope, rope_table, rms, l2norm, fill, combine, probe, fg, fold;
+        store, rope, rope_table, rms, l2norm, fill, combine, probe, fg, fold, gemm;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[7], gla1[7];           // rows per lane 1, 2, 4, .., 64
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
@@ -107,6 +107,8 @@ struct slm_hip {
     size_t ws_bytes = 0;
     float* part = nullptr;               // split partials of fused one-token linears (two halves)
     size_t part_bytes = 0;
+    float* gpart = nullptr;              // split partials of prompt GEMMs
+    size_t gpart_bytes = 0;
     unsigned char* stage_host = nullptr; // eager staging: pinned ring copied into a device ring
     unsigned char* stage_dev = nullptr;
     size_t stage_head = 0;
@@ -299,6 +301,16 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                 out.push_back(mk(k.lin_small[vec], (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
                                  (uint32_t)(nsl * 1024), p[0], p[1], p[2], (int)rows, (int)cols,
                                  (int)m));
+            } else if (vec) {  // the LDS-staged GEMM, one workgroup column per split
+                int64_t ns = (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
+                if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
+                    return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
+                out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
+                                 (uint32_t)ns, 256, 0, p[0], c->gpart, p[1], p[2], (int)rows,
+                                 (int)cols, (int)m));
+                if (ns > 1)
+                    out.push_back(mk(k.fold, blocks_for(m * rows), 1, 1, 256, 0, p[0],
+                                     (const float*)c->gpart, (long long)(m * rows), (int)ns));
             } else {
                 out.push_back(mk(k.lin_big[vec], (uint32_t)((rows + 63) / 64),
                                  (uint32_t)((m + 63) / 64), 1, 256, 0, p[0], p[1], p[2],
@@ -325,7 +337,9 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
         case OP_L2NORM: {  // p0 y, p1 x, p2 w; n0 groups, n1 size; f0 eps
             int64_t groups = n[0], size = n[1];
             int64_t stride = size | 1;
+            // up to 16 groups per workgroup, fewer when that leaves the chip half idle
             int64_t G = std::min<int64_t>(16, std::max<int64_t>(1, 16384 / stride));
+            G = std::max<int64_t>(1, std::min<int64_t>(G, groups / 512));
             uint32_t blocks = (uint32_t)((groups + G - 1) / G);
             uint32_t shmem = (uint32_t)(G * stride * 4);
             if (o.kind == OP_RMS)
@@ -351,9 +365,11 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             return SLM_OK;
         case OP_GLA: {  // p0 y, p1 s, p2 q, p3 k, p4 v, p5 decay, p6 bias; n0 m, n1 heads, n2 dh
             int i = pow2_index((n[2] + 3) / 4, 6);
-            size_t threads = (size_t)(n[1] * n[2] * 4);
-            out.push_back(mk(k.gla[i], (uint32_t)((threads + 255) / 256), 1, 1, 256, 0, p[0], p[1],
-                             p[2], p[3], p[4], p[5], p[6], (int)n[0], (int)n[1], (int)n[2]));
+            uint32_t threads = (uint32_t)((n[2] * 4 + 63) / 64 * 64);  // one workgroup per head
+            uint32_t shmem = (uint32_t)((SLM_GLA_T * 3 * n[2] + SLM_GLA_T) * 4);
+            int vec = (n[2] % 4 == 0 && aligned16(p[2]) && aligned16(p[3]) && aligned16(p[4])) ? 4 : 1;
+            out.push_back(mk(k.gla[i], (uint32_t)n[1], 1, 1, threads, shmem, p[0], p[1],
+                             p[2], p[3], p[4], p[5], p[6], (int)n[0], (int)n[1], (int)n[2], vec));
             return SLM_OK;
         }
         case OP_STORE:  // p0 cache, p1 src; n0 m, n1 cap, n2 heads, n3 dh, n4 pos
@@ -606,7 +622,7 @@ struct FgBuild {
 // alternating halves of c->part, so one kernel can read the last linear's partials while
 // it writes its own.
 int64_t nsplit_of(int64_t cols) {
-    int64_t nsl = (cols / 16 + SLM_KS - 1) / SLM_KS;
+    int64_t nsl = ((cols + 15) / 16 + SLM_KS - 1) / SLM_KS;
     return (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
 }
 
@@ -1309,6 +1325,14 @@ int need_part(slm_hip* c, size_t bytes) {
     return SLM_OK;
 }
 
+int need_gpart(slm_hip* c, size_t bytes) {
+    if (bytes <= c->gpart_bytes) return SLM_OK;
+    size_t nb = std::max(bytes, c->gpart_bytes * 2);
+    TRY(internal_realloc(c, (void**)&c->gpart, nb));
+    c->gpart_bytes = nb;
+    return SLM_OK;
+}
+
 int need_ws(slm_hip* c, size_t bytes) {
     bytes += 64;  // fused prologues read whole float4s past an odd-sized end
     if (bytes <= c->ws_bytes) return SLM_OK;
@@ -1396,7 +1420,7 @@ int load_kernels(slm_hip* c) {
                {&k.rms, "slm_rms"},             {&k.l2norm, "slm_l2norm"},
                {&k.fill, "slm_fill"},           {&k.combine, "slm_attn_combine"},
                {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
-               {&k.fold, "slm_fold"},
+               {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
                {&k.lin_small[0], "slm_linear_small_s"}, {&k.lin_small[1], "slm_linear_small_v"},
                {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
                {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
@@ -1487,6 +1511,7 @@ void slm_hip_close(slm_hip* c) {
     for (auto& a : c->allocs) hipFree((void*)a.first);
     if (c->ws) hipFree(c->ws);
     if (c->part) hipFree(c->part);
+    if (c->gpart) hipFree(c->gpart);
     if (c->stage_dev) hipFree(c->stage_dev);
     if (c->dyn_dev) hipFree(c->dyn_dev);
     if (c->stage_host) hipHostFree(c->stage_host);
@@ -1900,6 +1925,10 @@ int slm_hip_linear(slm_hip* c, float* y, const float* w, size_t rows, size_t col
     if (m == 1 && c->fusion_on && cols <= (size_t)VP_LEN_MAX) {
         int64_t ns = nsplit_of((int64_t)cols);
         if (ns > 1) TRY(need_part(c, (size_t)(2 * ns) * rows * 4));
+    }
+    if (m > 16) {
+        int64_t ns = nsplit_of((int64_t)cols);
+        if (ns > 1) TRY(need_gpart(c, (size_t)ns * m * rows * 4));
     }
     Op o = op(OP_LINEAR);
     o.p[0] = y;
