@@ -61,7 +61,7 @@ typedef struct {
     int32_t out, in0, in1;  // LDS float offsets
     int32_t w;              // LDS offset of the rms weight / combine / fold partials (-1: `part`)
     int32_t heads, dh, dp, nsb;
-    int32_t pad;
+    int32_t sync;           // 1: reads an element another thread's op produced (a barrier first)
     float* gout;            // global output, written by workgroup 0 (null: none)
     const float* part;      // combine partials in global memory (when w < 0)
     const long long* dyn;   // VP_SCALE factor on the device

@@ -217,21 +217,65 @@ KERNEL void __launch_bounds__(256) slm_l2norm(float* y, const float* x, int grou
 // gated linear attention (ops.rs:191-205, cpu.rs:284-329)
 // ---------------------------------------------------------------------------------------
 //
-// One workgroup per head, four lanes per state column b; lane j owns rows j·RPL ..
-// j·RPL+RPL-1 of S[h][:, b] in registers. Tokens run in order: d = 1/(1 + e^(decay +
-// bias)), S[a][b] = d·S[a][b] + k[a]·v[b], y[b] = Σ_a q[a]·S[a][b], where each lane sums
-// its rows in order and the four partial sums are added as (P0 + P1) + (P2 + P3). The
-// head's q, k and v for SLM_GLA_T tokens at a time are staged in LDS with coalesced loads.
+// Sixteen lanes per state column b (lanes 16c .. 16c+15 of a wave); lane j owns rows
+// j·RPL .. j·RPL+RPL-1 of S[h][:, b] in registers. Tokens run in order:
+// d = 1/(1 + e^(decay + bias)), S[a][b] = d·S[a][b] + k[a]·v[b], y[b] = Σ_a q[a]·S[a][b],
+// where each lane sums its rows in order and the sixteen lane sums are added pairwise
+// by lane distance 1, 2, 4, 8 (gla_colsum). The prompt kernel and the one-token kernel
+// (gla1_body) run the same expressions.
+
+// xor-1 and xor-2 lane swaps within quads (DPP quad_perm [1,0,3,2] and [2,3,0,1])
+__device__ __forceinline__ float dpp_xor1(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor2(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+}
+// The column total of the sixteen lane sums, in every lane of the sixteen.
+__device__ __forceinline__ float gla_colsum(float p) {
+    p = p + dpp_xor1(p);
+    p = p + dpp_xor2(p);
+    p = p + __shfl_xor(p, 4);
+    p = p + __shfl_xor(p, 8);
+    return p;
+}
+
+// One lane's rows for one token: st = d·st + k·v, and the lane's sum of q·st in order.
+template <int RPL>
+__device__ __forceinline__ float gla_rows(float (&st)[RPL], const float* kk, const float* qq,
+                                          float dc, float vb, int j, int dh) {
+    float part = 0.0f;
+    if ((j + 1) * RPL <= dh) {
+#pragma unroll
+        for (int rr = 0; rr < RPL; rr++) {
+            int a = j * RPL + rr;
+            st[rr] = dc * st[rr] + kk[a] * vb;
+            part = part + qq[a] * st[rr];
+        }
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < RPL; rr++) {
+            int a = j * RPL + rr;
+            if (a < dh) {
+                st[rr] = dc * st[rr] + kk[a] * vb;
+                part = part + qq[a] * st[rr];
+            }
+        }
+    }
+    return part;
+}
+
+// The prompt kernel: grid (heads, column groups of 16); each workgroup stages q and k of
+// its head and v of its columns for SLM_GLA_T tokens at a time in LDS.
 template <int RPL>
 __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                          const float* __restrict__ q, const float* __restrict__ k,
                          const float* __restrict__ v, const float* __restrict__ decay,
                          const float* __restrict__ bias, int m, int heads, int dh, int vec) {
-    extern __shared__ float lds[];  // [SLM_GLA_T][q | k | v] rows, then [SLM_GLA_T] decay factors
-    int h = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
-    int b = tid >> 2, j = tid & 3;
+    extern __shared__ float lds[];  // [SLM_GLA_T][q (dh) | k (dh) | v (16)], then [SLM_GLA_T] d
+    int h = blockIdx.x, c0 = blockIdx.y * 16, tid = threadIdx.x, nt = blockDim.x;
+    int b = c0 + (tid >> 4), j = tid & 15;
     bool live = b < dh;
-    bool full = live && (j + 1) * RPL <= dh;  // every row of this lane is a row of S
     float* Sh = S + (long long)h * dh * dh;
     float st[RPL];
 #pragma unroll
@@ -240,19 +284,25 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
         st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
     }
     float bh = bias[h];
-    int row3 = 3 * dh;
-    float* dcs = lds + SLM_GLA_T * row3;
-    // the staging loads: thread tid takes piece pc of tokens tt0, tt0 + tpar, ...
-    int lpt = row3 / vec, tpar = max(1, nt / lpt);
+    int rowl = 2 * dh + 16;
+    float* dcs = lds + SLM_GLA_T * rowl;
+    // staging: piece pc (of `vec` floats) of tokens tt0, tt0 + tpar, ...
+    int lpt = rowl / vec, tpar = max(1, nt / lpt);
     int tt0 = tid / lpt, pc = (tid % lpt) * vec;
-    int part = pc / dh, col = pc % dh;
-    const float* src0 = (part == 0 ? q : part == 1 ? k : v) + (long long)h * dh + col;
+    const float* src0 = nullptr;
+    if (pc < dh) src0 = q + (long long)h * dh + pc;
+    else if (pc < 2 * dh) src0 = k + (long long)h * dh + pc - dh;
+    else if (c0 + pc - 2 * dh < dh) src0 = v + (long long)h * dh + c0 + pc - 2 * dh;
     bool loader = tid < tpar * lpt;
     for (int i0 = 0; i0 < m; i0 += SLM_GLA_T) {
         int nt_tok = min(SLM_GLA_T, m - i0);
         for (int tt = tt0; loader && tt < nt_tok; tt += tpar) {
+            float* dst = lds + tt * rowl + pc;
+            if (!src0) {
+                for (int e = 0; e < vec; e++) dst[e] = 0.0f;
+                continue;
+            }
             const float* src = src0 + (long long)(i0 + tt) * heads * dh;
-            float* dst = lds + tt * row3 + pc;
             if (vec == 4) *(f4*)dst = *(const f4*)src;
             else *dst = *src;
         }
@@ -260,30 +310,11 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
             dcs[tt] = 1.0f / (1.0f + expf(decay[(long long)(i0 + tt) * heads + h] + bh));
         __syncthreads();
         for (int tt = 0; tt < nt_tok; tt++) {
-            const float* row = lds + tt * row3;
-            float dc = dcs[tt];
-            float vb = live ? row[2 * dh + b] : 0.0f;
-            float part_sum = 0.0f;
-            if (full) {
-#pragma unroll
-                for (int rr = 0; rr < RPL; rr++) {
-                    int a = j * RPL + rr;
-                    st[rr] = dc * st[rr] + row[dh + a] * vb;
-                    part_sum = part_sum + row[a] * st[rr];
-                }
-            } else if (live) {
-#pragma unroll
-                for (int rr = 0; rr < RPL; rr++) {
-                    int a = j * RPL + rr;
-                    if (a < dh) {
-                        st[rr] = dc * st[rr] + row[dh + a] * vb;
-                        part_sum = part_sum + row[a] * st[rr];
-                    }
-                }
-            }
-            float t1 = part_sum + __shfl_xor(part_sum, 1);
-            float t2 = t1 + __shfl_xor(t1, 2);
-            if (live && j == 0) y[((long long)(i0 + tt) * heads + h) * dh + b] = t2;
+            const float* row = lds + tt * rowl;
+            float vb = live ? row[2 * dh + (b - c0)] : 0.0f;
+            float part = live ? gla_rows<RPL>(st, row + dh, row, dcs[tt], vb, j, dh) : 0.0f;
+            float tot = gla_colsum(part);
+            if (live && j == 0) y[((long long)(i0 + tt) * heads + h) * dh + b] = tot;
         }
         __syncthreads();
     }
@@ -295,7 +326,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
 }
 
 #define GLA(R)                                                                          \
-    KERNEL void __launch_bounds__(1024)                                                 \
+    KERNEL void __launch_bounds__(256)                                                  \
         slm_gla_##R(float* y, float* S, const float* q, const float* k, const float* v, \
                     const float* decay, const float* bias, int m, int heads, int dh,    \
                     int vec) {                                                          \
@@ -306,8 +337,6 @@ GLA(2)
 GLA(4)
 GLA(8)
 GLA(16)
-GLA(32)
-GLA(64)
 
 // ---------------------------------------------------------------------------------------
 // linear: y[i][r] = Σ_c w[r][c]·x[i][c] (ops.rs:116-126)
@@ -934,14 +963,16 @@ __device__ __forceinline__ float dot16_lanes0(const float* in, int size, int l) 
 // One prologue operation on LDS vectors, run by every thread of the workgroup (the GEMV
 // waves' weights are in flight meanwhile; nothing here touches global memory, so their
 // loads never hold it up). Element c of every element-wise op is computed by the same
-// thread, so such ops follow each other without a barrier; rms and the combine wait for
-// the other threads where they need their results. misc[0]: the rms factor; misc[4 + k]:
+// thread, so an op that reads element c of an earlier op's output follows it without a
+// barrier; one that reads it at an offset (`sync`), rms and the combine wait for the other
+// threads. misc[0]: the rms factor; misc[4 + k]:
 // the dynamic factor of op k.
 __device__ void vp_run(const VpOp& o, float* lds, const float* misc, int k, int tid, int nt) {
     int n = o.n;
     const float* a = lds + o.in0;
     const float* b = o.in1 >= 0 ? lds + o.in1 : nullptr;
     float* out = o.out >= 0 ? lds + o.out : nullptr;
+    if (o.sync) __syncthreads();
     switch (o.kind) {
         case VP_RMS: {  // rms (cpu.rs:187-207) of one group; a and out may not alias
             __syncthreads();  // the input may come from other threads
@@ -1304,15 +1335,15 @@ KERNEL void slm_fold(float* __restrict__ y, const float* __restrict__ part, long
     }
 }
 
-// One token of gated linear attention per head (the m = 1 case of gla_body). When `l2`,
-// q and k are first l2-normalised per head (model.rs:465-467, the expressions of
-// slm_l2norm); when `fuse`, the head RMSNorm and the SiLU gate of model.rs:483-484
-// follow, in the expressions of slm_rms and slm_silu_mul.
+// One token of gated linear attention per head, one workgroup per head (the m = 1 case of
+// gla_body, same expressions). When `l2`, q and k are first l2-normalised per head
+// (model.rs:465-467, the expressions of slm_l2norm); when `fuse`, the head RMSNorm and the
+// SiLU gate of model.rs:483-484 follow, in the expressions of slm_rms and slm_silu_mul.
 template <int RPL>
 __device__ void gla1_body(const GlaDesc& g) {
     extern __shared__ float lds[];  // [dh + 4] rms, [dh] q, [dh] k, 4 norms
     int h = blockIdx.x, tid = threadIdx.x, dh = g.dh;
-    int b = tid >> 2, j = tid & 3;
+    int b = tid >> 4, j = tid & 15;
     bool live = b < dh;
     float* Sh = g.s + (long long)h * dh * dh;
     long long at = (long long)h * dh;
@@ -1322,47 +1353,40 @@ __device__ void gla1_body(const GlaDesc& g) {
         int a = j * RPL + rr;
         st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
     }
-    const float* q = g.q + at;
-    const float* k = g.k + at;
+    float* lq = lds + dh + 4;
+    float* lk = lq + dh;
+    float* nr = lk + dh;
+    for (int c = tid; c < dh; c += blockDim.x) {
+        lq[c] = g.q[at + c];
+        lk[c] = g.k[at + c];
+    }
+    __syncthreads();
     if (g.l2) {
-        float* lq = lds + dh + 4;
-        float* lk = lq + dh;
-        float* nr = lk + dh;
-        for (int c = tid; c < dh; c += blockDim.x) {
-            lq[c] = q[c];
-            lk[c] = k[c];
-        }
-        __syncthreads();
         if (tid < 32) {
             float d = dot16_self(tid < 16 ? lq : lk, dh, tid & 15);
             if ((tid & 15) == 0) nr[tid >> 4] = 1.0f / fmaxf(sqrtf(d), 1e-12f);
         }
         __syncthreads();
         float rq = nr[0], rk = nr[1];
-        for (int c = tid; c < dh; c += blockDim.x) {
-            float a = lq[c] * rq, bb = lk[c] * rk;
-            g.qn[at + c] = a;
-            g.kn[at + c] = bb;
-            lq[c] = a;
-            lk[c] = bb;
+        float aq = 0.0f, ak = 0.0f;
+        int c = tid;
+        if (c < dh) {
+            aq = lq[c] * rq;
+            ak = lk[c] * rk;
+            g.qn[at + c] = aq;
+            g.kn[at + c] = ak;
         }
         __syncthreads();
-        q = lq;
-        k = lk;
+        if (c < dh) {
+            lq[c] = aq;
+            lk[c] = ak;
+        }
+        __syncthreads();
     }
     float dc = 1.0f / (1.0f + expf(g.decay[h] + g.bias[h]));
     float vb = live ? g.v[at + b] : 0.0f;
-    float part = 0.0f;
-#pragma unroll
-    for (int rr = 0; rr < RPL; rr++) {
-        int a = j * RPL + rr;
-        if (live && a < dh) {
-            st[rr] = dc * st[rr] + k[a] * vb;
-            part = part + q[a] * st[rr];
-        }
-    }
-    float t1 = part + __shfl_xor(part, 1);
-    float t2 = t1 + __shfl_xor(t1, 2);
+    float part = live ? gla_rows<RPL>(st, lk, lq, dc, vb, j, dh) : 0.0f;
+    float t2 = gla_colsum(part);
 #pragma unroll
     for (int rr = 0; rr < RPL; rr++) {
         int a = j * RPL + rr;
@@ -1390,7 +1414,3 @@ __device__ void gla1_body(const GlaDesc& g) {
 GLA1(1)
 GLA1(2)
 GLA1(4)
-GLA1(8)
-GLA1(16)
-GLA1(32)
-GLA1(64)

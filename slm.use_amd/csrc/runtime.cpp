@@ -89,7 +89,7 @@ struct Kernels {
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
         store, rope, rope_table, rms, l2norm, fill, combine, probe, fg, fold, gemm;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
-    hipFunction_t gla[7], gla1[7];           // rows per lane 1, 2, 4, .., 64
+    hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
 };
 
@@ -364,12 +364,13 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                              p[2], p[3], (long long)n[0], (long long)n[1], (long long)n[2]));
             return SLM_OK;
         case OP_GLA: {  // p0 y, p1 s, p2 q, p3 k, p4 v, p5 decay, p6 bias; n0 m, n1 heads, n2 dh
-            int i = pow2_index((n[2] + 3) / 4, 6);
-            uint32_t threads = (uint32_t)((n[2] * 4 + 63) / 64 * 64);  // one workgroup per head
-            uint32_t shmem = (uint32_t)((SLM_GLA_T * 3 * n[2] + SLM_GLA_T) * 4);
+            // sixteen lanes per state column, sixteen columns per workgroup
+            int i = pow2_index((n[2] + 15) / 16, 4);
+            uint32_t shmem = (uint32_t)((SLM_GLA_T * (2 * n[2] + 16) + SLM_GLA_T) * 4);
             int vec = (n[2] % 4 == 0 && aligned16(p[2]) && aligned16(p[3]) && aligned16(p[4])) ? 4 : 1;
-            out.push_back(mk(k.gla[i], (uint32_t)n[1], 1, 1, threads, shmem, p[0], p[1],
-                             p[2], p[3], p[4], p[5], p[6], (int)n[0], (int)n[1], (int)n[2], vec));
+            out.push_back(mk(k.gla[i], (uint32_t)n[1], (uint32_t)((n[2] + 15) / 16), 1, 256, shmem,
+                             p[0], p[1], p[2], p[3], p[4], p[5], p[6], (int)n[0], (int)n[1],
+                             (int)n[2], vec));
             return SLM_OK;
         }
         case OP_STORE:  // p0 cache, p1 src; n0 m, n1 cap, n2 heads, n3 dh, n4 pos
@@ -764,6 +765,14 @@ struct Planner {
                 }
             }
         }
+        // an input that starts inside another op's output (not at its start) holds elements
+        // other threads wrote: a barrier comes first
+        for (int in : {o.in0, o.in1}) {
+            if (in < 0) continue;
+            for (size_t q = 0; q < b.slots.size(); q++)
+                if (b.slot_op[q] >= 0 && in > b.slots[q].off && in < b.slots[q].off + b.slots[q].n)
+                    o.sync = 1;
+        }
         o.out = b.alloc(v.n);
         o.gout = (float*)v.out[0];
         b.writes.push_back(rng0(v.out[0], v.n));
@@ -1070,7 +1079,7 @@ struct Planner {
         const Op& g = ops[i];
         if (g.n[0] != 1) return 0;
         int64_t heads = g.n[1], dh = g.n[2];
-        if (dh * 4 > 1024) return 0;
+        if (dh * 16 > 1024) return 0;  // a head per workgroup, sixteen lanes per column
         GlaDesc d;
         std::memset(&d, 0, sizeof d);
         d.y = (float*)g.p[0];
@@ -1132,8 +1141,8 @@ struct Planner {
                 used = 3;
             }
         }
-        int ri = pow2_index((dh + 3) / 4, 6);
-        out.push_back(mk_desc(c->k.gla1[ri], (uint32_t)heads, (uint32_t)((dh * 4 + 63) / 64 * 64),
+        int ri = pow2_index((dh + 15) / 16, 2);
+        out.push_back(mk_desc(c->k.gla1[ri], (uint32_t)heads, (uint32_t)((dh * 16 + 63) / 64 * 64),
                               (uint32_t)((4 * dh + 16) * 4), d));
         return used;
     }
@@ -1207,6 +1216,27 @@ int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fus
     Planner p{c, ops, out, {}};
     size_t before = out.size();
     TRY(p.run(fuse));
+    if (c->plan_trace) {
+        fprintf(stderr, "slm plan: %zu ops ->", ops.size());
+        for (size_t k = before; k < out.size(); k++) {
+            const char* nm = "?";
+            const Kernels& K = c->k;
+            if (out[k].f == K.fg) {
+                const FgDesc* d = (const FgDesc*)out[k].blob;
+                fprintf(stderr, " fg[%dx%d vp", d->seg[0].rows, d->cols);
+                for (int q = 0; q < d->nvp; q++)
+                    fprintf(stderr, "%s%d:%d%s", q ? "," : "", d->vp[q].kind, d->vp[q].n, d->vp[q].gout ? "w" : "");
+                fprintf(stderr, " pf%d]", d->npf);
+                continue;
+            }
+            for (auto& pr : {std::make_pair(K.gemm, "gemm"), std::make_pair(K.lin_small[1], "lin"),
+                             std::make_pair(K.fold, "fold"), std::make_pair(K.combine, "comb"),
+                             std::make_pair(K.add, "add"), std::make_pair(K.rms, "rms")})
+                if (out[k].f == pr.first) nm = pr.second;
+            fprintf(stderr, " %s", nm);
+        }
+        fprintf(stderr, "\n");
+    }
     c->last_ops = ops.size();
     c->last_kernels = out.size() - before;
     return SLM_OK;
@@ -1424,11 +1454,8 @@ int load_kernels(slm_hip* c) {
                {&k.lin_small[0], "slm_linear_small_s"}, {&k.lin_small[1], "slm_linear_small_v"},
                {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
                {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
-               {&k.gla[3], "slm_gla_8"},   {&k.gla[4], "slm_gla_16"},  {&k.gla[5], "slm_gla_32"},
-               {&k.gla[6], "slm_gla_64"},
+               {&k.gla[3], "slm_gla_8"},   {&k.gla[4], "slm_gla_16"},
                {&k.gla1[0], "slm_gla1_1"}, {&k.gla1[1], "slm_gla1_2"}, {&k.gla1[2], "slm_gla1_4"},
-               {&k.gla1[3], "slm_gla1_8"}, {&k.gla1[4], "slm_gla1_16"}, {&k.gla1[5], "slm_gla1_32"},
-               {&k.gla1[6], "slm_gla1_64"},
                {&k.attn[0], "slm_attn_part_1"}, {&k.attn[1], "slm_attn_part_2"},
                {&k.attn[2], "slm_attn_part_4"}, {&k.attn[3], "slm_attn_part_8"},
                {&k.attn[4], "slm_attn_part_16"}};

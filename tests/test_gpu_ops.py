@@ -273,7 +273,7 @@ def _step(hip, body, inv, cs, sn, fuse):
 
 
 FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "combine", "side_copy",
-                "split_fold", "split_flush", "gla_l2", "rounds"]
+                "split_fold", "split_flush", "gla_l2", "rounds", "row_offset"]
 
 
 @pytest.mark.parametrize("case", FUSION_CASES)
@@ -346,6 +346,11 @@ def test_fusion_pattern(hip, case):
         elif case == "split_flush":  # ... or in a kernel of their own
             hip.linear(o["h"].ptr, wdown.ptr, d, hid, xh.ptr, 1)
             hip.add(o["t"].ptr, res.ptr, o["h"].ptr, d)
+        elif case == "row_offset":  # a prologue op reading another's output at an offset
+            hip.add(o["up"].ptr, xh.ptr, xh.ptr, 2 * d)
+            hip.copy(o["s"].ptr, o["up"].at(d), d)
+            hip.rms(o["n"].ptr, o["s"].ptr, nw.ptr, 1, d, 1e-6)
+            hip.linear(o["y"].ptr, wsq.ptr, d, d, o["n"].ptr, 1)
         elif case == "rounds":  # 2000 tiles: each workgroup takes several rounds of two
             hip.rms(o["n"].ptr, x.ptr, nw.ptr, 1, d, 1e-6)
             hip.linear(o["lg"].ptr, whead.ptr, 32000, d, o["n"].ptr, 1)
