@@ -12,10 +12,10 @@ sliding window — then decodes greedily, reading the logits back every token
 decoded token.
 
 Printed: one JSON line. `value` is decode tok/s. `roofline` is the dominant decode kernel
-(the m = 1 GEMV, slm_linear_small_v) against HBM, timed with HIP events on the backend's
-stream over one decode step's exact sequence of GEMV shapes; `decode_roofline` is the whole
-step against HBM (algorithmic bytes per token); `prefill_roofline` is prefill against fp32
-MFMA peak. `cpu_baseline` times the oracle (a C++ restatement of src/cpu.rs +
+(the fused one-token GEMV, slm_fg) against HBM: its launches over `--timed-steps` further
+decode steps, each bracketed by HIP events on the backend's stream, and the algorithmic
+bytes they move (weights, prologue vectors, outputs); `decode_roofline` is the whole step
+against HBM (algorithmic bytes per token); `prefill` is prefill against fp32 MFMA peak. `cpu_baseline` times the oracle (a C++ restatement of src/cpu.rs +
 src/model.rs, OpenMP over the host's cores) on a bounded sample of the same workload.
 """
 
@@ -121,65 +121,6 @@ def prefill_flops(cfg, loops, start, count):
 
 
 # ---------------------------------------------------------------------------------------
-# HIP events on the backend's stream
-# ---------------------------------------------------------------------------------------
-
-class Events:
-    def __init__(self, stream: int):
-        self.hip = C.CDLL("libamdhip64.so")
-        self.stream = C.c_void_p(stream)
-        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-
-    def new(self):
-        e = C.c_void_p()
-        assert self.hip.hipEventCreate(C.byref(e)) == 0
-        return e
-
-    def record(self, e):
-        assert self.hip.hipEventRecord(e, self.stream) == 0
-
-    def sync(self, e):
-        assert self.hip.hipEventSynchronize(e) == 0
-
-    def ms(self, a, b) -> float:
-        out = C.c_float()
-        assert self.hip.hipEventElapsedTime(C.byref(out), a, b) == 0
-        return out.value
-
-
-def time_gemv_sequence(pkg, hip, shapes, reps=20):
-    """Average duration of one launch of the decode GEMV over one decode step's exact
-    sequence of shapes, each launch bracketed by its own pair of HIP events on the
-    backend's stream; and the algorithmic bytes per launch (weights + input + output)."""
-    rng = np.random.default_rng(0)
-    uniq = sorted(set(shapes))
-    w = {s: hip.upload(rng.standard_normal(s[0] * s[1], dtype=np.float32) * np.float32(0.02))
-         for s in uniq}
-    x = hip.upload(rng.standard_normal(max(c for _, c in uniq), dtype=np.float32))
-    y = hip.alloc(max(r for r, _ in uniq))
-    ev = Events(hip.stream())
-    pairs = [(ev.new(), ev.new()) for _ in shapes]
-    hip.set_graphs(False)
-    for _ in range(3):  # warm
-        for r, c in shapes:
-            hip.linear(y.ptr, w[(r, c)].ptr, r, c, x.ptr, 1)
-    total = 0.0
-    for _ in range(reps):
-        for (a, b), (r, c) in zip(pairs, shapes):
-            ev.record(a)
-            hip.linear(y.ptr, w[(r, c)].ptr, r, c, x.ptr, 1)
-            ev.record(b)
-        ev.sync(pairs[-1][1])
-        total += sum(ev.ms(a, b) for a, b in pairs)
-    hip.set_graphs(True)
-    for b in list(w.values()) + [x, y]:
-        b.free()
-    per_launch_s = total / 1e3 / (reps * len(shapes))
-    bytes_per_launch = sum(4 * (r * c + c + r) for r, c in shapes) / len(shapes)
-    return per_launch_s, bytes_per_launch
-
-
-# ---------------------------------------------------------------------------------------
 # the CPU baseline: the oracle on the host cores
 # ---------------------------------------------------------------------------------------
 
@@ -222,6 +163,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--no-graphs", action="store_true")
+    ap.add_argument("--timed-steps", type=int, default=16,
+                    help="decode steps whose kernels are timed one by one for the roofline")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -266,12 +209,23 @@ def main():
     # whole-step roofline (decode) and MFMA utilisation (prefill)
     bpt = np.mean([decode_bytes(cfg, a.loops, p) for p in range(pos0, pos0 + a.steps)])
     fl = prefill_flops(cfg, a.loops, 16, len(prompt))
-    # dominant kernel: the decode GEMV over one step's shapes, timed live with events
-    shapes = step_linears(cfg, a.loops)
-    per_launch, bpl = time_gemv_sequence(pkg, hip, shapes)
-    gemv_bw = bpl / per_launch
-    log(f"decode GEMV: {per_launch * 1e6:.2f} us/launch avg over {len(shapes)} shapes, "
-        f"{gemv_bw / 1e9:.0f} GB/s")
+    # dominant kernel: the fused decode GEMV (slm_fg), every launch of `--timed-steps` more
+    # decode steps bracketed by HIP events on the backend's stream (eager launches: the
+    # same kernels the step graph holds)
+    hip.set_graphs(False)
+    hip.set_timing(True)
+    se.decode_greedy(a.timed_steps)
+    se.logits()
+    kern = {n: hip.kernel_stat(n) for n in ("slm_fg", "slm_attn_part_4", "slm_gla1_4")}
+    hip.set_timing(False)
+    hip.set_graphs(not a.no_graphs)
+    fg = kern["slm_fg"]
+    per_launch = fg["us"] / 1e6 / max(fg["launches"], 1)
+    bpl = fg["bytes"] / max(fg["launches"], 1)
+    gemv_bw = bpl / per_launch if per_launch else 0.0
+    log(f"slm_fg: {fg['launches']} launches, {per_launch * 1e6:.2f} us/launch, "
+        f"{bpl / 1e6:.2f} MB/launch, {gemv_bw / 1e9:.0f} GB/s")
+    share = {n: round(v["us"] / max(a.timed_steps, 1), 1) for n, v in kern.items()}
 
     cpu = None
     if not a.no_cpu:
@@ -303,8 +257,9 @@ def main():
                    "prompt_tokens": len(prompt), "decode_from_pos": pos0},
         "roofline": {"bound": "hbm", "achieved": round(gemv_bw / 1e9, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(gemv_bw / HBM_PEAK, 4), "traffic": None,
-                     "kernel": "slm_linear_small_v",
-                     "bytes_per_launch": round(bpl), "us_per_launch": round(per_launch * 1e6, 3)},
+                     "kernel": "slm_fg", "launches": fg["launches"],
+                     "bytes_per_launch": round(bpl), "us_per_launch": round(per_launch * 1e6, 3),
+                     "us_per_step_by_kernel": share},
         "decode_roofline": {"bound": "hbm", "bytes_per_token": round(bpt),
                             "achieved": round(bpt * tok_s / 1e9, 1), "peak": 8000.0,
                             "unit": "GB/s", "frac": round(bpt * tok_s / HBM_PEAK, 4)},

@@ -2,9 +2,9 @@
  *
  * One entry point per method of the reference's operator trait `Ops` (src/ops.rs:68-228).
  * The reference's model (src/model.rs) drives that trait; a Rust `impl Ops for Hip`
- * binds these functions one to one the way src/cuda.rs binds its
- * CUDA kernels, so model.rs, the loop-count logic, the sampler, the CLI and the server
- * run unchanged above it.
+ * binds these functions one to one, the way src/cuda.rs binds its CUDA kernels, so
+ * model.rs, the loop-count logic, the sampler, the CLI and the server run unchanged
+ * above it.
  *
  * Conventions, all from src/ops.rs:1-9 and the trait signatures:
  *   - Every buffer is flat fp32 in device memory, allocated by slm_hip_alloc/upload.
@@ -145,6 +145,15 @@ int slm_hip_graph_stats(slm_hip* ctx, uint64_t* launched, uint64_t* captured,
                         uint64_t* eager);
 /* Operations recorded and kernel launches planned for the last step that was lowered. */
 int slm_hip_last_plan(slm_hip* ctx, uint64_t* ops, uint64_t* kernels);
+
+/* Kernel statistics (no counterpart in the reference; a measurement aid). While timing is
+ * on, every launch made outside a graph is bracketed by HIP events on the backend's stream;
+ * slm_hip_kernel_stat returns, for the kernel `name` (e.g. "slm_fg"), the launches, their
+ * summed duration in microseconds and the algorithmic bytes they move (weights, inputs and
+ * outputs). slm_hip_set_timing resets the statistics. */
+int slm_hip_set_timing(slm_hip* ctx, int on);
+int slm_hip_kernel_stat(slm_hip* ctx, const char* name, long long* launches, double* us,
+                        double* bytes);
 
 /* ---- diagnostics (no trait counterpart) ----
  * One v_mfma_f32_16x16x4f32 on one wave: lane l supplies a[l] and b[l] (device, 64 floats

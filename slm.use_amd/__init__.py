@@ -91,6 +91,9 @@ _SIGS = {
     "slm_hip_graph_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                  C.POINTER(C.c_uint64)]),
     "slm_hip_last_plan": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "slm_hip_set_timing": (_i, [_p, C.c_int]),
+    "slm_hip_kernel_stat": (_i, [_p, C.c_char_p, C.POINTER(C.c_longlong), C.POINTER(C.c_double),
+                                 C.POINTER(C.c_double)]),
     "slm_hip_probe_mfma": (_i, [_p, _p, _p, _p]),
     "slm_hip_stream": (_i, [_p, C.POINTER(_p)]),
     "slm_model_load": (_i, [_p, C.c_char_p, C.POINTER(_p)]),
@@ -206,6 +209,16 @@ class Hip:
         a, b = C.c_uint64(), C.c_uint64()
         self.check(lib.slm_hip_last_plan(self.ctx, C.byref(a), C.byref(b)))
         return dict(ops=a.value, kernels=b.value)
+
+    def set_timing(self, on: bool):
+        """Per-kernel HIP-event timing of launches made outside graphs (resets the stats)."""
+        self.check(lib.slm_hip_set_timing(self.ctx, int(on)))
+
+    def kernel_stat(self, name: str):
+        n, us, b = C.c_longlong(), C.c_double(), C.c_double()
+        self.check(lib.slm_hip_kernel_stat(self.ctx, name.encode(), C.byref(n), C.byref(us),
+                                           C.byref(b)))
+        return dict(launches=n.value, us=us.value, bytes=b.value)
 
     def set_fusion(self, on: bool):
         self.check(lib.slm_hip_set_fusion(self.ctx, int(on)))

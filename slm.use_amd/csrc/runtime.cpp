@@ -68,7 +68,18 @@ struct Op {
 struct Rec {
     hipFunction_t f;
     uint32_t gx, gy, gz, bx, shmem, nargs, bytes;
+    double abytes = 0.0;  // algorithmic bytes the launch moves (for the kernel statistics)
     alignas(16) unsigned char blob[BLOB];
+};
+
+struct KStat {  // per kernel, from HIP events around each eager launch (timing mode)
+    long long launches = 0;
+    double ms = 0.0, bytes = 0.0;
+};
+struct Timed {
+    hipEvent_t a, b;
+    hipFunction_t f;
+    double abytes;
 };
 
 struct Graph {
@@ -119,6 +130,11 @@ struct slm_hip {
     float* bounce = nullptr;
     std::map<uintptr_t, Table> tables;
     bool graphs_on = true, fusion_on = true, plan_trace = false;
+    bool timing = false, capturing = false;
+    std::vector<Timed> timed;             // launches whose events are not read yet
+    std::vector<hipEvent_t> ev_pool;
+    std::map<hipFunction_t, std::string> fname;
+    std::map<std::string, KStat> kstats;
     bool recording = false, tainted = false;
     std::vector<Op> ops;                 // the step being recorded
     std::vector<unsigned char> dyn;
@@ -231,6 +247,35 @@ Rec mk_desc(hipFunction_t f, uint32_t gx, uint32_t bx, uint32_t shmem, const D& 
     return r;
 }
 
+hipEvent_t pool_event(slm_hip* c) {
+    if (!c->ev_pool.empty()) {
+        hipEvent_t e = c->ev_pool.back();
+        c->ev_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Reads the events of the timed launches into the per-kernel statistics.
+int collect_timing(slm_hip* c) {
+    if (c->timed.empty()) return SLM_OK;
+    HIPC(c, hipStreamSynchronize(c->stream));
+    for (auto& t : c->timed) {
+        float ms = 0.0f;
+        HIPC(c, hipEventElapsedTime(&ms, t.a, t.b));
+        KStat& k = c->kstats[c->fname[t.f]];
+        k.launches++;
+        k.ms += ms;
+        k.bytes += t.abytes;
+        c->ev_pool.push_back(t.a);
+        c->ev_pool.push_back(t.b);
+    }
+    c->timed.clear();
+    return SLM_OK;
+}
+
 int launch_now(slm_hip* c, const Rec& r) {
     void* ptrs[MAX_ARGS];
     if (r.bytes) {
@@ -238,8 +283,21 @@ int launch_now(slm_hip* c, const Rec& r) {
     } else {
         for (uint32_t i = 0; i < r.nargs; i++) ptrs[i] = (void*)(r.blob + 8 * i);
     }
+    bool timed = c->timing && !c->capturing;
+    Timed t{nullptr, nullptr, r.f, r.abytes};
+    if (timed) {
+        t.a = pool_event(c);
+        t.b = pool_event(c);
+        if (!t.a || !t.b) return fail(c, SLM_E_HIP, "hipEventCreate failed");
+        HIPC(c, hipEventRecord(t.a, c->stream));
+    }
     HIPC(c, hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream, ptrs,
                                   nullptr));
+    if (timed) {
+        HIPC(c, hipEventRecord(t.b, c->stream));
+        c->timed.push_back(t);
+        if (c->timed.size() >= 4096) TRY(collect_timing(c));
+    }
     return SLM_OK;
 }
 
@@ -296,11 +354,13 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             }
             int vec = (cols % 4 == 0 && aligned16(p[1]) && aligned16(p[2])) ? 1 : 0;
             int64_t kblocks = (cols + 15) / 16, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
+            double ab = 4.0 * (double)(rows * cols + m * cols + m * rows);
             if (m <= 16 && nsl <= 64) {
                 uint32_t waves = (uint32_t)std::min<int64_t>(nsl, 8);
                 out.push_back(mk(k.lin_small[vec], (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
                                  (uint32_t)(nsl * 1024), p[0], p[1], p[2], (int)rows, (int)cols,
                                  (int)m));
+                out.back().abytes = ab;
             } else if (vec) {  // the LDS-staged GEMM, one workgroup column per split
                 int64_t ns = (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
                 if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
@@ -1055,6 +1115,9 @@ struct Planner {
         int threads = 64 * (W + SLM_FG_EPI_WAVES);
         uint32_t grid = (uint32_t)std::min(units, FG_GRID_MAX);
         out.push_back(mk_desc(c->k.fg, grid, (uint32_t)threads, (uint32_t)(total * 4), d));
+        double ab = 16.0 * d.pf4;  // prologue vectors, then weights and outputs
+        for (int k = 0; k < nseg; k++) ab += 4.0 * ((double)seg[k].rows * cols + seg[k].rows);
+        out.back().abytes = ab;
         if (nsplit > 1) {
             part_flip ^= 1;
             VpSrc f;
@@ -1411,14 +1474,17 @@ int finish_step(slm_hip* c) {
     g.used = c->clock;
     hipGraph_t graph = nullptr;
     HIPC(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
     for (auto& r : recs) {
         int rc = launch_now(c, r);
         if (rc) {
+            c->capturing = false;
             hipStreamEndCapture(c->stream, &graph);
             if (graph) hipGraphDestroy(graph);
             return rc;
         }
     }
+    c->capturing = false;
     HIPC(c, hipStreamEndCapture(c->stream, &graph));
     hipError_t e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
@@ -1459,7 +1525,10 @@ int load_kernels(slm_hip* c) {
                {&k.attn[0], "slm_attn_part_1"}, {&k.attn[1], "slm_attn_part_2"},
                {&k.attn[2], "slm_attn_part_4"}, {&k.attn[3], "slm_attn_part_8"},
                {&k.attn[4], "slm_attn_part_16"}};
-    for (auto& f : fns) TRY(get_fn(c, f.f, f.n));
+    for (auto& f : fns) {
+        TRY(get_fn(c, f.f, f.n));
+        c->fname[*f.f] = f.n;
+    }
     return SLM_OK;
 }
 
@@ -1539,6 +1608,8 @@ void slm_hip_close(slm_hip* c) {
     if (c->ws) hipFree(c->ws);
     if (c->part) hipFree(c->part);
     if (c->gpart) hipFree(c->gpart);
+    collect_timing(c);
+    for (auto e : c->ev_pool) hipEventDestroy(e);
     if (c->stage_dev) hipFree(c->stage_dev);
     if (c->dyn_dev) hipFree(c->dyn_dev);
     if (c->stage_host) hipHostFree(c->stage_host);
@@ -1660,6 +1731,26 @@ int slm_hip_graph_stats(slm_hip* c, uint64_t* launched, uint64_t* captured, uint
     if (launched) *launched = c->n_launched;
     if (captured) *captured = c->n_captured;
     if (eager) *eager = c->n_eager;
+    return SLM_OK;
+}
+
+int slm_hip_set_timing(slm_hip* c, int on) {
+    if (!c) return SLM_E_INVALID;
+    TRY(collect_timing(c));
+    c->timing = on != 0;
+    c->kstats.clear();
+    return SLM_OK;
+}
+
+int slm_hip_kernel_stat(slm_hip* c, const char* name, long long* launches, double* us,
+                        double* bytes) {
+    if (!c || !name) return SLM_E_INVALID;
+    TRY(collect_timing(c));
+    auto it = c->kstats.find(name);
+    KStat k = it == c->kstats.end() ? KStat{} : it->second;
+    if (launches) *launches = k.launches;
+    if (us) *us = 1e3 * k.ms;
+    if (bytes) *bytes = k.bytes;
     return SLM_OK;
 }
 

@@ -2,7 +2,7 @@
 the reference's PyTorch fixture and against the oracle (src/cpu.rs + src/model.rs
 restated), on the reference's own fixture and on seeded synthetic models.
 
-Bars (the north star's): per-position logits within 1e-4 relative (‖g − c‖∞ / ‖c‖∞) of the
+Bars: per-position logits within 1e-4 relative (‖g − c‖∞ / ‖c‖∞) of the
 CPU path, identical greedy token ids, and identical ring state (every buffer the model
 keeps across steps, model.rs:626-638) after a chunked prompt and after the same prompt
 token by token.
