@@ -1174,7 +1174,7 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
         f4 wa[SLM_KS], wb[SLM_KS];
         int u = blockIdx.x;
         fg_load(d, u, wave, i, g, wa);
-        fg_load(d, u + G, wave, i, g, wb);
+        if (u + G < d.units) fg_load(d, u + G, wave, i, g, wb);  // (a second unit only if any)
         __syncthreads();  // the prologue's vectors are in LDS
         for (int k = 0; k < d.nvp; k++)
             if (first || !d.vp[k].wg0) vp_run(d.vp[k], lds, misc, k, tid, (int)blockDim.x);
@@ -1188,7 +1188,7 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
             u += 2 * G;
             if (u >= d.units) break;
             fg_load(d, u, wave, i, g, wa);
-            fg_load(d, u + G, wave, i, g, wb);
+            if (u + G < d.units) fg_load(d, u + G, wave, i, g, wb);
         }
         return;
     }
