@@ -7,7 +7,7 @@
 //     first unit at once, then runs the canonical MFMA chain of its slice for every unit
 //     of the workgroup, the loads of the next unit in flight while one unit computes;
 //   - prologue/epilogue waves: they load every global vector the kernel reads into LDS,
-//     run the prologue (the step's element-wise ops, rms, the attention combine, the
+//     run the prologue (the step's element-wise ops, rms, the
 //     fold of a split linear's partials, rope-table rows, the embedding row) that makes
 //     the GEMV input, then, per unit, add the slice partials in order and run the
 //     epilogue (residual add, rope + ring store, SiLU of the gate/amp pair).
@@ -36,7 +36,6 @@ enum {
     VP_MIX,         // out = in0 + f·(in1 − in0)
     VP_SCALE,       // out = in0 · factor (dyn[0] as f32 bits, else f)
     VP_RMS,         // out = rms(in0) · lds[w], eps f
-    VP_COMBINE,     // out = attention combine of the partials (lds[w], or `part`), heads × dh
     VP_SILU,        // out = in1 · in0 / (1 + e^−in0)   (silu_mul with g = in0, u = in1)
     VP_FOLD,        // out = ((P0 + P1) + P2) + ...: the splits of a linear, lds[w] [nsb][n]
 };

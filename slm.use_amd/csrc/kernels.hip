@@ -774,7 +774,8 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
                                const float* __restrict__ kc, const float* __restrict__ vc,
                                const long long* __restrict__ dyn, long long pos_imm, int m,
                                long long reach, long long gap, long long cap, int heads,
-                               int key_heads, int dh, float scale, int wpp) {
+                               int key_heads, int dh, float scale, int wpp,
+                               float* __restrict__ y, int* __restrict__ ctr) {
     constexpr int DP = 16 * DT;
     constexpr int NT = 64 * SLM_SB_SEGS;
     extern __shared__ float lds[];  // [wpp][16][DP + 2] folds, then [waves][16][DP + 4] values
@@ -844,13 +845,83 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
             if (c2.valid && dd < dh) {
                 float* P = part + (((long long)blockIdx.z * m + c2.qidx) * heads + c2.head) *
                                       (long long)(DP + 2);
-                if (dd == 0) {
-                    P[0] = FM[u];
-                    P[1] = FL[u];
+                if (ctr) {  // written through to where every workgroup's loads see it
+                    if (dd == 0) {
+                        __hip_atomic_store(P, FM[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(P + 1, FL[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    __hip_atomic_store(P + 2 + dd, FO[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    if (dd == 0) {
+                        P[0] = FM[u];
+                        P[1] = FL[u];
+                    }
+                    P[2 + dd] = FO[u];
                 }
-                P[2 + dd] = FO[u];
             }
         }
+    }
+    if (!ctr) return;
+    // The last workgroup of this (query tile, key head) to finish combines its superblocks
+    // (the expressions of slm_attn_combine). Each workgroup's partial stores have completed
+    // before it counts itself in; the combining workgroup reads them with loads that see
+    // memory, not a stale cache line, and puts the counter back to zero for the next launch.
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ int last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int* c = ctr + (long long)blockIdx.x * gridDim.y + blockIdx.y;
+        int before = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = before == (int)gridDim.z - 1;
+        if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    // one invalidate of this workgroup's stale cache lines, then ordinary loads, eight
+    // superblocks in flight at a time
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    int nsb = (int)gridDim.z;
+    long long stride = (long long)m * heads * (DP + 2);
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        int t = threadIdx.x + NT * u;
+        if (t >= 16 * DP) continue;
+        int cc = t / DP, dd = t % DP;
+        Col c2 = column(cc, blockIdx.x, pos, m, reach, gap, group, qpt, kvh);
+        if (!c2.valid || dd >= dh) continue;
+        const float* P = part + (c2.qidx * heads + c2.head) * (long long)(DP + 2);
+        float M = NEG_INF;
+        for (int z0 = 0; z0 < nsb; z0 += 8) {
+            float lz[8], mz[8];
+#pragma unroll
+            for (int v = 0; v < 8; v++) {  // past the last superblock: reads the last again
+                int z = min(z0 + v, nsb - 1);
+                lz[v] = P[z * stride + 1];
+                mz[v] = P[z * stride];
+            }
+#pragma unroll
+            for (int v = 0; v < 8; v++)
+                if (z0 + v < nsb && lz[v] > 0.0f) M = fmaxf(M, mz[v]);
+        }
+        float L = 0.0f, O = 0.0f;
+        for (int z0 = 0; z0 < nsb; z0 += 8) {
+            float lz[8], mz[8], oz[8];
+#pragma unroll
+            for (int v = 0; v < 8; v++) {
+                const float* Q = P + min(z0 + v, nsb - 1) * stride;
+                lz[v] = Q[1];
+                mz[v] = Q[0];
+                oz[v] = Q[2 + dd];
+            }
+#pragma unroll
+            for (int v = 0; v < 8; v++)
+                if (z0 + v < nsb && lz[v] > 0.0f) {
+                    float w = expf(mz[v] - M);
+                    L = L + lz[v] * w;
+                    O = O + oz[v] * w;
+                }
+        }
+        y[(c2.qidx * heads + c2.head) * (long long)dh + dd] = L > 0.0f ? O / L : 0.0f;
     }
 }
 
@@ -858,9 +929,10 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
     KERNEL void __launch_bounds__(64 * SLM_SB_SEGS) slm_attn_part_##DT(                               \
         float* part, const float* q, const float* kc, const float* vc,                   \
         const long long* dyn, long long pos_imm, int m, long long reach, long long gap,  \
-        long long cap, int heads, int key_heads, int dh, float scale, int wpp) {         \
+        long long cap, int heads, int key_heads, int dh, float scale, int wpp, float* y,  \
+        int* ctr) {                                                                      \
         attn_part_body<DT>(part, q, kc, vc, dyn, pos_imm, m, reach, gap, cap, heads,      \
-                           key_heads, dh, scale, wpp);                                   \
+                           key_heads, dh, scale, wpp, y, ctr);                           \
     }
 ATTN_PART(1)
 ATTN_PART(2)
@@ -870,8 +942,8 @@ ATTN_PART(16)
 
 // y[qidx][head][dim] from the nsb superblock partials: with M the largest m of the
 // superblocks that saw a key, w_z = e^(m_z − M), L = Σ l_z·w_z and O = Σ o_z·w_z (both in
-// superblock order), y = O / L (0 when the query sees nothing, cpu.rs:378-382). The fused
-// decode prologue (VP_COMBINE) computes the same expressions.
+// superblock order), y = O / L (0 when the query sees nothing, cpu.rs:378-382). The last
+// workgroup of an attention launch that combines itself computes the same expressions.
 KERNEL void slm_attn_combine(float* __restrict__ y, const float* __restrict__ part, int m,
                              int heads, int dh, int dp, int nsb) {
     long long n = (long long)m * heads * dh;
@@ -960,87 +1032,31 @@ __device__ __forceinline__ float dot16_lanes0(const float* in, int size, int l) 
     return s + tail;
 }
 
-// One prologue operation on LDS vectors, run by every thread of the workgroup (the GEMV
-// waves' weights are in flight meanwhile; nothing here touches global memory, so their
-// loads never hold it up). Element c of every element-wise op is computed by the same
-// thread, so an op that reads element c of an earlier op's output follows it without a
-// barrier; one that reads it at an offset (`sync`), rms and the combine wait for the other
-// threads. misc[0]: the rms factor; misc[4 + k]:
-// the dynamic factor of op k.
-__device__ void vp_run(const VpOp& o, float* lds, const float* misc, int k, int tid, int nt) {
+// One prologue operation on LDS vectors, run by the prologue waves (threads tid of nt)
+// while the GEMV waves' weights stream in; nothing here touches global memory. Element c
+// of every element-wise op is computed by the same thread, so an op that reads element c
+// of an earlier op's output follows it without a barrier; one that reads it at an offset
+// (`sync`), rms and the combine wait for the other prologue waves (`bar`). misc[0]: the
+// rms factor; misc[4 + k]: the dynamic factor of op k.
+template <typename Bar>
+__device__ void vp_run(const VpOp o, float* lds, const float* misc, int k, int tid, int nt,
+                       Bar& bar) {
     int n = o.n;
     const float* a = lds + o.in0;
     const float* b = o.in1 >= 0 ? lds + o.in1 : nullptr;
     float* out = o.out >= 0 ? lds + o.out : nullptr;
-    if (o.sync) __syncthreads();
+    if (o.sync) bar();
     switch (o.kind) {
         case VP_RMS: {  // rms (cpu.rs:187-207) of one group; a and out may not alias
-            __syncthreads();  // the input may come from other threads
+            bar();  // the input may come from other threads
             if (tid < 64) {
                 float d = dot16_lanes0(a, n, tid & 15);
                 if (tid == 0) ((float*)misc)[0] = 1.0f / sqrtf(d / (float)n + o.f);
             }
-            __syncthreads();
+            bar();
             float r = misc[0];
             const float* wt = lds + o.w;
             for (int c = tid; c < n; c += nt) out[c] = a[c] * r * wt[c];
-            break;
-        }
-        case VP_COMBINE: {  // slm_attn_combine for one query; lds[in1]: [heads][nsb] weights
-            int rec = o.dp + 2, stride = rec * o.heads;
-            const float* P = lds + o.w;
-            float* wz = lds + o.in1;
-            for (int t = tid; t < o.heads * o.nsb; t += nt) {  // w_z of each head
-                int h = t / o.nsb, z = t % o.nsb;
-                float M = NEG_INF;
-                int q = 0;
-                for (; q + 4 <= o.nsb; q += 4) {
-                    float l4[4], m4[4];
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        l4[u] = P[(q + u) * stride + h * rec + 1];
-                        m4[u] = P[(q + u) * stride + h * rec];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 4; u++)
-                        if (l4[u] > 0.0f) M = fmaxf(M, m4[u]);
-                }
-                for (; q < o.nsb; q++)
-                    if (P[q * stride + h * rec + 1] > 0.0f) M = fmaxf(M, P[q * stride + h * rec]);
-                wz[t] = expf(P[z * stride + h * rec] - M);
-            }
-            __syncthreads();
-            for (int c = tid; c < n; c += nt) {
-                int h = c / o.dh, e = c % o.dh;
-                float L = 0.0f, O = 0.0f;
-                int z = 0;
-                for (; z + 4 <= o.nsb; z += 4) {
-                    float l4[4], w4[4], o4[4];
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        int at = (z + u) * stride + h * rec;
-                        l4[u] = P[at + 1];
-                        w4[u] = wz[h * o.nsb + z + u];
-                        o4[u] = P[at + 2 + e];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 4; u++)
-                        if (l4[u] > 0.0f) {
-                            L = L + l4[u] * w4[u];
-                            O = O + o4[u] * w4[u];
-                        }
-                }
-                for (; z < o.nsb; z++) {
-                    int at = z * stride + h * rec;
-                    float l = P[at + 1];
-                    if (l > 0.0f) {
-                        float w = wz[h * o.nsb + z];
-                        L = L + l * w;
-                        O = O + P[at + 2 + e] * w;
-                    }
-                }
-                out[c] = L > 0.0f ? O / L : 0.0f;
-            }
             break;
         }
         case VP_FOLD: {  // slm_fold: the splits of a linear added in order
@@ -1098,40 +1114,51 @@ __device__ __forceinline__ long long fg_row(const FgSeg& s, int t, int i) {
 // Sixteen zero bytes: what a lane past the end of a weight matrix loads.
 __device__ __attribute__((aligned(16))) float slm_zero16[4];
 
-// The weights of slice `sl` of one unit for this lane: four float4s. Lanes past the matrix
-// load zeros from slm_zero16, so the loads are always four and their results are used
-// as they arrive, without a select that would wait for them.
-__device__ __forceinline__ void fg_load(const FgDesc& d, int u, int wave, int i, int g, f4 (&wa)[SLM_KS]) {
-    int kblocks = d.cols >> 4;
-    bool live = u < d.units;
-    FgUnit un = fg_unit(d, live ? u : 0);
+// Where one GEMV lane's weights of unit u come from, worked out once per unit: the
+// lane's row start (or the zero page), the first 16-column block of its slice and how
+// many of the slice's four blocks lie inside the matrix (0: the slice is past the end).
+struct FgLane {
+    const float* base;
+    int kb0, nkb;
+};
+
+__device__ __forceinline__ FgLane fg_lane(const FgDesc& d, int u, int wave, int i, int g) {
+    FgLane p{slm_zero16, 0, 0};
+    if (u >= d.units) return p;
+    FgUnit un = fg_unit(d, u);
     const FgSeg& s = d.seg[un.seg];
     int sl = un.split * SLM_SPLIT + wave;
+    int kblocks = (d.cols + 15) >> 4;
+    if (sl >= d.nsl) return p;
+    p.kb0 = sl * SLM_KS;
+    p.nkb = min(SLM_KS, kblocks - p.kb0);
     long long row = fg_row(s, un.tile, i);
-    bool ok = live && sl < d.nsl && row < s.rows;
-    const float* base = s.w + (ok ? row : 0) * d.cols + 4 * g;
+    if (row < s.rows) p.base = s.w + row * d.cols + 4 * g;
+    return p;
+}
+
+// The weights of one unit's slice for this lane: four float4s. Lanes past the matrix load
+// zeros from slm_zero16, so the loads are always four and their results are used as they
+// arrive, without a select that would wait for them.
+__device__ __forceinline__ void fg_load(const FgLane& p, f4 (&wa)[SLM_KS]) {
+    bool ok = p.base != slm_zero16;
 #pragma unroll
     for (int q = 0; q < SLM_KS; q++) {
-        int kb = sl * SLM_KS + q;
-        const float* src = ok && kb < kblocks ? base + kb * 16 : slm_zero16;
+        const float* src = ok && q < p.nkb ? p.base + (p.kb0 + q) * 16 : slm_zero16;
         wa[q] = gld((const f4*)src);
     }
 }
 
-// The canonical chain of slice `wave` of unit u; lanes of row 0 of B hold the token.
-__device__ __forceinline__ void fg_chain(const FgDesc& d, int u, int wave, int i, int g,
-                                         const f4 (&wa)[SLM_KS], const float* xin, float* out) {
-    int kblocks = d.cols >> 4;
-    FgUnit cur = fg_unit(d, u);
-    int sl = cur.split * SLM_SPLIT + wave;
-    if (sl >= d.nsl) return;
+// The canonical chain of the lane's slice; lanes of row 0 of B hold the token.
+__device__ __forceinline__ void fg_chain(const FgLane& p, int i, int g, const f4 (&wa)[SLM_KS],
+                                         const float* xin, float* out) {
+    if (p.nkb <= 0) return;
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < SLM_KS; q++) {
-        int kb = sl * SLM_KS + q;
-        if (kb < kblocks) {
+        if (q < p.nkb) {
             f4 xb = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (i == 0) xb = *(const f4*)(xin + kb * 16 + 4 * g);
+            if (i == 0) xb = *(const f4*)(xin + (p.kb0 + q) * 16 + 4 * g);
 #pragma unroll
             for (int e = 0; e < 4; e++) acc = mfma4(wa[q][e], xb[e], acc);
         }
@@ -1150,11 +1177,11 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
     static_assert(sizeof(FgDesc) % 16 == 0, "descriptor copy in float4s");
     for (int q = threadIdx.x; q < (int)(sizeof(FgDesc) / 16); q += blockDim.x)
         ((f4*)&d)[q] = ((const f4*)&dk)[q];
-    if (threadIdx.x < 2) ((int*)(lds + dk.lds_vp + 28))[threadIdx.x] = 0;
+    if (threadIdx.x < 3) ((int*)(lds + dk.lds_vp + 28))[threadIdx.x] = 0;
     __syncthreads();
     float* misc = lds + d.lds_vp;   // 32 floats, then the prefetch table (SLM_FG_MISC)
     float* foldb = lds + d.fold_off;  // [2 rounds][2 units][W][16]
-    int* sync_ctr = (int*)(misc + 28);  // the prologue waves' barrier; misc + 29: loads issued
+    int* sync_ctr = (int*)(misc + 28);  // the prologue waves' barrier; +1: loads issued; +2: x ready
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int W = d.W;
     bool first = blockIdx.x == 0;
@@ -1173,22 +1200,27 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
         }
         f4 wa[SLM_KS], wb[SLM_KS];
         int u = blockIdx.x;
-        fg_load(d, u, wave, i, g, wa);
-        if (u + G < d.units) fg_load(d, u + G, wave, i, g, wb);  // (a second unit only if any)
-        __syncthreads();  // the prologue's vectors are in LDS
-        for (int k = 0; k < d.nvp; k++)
-            if (first || !d.vp[k].wg0) vp_run(d.vp[k], lds, misc, k, tid, (int)blockDim.x);
-        __syncthreads();  // the prologue is done: x is in LDS
+        FgLane pa = fg_lane(d, u, wave, i, g), pb = fg_lane(d, u + G, wave, i, g);
+        fg_load(pa, wa);
+        if (u + G < d.units) fg_load(pb, wb);  // (a second unit only if any)
+        // x is in LDS once the prologue waves say so (they ran the prologue meanwhile)
+        for (int it = 0; it < (1 << 24); it++) {
+            if (__hip_atomic_load(sync_ctr + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > 0) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         const float* xin = lds + d.xin;
         for (int par = 0;; par ^= 1) {  // rounds alternate between two halves of foldb
             float* fb = foldb + par * 2 * W * 16;
-            fg_chain(d, u, wave, i, g, wa, xin, fb + wave * 16);
-            if (u + G < d.units) fg_chain(d, u + G, wave, i, g, wb, xin, fb + (W + wave) * 16);
+            fg_chain(pa, i, g, wa, xin, fb + wave * 16);
+            fg_chain(pb, i, g, wb, xin, fb + (W + wave) * 16);
             __syncthreads();
             u += 2 * G;
             if (u >= d.units) break;
-            fg_load(d, u, wave, i, g, wa);
-            if (u + G < d.units) fg_load(d, u + G, wave, i, g, wb);
+            pa = fg_lane(d, u, wave, i, g);
+            pb = fg_lane(d, u + G, wave, i, g);
+            fg_load(pa, wa);
+            if (u + G < d.units) fg_load(pb, wb);
         }
         return;
     }
@@ -1233,10 +1265,11 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
     if (d.pf4 > 0 && ptid >= d.pf4 && lane == 0)  // a wave with no loads of its own
         __hip_atomic_fetch_add(sync_ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (has_sf) misc[4 + ptid] = sf;
-    __syncthreads();  // the prologue's vectors are in LDS
+    sync();  // the prologue's vectors are in LDS
     for (int k = 0; k < d.nvp; k++)
-        if (first || !d.vp[k].wg0) vp_run(d.vp[k], lds, misc, k, tid, (int)blockDim.x);
-    __syncthreads();  // x is ready for the GEMV waves
+        if (first || !d.vp[k].wg0) vp_run(d.vp[k], lds, misc, k, ptid, pnt, sync);
+    sync();  // x is ready: the GEMV waves may go
+    if (ptid == 0) __hip_atomic_fetch_add(sync_ctr + 2, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (first) {  // workgroup 0 writes out what the prologue made that later ops read
         for (int k = 0; k < d.nvp; k++) {
             const VpOp& o = d.vp[k];
@@ -1258,7 +1291,7 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
             int u = u0 + h * gridDim.x;
             if (ptid >= 16 || u >= d.units) continue;
             FgUnit cur = fg_unit(d, u);
-            const FgSeg& sg = d.seg[cur.seg];
+            const FgSeg sg = d.seg[cur.seg];
             long long R = fg_row(sg, cur.tile, r);
             if (R >= sg.rows || sg.nsplit > 1) continue;
             if (sg.epi == EPI_RESID) res[h] = gld(sg.res + R);
@@ -1274,7 +1307,7 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
             int u = u0 + h * gridDim.x;
             if (u >= d.units) break;
             FgUnit cur = fg_unit(d, u);
-            const FgSeg& sg = d.seg[cur.seg];
+            const FgSeg sg = d.seg[cur.seg];
             float v = 0.0f;
             if (ptid < 16) {  // the split's slice partials, read at once, added in order
                 int nsl = min(SLM_SPLIT, d.nsl - cur.split * SLM_SPLIT);

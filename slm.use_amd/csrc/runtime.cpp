@@ -44,7 +44,7 @@ constexpr size_t MAX_GRAPHS = 8;
 constexpr int VP_LEN_MAX = 4096;          // longest vector a fused prologue holds
 constexpr int LDS_MAX = 163840;            // gfx950: 160 KB of LDS per workgroup
 constexpr int FG_GRID_MAX = 256;           // workgroups of a fused GEMV: one per compute unit
-constexpr int64_t COMBINE_LDS_MAX = 24576; // attention partials a fused prologue holds in LDS
+constexpr int64_t ATTN_CTR_MAX = 65536;   // (query tile, key head) pairs one attention launch combines itself
 constexpr int ATTN_LDS_MAX = LDS_MAX;
 
 enum OpKind : uint32_t {
@@ -116,6 +116,7 @@ struct slm_hip {
     std::map<uintptr_t, size_t> allocs;  // live allocations: start -> bytes
     float* ws = nullptr;                 // attention partials
     size_t ws_bytes = 0;
+    int* attn_ctr = nullptr;             // [ATTN_CTR_MAX] finished superblocks per (query tile, key head)
     float* part = nullptr;               // split partials of fused one-token linears (two halves)
     size_t part_bytes = 0;
     float* gpart = nullptr;              // split partials of prompt GEMMs
@@ -449,13 +450,18 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int64_t wpp = SLM_SB_SEGS;
             while (wpp > 1 && shm(wpp) > ATTN_LDS_MAX) wpp /= 2;
             int64_t qpt = 16 / (heads / kh);
-            out.push_back(mk(k.attn[dti], (uint32_t)((m + qpt - 1) / qpt), (uint32_t)kh, (uint32_t)nsb,
+            int64_t qtiles = (m + qpt - 1) / qpt;
+            // the last workgroup of each (query tile, key head) combines the superblocks itself
+            // when its counter fits; otherwise slm_attn_combine runs after
+            bool self = qtiles * kh <= ATTN_CTR_MAX;
+            out.push_back(mk(k.attn[dti], (uint32_t)qtiles, (uint32_t)kh, (uint32_t)nsb,
                              64 * SLM_SB_SEGS, (uint32_t)shm(wpp), c->ws, p[1], p[2], p[3],
                              (const long long*)o.dyn, (long long)n[0], (int)m, (long long)n[2],
                              (long long)n[3], (long long)n[4], (int)heads, (int)kh, (int)dh, o.f[0],
-                             (int)wpp));
-            out.push_back(mk(k.combine, blocks_for(m * heads * dh), 1, 1, 256, 0, p[0],
-                             (const float*)c->ws, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
+                             (int)wpp, self ? p[0] : (float*)nullptr, self ? c->attn_ctr : (int*)nullptr));
+            if (!self)
+                out.push_back(mk(k.combine, blocks_for(m * heads * dh), 1, 1, 256, 0, p[0],
+                                 (const float*)c->ws, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
             return SLM_OK;
         }
     }
@@ -476,7 +482,7 @@ bool overlap(const Range& x, const Range& y) { return x.a < y.b && y.a < x.b; }
 
 // An element-wise one-token op as prologue material: what it reads and writes.
 enum { SRC_COPY = 1, SRC_ADD, SRC_MIX, SRC_SCALE, SRC_GATHER, SRC_RMS, SRC_ROPE_TABLE, SRC_SILU,
-       SRC_COMBINE, SRC_FOLD };
+       SRC_FOLD };
 struct VpSrc {
     int kind = 0;
     int n = 0;
@@ -533,7 +539,6 @@ bool vp_of(const Op& o, VpSrc* v) {
     return v->n > 0 && v->n <= VP_LEN_MAX && v->n % 4 == 0;
 }
 
-int combine_dp(int64_t dh) { return 16 << pow2_index((dh + 15) / 16, 4); }
 
 // What an op reads and writes, in bytes of device memory (ring and state updates count as
 // both). The embedding table and the rope tables are only ever read.
@@ -712,13 +717,7 @@ struct Planner {
 
     int flush_pending() {
         for (auto& v : pend) {
-            if (v.kind == SRC_COMBINE) {
-                const Op& o = *v.op;
-                int64_t heads = o.n[5], dh = o.n[7], nsb = o.n[8];
-                out.push_back(mk(c->k.combine, blocks_for(heads * dh), 1, 1, 256, 0, o.p[0],
-                                 (const float*)c->ws, 1, (int)heads, (int)dh, combine_dp(dh),
-                                 (int)nsb));
-            } else if (v.kind == SRC_FOLD) {
+            if (v.kind == SRC_FOLD) {
                 out.push_back(mk(c->k.fold, blocks_for(v.n), 1, 1, 256, 0, v.out[0], v.in[0],
                                  (long long)v.n, v.nsplit));
             } else {
@@ -784,22 +783,6 @@ struct Planner {
                 b.writes.push_back(rng0(v.out[0], v.n));
                 b.writes.push_back(rng0(v.out[1], v.n));
                 return true;
-            }
-            case SRC_COMBINE: {
-                int64_t heads = so.n[5], dh = so.n[7], nsb = so.n[8];
-                int dp = combine_dp(dh);
-                int64_t pn = nsb * heads * (dp + 2);
-                o.kind = VP_COMBINE;
-                o.heads = (int32_t)heads;
-                o.dh = (int32_t)dh;
-                o.dp = dp;
-                o.nsb = (int32_t)nsb;
-                if (pn > COMBINE_LDS_MAX) return false;
-                o.part = c->ws;
-                o.in1 = b.alloc((int)(heads * nsb));  // the superblock weights
-                b.reads.push_back(rng(c->ws, pn));
-                if (!b.prefetch(c->ws, (int)pn, nullptr, 0, &o.w)) return false;
-                break;
             }
             case SRC_FOLD: {
                 o.kind = VP_FOLD;
@@ -1250,23 +1233,6 @@ struct Planner {
                 }
             }
             TRY(flush_l2());
-            if (fuse && o.kind == OP_ATTEND && o.n[1] == 1) {
-                std::vector<Rec> two;
-                TRY(lower_one(c, o, two));
-                out.push_back(two[0]);  // the partials; the combine waits for the next linear
-                VpSrc cv;
-                cv.kind = SRC_COMBINE;
-                cv.n = (int)(o.n[5] * o.n[7]);
-                cv.out[0] = o.p[0];
-                cv.op = &o;
-                int64_t pn = o.n[8] * o.n[5] * (combine_dp(o.n[7]) + 2);
-                if (cv.n % 4 == 0 && cv.n <= VP_LEN_MAX && pn <= COMBINE_LDS_MAX)
-                    pend.push_back(cv);
-                else
-                    out.push_back(two[1]);
-                i++;
-                continue;
-            }
             TRY(lower_one(c, o, out));
             i++;
         }
@@ -1583,6 +1549,8 @@ int slm_hip_open(int device, slm_hip** out) {
     OPEN_HIP(hipHostMalloc((void**)&c->bounce, BOUNCE_CAP, hipHostMallocDefault));
     c->ws_bytes = 1 << 20;
     OPEN_HIP(hipMalloc((void**)&c->ws, c->ws_bytes));
+    OPEN_HIP(hipMalloc((void**)&c->attn_ctr, ATTN_CTR_MAX * sizeof(int)));
+    OPEN_HIP(hipMemset(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int)));
     c->dyn.reserve(DYN_CAP);
     c->ops.reserve(4096);
     c->plan_trace = getenv("SLM_HIP_PLAN_TRACE") != nullptr;
@@ -1606,6 +1574,7 @@ void slm_hip_close(slm_hip* c) {
     }
     for (auto& a : c->allocs) hipFree((void*)a.first);
     if (c->ws) hipFree(c->ws);
+    if (c->attn_ctr) hipFree(c->attn_ctr);
     if (c->part) hipFree(c->part);
     if (c->gpart) hipFree(c->gpart);
     collect_timing(c);
