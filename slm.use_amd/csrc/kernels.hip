@@ -994,7 +994,6 @@ __device__ __forceinline__ void esync(int* ctr, int& target, int nw) {
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     for (int it = 0; it < (1 << 24); it++) {
         if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
-        __builtin_amdgcn_s_sleep(1);
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
@@ -1005,10 +1004,12 @@ struct ESync {
     __device__ __forceinline__ void operator()() { esync(ctr, target, nw); }
 };
 
-// Sum of squares of in[0..size) in the order of dot16_self, run by lanes 0..15 of one
-// wave: each lane's 16 partial sums in registers, the lane totals added left to right
-// through readlane.
-__device__ __forceinline__ float dot16_lanes0(const float* in, int size, int l) {
+// Sum of squares of in[0..size) in the order of dot16_self, run by one wave: lane l and
+// lane l + 16k keep the same running sum of elements l, l + 16, ... (sixteen loads in
+// flight), then the sixteen sums are added left to right through readlane, so every lane
+// returns the same value.
+__device__ __forceinline__ float dot16_wave(const float* in, int size, int lane) {
+    int l = lane & 15;
     int chunks = size / 16;
     float acc = 0.0f;
     int c = 0;
@@ -1032,60 +1033,157 @@ __device__ __forceinline__ float dot16_lanes0(const float* in, int size, int l) 
     return s + tail;
 }
 
-// One prologue operation on LDS vectors, run by the prologue waves (threads tid of nt)
-// while the GEMV waves' weights stream in; nothing here touches global memory. Element c
-// of every element-wise op is computed by the same thread, so an op that reads element c
-// of an earlier op's output follows it without a barrier; one that reads it at an offset
-// (`sync`), rms and the combine wait for the other prologue waves (`bar`). misc[0]: the
-// rms factor; misc[4 + k]: the dynamic factor of op k.
-template <typename Bar>
-__device__ void vp_run(const VpOp o, float* lds, const float* misc, int k, int tid, int nt,
-                       Bar& bar) {
+// The prologue's element-wise ops, one loop per kind so each compiles to its own
+// straight-line code (the expressions of the per-op kernels). Every lane reads all its
+// float4s of a 1024-element chunk before it writes any.
+template <int KIND>
+__device__ __forceinline__ float vp_elem(float a, float b, float f, float r) {
+    if (KIND == VP_COPY) return a;
+    if (KIND == VP_ADD) return a + b;
+    if (KIND == VP_MIX) return a + f * (b - a);
+    if (KIND == VP_SCALE) return a * f;
+    if (KIND == VP_RMS) return a * r * b;  // b: the rms weight
+    return b * a / (1.0f + expf(-a));      // VP_SILU: g = a, u = b
+}
+
+template <int KIND>
+__device__ __forceinline__ void vp_map4(const f4* a, const f4* b, f4* out, int n4, float f,
+                                        float r, int tid, int nt) {
+    for (int c0 = tid; c0 < n4; c0 += 4 * nt) {
+        f4 A[4], B[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {  // past the end: reads the last float4 again
+            int c = min(c0 + nt * j, n4 - 1);
+            A[j] = a[c];
+            if (KIND != VP_COPY && KIND != VP_SCALE) B[j] = b[c];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int c = c0 + nt * j;
+            if (c >= n4) break;
+            f4 v;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = vp_elem<KIND>(A[j][e], B[j][e], f, r);
+            out[c] = v;
+        }
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void vp_map1(const float* a, const float* b, float* out, int n,
+                                        float f, float r, int tid, int nt) {
+    for (int c0 = tid; c0 < n; c0 += 4 * nt) {
+        float A[4], B[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int c = min(c0 + nt * j, n - 1);
+            A[j] = a[c];
+            if (KIND != VP_COPY && KIND != VP_SCALE) B[j] = b[c];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int c = c0 + nt * j;
+            if (c >= n) break;
+            out[c] = vp_elem<KIND>(A[j], B[j], f, r);
+        }
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void vp_map(const float* a, const float* b, float* out, int n,
+                                       bool v4, float f, float r, int tid, int nt) {
+    if (v4) vp_map4<KIND>((const f4*)a, (const f4*)b, (f4*)out, n >> 2, f, r, tid, nt);
+    else vp_map1<KIND>(a, b, out, n, f, r, tid, nt);
+}
+
+// slm_fold in LDS: out[c] = ((P0[c] + P1[c]) + P2[c]) + ..., parts [nsplit][n]; all the
+// splits of a float4 are read before the sums.
+__device__ __forceinline__ void vp_fold(const float* part, float* out, int n, int nsplit,
+                                        bool v4, int tid, int nt) {
+    constexpr int ZMAX = 8;
+    if (v4 && nsplit <= ZMAX) {
+        int n4 = n >> 2;
+        const f4* p4 = (const f4*)part;
+        for (int c0 = tid; c0 < n4; c0 += 2 * nt) {
+            f4 P[2][ZMAX];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int z = 0; z < ZMAX; z++)
+                    if (z < nsplit) P[j][z] = p4[z * n4 + min(c0 + nt * j, n4 - 1)];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                int c = c0 + nt * j;
+                if (c >= n4) break;
+                f4 v = P[j][0];
+#pragma unroll
+                for (int z = 1; z < ZMAX; z++)
+                    if (z < nsplit) v = v + P[j][z];
+                ((f4*)out)[c] = v;
+            }
+        }
+        return;
+    }
+    for (int c = tid; c < n; c += nt) {
+        float v = part[c];
+        for (int z = 1; z < nsplit; z++) v = v + part[z * n + c];
+        out[c] = v;
+    }
+}
+
+// Whether an op runs on float4s: its length and every vector offset a multiple of four.
+__device__ __forceinline__ bool vp_v4(const VpOp& o) {
+    return ((o.in0 | (o.in1 >= 0 ? o.in1 : 0) | (o.out >= 0 ? o.out : 0) | (o.w >= 0 ? o.w : 0) |
+             o.n) & 3) == 0;
+}
+
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// An op read from the descriptor in LDS, its fields made wave-uniform (they are), so its
+// tests compile to scalar branches.
+__device__ __forceinline__ VpOp vp_load(const VpOp& src) {
+    VpOp o = src;
+    o.kind = uni(o.kind);
+    o.n = uni(o.n);
+    o.wg0 = uni(o.wg0);
+    o.out = uni(o.out);
+    o.in0 = uni(o.in0);
+    o.in1 = uni(o.in1);
+    o.w = uni(o.w);
+    o.nsb = uni(o.nsb);
+    o.sync = uni(o.sync);
+    o.f = __int_as_float(uni(__float_as_int(o.f)));
+    return o;
+}
+
+// One prologue operation on LDS vectors, run by the prologue waves (thread tid of nt)
+// while the GEMV waves' weights stream in. Thread tid owns float4s (or, for an op that is
+// not float4-aligned, elements) tid, tid + nt, ... of every vector, so an element-wise op
+// that reads what an earlier op of the same kind of layout wrote needs no barrier; the
+// caller puts one before an op that reads other threads' elements. rms sums the whole
+// input in every wave (the same sum), so its factor needs no barrier either. `f` is the
+// op's factor (the dynamic one of a VP_SCALE already read).
+__device__ void vp_run(const VpOp& o, float* lds, float f, int tid, int nt) {
+    if (o.out < 0) return;  // a copy whose source slot is written out as it is
     int n = o.n;
     const float* a = lds + o.in0;
-    const float* b = o.in1 >= 0 ? lds + o.in1 : nullptr;
-    float* out = o.out >= 0 ? lds + o.out : nullptr;
-    if (o.sync) bar();
+    const float* b = lds + (o.in1 >= 0 ? o.in1 : o.w >= 0 ? o.w : o.in0);
+    float* out = lds + o.out;
+    bool v4 = vp_v4(o);
     switch (o.kind) {
-        case VP_RMS: {  // rms (cpu.rs:187-207) of one group; a and out may not alias
-            bar();  // the input may come from other threads
-            if (tid < 64) {
-                float d = dot16_lanes0(a, n, tid & 15);
-                if (tid == 0) ((float*)misc)[0] = 1.0f / sqrtf(d / (float)n + o.f);
-            }
-            bar();
-            float r = misc[0];
-            const float* wt = lds + o.w;
-            for (int c = tid; c < n; c += nt) out[c] = a[c] * r * wt[c];
+        case VP_COPY: vp_map<VP_COPY>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_ADD: vp_map<VP_ADD>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_MIX: vp_map<VP_MIX>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_SCALE: vp_map<VP_SCALE>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_SILU: vp_map<VP_SILU>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_FOLD: vp_fold(lds + o.w, out, n, o.nsb, v4, tid, nt); break;
+        case VP_RMS: {  // rms (cpu.rs:187-207) of one group: out = a·r·w
+            float dsum = dot16_wave(a, n, tid & 63);
+            float r = 1.0f / sqrtf(dsum / (float)n + o.f);
+            vp_map<VP_RMS>(a, b, out, n, v4, f, r, tid, nt);
             break;
         }
-        case VP_FOLD: {  // slm_fold: the splits of a linear added in order
-            const float* part = lds + o.w;
-            for (int c = tid; c < n; c += nt) {
-                float v = part[c];
-                for (int z = 1; z < o.nsb; z++) v = v + part[z * n + c];
-                out[c] = v;
-            }
-            break;
-        }
-        default: {
-            float factor = o.kind == VP_SCALE && o.dyn ? misc[4 + k] : o.f;
-            if (!out) break;  // a copy whose source slot is written out as it is
-            for (int c = tid; c < n; c += nt) {
-                float v;
-                switch (o.kind) {
-                    case VP_COPY: v = a[c]; break;
-                    case VP_ADD: v = a[c] + b[c]; break;
-                    case VP_MIX: v = a[c] + factor * (b[c] - a[c]); break;
-                    case VP_SCALE: v = a[c] * factor; break;
-                    default: {  // VP_SILU
-                        float gg = a[c];
-                        v = b[c] * gg / (1.0f + expf(-gg));
-                    }
-                }
-                out[c] = v;
-            }
-        }
+        default: break;
     }
 }
 
@@ -1177,11 +1275,11 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
     static_assert(sizeof(FgDesc) % 16 == 0, "descriptor copy in float4s");
     for (int q = threadIdx.x; q < (int)(sizeof(FgDesc) / 16); q += blockDim.x)
         ((f4*)&d)[q] = ((const f4*)&dk)[q];
-    if (threadIdx.x < 3) ((int*)(lds + dk.lds_vp + 28))[threadIdx.x] = 0;
+    if (threadIdx.x < 4) ((int*)(lds + dk.lds_vp + 28))[threadIdx.x] = 0;
     __syncthreads();
     float* misc = lds + d.lds_vp;   // 32 floats, then the prefetch table (SLM_FG_MISC)
     float* foldb = lds + d.fold_off;  // [2 rounds][2 units][W][16]
-    int* sync_ctr = (int*)(misc + 28);  // the prologue waves' barrier; +1: loads issued; +2: x ready
+    int* sync_ctr = (int*)(misc + 28);  // the prologue waves' barrier; +1: their loads are issued; +2: x is ready
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int W = d.W;
     bool first = blockIdx.x == 0;
@@ -1224,81 +1322,89 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
         }
         return;
     }
-    // prologue / epilogue waves: where each prefetch comes from, then the loads, many in
-    // flight per thread
-    int ptid = tid - 64 * W, pnt = (int)blockDim.x - 64 * W;
+    // The prologue / epilogue waves: the prefetches go straight into LDS, wave ew taking
+    // 64-float4 chunks ew, ew + 4, ... of each; then the prologue ops.
+    int ew = wave - W, ptid = tid - 64 * W, pnt = 64 * SLM_FG_EPI_WAVES;
     ESync sync{sync_ctr, 0, SLM_FG_EPI_WAVES};
-    const float** pf_src = (const float**)(misc + 32);  // [SLM_PF_MAX]
-    int* pf_tab = (int*)(misc + 32 + 2 * SLM_PF_MAX);   // [SLM_PF_MAX][2]: lds, first4
-    float sf = 0.0f;  // a dynamic scale factor, loaded with the table, stored after the loads
-    if (ptid < d.npf) {
-        const PfOp& p = d.pf[ptid];
-        pf_src[ptid] = p.src + (p.dyn ? gld(p.dyn) * p.stride : 0);
-        pf_tab[2 * ptid] = p.lds;
-        pf_tab[2 * ptid + 1] = p.first4;
-    }
-    bool has_sf = ptid < d.nvp && d.vp[ptid].kind == VP_SCALE && d.vp[ptid].dyn;
-    if (has_sf) sf = gld((const float*)d.vp[ptid].dyn);
-    sync();
-    for (int base = ptid; base < d.pf4; base += 8 * pnt) {
-        f4 v[8];
-        int dst[8];
+    int npf = uni(d.npf), nvp = uni(d.nvp);
+    const float* src[SLM_PF_MAX];  // where each prefetch comes from this step
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            int f = base + q * pnt;
-            dst[q] = -1;
-            if (f < d.pf4) {
-                int j = 0;
-                for (int t = 1; t < d.npf; t++)
-                    if (f >= pf_tab[2 * t + 1]) j = t;
-                int c4 = f - pf_tab[2 * j + 1];
-                v[q] = gld((const f4*)(pf_src[j] + 4 * c4));
-                dst[q] = pf_tab[2 * j] + 4 * c4;
-            }
+    for (int j = 0; j < SLM_PF_MAX; j++) {
+        src[j] = nullptr;
+        if (j < npf) {
+            const PfOp& p = d.pf[j];
+            src[j] = p.src + (p.dyn ? gld(p.dyn) * p.stride : 0);
         }
-        if (base == ptid && lane == 0)  // this wave's first loads are out: the weights may go
-            __hip_atomic_fetch_add(sync_ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-            if (dst[q] >= 0) *(f4*)(lds + dst[q]) = v[q];
     }
-    if (d.pf4 > 0 && ptid >= d.pf4 && lane == 0)  // a wave with no loads of its own
+    float sf = 0.0f;  // lane k of each wave: the dynamic factor of a VP_SCALE op k
+    if (lane < nvp && d.vp[lane].kind == VP_SCALE && d.vp[lane].dyn)
+        sf = gld((const float*)d.vp[lane].dyn);
+#pragma unroll
+    for (int j = 0; j < SLM_PF_MAX; j++) {
+        if (j >= npf) break;
+        int n4 = uni(d.pf[j].n) >> 2, at = uni(d.pf[j].lds);
+        for (int c0 = 64 * ew; c0 < n4; c0 += pnt)
+            if (c0 + lane < n4)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src[j] + 4 * (c0 + lane)),
+                                                 (__attribute__((address_space(3))) void*)(lds + at + 4 * c0), 16, 0, 0);
+    }
+    if (lane == 0)  // this wave's loads are out: the weights may go
         __hip_atomic_fetch_add(sync_ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (has_sf) misc[4 + ptid] = sf;
-    sync();  // the prologue's vectors are in LDS
-    for (int k = 0; k < d.nvp; k++)
-        if (first || !d.vp[k].wg0) vp_run(d.vp[k], lds, misc, k, ptid, pnt, sync);
-    sync();  // x is ready: the GEMV waves may go
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's prefetches are in LDS
+    sync();                         // and every wave's
+    bool prev_v4 = true;
+    for (int k = 0; k < nvp; k++) {
+        const VpOp o = vp_load(d.vp[k]);
+        if (!first && o.wg0) continue;
+        bool v4 = vp_v4(o);
+        // a barrier when this op reads elements other threads wrote: an offset read, rms,
+        // or a change between float4 and element layout
+        if (o.sync || o.kind == VP_RMS || v4 != prev_v4) sync();
+        prev_v4 = v4;
+        float f = o.f;
+        if (o.kind == VP_SCALE && o.dyn)
+            f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), k));
+        vp_run(o, lds, f, ptid, pnt);
+    }
+    sync();  // x is complete: the GEMV waves may go
     if (ptid == 0) __hip_atomic_fetch_add(sync_ctr + 2, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (first) {  // workgroup 0 writes out what the prologue made that later ops read
-        for (int k = 0; k < d.nvp; k++) {
-            const VpOp& o = d.vp[k];
-            if (!o.gout) continue;
-            const float* src = lds + (o.out >= 0 ? o.out : o.in0);
-            for (int c = ptid; c < o.n; c += pnt) gst(o.gout + c, src[c]);
+        for (int k = 0; k < nvp; k++) {
+            const VpOp o = vp_load(d.vp[k]);
+            if (!d.vp[k].gout) continue;
+            const float* v = lds + (o.out >= 0 ? o.out : o.in0);
+            for (int c = ptid; c < o.n; c += pnt) gst(d.vp[k].gout + c, v[c]);
         }
     }
+    if (ew > 0) return;  // the epilogue is wave 0's (a wave that has ended leaves barriers)
+    // The epilogue, per round of (up to) two units: lanes 0..15 hold rows 0..15 of a tile.
+    // Everything but the partials is worked out before the GEMV waves are waited for.
+    int r = lane & 15;
     for (int u0 = blockIdx.x, par = 0; u0 < d.units; u0 += 2 * gridDim.x, par ^= 1) {
         // the GEMV waves write the next round's partials into the other half of foldb
         // while this round's are read here
         const float* fb = foldb + par * 2 * W * 16;
-        // epilogue inputs of both units go out before the wait for the partials
+        FgSeg sg[2];
+        FgUnit cur[2];
+        int R[2] = {0, 0}, nsl[2] = {0, 0};
+        bool live[2] = {false, false};
         float res[2] = {0.0f, 0.0f};
         long long slot[2] = {0, 0};
-        int r = ptid & 15;  // row r of the tile (lanes 0..15 of the first epilogue wave)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             int u = u0 + h * gridDim.x;
-            if (ptid >= 16 || u >= d.units) continue;
-            FgUnit cur = fg_unit(d, u);
-            const FgSeg sg = d.seg[cur.seg];
-            long long R = fg_row(sg, cur.tile, r);
-            if (R >= sg.rows || sg.nsplit > 1) continue;
-            if (sg.epi == EPI_RESID) res[h] = gld(sg.res + R);
-            if (sg.epi == EPI_ROPE) {
-                int part = (int)(R / sg.d);
-                if (part == 1) slot[h] = (sg.dyn ? gld(sg.dyn) : sg.imm) % sg.cap;
-                if (part == 2) slot[h] = (sg.dyn2 ? gld(sg.dyn2) : sg.imm2) % sg.cap;
+            if (u >= d.units) continue;
+            cur[h] = fg_unit(d, u);
+            sg[h] = d.seg[cur[h].seg];
+            R[h] = (int)fg_row(sg[h], cur[h].tile, r);
+            nsl[h] = min(SLM_SPLIT, d.nsl - cur[h].split * SLM_SPLIT);
+            live[h] = lane < 16 && R[h] < sg[h].rows;
+            if (!live[h] || sg[h].nsplit > 1) continue;
+            if (sg[h].epi == EPI_RESID) res[h] = gld(sg[h].res + R[h]);
+            if (sg[h].epi == EPI_ROPE) {
+                int part = R[h] / sg[h].d;
+                if (part == 1) slot[h] = (sg[h].dyn ? gld(sg[h].dyn) : sg[h].imm) % sg[h].cap;
+                if (part == 2) slot[h] = (sg[h].dyn2 ? gld(sg[h].dyn2) : sg[h].imm2) % sg[h].cap;
             }
         }
         __syncthreads();
@@ -1306,49 +1412,44 @@ KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
         for (int h = 0; h < 2; h++) {
             int u = u0 + h * gridDim.x;
             if (u >= d.units) break;
-            FgUnit cur = fg_unit(d, u);
-            const FgSeg sg = d.seg[cur.seg];
-            float v = 0.0f;
-            if (ptid < 16) {  // the split's slice partials, read at once, added in order
-                int nsl = min(SLM_SPLIT, d.nsl - cur.split * SLM_SPLIT);
-                float pv[SLM_SPLIT];
+            float pv[SLM_SPLIT];  // the split's slice partials, read at once, added in order
 #pragma unroll
-                for (int s = 0; s < SLM_SPLIT; s++) pv[s] = s < nsl ? fb[(h * W + s) * 16 + r] : 0.0f;
-                v = pv[0];
+            for (int q = 0; q < SLM_SPLIT; q++) pv[q] = fb[(h * W + min(q, nsl[h] - 1)) * 16 + r];
+            float v = pv[0];
 #pragma unroll
-                for (int s = 1; s < SLM_SPLIT; s++)
-                    if (s < nsl) v = v + pv[s];
-            }
+            for (int q = 1; q < SLM_SPLIT; q++)
+                if (q < nsl[h]) v = v + pv[q];
             float partner = __shfl_xor(v, 8);
-            long long R = fg_row(sg, cur.tile, r);
-            if (ptid >= 16 || R >= sg.rows) continue;
-            if (sg.nsplit > 1) {
-                gst(sg.part + (long long)cur.split * sg.rows + R, v);
+            if (!live[h]) continue;
+            const FgSeg& g = sg[h];
+            int Rh = R[h];
+            if (g.nsplit > 1) {
+                gst(g.part + (long long)cur[h].split * g.rows + Rh, v);
                 continue;
             }
-            gst(sg.y + R, v);
-            switch (sg.epi) {
+            gst(g.y + Rh, v);
+            switch (g.epi) {
                 case EPI_RESID:
-                    gst(sg.o1 + R, res[h] + v);
+                    gst(g.o1 + Rh, res[h] + v);
                     break;
                 case EPI_SILU:
-                    if (r < 8) gst(sg.o1 + cur.tile * 8 + r, partner * v / (1.0f + expf(-v)));
+                    if (r < 8) gst(g.o1 + cur[h].tile * 8 + r, partner * v / (1.0f + expf(-v)));
                     break;
                 case EPI_ROPE: {
-                    int part = (int)(R / sg.d), j = (int)(R % sg.d);
-                    int e = j % sg.dh, half = sg.dh / 2, head = j / sg.dh;
+                    int part = Rh / g.d, j = Rh % g.d;
+                    int e = j % g.dh, half = g.dh / 2, head = j / g.dh;
                     if (part < 2) {
                         int ie = e < half ? e : e - half;
-                        float cs = lds[sg.cs_lds + ie], sn = lds[sg.sn_lds + ie];
+                        float cs = lds[g.cs_lds + ie], sn = lds[g.sn_lds + ie];
                         float o = e < half ? v * cs - partner * sn : partner * sn + v * cs;
                         if (part == 0) {
-                            gst(sg.o1 + j, o);
+                            gst(g.o1 + j, o);
                         } else {
-                            gst(sg.o2 + j, o);
-                            gst(sg.o3 + ((long long)head * sg.cap + slot[h]) * sg.dh + e, o);
+                            gst(g.o2 + j, o);
+                            gst(g.o3 + ((long long)head * g.cap + slot[h]) * g.dh + e, o);
                         }
                     } else {
-                        gst(sg.o4 + ((long long)head * sg.cap + slot[h]) * sg.dh + e, v);
+                        gst(g.o4 + ((long long)head * g.cap + slot[h]) * g.dh + e, v);
                     }
                     break;
                 }
