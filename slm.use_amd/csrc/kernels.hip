@@ -203,6 +203,51 @@ __device__ void norm_body(float* __restrict__ y, const float* __restrict__ x,
     for (int j = l; j < size; j += 16) out[j] = MODE == 0 ? in[j] * r * w[j] : in[j] * r;
 }
 
+// Wide groups (size a multiple of 4, at most 4096, vectors 16-byte aligned): one wave per
+// group, four groups per workgroup. The wave stages its group in LDS with float4 loads,
+// sums the squares in the order of dot16_self (dot16_wave, defined with the fused kernels
+// below), then scales the float4s it loaded. Same expressions as norm_body.
+__device__ float dot16_wave(const float* in, int size, int lane);
+template <int MODE>
+__device__ void norm_wave_body(float* __restrict__ y, const float* __restrict__ x,
+                               const float* __restrict__ w, int groups, int size, float eps) {
+    extern __shared__ float buf[];
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    long long grp = (long long)blockIdx.x * 4 + wave;
+    if (grp >= groups) return;  // the wave's group is past the end (its lanes leave together)
+    float* row = buf + wave * size;
+    const f4* src = (const f4*)(x + grp * size);
+    int n4 = size >> 2;
+    for (int c = lane; c < n4; c += 64) ((f4*)row)[c] = src[c];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    float d = dot16_wave(row, size, lane);
+    float r = MODE == 0 ? 1.0f / sqrtf(d / (float)size + eps) : 1.0f / fmaxf(sqrtf(d), 1e-12f);
+    f4* out = (f4*)(y + grp * size);
+    for (int c = lane; c < n4; c += 64) {
+        f4 v = ((const f4*)row)[c], o;
+        if (MODE == 0) {
+            f4 wv = ((const f4*)w)[c];
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = v[e] * r * wv[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = v[e] * r;
+        }
+        out[c] = o;
+    }
+}
+
+KERNEL void __launch_bounds__(256) slm_rms_wave(float* y, const float* x, const float* w,
+                                                int groups, int size, float eps) {
+    norm_wave_body<0>(y, x, w, groups, size, eps);
+}
+
+KERNEL void __launch_bounds__(256) slm_l2norm_wave(float* y, const float* x, int groups,
+                                                   int size) {
+    norm_wave_body<1>(y, x, nullptr, groups, size, 0.0f);
+}
+
 KERNEL void __launch_bounds__(256) slm_rms(float* y, const float* x, const float* w, int groups,
                                            int size, float eps, int G) {
     norm_body<0>(y, x, w, groups, size, eps, G);
@@ -609,6 +654,133 @@ KERNEL void __launch_bounds__(256) slm_gemm(float* __restrict__ y, float* __rest
     }
 }
 
+// The same GEMM with a deeper pipeline, for cols a multiple of 64 and 16-byte aligned rows:
+// tiles of BM rows x 64 tokens, 64-column slices copied straight into LDS (no registers) by
+// the four waves, GEMM_STAGES slices in flight, one barrier per slice. In LDS, row r of a
+// slice is 16 chunks of 16 bytes with chunk c at position c ^ (r & 15), so the MFMA operand
+// reads (sixteen rows at one chunk) fall on distinct banks; the copy puts each lane's chunk
+// there by permuting the global addresses it reads. Waves 2 x 2 over the tile, each
+// (BM / 2) x 32. The arithmetic is slm_gemm's: the same MFMA chain per slice, slices added
+// in order within the split, one split per blockIdx.z.
+#define GEMM_STAGES 3
+__device__ __forceinline__ int gsw(int row, int chunk) { return row * 64 + 4 * (chunk ^ (row & 15)); }
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N), other counters untouched
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM>
+__device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
+                           const float* __restrict__ w, const float* __restrict__ x, int rows,
+                           int cols, int m) {
+    constexpr int SW = BM * 64, SX = 64 * 64, STAGE = SW + SX;  // floats per stage
+    constexpr int MU = BM / 32;                                 // 16-row MFMA tiles per wave
+    constexpr int NDMA = (BM + 64) / 16;                        // copies per wave per stage
+    extern __shared__ float lds[];  // [GEMM_STAGES][w: BM x 64 | x: 64 x 64]
+    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int i = lane & 15, g = lane >> 4;
+    int wr = (wave & 1) * (BM / 2), wt = (wave >> 1) * 32;
+    long long r0 = (long long)blockIdx.x * BM, t0 = (long long)blockIdx.y * 64;
+    int nsl = cols >> 6;
+    int s_first = blockIdx.z * SLM_SPLIT, s_end = min(nsl, s_first + SLM_SPLIT), ns = s_end - s_first;
+    // Stage copy: instruction k of this wave covers rows 4k' .. 4k'+3 of the stage's (BM + 64)
+    // rows (w rows first, then x rows), k' = wave + 4k; lane L takes row 4k' + L/16, position
+    // L % 16, i.e. chunk (L % 16) ^ (row & 15) of that row.
+    auto issue = [&](int sl, int buf) {
+#pragma unroll
+        for (int k = 0; k < NDMA; k++) {
+            int rr = 4 * (wave + 4 * k) + (lane >> 4), pos = lane & 15;
+            int rl = rr < BM ? rr : rr - BM;  // row within the w or x tile
+            int chunk = pos ^ (rl & 15);
+            const float* src;
+            bool ok;
+            if (rr < BM) {
+                ok = r0 + rl < rows;
+                src = w + (ok ? (r0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
+            } else {
+                ok = t0 + rl < m;
+                src = x + (ok ? (t0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
+            }
+            float* dst = lds + buf * STAGE + (4 * (wave + 4 * k)) * 64;  // uniform: 4 rows
+            // a row past the end copies row 0 instead (its outputs are never stored), so every
+            // copy runs and the waits below count them exactly
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                             (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        }
+    };
+    f4 sp[MU][2];
+#pragma unroll
+    for (int u = 0; u < MU; u++)
+#pragma unroll
+        for (int v = 0; v < 2; v++) sp[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int p = 0; p < GEMM_STAGES - 1; p++)
+        if (p < ns) issue(s_first + p, p);
+    for (int q0 = 0; q0 < ns; q0++) {
+        // this slice's copies are done (the later ones may still run), then everyone's are,
+        // and everyone has finished the previous slice, whose buffer the next copy reuses
+        if (q0 + 1 < ns) vm_wait<NDMA * (GEMM_STAGES - 2)>();
+        else vm_wait<0>();
+        // a barrier without the fence of __syncthreads, which would wait for every copy in
+        // flight; this wave's LDS reads of the previous slice are done (their values were used)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (q0 + GEMM_STAGES - 1 < ns) issue(s_first + q0 + GEMM_STAGES - 1, (q0 + GEMM_STAGES - 1) % GEMM_STAGES);
+        const float* sw = lds + (q0 % GEMM_STAGES) * STAGE;
+        const float* sx = sw + SW;
+        f4 acc[MU][2];
+#pragma unroll
+        for (int u = 0; u < MU; u++)
+#pragma unroll
+            for (int v = 0; v < 2; v++) acc[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < SLM_KS; q++) {
+            f4 a[MU], bb[2];
+#pragma unroll
+            for (int u = 0; u < MU; u++) a[u] = *(const f4*)(sw + gsw(wr + 16 * u + i, 4 * q + g));
+#pragma unroll
+            for (int v = 0; v < 2; v++) bb[v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int u = 0; u < MU; u++)
+#pragma unroll
+                    for (int v = 0; v < 2; v++) acc[u][v] = mfma4(a[u][e], bb[v][e], acc[u][v]);
+        }
+        // slice sums in order within the split
+#pragma unroll
+        for (int u = 0; u < MU; u++)
+#pragma unroll
+            for (int v = 0; v < 2; v++) sp[u][v] = q0 == 0 ? acc[u][v] : sp[u][v] + acc[u][v];
+    }
+    // out: D[4g + r][i] is row wr + 16u + 4g + r, token wt + 16v + i; through LDS so the
+    // stores run along rows
+    __syncthreads();
+    float* so = lds;  // [64 tokens][BM + 1]
+#pragma unroll
+    for (int u = 0; u < MU; u++)
+#pragma unroll
+        for (int v = 0; v < 2; v++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
+    __syncthreads();
+    float* out = gridDim.z > 1 ? part + (long long)blockIdx.z * m * rows : y;
+    for (int e = tid; e < 64 * BM; e += 256) {
+        int tok = e / BM, row = e % BM;
+        if (t0 + tok < m && r0 + row < rows) out[(t0 + tok) * rows + r0 + row] = so[tok * (BM + 1) + row];
+    }
+}
+
+KERNEL void __launch_bounds__(256) slm_gemm2_64(float* y, float* part, const float* w,
+                                               const float* x, int rows, int cols, int m) {
+    gemm2_body<64>(y, part, w, x, rows, cols, m);
+}
+KERNEL void __launch_bounds__(256) slm_gemm2_32(float* y, float* part, const float* w,
+                                               const float* x, int rows, int cols, int m) {
+    gemm2_body<32>(y, part, w, x, rows, cols, m);
+}
+
 // ---------------------------------------------------------------------------------------
 // attention (ops.rs:31-66, 218-227; cpu.rs:352-403)
 // ---------------------------------------------------------------------------------------
@@ -1008,7 +1180,7 @@ struct ESync {
 // lane l + 16k keep the same running sum of elements l, l + 16, ... (sixteen loads in
 // flight), then the sixteen sums are added left to right through readlane, so every lane
 // returns the same value.
-__device__ __forceinline__ float dot16_wave(const float* in, int size, int lane) {
+__device__ float dot16_wave(const float* in, int size, int lane) {
     int l = lane & 15;
     int chunks = size / 16;
     float acc = 0.0f;

@@ -46,6 +46,7 @@ constexpr int LDS_MAX = 163840;            // gfx950: 160 KB of LDS per workgrou
 constexpr int FG_GRID_MAX = 256;           // workgroups of a fused GEMV: one per compute unit
 constexpr int64_t ATTN_CTR_MAX = 65536;   // (query tile, key head) pairs one attention launch combines itself
 constexpr int ATTN_LDS_MAX = LDS_MAX;
+constexpr int GEMM_STAGES_HOST = 3;          // slices in flight in slm_gemm2 (GEMM_STAGES)
 
 enum OpKind : uint32_t {
     OP_GATHER = 1, OP_COPY, OP_SHIFT, OP_COLUMNS, OP_LINEAR, OP_ADD, OP_ADD_ROW, OP_SCALE_ROWS,
@@ -98,7 +99,8 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 
 struct Kernels {
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
-        store, rope, rope_table, rms, l2norm, fill, combine, probe, fg, fold, gemm;
+        store, rope, rope_table, rms, l2norm, rms_wave, l2norm_wave, fill, combine, probe, fg, fold,
+        gemm, gemm2_32, gemm2_64;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
@@ -366,9 +368,19 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                 int64_t ns = (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
                 if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
                     return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
-                out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
-                                 (uint32_t)ns, 256, 0, p[0], c->gpart, p[1], p[2], (int)rows,
-                                 (int)cols, (int)m));
+                if (cols % 64 == 0) {
+                    // the pipelined GEMM; 32-row tiles when 64-row ones leave the chip idle
+                    int64_t tiles64 = ((rows + 63) / 64) * ((m + 63) / 64) * ns;
+                    int bm = tiles64 < 192 ? 32 : 64;
+                    uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
+                    out.push_back(mk(bm == 32 ? k.gemm2_32 : k.gemm2_64, (uint32_t)((rows + bm - 1) / bm),
+                                     (uint32_t)((m + 63) / 64), (uint32_t)ns, 256, shmem, p[0], c->gpart,
+                                     p[1], p[2], (int)rows, (int)cols, (int)m));
+                } else {
+                    out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
+                                     (uint32_t)ns, 256, 0, p[0], c->gpart, p[1], p[2], (int)rows,
+                                     (int)cols, (int)m));
+                }
                 if (ns > 1)
                     out.push_back(mk(k.fold, blocks_for(m * rows), 1, 1, 256, 0, p[0],
                                      (const float*)c->gpart, (long long)(m * rows), (int)ns));
@@ -397,6 +409,18 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
         case OP_RMS:
         case OP_L2NORM: {  // p0 y, p1 x, p2 w; n0 groups, n1 size; f0 eps
             int64_t groups = n[0], size = n[1];
+            bool wide = size >= 256 && size <= 4096 && size % 4 == 0 && aligned16(p[0]) &&
+                        aligned16(p[1]) && (o.kind != OP_RMS || aligned16(p[2]));
+            if (wide) {  // one wave per group
+                uint32_t blocks = (uint32_t)((groups + 3) / 4), shmem = (uint32_t)(4 * size * 4);
+                if (o.kind == OP_RMS)
+                    out.push_back(mk(k.rms_wave, blocks, 1, 1, 256, shmem, p[0], p[1], p[2],
+                                     (int)groups, (int)size, o.f[0]));
+                else
+                    out.push_back(mk(k.l2norm_wave, blocks, 1, 1, 256, shmem, p[0], p[1],
+                                     (int)groups, (int)size));
+                return SLM_OK;
+            }
             int64_t stride = size | 1;
             // up to 16 groups per workgroup, fewer when that leaves the chip half idle
             int64_t G = std::min<int64_t>(16, std::max<int64_t>(1, 16384 / stride));
@@ -1480,9 +1504,11 @@ int load_kernels(slm_hip* c) {
                {&k.gather, "slm_gather"},       {&k.store, "slm_store"},
                {&k.rope, "slm_rope"},           {&k.rope_table, "slm_rope_table"},
                {&k.rms, "slm_rms"},             {&k.l2norm, "slm_l2norm"},
+               {&k.rms_wave, "slm_rms_wave"},   {&k.l2norm_wave, "slm_l2norm_wave"},
                {&k.fill, "slm_fill"},           {&k.combine, "slm_attn_combine"},
                {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
                {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
+               {&k.gemm2_32, "slm_gemm2_32"},   {&k.gemm2_64, "slm_gemm2_64"},
                {&k.lin_small[0], "slm_linear_small_s"}, {&k.lin_small[1], "slm_linear_small_v"},
                {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
                {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
