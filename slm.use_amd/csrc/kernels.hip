@@ -671,50 +671,52 @@ __device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N), other counte
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM>
+template <int BM, int WAVES>
 __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                            const float* __restrict__ w, const float* __restrict__ x, int rows,
                            int cols, int m) {
     constexpr int SW = BM * 64, SX = 64 * 64, STAGE = SW + SX;  // floats per stage
+    constexpr int NV = WAVES == 4 ? 2 : 1;                      // 16-token MFMA tiles per wave
     constexpr int MU = BM / 32;                                 // 16-row MFMA tiles per wave
-    constexpr int NDMA = (BM + 64) / 16;                        // copies per wave per stage
+    constexpr int NDMA = (BM + 64) / (4 * WAVES);               // copies per wave per stage
+    static_assert((BM + 64) % (4 * WAVES) == 0, "copies per wave");
     extern __shared__ float lds[];  // [GEMM_STAGES][w: BM x 64 | x: 64 x 64]
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int i = lane & 15, g = lane >> 4;
-    int wr = (wave & 1) * (BM / 2), wt = (wave >> 1) * 32;
+    // waves: two halves of the rows times (64 / 16NV) groups of tokens
+    int wr = (wave & 1) * (BM / 2), wt = (wave >> 1) * 16 * NV;
     long long r0 = (long long)blockIdx.x * BM, t0 = (long long)blockIdx.y * 64;
     int nsl = cols >> 6;
     int s_first = blockIdx.z * SLM_SPLIT, s_end = min(nsl, s_first + SLM_SPLIT), ns = s_end - s_first;
     // Stage copy: instruction k of this wave covers rows 4k' .. 4k'+3 of the stage's (BM + 64)
-    // rows (w rows first, then x rows), k' = wave + 4k; lane L takes row 4k' + L/16, position
-    // L % 16, i.e. chunk (L % 16) ^ (row & 15) of that row.
+    // rows (w rows first, then x rows), k' = wave + WAVES k; lane L takes row 4k' + L/16,
+    // position L % 16, i.e. chunk (L % 16) ^ (row & 15) of that row.
     auto issue = [&](int sl, int buf) {
 #pragma unroll
         for (int k = 0; k < NDMA; k++) {
-            int rr = 4 * (wave + 4 * k) + (lane >> 4), pos = lane & 15;
+            int rr = 4 * (wave + WAVES * k) + (lane >> 4), pos = lane & 15;
             int rl = rr < BM ? rr : rr - BM;  // row within the w or x tile
             int chunk = pos ^ (rl & 15);
             const float* src;
-            bool ok;
             if (rr < BM) {
-                ok = r0 + rl < rows;
+                bool ok = r0 + rl < rows;
                 src = w + (ok ? (r0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
             } else {
-                ok = t0 + rl < m;
+                bool ok = t0 + rl < m;
                 src = x + (ok ? (t0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
             }
-            float* dst = lds + buf * STAGE + (4 * (wave + 4 * k)) * 64;  // uniform: 4 rows
+            float* dst = lds + buf * STAGE + (4 * (wave + WAVES * k)) * 64;  // uniform: 4 rows
             // a row past the end copies row 0 instead (its outputs are never stored), so every
             // copy runs and the waits below count them exactly
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                              (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
         }
     };
-    f4 sp[MU][2];
+    f4 sp[MU][NV];
 #pragma unroll
     for (int u = 0; u < MU; u++)
 #pragma unroll
-        for (int v = 0; v < 2; v++) sp[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int v = 0; v < NV; v++) sp[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int p = 0; p < GEMM_STAGES - 1; p++)
         if (p < ns) issue(s_first + p, p);
@@ -729,30 +731,30 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         if (q0 + GEMM_STAGES - 1 < ns) issue(s_first + q0 + GEMM_STAGES - 1, (q0 + GEMM_STAGES - 1) % GEMM_STAGES);
         const float* sw = lds + (q0 % GEMM_STAGES) * STAGE;
         const float* sx = sw + SW;
-        f4 acc[MU][2];
+        f4 acc[MU][NV];
 #pragma unroll
         for (int u = 0; u < MU; u++)
 #pragma unroll
-            for (int v = 0; v < 2; v++) acc[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int v = 0; v < NV; v++) acc[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int q = 0; q < SLM_KS; q++) {
-            f4 a[MU], bb[2];
+            f4 a[MU], bb[NV];
 #pragma unroll
             for (int u = 0; u < MU; u++) a[u] = *(const f4*)(sw + gsw(wr + 16 * u + i, 4 * q + g));
 #pragma unroll
-            for (int v = 0; v < 2; v++) bb[v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
+            for (int v = 0; v < NV; v++) bb[v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
                 for (int u = 0; u < MU; u++)
 #pragma unroll
-                    for (int v = 0; v < 2; v++) acc[u][v] = mfma4(a[u][e], bb[v][e], acc[u][v]);
+                    for (int v = 0; v < NV; v++) acc[u][v] = mfma4(a[u][e], bb[v][e], acc[u][v]);
         }
         // slice sums in order within the split
 #pragma unroll
         for (int u = 0; u < MU; u++)
 #pragma unroll
-            for (int v = 0; v < 2; v++) sp[u][v] = q0 == 0 ? acc[u][v] : sp[u][v] + acc[u][v];
+            for (int v = 0; v < NV; v++) sp[u][v] = q0 == 0 ? acc[u][v] : sp[u][v] + acc[u][v];
     }
     // out: D[4g + r][i] is row wr + 16u + 4g + r, token wt + 16v + i; through LDS so the
     // stores run along rows
@@ -761,25 +763,26 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
     for (int u = 0; u < MU; u++)
 #pragma unroll
-        for (int v = 0; v < 2; v++)
+        for (int v = 0; v < NV; v++)
 #pragma unroll
             for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
     __syncthreads();
     float* out = gridDim.z > 1 ? part + (long long)blockIdx.z * m * rows : y;
-    for (int e = tid; e < 64 * BM; e += 256) {
+    for (int e = tid; e < 64 * BM; e += 64 * WAVES) {
         int tok = e / BM, row = e % BM;
         if (t0 + tok < m && r0 + row < rows) out[(t0 + tok) * rows + r0 + row] = so[tok * (BM + 1) + row];
     }
 }
 
-KERNEL void __launch_bounds__(256) slm_gemm2_64(float* y, float* part, const float* w,
-                                               const float* x, int rows, int cols, int m) {
-    gemm2_body<64>(y, part, w, x, rows, cols, m);
-}
-KERNEL void __launch_bounds__(256) slm_gemm2_32(float* y, float* part, const float* w,
-                                               const float* x, int rows, int cols, int m) {
-    gemm2_body<32>(y, part, w, x, rows, cols, m);
-}
+#define GEMM2(BM, WAVES)                                                                  \
+    KERNEL void __launch_bounds__(64 * WAVES) slm_gemm2_##BM(float* y, float* part, const float* w, \
+                                                           const float* x, int rows, int cols, int m) { \
+        gemm2_body<BM, WAVES>(y, part, w, x, rows, cols, m);                              \
+    }
+GEMM2(32, 4)
+GEMM2(64, 8)
+GEMM2(96, 8)
+GEMM2(128, 8)
 
 // ---------------------------------------------------------------------------------------
 // attention (ops.rs:31-66, 218-227; cpu.rs:352-403)

@@ -47,6 +47,7 @@ constexpr int FG_GRID_MAX = 256;           // workgroups of a fused GEMV: one pe
 constexpr int64_t ATTN_CTR_MAX = 65536;   // (query tile, key head) pairs one attention launch combines itself
 constexpr int ATTN_LDS_MAX = LDS_MAX;
 constexpr int GEMM_STAGES_HOST = 3;          // slices in flight in slm_gemm2 (GEMM_STAGES)
+constexpr int64_t CU_COUNT = 256;           // MI355X compute units
 
 enum OpKind : uint32_t {
     OP_GATHER = 1, OP_COPY, OP_SHIFT, OP_COLUMNS, OP_LINEAR, OP_ADD, OP_ADD_ROW, OP_SCALE_ROWS,
@@ -100,7 +101,7 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 struct Kernels {
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
         store, rope, rope_table, rms, l2norm, rms_wave, l2norm_wave, fill, combine, probe, fg, fold,
-        gemm, gemm2_32, gemm2_64;
+        gemm, gemm2_32, gemm2_64, gemm2_96, gemm2_128;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
@@ -369,12 +370,24 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                 if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
                     return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
                 if (cols % 64 == 0) {
-                    // the pipelined GEMM; 32-row tiles when 64-row ones leave the chip idle
-                    int64_t tiles64 = ((rows + 63) / 64) * ((m + 63) / 64) * ns;
-                    int bm = tiles64 < 192 ? 32 : 64;
+                    // the pipelined GEMM, with the row tile that leaves the busiest CU the
+                    // least work: rows per tile times the workgroups a CU runs (32-row tiles
+                    // of four waves go two to a CU, the others of eight waves one), the larger
+                    // tile on a tie
+                    int bm = 32;
+                    int64_t best = -1;
+                    for (int t : {32, 64, 96, 128}) {
+                        int64_t wgs = ((rows + t - 1) / t) * ((m + 63) / 64) * ns;
+                        int64_t per_cu = t == 32 ? 2 : 1;
+                        int64_t rounds = (wgs + per_cu * CU_COUNT - 1) / (per_cu * CU_COUNT);
+                        int64_t sharing = std::min<int64_t>(per_cu, (wgs + CU_COUNT - 1) / CU_COUNT);
+                        int64_t cost = rounds * t * sharing;
+                        if (best < 0 || cost <= best) best = cost, bm = t;
+                    }
                     uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
-                    out.push_back(mk(bm == 32 ? k.gemm2_32 : k.gemm2_64, (uint32_t)((rows + bm - 1) / bm),
-                                     (uint32_t)((m + 63) / 64), (uint32_t)ns, 256, shmem, p[0], c->gpart,
+                    hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
+                    out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
+                                     (uint32_t)ns, bm == 32 ? 256 : 512, shmem, p[0], c->gpart,
                                      p[1], p[2], (int)rows, (int)cols, (int)m));
                 } else {
                     out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
@@ -1509,6 +1522,7 @@ int load_kernels(slm_hip* c) {
                {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
                {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
                {&k.gemm2_32, "slm_gemm2_32"},   {&k.gemm2_64, "slm_gemm2_64"},
+               {&k.gemm2_96, "slm_gemm2_96"},   {&k.gemm2_128, "slm_gemm2_128"},
                {&k.lin_small[0], "slm_linear_small_s"}, {&k.lin_small[1], "slm_linear_small_v"},
                {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
                {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
