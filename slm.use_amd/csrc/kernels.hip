@@ -677,14 +677,15 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                            int cols, int m) {
     constexpr int SW = BM * 64, SX = 64 * 64, STAGE = SW + SX;  // floats per stage
     constexpr int NV = WAVES == 4 ? 2 : 1;                      // 16-token MFMA tiles per wave
-    constexpr int MU = BM / 32;                                 // 16-row MFMA tiles per wave
+    constexpr int RG = WAVES == 16 ? 4 : 2;                     // groups of rows over the waves
+    constexpr int MU = BM / (16 * RG);                          // 16-row MFMA tiles per wave
     constexpr int NDMA = (BM + 64) / (4 * WAVES);               // copies per wave per stage
-    static_assert((BM + 64) % (4 * WAVES) == 0, "copies per wave");
+    static_assert((BM + 64) % (4 * WAVES) == 0 && MU >= 1, "copies per wave, rows per wave");
     extern __shared__ float lds[];  // [GEMM_STAGES][w: BM x 64 | x: 64 x 64]
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int i = lane & 15, g = lane >> 4;
-    // waves: two halves of the rows times (64 / 16NV) groups of tokens
-    int wr = (wave & 1) * (BM / 2), wt = (wave >> 1) * 16 * NV;
+    // waves: RG groups of the rows times (64 / 16NV) groups of tokens
+    int wr = (wave % RG) * (BM / RG), wt = (wave / RG) * 16 * NV;
     long long r0 = (long long)blockIdx.x * BM, t0 = (long long)blockIdx.y * 64;
     int nsl = cols >> 6;
     int s_first = blockIdx.z * SLM_SPLIT, s_end = min(nsl, s_first + SLM_SPLIT), ns = s_end - s_first;
@@ -736,20 +737,23 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         for (int u = 0; u < MU; u++)
 #pragma unroll
             for (int v = 0; v < NV; v++) acc[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        // the whole slice's operands first (one LDS round trip), then its MFMAs back to back
+        f4 a[SLM_KS][MU], bb[SLM_KS][NV];
 #pragma unroll
         for (int q = 0; q < SLM_KS; q++) {
-            f4 a[MU], bb[NV];
 #pragma unroll
-            for (int u = 0; u < MU; u++) a[u] = *(const f4*)(sw + gsw(wr + 16 * u + i, 4 * q + g));
+            for (int u = 0; u < MU; u++) a[q][u] = *(const f4*)(sw + gsw(wr + 16 * u + i, 4 * q + g));
 #pragma unroll
-            for (int v = 0; v < NV; v++) bb[v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
+            for (int v = 0; v < NV; v++) bb[q][v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
+        }
+#pragma unroll
+        for (int q = 0; q < SLM_KS; q++)
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
                 for (int u = 0; u < MU; u++)
 #pragma unroll
-                    for (int v = 0; v < NV; v++) acc[u][v] = mfma4(a[u][e], bb[v][e], acc[u][v]);
-        }
+                    for (int v = 0; v < NV; v++) acc[u][v] = mfma4(a[q][u][e], bb[q][v][e], acc[u][v]);
         // slice sums in order within the split
 #pragma unroll
         for (int u = 0; u < MU; u++)
@@ -780,9 +784,9 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         gemm2_body<BM, WAVES>(y, part, w, x, rows, cols, m);                              \
     }
 GEMM2(32, 4)
-GEMM2(64, 8)
+GEMM2(64, 16)
 GEMM2(96, 8)
-GEMM2(128, 8)
+GEMM2(128, 16)
 
 // ---------------------------------------------------------------------------------------
 // attention (ops.rs:31-66, 218-227; cpu.rs:352-403)

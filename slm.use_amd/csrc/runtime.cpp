@@ -387,7 +387,7 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                     uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
                     hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
                     out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
-                                     (uint32_t)ns, bm == 32 ? 256 : 512, shmem, p[0], c->gpart,
+                                     (uint32_t)ns, bm == 32 ? 256 : bm == 96 ? 512 : 1024, shmem, p[0], c->gpart,
                                      p[1], p[2], (int)rows, (int)cols, (int)m));
                 } else {
                     out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
