@@ -54,7 +54,8 @@ def test_mfma_lane_layout(hip):
 
 LINEAR_SHAPES = [(96, 32, 1), (2304, 768, 1), (768, 3072, 1), (32000, 768, 1), (768, 768, 5),
                  (13, 37, 3), (768, 768, 16), (768, 768, 17), (2304, 768, 256),
-                 (6144, 768, 256), (768, 3072, 256), (12, 768, 256), (50, 21, 70)]
+                 (6144, 768, 256), (768, 3072, 256), (12, 768, 256), (50, 21, 70),
+                 (2300, 768, 200), (100, 1536, 100)]
 
 
 @pytest.mark.parametrize("rows,cols,m", LINEAR_SHAPES)
@@ -69,9 +70,10 @@ def test_linear(hip, rows, cols, m):
 
 
 @pytest.mark.parametrize("rows,cols", [(768, 768), (6144, 768), (768, 3072), (97, 32), (40, 52),
-                                       (64, 1600)])
+                                       (64, 1600), (8192, 768), (2300, 768), (6150, 768)])
 def test_linear_same_bits_for_any_m(hip, rows, cols):
-    """The decode kernel (m <= 16) and the prompt kernel (m > 16) run one MFMA chain."""
+    """The decode kernel (m <= 16) and the prompt kernels (m > 16, every row tile: 32, 64,
+    96 and 128 rows, ragged last tiles) run one MFMA chain."""
     m = 256
     w = rnd(rows, cols, scale=0.02)
     x = rnd(m, cols)
