@@ -153,6 +153,19 @@ def cpu_baseline(folder, cfg, loops, prompt, decode_tokens):
 
 # ---------------------------------------------------------------------------------------
 
+def traffic():
+    """HBM bytes per slm_fg launch in the a86 decode step, as the committed counter profile
+    measured them (FETCH_SIZE and WRITE_SIZE passes, each scaled by what the same counter reads
+    for a copy of known size); None when the profile is absent."""
+    f = ROOT / "profiles" / "slm_fg_a86_decode_traffic.md"
+    if not f.exists():
+        return None
+    for ln in f.read_text().splitlines():
+        if ln.startswith("traffic_bytes_per_launch:"):
+            return int(ln.split(":")[1])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,6 +178,9 @@ def main():
     ap.add_argument("--no-graphs", action="store_true")
     ap.add_argument("--timed-steps", type=int, default=16,
                     help="decode steps whose kernels are timed one by one for the roofline")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only copy this many MiB four times through slm_hip_copy and exit (a "
+                         "known-size workload that calibrates the FETCH_SIZE/WRITE_SIZE counters)")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -175,6 +191,17 @@ def main():
     pkg = package()
     sys.path.insert(0, str(ROOT / "slm.use_amd"))
     import synth
+
+    if a.copy_mib:
+        hip = pkg.Hip(0)
+        n = a.copy_mib << 18  # floats
+        src, dst = hip.alloc(n), hip.alloc(n)
+        for _ in range(4):
+            hip.copy(dst.ptr, src.ptr, n)
+        dst.read(4)
+        log(f"copied {a.copy_mib} MiB four times")
+        hip.close()
+        return
 
     cache = Path(os.environ.get("SLM_MODEL_CACHE", "/tmp")) / "slm_models"
     folder = synth.write_model(cache / "a86-2", "a86", 2)
@@ -256,7 +283,7 @@ def main():
                    "ffn": 3072, "vocab": 32000, "window": 4096, "layers": "SS|LS|SS",
                    "prompt_tokens": len(prompt), "decode_from_pos": pos0},
         "roofline": {"bound": "hbm", "achieved": round(gemv_bw / 1e9, 1), "peak": 8000.0,
-                     "unit": "GB/s", "frac": round(gemv_bw / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gemv_bw / HBM_PEAK, 4), "traffic": traffic(),
                      "kernel": "slm_fg", "launches": fg["launches"],
                      "bytes_per_launch": round(bpl), "us_per_launch": round(per_launch * 1e6, 3),
                      "us_per_step_by_kernel": share},
