@@ -1119,6 +1119,286 @@ ATTN_PART(4)
 ATTN_PART(8)
 ATTN_PART(16)
 
+// One-token attention (m = 1) on the vector ALUs, with the arithmetic of slm_attn_part_*
+// element for element. A 16x16x4 f32 MFMA step is, bit for bit, fmaf over k = 0..3 in
+// order (denormals kept), so a score is the fmaf chain from 0 over dims 16t + 4g + c with t,
+// then c, then g outermost to innermost, and an output dim is o·α followed by the fmaf chain
+// over the keys 4g + r of a 16-key tile, r outer and g inner; the tile softmax, the row-sum
+// order ((p0 + p1) + p2) + p3 per four keys then (s0 + s1) + (s2 + s3), the segment fold and
+// the superblock combine are the same expressions. Dims at or past dh, zero in both operands
+// there, leave a chain unchanged and are skipped. Grid (key heads, superblock slots);
+// SLM_SB_SEGS waves, wave w takes segment w of superblock sb. Each wave copies its segment's
+// 64 keys and values into its own LDS (rows of 16 chunks of 16 bytes, chunk c at position
+// c ^ (key & 15), so one chunk of sixteen keys and one row of sixteen chunks both fall on
+// distinct banks), scores one key per lane and accumulates one output dim per lane.
+// Output: part[z][0][head][2 + 16·DT], as slm_attn_part_*; with `ctr` the last workgroup of
+// a key head combines the superblocks into y (its partials fit in LDS: the host checks).
+#define ADEC_WAVE_FLOATS (2 * 64 * 64 + 1024)  // a wave's LDS: keys [64][64], values [64][64], queries
+template <int DT>
+__device__ void attn_dec_body(float* __restrict__ part, const float* __restrict__ q,
+                              const float* __restrict__ kc, const float* __restrict__ vc,
+                              const long long* __restrict__ dyn, long long pos_imm,
+                              long long reach, long long gap, long long cap, int heads,
+                              int key_heads, int dh, float scale, float* __restrict__ y,
+                              int* __restrict__ ctr) {
+    static_assert(DT >= 1 && DT <= 4, "one-token attention: head size at most 64");
+    constexpr int DP = 16 * DT;
+    extern __shared__ float lds[];
+    long long pos = dyn_or(dyn, pos_imm);
+    int lane = threadIdx.x & 63;
+    int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int group = heads / key_heads, kvh = blockIdx.x;
+    int nch = dh >> 2;  // 16-byte chunks per row
+    long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
+    long long sb = first / SLM_SB_KEYS + blockIdx.y;
+    long long seg_lo = (sb * SLM_SB_SEGS + wave) * 64;
+    const char* kb = (const char*)(kc + (long long)kvh * cap * dh);
+    const char* vb = (const char*)(vc + (long long)kvh * cap * dh);
+    float* kt = lds + wave * ADEC_WAVE_FLOATS;  // keys; then p and the fold slots
+    float* vt = kt + 64 * 64;                    // values
+    float* qt = vt + 64 * 64;                    // the key head's queries [group][dh]
+    // the copies, queries first: the group's query rows are contiguous (one token), 64
+    // chunks per instruction (a lane past the end copies the last chunk into unused LDS)
+    int nqc = (group * dh) >> 2;
+    const float* qg = q + (long long)kvh * group * dh;
+    for (int k = 0; k < (nqc + 63) / 64; k++) {
+        int ch = min(64 * k + lane, nqc - 1);
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(qg + 4 * ch),
+                                         (__attribute__((address_space(3))) void*)(qt + 256 * k), 16, 0, 0);
+    }
+    // keys, then values: instruction k covers keys 4k .. 4k+3; lane L takes key 4k + L/16 and
+    // puts chunk (L % 16) ^ (key & 15) of its row at position L % 16 (a chunk at or past dh
+    // copies the row's last one: it is never read). Key 4k + g is ring slot (seg_lo + 4k + g)
+    // mod cap; with cap >= 64 each step of four keys wraps at most once, and a key head's
+    // ring is under 4 GB, so byte offsets are 32-bit (the host checks both).
+    unsigned rowb = (unsigned)dh * 4u, wrapb = (unsigned)cap * rowb;
+    unsigned slot = (unsigned)(seg_lo % cap) + (unsigned)(lane >> 4);
+    if (slot >= (unsigned)cap) slot -= (unsigned)cap;
+    unsigned roff = slot * rowb;
+    unsigned off[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        int key = 4 * k + (lane >> 4);
+        off[k] = roff + 16u * (unsigned)min((lane & 15) ^ (key & 15), nch - 1);
+        roff += 4 * rowb;
+        if (roff >= wrapb) roff -= wrapb;
+    }
+    // (non-temporal: the keys and values are read once per token, and should not push this
+    // kernel's code and the partials out of L2)
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off[k]),
+                                         (__attribute__((address_space(3))) void*)(kt + 256 * k), 16, 0, 2);
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off[k]),
+                                         (__attribute__((address_space(3))) void*)(vt + 256 * k), 16, 0, 2);
+    vm_wait<16>();  // the queries and keys are in (the values may still be on their way)
+    asm volatile("" ::: "memory");
+    // this lane's key: dims 16t + 4g .. +3 as kr[t][g]
+    int j = lane;
+    f4 kr[DT][4];
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) kr[t][g] = *(const f4*)(kt + 4 * (16 * j + ((4 * t + g) ^ (j & 15))));
+    long long kp = seg_lo + j;
+    float* pt = kt;             // p of the current tile [16], over the keys once read
+    float* fs = kt + 64;        // fold slots [group][DP + 2]
+    // value reads of one output dim: key 4g + r of a tile is at row offset
+    // 4·(16·(4g + r) + ((d / 4) ^ (4g + r))) + d % 4 from the tile's first row
+    int d = lane, dc = d >> 2, dw = d & 3;
+    int va[16];
+#pragma unroll
+    for (int kk = 0; kk < 16; kk++) va[kk] = 4 * (16 * kk + (dc ^ kk)) + dw;
+    bool vwait = true;
+    for (int c = 0; c < group; c++) {
+        Col col = column(c, 0, pos, 1, reach, gap, group, 16 / group, kvh);
+        f4 qv[DT][4];  // the same for every lane (LDS broadcast)
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) qv[t][g] = *(const f4*)(qt + c * dh + min(16 * t + 4 * g, dh - 4));
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    if (16 * t + 4 * g < dh) s = fmaf(kr[t][g][e], qv[t][g][e], s);
+        bool ok = kp >= col.lo && kp < col.hi;
+        float sv = ok ? s * scale : NEG_INF;
+        float tm = sv;  // tile maxima
+        tm = fmaxf(tm, __shfl_xor(tm, 1));
+        tm = fmaxf(tm, __shfl_xor(tm, 2));
+        tm = fmaxf(tm, __shfl_xor(tm, 4));
+        tm = fmaxf(tm, __shfl_xor(tm, 8));
+        unsigned long long okm = __ballot(ok);
+        if (vwait) {  // the values are in
+            vm_wait<0>();
+            asm volatile("" ::: "memory");
+            vwait = false;
+        }
+        // tile by tile: the running maximum and α of the MFMA path (uniform), this tile's p,
+        // then one output dim per lane
+        float mo = NEG_INF, lo = 0.0f, o = 0.0f;
+#pragma unroll 1
+        for (int st = 0; st < 4; st++) {
+            float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tm), 16 * st));
+            bool any = ((okm >> (16 * st)) & 0xffffull) != 0;
+            float mnew = fmaxf(mo, mx);
+            float muse = mnew == NEG_INF ? 0.0f : mnew;
+            float alpha = expf(mo - muse);
+            if (!any) continue;
+            if ((j >> 4) == st) pt[j & 15] = sv == NEG_INF ? 0.0f : expf(sv - muse);
+            float p[16];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                f4 pv = *(const f4*)(pt + 4 * u);
+                p[4 * u] = pv.x;
+                p[4 * u + 1] = pv.y;
+                p[4 * u + 2] = pv.z;
+                p[4 * u + 3] = pv.w;
+            }
+            float r0 = ((p[0] + p[1]) + p[2]) + p[3], r1 = ((p[4] + p[5]) + p[6]) + p[7];
+            float r2 = ((p[8] + p[9]) + p[10]) + p[11], r3 = ((p[12] + p[13]) + p[14]) + p[15];
+            float rs = (r0 + r1) + (r2 + r3);
+            const float* vrow = vt + 1024 * st;
+            float on = o * alpha;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) on = fmaf(vrow[va[4 * g + r]], p[4 * g + r], on);
+            lo = lo * alpha + rs;
+            mo = mnew;
+            o = on;
+            // the next tile's p overwrites this one's only after every lane has read it
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        float* F = fs + c * (DP + 2);
+        if (d < dh) F[2 + d] = o;
+        if (lane == 0) {
+            F[0] = mo;
+            F[1] = lo;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    // fold the four segments in order, one (column, dim) per thread
+    for (int t = threadIdx.x; t < group * DP; t += 64 * SLM_SB_SEGS) {
+        int cc = t / DP, dd = t % DP;
+        if (dd >= dh) continue;
+        float FM = NEG_INF, FL = 0.0f, FO = 0.0f;
+#pragma unroll
+        for (int w = 0; w < SLM_SB_SEGS; w++) {
+            const float* F = lds + w * ADEC_WAVE_FLOATS + 64 + cc * (DP + 2);
+            fold(FM, FL, FO, F[0], F[1], F[2 + dd]);
+        }
+        int head = kvh * group + cc;
+        float* P = part + ((long long)blockIdx.y * heads + head) * (long long)(DP + 2);
+        if (ctr) {  // written through to where every workgroup's loads see it
+            if (dd == 0) {
+                __hip_atomic_store(P, FM, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(P + 1, FL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __hip_atomic_store(P + 2 + dd, FO, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            if (dd == 0) {
+                P[0] = FM;
+                P[1] = FL;
+            }
+            P[2 + dd] = FO;
+        }
+    }
+    if (!ctr) return;
+    // the last workgroup of this key head combines the superblocks (slm_attn_combine's
+    // expressions) from a copy of every partial in LDS, read in one pass
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ int last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int* cp = ctr + blockIdx.x;
+        int before = __hip_atomic_fetch_add(cp, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = before == (int)gridDim.y - 1;
+        if (last) __hip_atomic_store(cp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // the key head's slots are group·(DP + 2) contiguous floats per superblock; thread f of a
+    // pass takes float f mod 2^sh of slot f / 2^sh (2^sh: that count rounded up to a power of 2)
+    int nsb = (int)gridDim.y, sr = group * (DP + 2);
+    int sh = 32 - __clz(sr - 1);
+    int nf = nsb << sh;
+    for (int b = 0; b < nf; b += 8 * 64 * SLM_SB_SEGS) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            int f = b + threadIdx.x + u * 64 * SLM_SB_SEGS;
+            int z = min(f >> sh, nsb - 1), e = min(f & ((1 << sh) - 1), sr - 1);
+            v[u] = part[((long long)z * heads + kvh * group) * (DP + 2) + e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            int f = b + threadIdx.x + u * 64 * SLM_SB_SEGS;
+            int z = f >> sh, e = f & ((1 << sh) - 1);
+            if (z < nsb && e < sr) lds[z * sr + e] = v[u];
+        }
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < group * DP; t += 64 * SLM_SB_SEGS) {
+        int cc = t / DP, dd = t % DP;
+        if (dd >= dh) continue;
+        const float* P = lds + cc * (DP + 2);
+        float M = NEG_INF;
+        for (int z0 = 0; z0 < nsb; z0 += 8) {
+            float lz[8], mz[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {  // past the last superblock: reads the last again
+                int z = min(z0 + u, nsb - 1);
+                lz[u] = P[z * sr + 1];
+                mz[u] = P[z * sr];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (z0 + u < nsb && lz[u] > 0.0f) M = fmaxf(M, mz[u]);
+        }
+        float L = 0.0f, O = 0.0f;
+        for (int z0 = 0; z0 < nsb; z0 += 8) {
+            float lz[8], mz[8], oz[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float* Q = P + min(z0 + u, nsb - 1) * sr;
+                lz[u] = Q[1];
+                mz[u] = Q[0];
+                oz[u] = Q[2 + dd];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (z0 + u < nsb && lz[u] > 0.0f) {
+                    float w = expf(mz[u] - M);
+                    L = L + lz[u] * w;
+                    O = O + oz[u] * w;
+                }
+        }
+        y[(long long)(kvh * group + cc) * dh + dd] = L > 0.0f ? O / L : 0.0f;
+    }
+}
+
+#define ATTN_DEC(DT)                                                                     \
+    KERNEL void __launch_bounds__(64 * SLM_SB_SEGS) slm_attn_dec_##DT(                    \
+        float* part, const float* q, const float* kc, const float* vc,                   \
+        const long long* dyn, long long pos_imm, long long reach, long long gap,         \
+        long long cap, int heads, int key_heads, int dh, float scale, float* y,          \
+        int* ctr) {                                                                      \
+        attn_dec_body<DT>(part, q, kc, vc, dyn, pos_imm, reach, gap, cap, heads,          \
+                          key_heads, dh, scale, y, ctr);                                 \
+    }
+ATTN_DEC(1)
+ATTN_DEC(2)
+ATTN_DEC(4)
+
 // y[qidx][head][dim] from the nsb superblock partials: with M the largest m of the
 // superblocks that saw a key, w_z = e^(m_z − M), L = Σ l_z·w_z and O = Σ o_z·w_z (both in
 // superblock order), y = O / L (0 when the query sees nothing, cpu.rs:378-382). The last

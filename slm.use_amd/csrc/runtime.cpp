@@ -46,6 +46,7 @@ constexpr int LDS_MAX = 163840;            // gfx950: 160 KB of LDS per workgrou
 constexpr int FG_GRID_MAX = 256;           // workgroups of a fused GEMV: one per compute unit
 constexpr int64_t ATTN_CTR_MAX = 65536;   // (query tile, key head) pairs one attention launch combines itself
 constexpr int ATTN_LDS_MAX = LDS_MAX;
+constexpr int ATTN_DEC_LDS = SLM_SB_SEGS * (2 * 64 * 64 + 1024) * 4;  // one-token attention: 256 keys and values, queries
 constexpr int GEMM_STAGES_HOST = 3;          // slices in flight in slm_gemm2 (GEMM_STAGES)
 constexpr int64_t CU_COUNT = 256;           // MI355X compute units
 
@@ -105,6 +106,7 @@ struct Kernels {
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
+    hipFunction_t attn_dec[3];               // one-token attention, dim tiles 1, 2, 4
 };
 
 }  // namespace
@@ -482,6 +484,22 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int64_t m = n[1], heads = n[5], kh = n[6], dh = n[7], nsb = n[8];
             int dti = pow2_index((dh + 15) / 16, 4);
             int64_t dp = (int64_t)16 << dti;
+            if (m == 1 && dh <= 64 && n[4] >= 64 && n[4] * dh * 4 < ((int64_t)1 << 32)) {
+                // one token: the vector-ALU kernel (the same arithmetic; its ring offsets step
+                // four slots at a time and are 32-bit). It combines the superblocks itself when
+                // every partial of a key head fits in its LDS
+                bool self = kh <= ATTN_CTR_MAX && nsb * (heads / kh) * (dp + 2) <= ATTN_DEC_LDS / 4;
+                out.push_back(mk(k.attn_dec[dti], (uint32_t)kh, (uint32_t)nsb, 1, 64 * SLM_SB_SEGS,
+                                 (uint32_t)ATTN_DEC_LDS, c->ws, p[1], p[2], p[3],
+                                 (const long long*)o.dyn, (long long)n[0], (long long)n[2],
+                                 (long long)n[3], (long long)n[4], (int)heads, (int)kh, (int)dh,
+                                 o.f[0], self ? p[0] : (float*)nullptr,
+                                 self ? c->attn_ctr : (int*)nullptr));
+                if (!self)
+                    out.push_back(mk(k.combine, blocks_for(heads * dh), 1, 1, 256, 0, p[0],
+                                     (const float*)c->ws, 1, (int)heads, (int)dh, (int)dp, (int)nsb));
+                return SLM_OK;
+            }
             // LDS: wpp segment partials being folded, then each wave's tile of values
             auto shm = [&](int64_t w) { return (w * 16 * (dp + 2) + SLM_SB_SEGS * 16 * (dp + 4)) * 4; };
             int64_t wpp = SLM_SB_SEGS;
@@ -1295,10 +1313,8 @@ int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fus
                 fprintf(stderr, " pf%d]", d->npf);
                 continue;
             }
-            for (auto& pr : {std::make_pair(K.gemm, "gemm"), std::make_pair(K.lin_small[1], "lin"),
-                             std::make_pair(K.fold, "fold"), std::make_pair(K.combine, "comb"),
-                             std::make_pair(K.add, "add"), std::make_pair(K.rms, "rms")})
-                if (out[k].f == pr.first) nm = pr.second;
+            auto it = c->fname.find(out[k].f);
+            if (it != c->fname.end()) nm = it->second.c_str() + (it->second.rfind("slm_", 0) == 0 ? 4 : 0);
             fprintf(stderr, " %s", nm);
         }
         fprintf(stderr, "\n");
@@ -1530,7 +1546,9 @@ int load_kernels(slm_hip* c) {
                {&k.gla1[0], "slm_gla1_1"}, {&k.gla1[1], "slm_gla1_2"}, {&k.gla1[2], "slm_gla1_4"},
                {&k.attn[0], "slm_attn_part_1"}, {&k.attn[1], "slm_attn_part_2"},
                {&k.attn[2], "slm_attn_part_4"}, {&k.attn[3], "slm_attn_part_8"},
-               {&k.attn[4], "slm_attn_part_16"}};
+               {&k.attn[4], "slm_attn_part_16"},
+               {&k.attn_dec[0], "slm_attn_dec_1"}, {&k.attn_dec[1], "slm_attn_dec_2"},
+               {&k.attn_dec[2], "slm_attn_dec_4"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;
@@ -2135,6 +2153,8 @@ int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const fl
     }
     size_t qpt = 16 / group;
     size_t qtiles = (m + qpt - 1) / qpt;
+    if (a->cap >= ((size_t)1 << 31))
+        return fail(c, SLM_E_UNSUPPORTED, "attend: ring of %zu slots (at most 2^31 - 1)", a->cap);
     if (qtiles > UINT32_MAX || nsb > 65535)
         return fail(c, SLM_E_UNSUPPORTED, "attend: %zu query tiles x %zu superblocks", qtiles, nsb);
     size_t dp = (size_t)16 << pow2_index((dh + 15) / 16, 4);

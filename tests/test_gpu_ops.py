@@ -233,6 +233,12 @@ ATTN_CASES = [
     dict(pos=600, m=33, reach=200, gap=0, cap=456, heads=6, key_heads=3, dh=32),
     dict(pos=700, m=20, reach=512, gap=0, cap=600, heads=4, key_heads=2, dh=128),
     dict(pos=300, m=5, reach=O.USIZE_MAX, gap=0, cap=320, heads=2, key_heads=2, dh=256),
+    # one-token kernel edges: sixteen query heads per key head, head sizes 48 and 4, and a
+    # span whose superblock partials do not fit its LDS (combined by a second kernel)
+    dict(pos=1000, m=3, reach=O.USIZE_MAX, gap=0, cap=1100, heads=16, key_heads=1, dh=64),
+    dict(pos=400, m=4, reach=300, gap=0, cap=512, heads=4, key_heads=2, dh=48),
+    dict(pos=90, m=2, reach=64, gap=0, cap=100, heads=2, key_heads=1, dh=4),
+    dict(pos=9000, m=2, reach=O.USIZE_MAX, gap=0, cap=9100, heads=16, key_heads=1, dh=64),
 ]
 
 
