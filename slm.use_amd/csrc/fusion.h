@@ -124,4 +124,51 @@ typedef struct {
     float pad;
 } GlaDesc;
 
+// A prompt row chain (m > 1 tokens): consecutive row-local element-wise ops between two
+// GEMMs run as one launch, one workgroup per token row. Each op's operands come from the
+// LDS copy of an earlier op's output row or from global memory (row r at g + r·stride;
+// stride 0: one vector for every row); its output row goes to LDS (when a later op reads
+// it) and to global memory (unless a later op of the chain overwrites the same rows).
+// Every element is computed with the expression of the per-op kernel.
+#define SLM_ROW_OPS 10
+#define SLM_ROW_PF 8
+enum {
+    R_COPY = 1,  // out = a                                   (copy, columns)
+    R_ADD,       // out = a + b                               (add, add_row with b.stride 0)
+    R_MIX,       // out = a + f0·(b − a)
+    R_SILU,      // out = b · a / (1 + e^−a)                  (silu_mul, a = gate)
+    R_ROPE,      // i0 heads of i1 dims: half-split rotation of a by cos c, sin d
+    R_STORE,     // ring y [i0 heads][q0 slots][i1] at slot (pos + r) mod q0 ← a
+    R_RMS,       // groups of i0: a · (1/sqrt(dot/i0 + f0)) · b   (b: weights, stride 0)
+    R_L2NORM,    // groups of i0: a · (1/max(sqrt(dot), 1e-12))
+    R_FOLD,      // out = ((a + a[q0]) + a[2·q0]) + ...: i0 split partials, q0 apart
+};
+typedef struct {
+    const float* g;  // global base (row r at g + r·stride), when the LDS offset is -1
+    int64_t stride;
+} RowIn;
+typedef struct {
+    int32_t kind, n;                 // n: elements per row of the output
+    int32_t la, lb, lc, ld;          // LDS offsets of operands a..d, or -1 (global)
+    int32_t out, tmp;                // LDS offset of the output row (-1: none); norms: a staging row
+    int32_t i0, i1;
+    float f0;
+    int32_t vec;                     // every operand, output and row length in float4s
+    RowIn a, b, c, d;
+    float* y;                        // global output (row r at y + r·ystride), or null
+    int64_t ystride;
+    int64_t q0, q1;                  // store: ring slots, position; fold: partial stride
+    const long long* dyn;            // store: the position on the device (or null: q1)
+} RowOp;
+typedef struct {  // a global operand row copied into LDS before the first op
+    const float* g;  // row r at g + r·stride
+    int64_t stride;
+    int32_t n, lds;  // floats (a multiple of 4, 16-byte aligned rows), LDS offset
+} RowPf;
+typedef struct {
+    int32_t nops, npf, pad1, pad2;
+    RowPf pf[SLM_ROW_PF];
+    RowOp op[SLM_ROW_OPS];
+} RowDesc;
+
 #endif

@@ -1928,6 +1928,260 @@ KERNEL void slm_fold(float* __restrict__ y, const float* __restrict__ part, long
     }
 }
 
+// A prompt row chain: workgroup r runs the ops on token row r, each op over the row with
+// the expression of its own kernel (slm_copy / slm_columns, slm_add / slm_add_row,
+// slm_mix, slm_silu_mul, slm_rope, slm_store, slm_rms / slm_l2norm, slm_fold). Between two
+// ops a barrier orders LDS only: a later op reads what an earlier one made from LDS, never
+// from global memory (the planner sees to it), so no global write has to land first.
+// With `vec` the ops move float4s, each thread issuing all loads of a batch of four before
+// it uses any.
+__device__ __forceinline__ float row_in(const float* lds, int off, const RowIn& s, long long r,
+                                        int i) {
+    return off >= 0 ? lds[off + i] : s.g[r * s.stride + i];
+}
+__device__ __forceinline__ void row_put(float* lds, const RowOp& o, float* yr, int i, float v) {
+    if (o.out >= 0) lds[o.out + i] = v;
+    if (yr) yr[i] = v;
+}
+__device__ __forceinline__ f4 row_in4(const float* lds, int off, const RowIn& s, long long r,
+                                      int i) {  // i: a multiple of 4
+    return off >= 0 ? *(const f4*)(lds + off + i) : *(const f4*)(s.g + r * s.stride + i);
+}
+__device__ __forceinline__ void row_put4(float* lds, const RowOp& o, float* yr, int i, f4 v) {
+    if (o.out >= 0) *(f4*)(lds + o.out + i) = v;
+    if (yr) *(f4*)(yr + i) = v;
+}
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+template <int KIND>
+__device__ __forceinline__ float row_ew(float a, float b, float f) {
+    if (KIND == R_COPY) return a;
+    if (KIND == R_ADD) return a + b;
+    if (KIND == R_MIX) return a + f * (b - a);
+    return b * a / (1.0f + expf(-a));  // R_SILU: a = gate, b = up
+}
+// out = f(a, b) element by element
+template <int KIND>
+__device__ __forceinline__ void row_elementwise(const RowOp& o, float* lds, float* yr, long long r,
+                                                int tid) {
+    int n = o.n;
+    bool two = KIND != R_COPY;
+    if (o.vec) {
+        for (int b0 = 0; b0 < n; b0 += 4 * 1024) {
+            f4 av[4], bv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                int i = b0 + 4 * (tid + 256 * u);
+                if (i < n) {
+                    av[u] = row_in4(lds, o.la, o.a, r, i);
+                    if (two) bv[u] = row_in4(lds, o.lb, o.b, r, i);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                int i = b0 + 4 * (tid + 256 * u);
+                if (i < n) {
+                    f4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = row_ew<KIND>(av[u][e], two ? bv[u][e] : 0.0f, o.f0);
+                    row_put4(lds, o, yr, i, v);
+                }
+            }
+        }
+        return;
+    }
+    for (int i = tid; i < n; i += 256)
+        row_put(lds, o, yr, i, row_ew<KIND>(row_in(lds, o.la, o.a, r, i),
+                                              two ? row_in(lds, o.lb, o.b, r, i) : 0.0f, o.f0));
+}
+// An op read from the descriptor in LDS, its fields made wave-uniform (they are).
+__device__ __forceinline__ const float* uni_ptr(const float* p) {
+    unsigned long long v = (unsigned long long)p;
+    unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v), hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return (const float*)(((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ long long uni_ll(long long x) {
+    unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)x), hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)x >> 32));
+    return (long long)(((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ RowOp row_load(const RowOp& src) {
+    RowOp o = src;
+    o.kind = uni(o.kind); o.n = uni(o.n);
+    o.la = uni(o.la); o.lb = uni(o.lb); o.lc = uni(o.lc); o.ld = uni(o.ld);
+    o.out = uni(o.out); o.tmp = uni(o.tmp); o.i0 = uni(o.i0); o.i1 = uni(o.i1); o.vec = uni(o.vec);
+    o.f0 = __int_as_float(uni(__float_as_int(o.f0)));
+    o.a.g = uni_ptr(o.a.g); o.b.g = uni_ptr(o.b.g); o.c.g = uni_ptr(o.c.g); o.d.g = uni_ptr(o.d.g);
+    o.a.stride = uni_ll(o.a.stride); o.b.stride = uni_ll(o.b.stride);
+    o.c.stride = uni_ll(o.c.stride); o.d.stride = uni_ll(o.d.stride);
+    o.y = (float*)uni_ptr(o.y); o.ystride = uni_ll(o.ystride);
+    o.q0 = uni_ll(o.q0); o.q1 = uni_ll(o.q1);
+    o.dyn = (const long long*)uni_ptr((const float*)o.dyn);
+    return o;
+}
+KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
+    // the descriptor goes to LDS with one wide load per thread: its fields then cost one
+    // memory round trip, not one per op
+    __shared__ RowDesc d;
+    static_assert(sizeof(RowDesc) % 16 == 0, "descriptor copy in float4s");
+    for (int q = threadIdx.x; q < (int)(sizeof(RowDesc) / 16); q += blockDim.x)
+        ((f4*)&d)[q] = ((const f4*)&dk)[q];
+    __syncthreads();
+    extern __shared__ float lds[];
+    long long r = blockIdx.x;
+    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int nops = uni(d.nops);
+    // the operand rows the chain reads from global memory, copied straight into LDS, all in
+    // flight at once (instruction j of an entry: float4s 64j .. 64j + 63, one per lane)
+    int npf = uni(d.npf);
+    if (npf > 0) {
+        for (int e = 0; e < npf; e++) {
+            const float* src = uni_ptr(d.pf[e].g) + r * uni_ll(d.pf[e].stride);
+            int n4 = uni(d.pf[e].n) >> 2, plds = uni(d.pf[e].lds);
+            for (int j = wave; 64 * j < n4; j += 4) {
+                int c = 64 * j + lane;
+                if (c < n4)
+                    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + 4 * c),
+                                                     (__attribute__((address_space(3))) void*)(lds + plds + 256 * j),
+                                                     16, 0, 0);
+            }
+        }
+        vm_wait<0>();
+        lds_barrier();
+    }
+    for (int k = 0; k < nops; k++) {
+        const RowOp o = row_load(d.op[k]);
+        int kind = o.kind, n = o.n;
+        float* yr = o.y ? o.y + r * o.ystride : nullptr;
+        if (kind == R_COPY) {
+            row_elementwise<R_COPY>(o, lds, yr, r, tid);
+        } else if (kind == R_ADD) {
+            row_elementwise<R_ADD>(o, lds, yr, r, tid);
+        } else if (kind == R_MIX) {
+            row_elementwise<R_MIX>(o, lds, yr, r, tid);
+        } else if (kind == R_SILU) {
+            row_elementwise<R_SILU>(o, lds, yr, r, tid);
+        } else if (kind == R_ROPE) {
+            int heads = o.i0, dh = o.i1, half = dh / 2;
+            if (o.vec) {  // four consecutive i of one head per thread
+                int q4 = half >> 2;
+                for (int t = tid; t < heads * q4; t += 256) {
+                    int h = t / q4, i = 4 * (t % q4), at = h * dh;
+                    f4 c = row_in4(lds, o.lc, o.c, r, i), sn = row_in4(lds, o.ld, o.d, r, i);
+                    f4 a = row_in4(lds, o.la, o.a, r, at + i), b = row_in4(lds, o.la, o.a, r, at + half + i);
+                    f4 v0, v1;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        v0[e] = a[e] * c[e] - b[e] * sn[e];
+                        v1[e] = a[e] * sn[e] + b[e] * c[e];
+                    }
+                    row_put4(lds, o, yr, at + i, v0);
+                    row_put4(lds, o, yr, at + half + i, v1);
+                }
+            } else {
+                for (int t = tid; t < heads * half; t += 256) {
+                    int h = t / half, i = t % half, at = h * dh;
+                    float c = row_in(lds, o.lc, o.c, r, i), sn = row_in(lds, o.ld, o.d, r, i);
+                    float a = row_in(lds, o.la, o.a, r, at + i), b = row_in(lds, o.la, o.a, r, at + half + i);
+                    row_put(lds, o, yr, at + i, a * c - b * sn);
+                    row_put(lds, o, yr, at + half + i, a * sn + b * c);
+                }
+            }
+        } else if (kind == R_STORE) {
+            int heads = o.i0, dh = o.i1;
+            long long pos = dyn_or(o.dyn, o.q1);
+            long long slot = (pos + r) % o.q0;
+            if (o.vec) {
+                int d4 = dh >> 2;
+                for (int t = tid; t < heads * d4; t += 256) {
+                    int h = t / d4, e = 4 * (t % d4);
+                    *(f4*)(o.y + ((long long)h * o.q0 + slot) * dh + e) = row_in4(lds, o.la, o.a, r, h * dh + e);
+                }
+            } else {
+                for (int t = tid; t < heads * dh; t += 256) {
+                    int h = t / dh, e = t % dh;
+                    o.y[((long long)h * o.q0 + slot) * dh + e] = row_in(lds, o.la, o.a, r, t);
+                }
+            }
+        } else if (kind == R_RMS || kind == R_L2NORM) {
+            int size = o.i0, groups = n / size;
+            int src = o.la;
+            if (src < 0) {  // the row goes to LDS first, where the sums read it
+                if (o.vec) {
+                    for (int b0 = 0; b0 < n; b0 += 4 * 1024) {
+                        f4 av[4];
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            int i = b0 + 4 * (tid + 256 * u);
+                            if (i < n) av[u] = *(const f4*)(o.a.g + r * o.a.stride + i);
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            int i = b0 + 4 * (tid + 256 * u);
+                            if (i < n) *(f4*)(lds + o.tmp + i) = av[u];
+                        }
+                    }
+                } else {
+                    for (int i = tid; i < n; i += 256) lds[o.tmp + i] = o.a.g[r * o.a.stride + i];
+                }
+                lds_barrier();
+                src = o.tmp;
+            }
+            for (int grp = wave; grp < groups; grp += 4) {  // one wave per group
+                const float* in = lds + src + grp * size;
+                float dd = dot16_wave(in, size, lane);
+                float rr = kind == R_RMS ? 1.0f / sqrtf(dd / (float)size + o.f0)
+                                         : 1.0f / fmaxf(sqrtf(dd), 1e-12f);
+                if (o.vec) {
+                    for (int j = 4 * lane; j < size; j += 256) {
+                        f4 v = *(const f4*)(in + j), w, out;
+                        if (kind == R_RMS) w = row_in4(lds, o.lb, o.b, 0, j);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) out[e] = kind == R_RMS ? v[e] * rr * w[e] : v[e] * rr;
+                        row_put4(lds, o, yr, grp * size + j, out);
+                    }
+                } else {
+                    for (int j = lane; j < size; j += 64) {
+                        float v = kind == R_RMS ? in[j] * rr * row_in(lds, o.lb, o.b, 0, j) : in[j] * rr;
+                        row_put(lds, o, yr, grp * size + j, v);
+                    }
+                }
+            }
+        } else if (kind == R_FOLD) {
+            if (o.vec) {
+                for (int b0 = 0; b0 < n; b0 += 4 * 256) {
+                    int i = b0 + 4 * tid;
+                    if (i >= n) continue;
+                    const float* pp = o.a.g + r * o.a.stride + i;
+                    f4 v = *(const f4*)pp;
+                    for (int z0 = 1; z0 < o.i0; z0 += 4) {  // four partials in flight
+                        f4 w[4];
+#pragma unroll
+                        for (int u = 0; u < 4; u++)
+                            if (z0 + u < o.i0) w[u] = *(const f4*)(pp + (z0 + u) * o.q0);
+#pragma unroll
+                        for (int u = 0; u < 4; u++)
+                            if (z0 + u < o.i0)
+#pragma unroll
+                                for (int e = 0; e < 4; e++) v[e] = v[e] + w[u][e];
+                    }
+                    row_put4(lds, o, yr, i, v);
+                }
+            } else {
+                for (int i = tid; i < n; i += 256) {
+                    const float* pp = o.a.g + r * o.a.stride + i;
+                    float v = pp[0];
+                    for (int z = 1; z < o.i0; z++) v = v + pp[z * o.q0];
+                    row_put(lds, o, yr, i, v);
+                }
+            }
+        }
+        lds_barrier();
+    }
+}
+
 // One token of gated linear attention per head, one workgroup per head (the m = 1 case of
 // gla_body, same expressions). When `l2`, q and k are first l2-normalised per head
 // (model.rs:465-467, the expressions of slm_l2norm); when `fuse`, the head RMSNorm and the

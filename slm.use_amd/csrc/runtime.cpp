@@ -107,6 +107,7 @@ struct Kernels {
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
     hipFunction_t attn_dec[3];               // one-token attention, dim tiles 1, 2, 4
+    hipFunction_t rows;                      // prompt row chains
 };
 
 }  // namespace
@@ -330,6 +331,70 @@ void drop_graphs(slm_hip* c) {
 // per-op lowering (the unfused kernels)
 // ---------------------------------------------------------------------------------------
 
+// A linear (p0 y, p1 w, p2 x; n0 rows, n1 cols, n2 m). With `fold_ns`, a split GEMM's
+// partials are left in c->gpart for the caller to add (*fold_ns: the split count, 1 when
+// the GEMM wrote y itself).
+int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_ns) {
+    const Kernels& k = c->k;
+    const float* const* p = o.p;
+    const int64_t* n = o.n;
+    if (fold_ns) *fold_ns = 1;
+    int64_t rows = n[0], cols = n[1], m = n[2];
+    if (cols == 0) {
+        out.push_back(mk(k.fill, blocks_for(m * rows), 1, 1, 256, 0, p[0],
+                         (long long)(m * rows), 0.0f));
+        return SLM_OK;
+    }
+    int vec = (cols % 4 == 0 && aligned16(p[1]) && aligned16(p[2])) ? 1 : 0;
+    int64_t kblocks = (cols + 15) / 16, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
+    double ab = 4.0 * (double)(rows * cols + m * cols + m * rows);
+    if (m <= 16 && nsl <= 64) {
+        uint32_t waves = (uint32_t)std::min<int64_t>(nsl, 8);
+        out.push_back(mk(k.lin_small[vec], (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
+                         (uint32_t)(nsl * 1024), p[0], p[1], p[2], (int)rows, (int)cols,
+                         (int)m));
+        out.back().abytes = ab;
+    } else if (vec) {  // the LDS-staged GEMM, one workgroup column per split
+        int64_t ns = (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
+        if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
+            return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
+        if (cols % 64 == 0) {
+            // the pipelined GEMM, with the row tile that leaves the busiest CU the
+            // least work: rows per tile times the workgroups a CU runs (32-row tiles
+            // of four waves go two to a CU, the others of eight waves one), the larger
+            // tile on a tie
+            int bm = 32;
+            int64_t best = -1;
+            for (int t : {32, 64, 96, 128}) {
+                int64_t wgs = ((rows + t - 1) / t) * ((m + 63) / 64) * ns;
+                int64_t per_cu = t == 32 ? 2 : 1;
+                int64_t rounds = (wgs + per_cu * CU_COUNT - 1) / (per_cu * CU_COUNT);
+                int64_t sharing = std::min<int64_t>(per_cu, (wgs + CU_COUNT - 1) / CU_COUNT);
+                int64_t cost = rounds * t * sharing;
+                if (best < 0 || cost <= best) best = cost, bm = t;
+            }
+            uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
+            hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
+            out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
+                             (uint32_t)ns, bm == 32 ? 256 : bm == 96 ? 512 : 1024, shmem, p[0], c->gpart,
+                             p[1], p[2], (int)rows, (int)cols, (int)m));
+        } else {
+            out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
+                             (uint32_t)ns, 256, 0, p[0], c->gpart, p[1], p[2], (int)rows,
+                             (int)cols, (int)m));
+        }
+        if (fold_ns) *fold_ns = ns;  // the caller adds the partials
+        else if (ns > 1)
+            out.push_back(mk(k.fold, blocks_for(m * rows), 1, 1, 256, 0, p[0],
+                             (const float*)c->gpart, (long long)(m * rows), (int)ns));
+    } else {
+        out.push_back(mk(k.lin_big[vec], (uint32_t)((rows + 63) / 64),
+                         (uint32_t)((m + 63) / 64), 1, 256, 0, p[0], p[1], p[2],
+                         (int)rows, (int)cols, (int)m));
+    }
+    return SLM_OK;
+}
+
 int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
     const Kernels& k = c->k;
     const float* const* p = o.p;
@@ -351,61 +416,8 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                              (long long)(n[0] * n[3]), (long long)n[1], (long long)n[2],
                              (long long)n[3]));
             return SLM_OK;
-        case OP_LINEAR: {  // p0 y, p1 w, p2 x; n0 rows, n1 cols, n2 m
-            int64_t rows = n[0], cols = n[1], m = n[2];
-            if (cols == 0) {
-                out.push_back(mk(k.fill, blocks_for(m * rows), 1, 1, 256, 0, p[0],
-                                 (long long)(m * rows), 0.0f));
-                return SLM_OK;
-            }
-            int vec = (cols % 4 == 0 && aligned16(p[1]) && aligned16(p[2])) ? 1 : 0;
-            int64_t kblocks = (cols + 15) / 16, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
-            double ab = 4.0 * (double)(rows * cols + m * cols + m * rows);
-            if (m <= 16 && nsl <= 64) {
-                uint32_t waves = (uint32_t)std::min<int64_t>(nsl, 8);
-                out.push_back(mk(k.lin_small[vec], (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
-                                 (uint32_t)(nsl * 1024), p[0], p[1], p[2], (int)rows, (int)cols,
-                                 (int)m));
-                out.back().abytes = ab;
-            } else if (vec) {  // the LDS-staged GEMM, one workgroup column per split
-                int64_t ns = (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
-                if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
-                    return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
-                if (cols % 64 == 0) {
-                    // the pipelined GEMM, with the row tile that leaves the busiest CU the
-                    // least work: rows per tile times the workgroups a CU runs (32-row tiles
-                    // of four waves go two to a CU, the others of eight waves one), the larger
-                    // tile on a tie
-                    int bm = 32;
-                    int64_t best = -1;
-                    for (int t : {32, 64, 96, 128}) {
-                        int64_t wgs = ((rows + t - 1) / t) * ((m + 63) / 64) * ns;
-                        int64_t per_cu = t == 32 ? 2 : 1;
-                        int64_t rounds = (wgs + per_cu * CU_COUNT - 1) / (per_cu * CU_COUNT);
-                        int64_t sharing = std::min<int64_t>(per_cu, (wgs + CU_COUNT - 1) / CU_COUNT);
-                        int64_t cost = rounds * t * sharing;
-                        if (best < 0 || cost <= best) best = cost, bm = t;
-                    }
-                    uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
-                    hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
-                    out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
-                                     (uint32_t)ns, bm == 32 ? 256 : bm == 96 ? 512 : 1024, shmem, p[0], c->gpart,
-                                     p[1], p[2], (int)rows, (int)cols, (int)m));
-                } else {
-                    out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
-                                     (uint32_t)ns, 256, 0, p[0], c->gpart, p[1], p[2], (int)rows,
-                                     (int)cols, (int)m));
-                }
-                if (ns > 1)
-                    out.push_back(mk(k.fold, blocks_for(m * rows), 1, 1, 256, 0, p[0],
-                                     (const float*)c->gpart, (long long)(m * rows), (int)ns));
-            } else {
-                out.push_back(mk(k.lin_big[vec], (uint32_t)((rows + 63) / 64),
-                                 (uint32_t)((m + 63) / 64), 1, 256, 0, p[0], p[1], p[2],
-                                 (int)rows, (int)cols, (int)m));
-            }
-            return SLM_OK;
-        }
+        case OP_LINEAR:
+            return lower_linear(c, o, out, nullptr);
         case OP_ADD:
             out.push_back(mk(k.add, blocks_for(n[0]), 1, 1, 256, 0, p[0], p[1], p[2], (long long)n[0]));
             return SLM_OK;
@@ -756,6 +768,299 @@ struct Planner {
     std::vector<VpSrc> next_pend;  // what a fused kernel leaves pending (a split's fold)
     const Op* l2q = nullptr;  // l2norm ops held back for the GLA kernel that reads them
     const Op* l2k = nullptr;
+
+    // ---- prompt row chains (m > 1): see RowDesc ----
+    struct RSlot {  // rows [g + r·stride, + n) of an op's output, held in LDS at `lds`
+        const float* g;
+        int64_t stride, n;
+        int lds;
+    };
+    int64_t rrows = 0;               // the chain's token rows (0: no chain)
+    size_t rnext = 0;                // index of the first op after the chain
+    int64_t last_m = 0;              // tokens of the last prompt linear
+    RowDesc rd{};
+    std::vector<const Op*> rsrc;     // the op of each chain entry (null: a split's fold)
+    Rec rfold{};                     // what a chain holding only a fold launches instead
+    std::vector<RSlot> rslots;
+    std::vector<Range> rwr;          // every global range the chain's ops write (all rows)
+    std::vector<char> rwr_slot;      // ... and whether an LDS slot holds it
+    int rlds = 0;                    // LDS floats the chain uses
+    static constexpr int ROW_LDS_MAX = 40000;
+
+    static Range rows_rng(const float* g, int64_t stride, int64_t n, int64_t R) {
+        return Range{(uintptr_t)g, (uintptr_t)(g + (R - 1) * stride + n)};
+    }
+    // Rows the op states itself (0: it is a flat vector, split by the chain's rows).
+    static int64_t op_rows(const Op& o) {
+        switch (o.kind) {
+            case OP_COLUMNS: case OP_ROPE: case OP_STORE: case OP_ADD_ROW: return o.n[0];
+            default: return 0;
+        }
+    }
+    // The op as a row op over R rows (operands unresolved); false if it is not row-local.
+    static bool row_lower(const Op& o, int64_t R, RowOp* ro, Range* foot) {
+        const float* const* p = o.p;
+        const int64_t* n = o.n;
+        std::memset(ro, 0, sizeof *ro);
+        ro->la = ro->lb = ro->lc = ro->ld = ro->out = ro->tmp = -1;
+        auto flat = [&](int64_t total, int64_t* len) {
+            if (total <= 0 || total % R) return false;
+            *len = total / R;
+            return true;
+        };
+        int64_t len = 0;
+        switch (o.kind) {
+            case OP_COPY:
+                if (!flat(n[0], &len)) return false;
+                ro->kind = R_COPY; ro->a = {p[1], len};
+                break;
+            case OP_COLUMNS:  // n0 m, n1 stride, n2 off, n3 len
+                if (n[0] != R) return false;
+                len = n[3];
+                ro->kind = R_COPY; ro->a = {p[1] + n[2], n[1]};
+                break;
+            case OP_ADD:
+                if (!flat(n[0], &len)) return false;
+                ro->kind = R_ADD; ro->a = {p[1], len}; ro->b = {p[2], len};
+                break;
+            case OP_ADD_ROW:  // n0 m, n1 d
+                if (n[0] != R) return false;
+                len = n[1];
+                ro->kind = R_ADD; ro->a = {p[1], len}; ro->b = {p[2], 0};
+                break;
+            case OP_MIX:
+                if (!flat(n[0], &len)) return false;
+                ro->kind = R_MIX; ro->a = {p[1], len}; ro->b = {p[2], len}; ro->f0 = o.f[0];
+                break;
+            case OP_SILU_MUL:
+                if (!flat(n[0], &len)) return false;
+                ro->kind = R_SILU; ro->a = {p[1], len}; ro->b = {p[2], len};
+                break;
+            case OP_ROPE:  // n0 m, n1 heads, n2 dh
+                if (n[0] != R || n[2] % 2) return false;
+                len = n[1] * n[2];
+                ro->kind = R_ROPE; ro->a = {p[1], len}; ro->c = {p[2], n[2] / 2}; ro->d = {p[3], n[2] / 2};
+                ro->i0 = (int32_t)n[1]; ro->i1 = (int32_t)n[2];
+                break;
+            case OP_STORE:  // p0 cache, p1 src; n0 m, n1 cap, n2 heads, n3 dh, n4 pos
+                if (n[0] != R) return false;
+                len = n[2] * n[3];
+                ro->kind = R_STORE; ro->a = {p[1], len};
+                ro->i0 = (int32_t)n[2]; ro->i1 = (int32_t)n[3]; ro->q0 = n[1]; ro->q1 = n[4];
+                ro->dyn = (const long long*)o.dyn;
+                ro->n = (int32_t)len;
+                ro->y = (float*)p[0];
+                *foot = rng(p[0], n[2] * n[1] * n[3]);
+                return true;
+            case OP_RMS:
+            case OP_L2NORM:  // n0 groups, n1 size; f0 eps
+                if (n[0] % R || n[1] <= 0) return false;
+                len = n[0] / R * n[1];
+                ro->kind = o.kind == OP_RMS ? R_RMS : R_L2NORM;
+                ro->a = {p[1], len};
+                if (o.kind == OP_RMS) ro->b = {p[2], 0};
+                ro->i0 = (int32_t)n[1]; ro->f0 = o.f[0];
+                break;
+            default:
+                return false;
+        }
+        if (len <= 0 || len > 16384) return false;
+        ro->n = (int32_t)len;
+        ro->y = (float*)p[0];
+        ro->ystride = len;
+        *foot = rows_rng(p[0], len, len, R);
+        return true;
+    }
+    // Where operand `in` (n floats a row) comes from: an LDS slot, global memory (-1), or
+    // nowhere safe (false: an earlier op of the chain wrote part of it).
+    bool row_src(const RowIn& in, int64_t n, int* lds) {
+        Range f = rows_rng(in.g, in.stride, n, rrows);
+        for (size_t q = rslots.size(); q-- > 0;) {
+            const RSlot& sl = rslots[q];
+            if (!overlap(f, rows_rng(sl.g, sl.stride, sl.n, rrows))) continue;
+            if (in.stride == sl.stride && in.g >= sl.g && in.g + n <= sl.g + sl.n) {
+                *lds = sl.lds + (int)(in.g - sl.g);
+                return true;
+            }
+            return false;
+        }
+        for (size_t q = 0; q < rwr.size(); q++)
+            if (!rwr_slot[q] && overlap(f, rwr[q])) return false;
+        *lds = -1;
+        return true;
+    }
+    // Appends op `src` (or a fold when null) to the chain; false when it cannot join.
+    // Hazards between workgroups (rows) are ruled out: a global range the chain reads may
+    // be written later in the chain only with the same row mapping (each row by its own
+    // workgroup, after that workgroup read it); what an op reads that an earlier op wrote
+    // comes from that op's LDS row; an output may overwrite an earlier one only exactly.
+    struct GRead {
+        const float* g;
+        int64_t stride, len;
+        Range f;
+    };
+    std::vector<GRead> rreads;
+    bool row_add(const Op* src, RowOp ro, Range foot) {
+        if (rd.nops >= SLM_ROW_OPS) return false;
+        int n = ro.n;
+        bool store = ro.kind == R_STORE, norm = ro.kind == R_RMS || ro.kind == R_L2NORM;
+        struct Operand { RowIn* in; int* l; int64_t len; };
+        Operand opd[4] = {{&ro.a, &ro.la, (int64_t)n},
+                          {&ro.b, &ro.lb, norm ? (int64_t)ro.i0 : (int64_t)n},
+                          {&ro.c, &ro.lc, (int64_t)ro.i1 / 2},
+                          {&ro.d, &ro.ld, (int64_t)ro.i1 / 2}};
+        std::vector<GRead> reads;
+        for (auto& q : opd) {
+            if (!q.in->g) continue;
+            if (ro.kind == R_FOLD && q.in == &ro.a) {  // the partials of the GEMM before
+                reads.push_back({ro.a.g, ro.a.stride, n,
+                                 Range{(uintptr_t)ro.a.g, (uintptr_t)(ro.a.g + ro.i0 * ro.q0)}});
+                continue;
+            }
+            if (!row_src(*q.in, q.len, q.l)) return false;
+            if (*q.l < 0) reads.push_back({q.in->g, q.in->stride, q.len, rows_rng(q.in->g, q.in->stride, q.len, rrows)});
+        }
+        auto rowwise = [&](const GRead& x) {
+            return !store && x.g == ro.y && x.stride == ro.ystride && x.len == n;
+        };
+        for (auto& x : reads)
+            if (overlap(x.f, foot) && !rowwise(x)) return false;
+        for (auto& x : rreads)
+            if (overlap(x.f, foot) && !rowwise(x)) return false;
+        int elide = -1;
+        for (size_t q = 0; q < rwr.size(); q++) {
+            if (!overlap(rwr[q], foot)) continue;
+            const RowOp& e = rd.op[q];
+            if (store || e.kind == R_STORE || e.y != ro.y || e.ystride != ro.ystride || e.n != ro.n ||
+                elide >= 0)
+                return false;
+            elide = (int)q;
+        }
+        // float4 moves: every row length, offset and stride a multiple of 4, every global
+        // base 16-byte aligned
+        bool vec = n % 4 == 0 && (ro.kind != R_ROPE || ro.i1 % 8 == 0) &&
+                   (ro.kind != R_STORE || ro.i1 % 4 == 0) && (!norm || ro.i0 % 4 == 0) &&
+                   (!ro.y || (aligned16(ro.y) && ro.ystride % 4 == 0)) &&
+                   (ro.kind != R_FOLD || ro.q0 % 4 == 0);
+        for (auto& q : opd) {
+            if (!q.in->g) continue;
+            if (*q.l >= 0) vec = vec && *q.l % 4 == 0;
+            else vec = vec && aligned16(q.in->g) && q.in->stride % 4 == 0;
+        }
+        ro.vec = vec ? 1 : 0;
+        // global operand rows go to LDS before the first op when they fit the table: an
+        // entry that already holds the rows serves again
+        int pf_need = 0;
+        std::vector<std::pair<int, int>> pf_new;  // (operand, entry) of new entries
+        struct PfUse { int q, entry; int64_t off; };
+        std::vector<PfUse> pf_use;
+        for (int q = 0; q < 4; q++) {
+            Operand& x = opd[q];
+            if (!x.in->g || *x.l >= 0 || (ro.kind == R_FOLD && q == 0)) continue;
+            if (x.len % 4 || !aligned16(x.in->g) || x.in->stride % 4) continue;
+            int hit = -1;
+            int64_t off = 0;
+            for (int e = 0; e < rd.npf; e++) {
+                const RowPf& p = rd.pf[e];
+                if (p.stride == x.in->stride && x.in->g >= p.g && x.in->g + x.len <= p.g + p.n) {
+                    hit = e;
+                    off = x.in->g - p.g;
+                    break;
+                }
+            }
+            if (hit < 0) {
+                if (rd.npf + (int)pf_new.size() >= SLM_ROW_PF) continue;
+                hit = rd.npf + (int)pf_new.size();
+                pf_new.push_back({q, hit});
+                pf_need += (int)((x.len + 255) / 256 * 256);
+            }
+            pf_use.push_back({q, hit, off});
+        }
+        int need = store ? 0 : (n + 3) & ~3;
+        bool a_pf = false;
+        for (auto& u : pf_use) a_pf |= u.q == 0;
+        int tmp = norm && ro.la < 0 && !a_pf ? (n + 3) & ~3 : 0;
+        if (rlds + need + tmp + pf_need > ROW_LDS_MAX) return false;
+        for (auto& pn : pf_new) {  // a new entry: the operand's rows, in whole 64-float4 runs
+            Operand& x = opd[pn.first];
+            RowPf& p = rd.pf[pn.second];
+            p.g = x.in->g;
+            p.stride = x.in->stride;
+            p.n = (int32_t)x.len;
+            p.lds = rlds;
+            rlds += (int)((x.len + 255) / 256 * 256);
+        }
+        rd.npf += (int)pf_new.size();
+        for (auto& u : pf_use) {
+            *opd[u.q].l = rd.pf[u.entry].lds + (int)u.off;
+            if (u.off % 4) ro.vec = 0;
+        }
+        // what the chain now reads from LDS it read at the start: the ranges stay recorded
+        // as read, so later writes into them are held to the same rows
+        if (tmp) {
+            ro.tmp = rlds;
+            rlds += tmp;
+        }
+        if (!store) {
+            ro.out = rlds;
+            rlds += need;
+        }
+        if (elide >= 0) rd.op[elide].y = nullptr;
+        for (auto& x : reads) rreads.push_back(x);
+        rd.op[rd.nops++] = ro;
+        rsrc.push_back(src);
+        rwr.push_back(foot);
+        rwr_slot.push_back(!store);
+        if (!store) rslots.push_back({ro.y, ro.ystride, (int64_t)n, ro.out});
+        return true;
+    }
+    void row_reset() {
+        rrows = 0;
+        std::memset(&rd, 0, sizeof rd);
+        rsrc.clear();
+        rslots.clear();
+        rwr.clear();
+        rwr_slot.clear();
+        rreads.clear();
+        rlds = 0;
+    }
+    int row_flush() {
+        if (!rrows) return SLM_OK;
+        if (rd.nops == 1) {  // alone: its own kernel
+            if (rsrc[0]) TRY(lower_one(c, *rsrc[0], out));
+            else out.push_back(rfold);
+        } else if (rd.nops > 1) {
+            // the last op of each global range writes it, unless no later op reads it (the
+            // chain's own readers take the LDS row)
+            for (int q = 0; q < rd.nops; q++)
+                if (rd.op[q].y && rd.op[q].kind != R_STORE && dead_after(ops, rnext, rwr[q]))
+                    rd.op[q].y = nullptr;
+            Rec r = mk_desc(c->k.rows, (uint32_t)rrows, 256, (uint32_t)(rlds * 4), rd);
+            out.push_back(r);
+        }
+        row_reset();
+        return SLM_OK;
+    }
+    // Tries op o as the chain's next op (starting a chain if there is none).
+    bool row_try(const Op& o) {
+        int64_t R = op_rows(o);
+        if (!rrows) {
+            if (!R) R = last_m;
+            if (R < 2) return false;
+            RowOp ro;
+            Range foot;
+            if (!row_lower(o, R, &ro, &foot)) return false;
+            rrows = R;
+            if (row_add(&o, ro, foot)) return true;
+            row_reset();
+            return false;
+        }
+        if (R && R != rrows) return false;
+        RowOp ro;
+        Range foot;
+        if (!row_lower(o, rrows, &ro, &foot)) return false;
+        return row_add(&o, ro, foot);
+    }
 
     // Why a one-token linear runs unfused: printed when SLM_HIP_PLAN_TRACE is set.
     size_t nofuse(size_t i, const char* why) {
@@ -1254,6 +1559,7 @@ struct Planner {
             const Op& o = ops[i];
             VpSrc v;
             if (fuse && pend.size() < SLM_VP_MAX && vp_of(o, &v)) {
+                TRY(row_flush());
                 // a held l2norm's output may not be touched before the GLA kernel
                 bool clash = false;
                 for (const Op* h : {l2q, l2k})
@@ -1268,6 +1574,7 @@ struct Planner {
                 i++;
                 continue;
             }
+            if (o.kind == OP_LINEAR && o.n[2] == 1) last_m = 0;
             if (fuse && o.kind == OP_LINEAR && o.n[2] == 1 && !l2q) {
                 next_pend.clear();
                 size_t used = try_fg(i);
@@ -1279,7 +1586,40 @@ struct Planner {
                     continue;
                 }
             }
+            // prompt rows: element-wise ops join a row chain; a split GEMM's fold starts one
+            if (fuse && pend.empty() && !l2q && o.kind != OP_LINEAR && row_try(o)) {
+                rnext = ++i;
+                continue;
+            }
+            TRY(row_flush());
             TRY(flush_pending());
+            if (fuse && o.kind == OP_LINEAR && o.n[2] > 1 && !l2q) {
+                int64_t ns = 1, rows = o.n[0], m = o.n[2];
+                TRY(lower_linear(c, o, out, &ns));
+                last_m = m;
+                if (ns > 1) {
+                    rfold = mk(c->k.fold, blocks_for(m * rows), 1, 1, 256, 0, o.p[0],
+                               (const float*)c->gpart, (long long)(m * rows), (int)ns);
+                    RowOp ro;
+                    std::memset(&ro, 0, sizeof ro);
+                    ro.kind = R_FOLD;
+                    ro.la = ro.lb = ro.lc = ro.ld = ro.out = ro.tmp = -1;
+                    ro.n = (int32_t)rows;
+                    ro.a = {c->gpart, rows};
+                    ro.i0 = (int32_t)ns;
+                    ro.q0 = m * rows;
+                    ro.y = (float*)o.p[0];
+                    ro.ystride = rows;
+                    rrows = m;
+                    rnext = i + 1;
+                    if (rows > 16384 || !row_add(nullptr, ro, rows_rng(o.p[0], rows, rows, m))) {
+                        row_reset();
+                        out.push_back(rfold);
+                    }
+                }
+                i++;
+                continue;
+            }
             if (fuse && o.kind == OP_GLA) {
                 size_t used = try_gla(i);
                 if (used) {
@@ -1291,6 +1631,7 @@ struct Planner {
             TRY(lower_one(c, o, out));
             i++;
         }
+        TRY(row_flush());
         TRY(flush_pending());
         return flush_l2();
     }
@@ -1548,7 +1889,7 @@ int load_kernels(slm_hip* c) {
                {&k.attn[2], "slm_attn_part_4"}, {&k.attn[3], "slm_attn_part_8"},
                {&k.attn[4], "slm_attn_part_16"},
                {&k.attn_dec[0], "slm_attn_dec_1"}, {&k.attn_dec[1], "slm_attn_dec_2"},
-               {&k.attn_dec[2], "slm_attn_dec_4"}};
+               {&k.attn_dec[2], "slm_attn_dec_4"}, {&k.rows, "slm_rows"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;
