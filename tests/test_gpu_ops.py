@@ -385,3 +385,95 @@ def test_fusion_pattern(hip, case):
         assert pb["kernels"] < pa["kernels"]
     for k in a:
         assert np.array_equal(a[k], b[k]), (case, k, float(np.abs(a[k] - b[k]).max()))
+
+
+# ---------------------------------------------------------------------------------------
+# prompt row chains: the element-wise ops between two GEMMs as one launch per chain
+# ---------------------------------------------------------------------------------------
+
+ROW_CASES = ["attn_in", "mlp", "inplace", "overlap"]
+
+
+@pytest.mark.parametrize("m", [37, 256])
+@pytest.mark.parametrize("case", ROW_CASES)
+def test_row_chain(hip, case, m):
+    """A prompt chunk's element-wise ops fused into row chains give the bits of one launch
+    per op, for in-place updates, operands read from an earlier op's output at an offset,
+    a shared vector read by every row and outputs overwritten later in the chain."""
+    d, heads, dh, hid, cap, pos = 768, 12, 64, 3072, 4352, 100
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(m * 32), hip.alloc(m * 32)
+    wsq = hip.upload(rnd(d, d, scale=0.02))
+    wqkv = hip.upload(rnd(3 * d, d, scale=0.02))
+    wup = hip.upload(rnd(2 * hid, d, scale=0.02))
+    wdown = hip.upload(rnd(d, hid, scale=0.02))
+    x = hip.upload(rnd(m, d))
+    res = hip.upload(rnd(m, d))
+    row = hip.upload(rnd(d))
+    nw = hip.upload(rnd(d))
+    kr0, vr0 = rnd(heads, cap, dh), rnd(heads, cap, dh)
+
+    def outs():
+        o = {k: hip.alloc(n) for k, n in
+             dict(y=m * 3 * d, q=m * d, k=m * d, k2=m * d, v=m * d, up=m * 2 * hid, g=m * hid,
+                  u=m * hid, h=m * hid, dn=m * d, t=m * d, n=m * d, z=m * d, s=m * d,
+                  y2=m * d, a=m * d // 2, b=m * d, c2=m * d // 2,
+                  kr=heads * cap * dh, vr=heads * cap * dh).items()}
+        hip.write(o["kr"], kr0)
+        hip.write(o["vr"], vr0)
+        return o
+
+    def body(o):
+        if case == "attn_in":
+            hip.linear(o["y"].ptr, wqkv.ptr, 3 * d, d, x.ptr, m)
+            hip.columns(o["q"].ptr, o["y"].ptr, m, 3 * d, 0, d)
+            hip.rope(o["q"].ptr, o["q"].ptr, cs.ptr, sn.ptr, m, heads, dh)
+            hip.columns(o["k"].ptr, o["y"].ptr, m, 3 * d, d, d)
+            hip.rope(o["k2"].ptr, o["k"].ptr, cs.ptr, sn.ptr, m, heads, dh)
+            hip.columns(o["v"].ptr, o["y"].ptr, m, 3 * d, 2 * d, d)
+            hip.store(o["kr"].ptr, o["k2"].ptr, pos, m, cap, heads, dh)
+            hip.store(o["vr"].ptr, o["v"].ptr, pos, m, cap, heads, dh)
+            hip.linear(o["t"].ptr, wsq.ptr, d, d, o["q"].ptr, m)
+        elif case == "mlp":  # a split GEMM's fold opens the second chain
+            hip.linear(o["up"].ptr, wup.ptr, 2 * hid, d, x.ptr, m)
+            hip.columns(o["g"].ptr, o["up"].ptr, m, 2 * hid, 0, hid)
+            hip.columns(o["u"].ptr, o["up"].ptr, m, 2 * hid, hid, hid)
+            hip.silu_mul(o["h"].ptr, o["g"].ptr, o["u"].ptr, m * hid)
+            hip.linear(o["dn"].ptr, wdown.ptr, d, hid, o["h"].ptr, m)
+            hip.add(o["t"].ptr, res.ptr, o["dn"].ptr, m * d)
+            hip.rms(o["n"].ptr, o["t"].ptr, nw.ptr, m, d, 1e-6)
+            hip.linear(o["z"].ptr, wsq.ptr, d, d, o["n"].ptr, m)
+        elif case == "inplace":
+            hip.linear(o["t"].ptr, wsq.ptr, d, d, x.ptr, m)
+            hip.add(o["t"].ptr, o["t"].ptr, res.ptr, m * d)
+            hip.rms(o["t"].ptr, o["t"].ptr, nw.ptr, m, d, 1e-6)
+            hip.add_row(o["t"].ptr, o["t"].ptr, row.ptr, m, d)
+            hip.mix(o["z"].ptr, o["t"].ptr, res.ptr, m * d, 0.3)
+            hip.copy(o["s"].ptr, o["z"].ptr, m * d)
+            hip.l2norm(o["n"].ptr, o["s"].ptr, m * heads, dh)
+        elif case == "overlap":
+            hip.linear(o["t"].ptr, wsq.ptr, d, d, x.ptr, m)
+            hip.add(o["y2"].ptr, o["t"].ptr, res.ptr, m * d)
+            hip.columns(o["a"].ptr, o["y2"].ptr, m, d, d // 4, d // 2)
+            hip.rope(o["b"].ptr, o["y2"].ptr, cs.ptr, sn.ptr, m, heads, dh)
+            hip.add_row(o["z"].ptr, o["b"].ptr, row.ptr, m, d)
+            hip.add(o["y2"].ptr, o["z"].ptr, o["y2"].ptr, m * d)
+            hip.rms(o["n"].ptr, o["y2"].ptr, nw.ptr, m, d, 1e-6)
+            hip.columns(o["c2"].ptr, o["n"].ptr, m, d, 0, d // 2)
+            hip.copy(o["s"].ptr, o["y2"].ptr, m * d)
+
+    got = []
+    for fuse in (True, False, True):  # the first pass grows the backend's buffers (a growth
+        o = outs()                     # ends the recorded step early)
+        hip.set_fusion(fuse)
+        hip.rope_table(cs.ptr, sn.ptr, inv.ptr, pos, m, 32)
+        body(o)
+        hip.flush()
+        plan = hip.last_plan()
+        hip.set_fusion(True)
+        got.append(({k: b.read() for k, b in o.items()}, plan))
+    _, (a, pa), (b, pb) = got
+    print(case, m, "unfused", pa, "fused", pb)
+    assert pb["kernels"] < pa["kernels"]
+    for k in a:
+        assert np.array_equal(a[k], b[k]), (case, m, k, float(np.abs(a[k] - b[k]).max()))
