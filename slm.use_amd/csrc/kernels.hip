@@ -1119,6 +1119,194 @@ ATTN_PART(4)
 ATTN_PART(8)
 ATTN_PART(16)
 
+// Prompt attention with the keys and values of a superblock shared in LDS: a workgroup of
+// 16 waves takes ATTN_QG query tiles of one key head against one superblock. The waves
+// first copy the superblock's 256 keys and values into LDS (rows of 16 chunks of 16 bytes,
+// chunk c at c ^ (key & 15)); then wave w runs segment w % 4 for query tile w / 4 with the
+// arithmetic of attn_segment (operands from LDS instead of registers; dims at or past dh
+// read as zero, as there). The segments of each tile are folded in order into superblock
+// partials part[z][qidx][head][2 + 16·DT], which slm_attn_combine then combines. Grid
+// (query tile groups, key heads, superblock slots).
+#define ATTN_QG 4
+template <int DT>
+__device__ void attn_seg_lds(const Col& col, const f4 (&qv)[DT], const float* kt,
+                             const float* vt, long long seg_lo, int dh, float scale, float& mo,
+                             float& lo, f4 (&o)[DT]) {
+    int lane = threadIdx.x & 63;
+    int i = lane & 15, g = lane >> 4;
+    mo = NEG_INF;
+    lo = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+    for (int st = 0; st < 4; st++) {
+        long long b0 = seg_lo + 16 * st;
+        bool sees = col.valid && col.lo < b0 + 16 && col.hi > b0;
+        if (__ballot(sees) == 0) continue;
+        // scores: key 16st + i of the segment, dims 16t + 4g .. +3 as the A operand
+        int kk = 16 * st + i;
+        f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < DT; t++) {
+            f4 kr = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (16 * t + 4 * g < dh) kr = *(const f4*)(kt + 4 * (16 * kk + ((4 * t + g) ^ (kk & 15))));
+            s = mfma4(kr.x, qv[t].x, s);
+            s = mfma4(kr.y, qv[t].y, s);
+            s = mfma4(kr.z, qv[t].z, s);
+            s = mfma4(kr.w, qv[t].w, s);
+        }
+        // values: MFMA r takes value of key 16st + 4g + r, dim 16dt + i
+        float vr[4][DT];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int kv = 16 * st + 4 * g + r;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                int dd = 16 * dt + i;
+                vr[r][dt] = dd < dh ? vt[4 * (16 * kv + ((dd >> 2) ^ (kv & 15))) + (dd & 3)] : 0.0f;
+            }
+        }
+        float sv[4];
+        bool any = false;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            long long kp = b0 + 4 * g + r;
+            bool ok = kp >= col.lo && kp < col.hi;
+            sv[r] = ok ? s[r] * scale : NEG_INF;
+            any = any || ok;
+        }
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        int anyi = any ? 1 : 0;
+        anyi |= __shfl_xor(anyi, 16);
+        anyi |= __shfl_xor(anyi, 32);
+        float mnew = fmaxf(mo, mx);
+        float muse = mnew == NEG_INF ? 0.0f : mnew;
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) p[r] = sv[r] == NEG_INF ? 0.0f : expf(sv[r] - muse);
+        float rs = ((p[0] + p[1]) + p[2]) + p[3];
+        rs = rs + __shfl_xor(rs, 16);
+        rs = rs + __shfl_xor(rs, 32);
+        float alpha = expf(mo - muse);
+        f4 on[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) on[dt] = o[dt] * alpha;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) on[dt] = mfma4(vr[r][dt], p[r], on[dt]);
+        if (anyi) {
+            lo = lo * alpha + rs;
+            mo = mnew;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) o[dt] = on[dt];
+        }
+    }
+}
+
+template <int DT>
+__device__ void attn_pq_body(float* __restrict__ part, const float* __restrict__ q,
+                             const float* __restrict__ kc, const float* __restrict__ vc,
+                             const long long* __restrict__ dyn, long long pos_imm, int m,
+                             long long reach, long long gap, long long cap, int heads,
+                             int key_heads, int dh, float scale) {
+    static_assert(DT >= 1 && DT <= 4, "shared-superblock attention: head size at most 64");
+    constexpr int DP = 16 * DT;
+    constexpr int NT = 64 * SLM_SB_SEGS * ATTN_QG;
+    extern __shared__ float lds[];  // keys [256][64], values [256][64]; then the fold slots
+    float* kt = lds;
+    float* vt = lds + SLM_SB_KEYS * 64;
+    long long pos = dyn_or(dyn, pos_imm);
+    int lane = threadIdx.x & 63;
+    int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int seg = wave % SLM_SB_SEGS, qt = wave / SLM_SB_SEGS;
+    int i = lane & 15, g = lane >> 4;
+    int group = heads / key_heads, qpt = 16 / group;
+    int kvh = blockIdx.y;
+    long long qtile = (long long)blockIdx.x * ATTN_QG + qt;
+    long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
+    long long sb = first / SLM_SB_KEYS + blockIdx.z;
+    // the superblock's keys and values: instruction kk of a tensor covers keys 4kk .. 4kk+3,
+    // lane L taking key 4kk + L/16, chunk (L % 16) ^ (key & 15) (a chunk at or past dh
+    // copies the row's last one; those dims read as zero below)
+    const float* kb = kc + (long long)kvh * cap * dh;
+    const float* vb = vc + (long long)kvh * cap * dh;
+    unsigned base = (unsigned)((sb * SLM_SB_KEYS) % cap), cap32 = (unsigned)cap;
+    int nch = dh >> 2;
+#pragma unroll
+    for (int u = 0; u < SLM_SB_KEYS / 4 / (SLM_SB_SEGS * ATTN_QG); u++) {
+        int kk = wave + SLM_SB_SEGS * ATTN_QG * u;
+        int key = 4 * kk + (lane >> 4);
+        int chunk = min((lane & 15) ^ (key & 15), nch - 1);
+        long long off = (long long)((base + (unsigned)key) % cap32) * dh + 4 * chunk;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off),
+                                         (__attribute__((address_space(3))) void*)(kt + 256 * kk), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off),
+                                         (__attribute__((address_space(3))) void*)(vt + 256 * kk), 16, 0, 0);
+    }
+    Col col = column(i, qtile, pos, m, reach, gap, group, qpt, kvh);
+    // this lane's share of its column's query: B[k = g][j = i] for each 16-dim block
+    f4 qv[DT];
+    const float* qrow = q + (col.qidx * heads + col.head) * (long long)dh;
+#pragma unroll
+    for (int t = 0; t < DT; t++) {
+        int c = 16 * t + 4 * g;
+        qv[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (col.valid && c < dh) qv[t] = *(const f4*)(qrow + c);
+    }
+    vm_wait<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    float mo, lo;
+    f4 o[DT];
+    attn_seg_lds<DT>(col, qv, kt + seg * 64 * 64, vt + seg * 64 * 64,
+                     (sb * SLM_SB_SEGS + seg) * 64, dh, scale, mo, lo, o);
+    __syncthreads();  // every wave is done with the keys and values: their LDS holds the folds
+    {
+        float* L = lds + (wave * 16 + i) * (DP + 2);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) L[2 + 16 * dt + 4 * g + r] = o[dt][r];
+        if (g == 0) {
+            L[0] = mo;
+            L[1] = lo;
+        }
+    }
+    __syncthreads();
+    // fold each tile's segments in order, one (tile, column, dim) per thread and pass
+    for (int t = threadIdx.x; t < ATTN_QG * 16 * DP; t += NT) {
+        int qq = t / (16 * DP), cc = (t / DP) % 16, dd = t % DP;
+        Col c2 = column(cc, (long long)blockIdx.x * ATTN_QG + qq, pos, m, reach, gap, group, qpt, kvh);
+        if (!c2.valid || dd >= dh) continue;
+        float FM = NEG_INF, FL = 0.0f, FO = 0.0f;
+#pragma unroll
+        for (int w = 0; w < SLM_SB_SEGS; w++) {
+            const float* F = lds + ((qq * SLM_SB_SEGS + w) * 16 + cc) * (DP + 2);
+            fold(FM, FL, FO, F[0], F[1], F[2 + dd]);
+        }
+        float* P = part + (((long long)blockIdx.z * m + c2.qidx) * heads + c2.head) * (long long)(DP + 2);
+        if (dd == 0) {
+            P[0] = FM;
+            P[1] = FL;
+        }
+        P[2 + dd] = FO;
+    }
+}
+
+#define ATTN_PQ(DT)                                                                      \
+    KERNEL void __launch_bounds__(64 * SLM_SB_SEGS * ATTN_QG) slm_attn_pq_##DT(           \
+        float* part, const float* q, const float* kc, const float* vc,                   \
+        const long long* dyn, long long pos_imm, int m, long long reach, long long gap,  \
+        long long cap, int heads, int key_heads, int dh, float scale) {                  \
+        attn_pq_body<DT>(part, q, kc, vc, dyn, pos_imm, m, reach, gap, cap, heads,        \
+                         key_heads, dh, scale);                                          \
+    }
+ATTN_PQ(1)
+ATTN_PQ(2)
+ATTN_PQ(4)
+
 // One-token attention (m = 1) on the vector ALUs, with the arithmetic of slm_attn_part_*
 // element for element. A 16x16x4 f32 MFMA step is, bit for bit, fmaf over k = 0..3 in
 // order (denormals kept), so a score is the fmaf chain from 0 over dims 16t + 4g + c with t,
@@ -1403,28 +1591,52 @@ ATTN_DEC(4)
 // superblocks that saw a key, w_z = e^(m_z − M), L = Σ l_z·w_z and O = Σ o_z·w_z (both in
 // superblock order), y = O / L (0 when the query sees nothing, cpu.rs:378-382). The last
 // workgroup of an attention launch that combines itself computes the same expressions.
-KERNEL void slm_attn_combine(float* __restrict__ y, const float* __restrict__ part, int m,
+KERNEL void __launch_bounds__(256) slm_attn_combine(float* __restrict__ y, const float* __restrict__ part, int m,
                              int heads, int dh, int dp, int nsb) {
-    long long n = (long long)m * heads * dh;
+    // one wave per (query, head) row: lane z holds superblock z's m and l (64 at a time),
+    // lane d the o values of dim d of every superblock, all loads of a batch in flight
+    int lane = threadIdx.x & 63;
+    long long rw = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (rw >= (long long)m * heads) return;
+    const float* P = part + rw * (dp + 2);
     long long stride = (long long)m * heads * (dp + 2);
-    GRID_LOOP(t, n) {
-        long long row = t / dh;
-        int dd = (int)(t % dh);
-        const float* P = part + row * (dp + 2);
-        float M = NEG_INF;
-        for (int z = 0; z < nsb; z++)
-            if (P[z * stride + 1] > 0.0f) M = fmaxf(M, P[z * stride]);
+    float M = NEG_INF;
+    for (int z0 = 0; z0 < nsb; z0 += 64) {
+        int z = z0 + lane;
+        float mz = z < nsb ? P[z * stride] : NEG_INF, lz = z < nsb ? P[z * stride + 1] : 0.0f;
+        float mm = lz > 0.0f ? mz : NEG_INF;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
+        M = fmaxf(M, mm);
+    }
+    for (int d0 = 0; d0 < dh; d0 += 64) {
+        int dd = d0 + lane;
         float L = 0.0f, O = 0.0f;
-        for (int z = 0; z < nsb; z++) {
-            const float* Q = P + z * stride;
-            float l = Q[1];
-            if (l > 0.0f) {
-                float w = expf(Q[0] - M);
-                L = L + l * w;
-                O = O + Q[2 + dd] * w;
+        for (int z0 = 0; z0 < nsb; z0 += 64) {
+            int z = z0 + lane;
+            float mz = z < nsb ? P[z * stride] : NEG_INF, lz = z < nsb ? P[z * stride + 1] : 0.0f;
+            float wz = lz > 0.0f ? expf(mz - M) : 0.0f;  // lane z: superblock z's weight
+            int nz = min(64, nsb - z0);
+            for (int u0 = 0; u0 < nz; u0 += 16) {
+                float oz[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) {  // past the last superblock: reads the last again
+                    int zz = z0 + min(u0 + u, nz - 1);
+                    oz[u] = dd < dh ? P[zz * stride + 2 + dd] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 16; u++) {
+                    if (u0 + u >= nz) break;
+                    float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lz), u0 + u));
+                    float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wz), u0 + u));
+                    if (l > 0.0f) {
+                        L = L + l * w;
+                        O = O + oz[u] * w;
+                    }
+                }
             }
         }
-        y[t] = L > 0.0f ? O / L : 0.0f;
+        if (dd < dh) y[rw * dh + dd] = L > 0.0f ? O / L : 0.0f;
     }
 }
 

@@ -46,6 +46,7 @@ constexpr int LDS_MAX = 163840;            // gfx950: 160 KB of LDS per workgrou
 constexpr int FG_GRID_MAX = 256;           // workgroups of a fused GEMV: one per compute unit
 constexpr int64_t ATTN_CTR_MAX = 65536;   // (query tile, key head) pairs one attention launch combines itself
 constexpr int ATTN_LDS_MAX = LDS_MAX;
+constexpr int ATTN_QG_HOST = 4;   // query tiles per workgroup of the prompt attention (ATTN_QG)
 constexpr int ATTN_DEC_LDS = SLM_SB_SEGS * (2 * 64 * 64 + 1024) * 4;  // one-token attention: 256 keys and values, queries
 constexpr int GEMM_STAGES_HOST = 3;          // slices in flight in slm_gemm2 (GEMM_STAGES)
 constexpr int64_t CU_COUNT = 256;           // MI355X compute units
@@ -108,6 +109,7 @@ struct Kernels {
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
     hipFunction_t attn_dec[3];               // one-token attention, dim tiles 1, 2, 4
     hipFunction_t rows;                      // prompt row chains
+    hipFunction_t attn_pq[3];                // prompt attention, superblock shared in LDS
 };
 
 }  // namespace
@@ -508,8 +510,23 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                                  o.f[0], self ? p[0] : (float*)nullptr,
                                  self ? c->attn_ctr : (int*)nullptr));
                 if (!self)
-                    out.push_back(mk(k.combine, blocks_for(heads * dh), 1, 1, 256, 0, p[0],
+                    out.push_back(mk(k.combine, (uint32_t)((heads + 3) / 4), 1, 1, 256, 0, p[0],
                                      (const float*)c->ws, 1, (int)heads, (int)dh, (int)dp, (int)nsb));
+                return SLM_OK;
+            }
+            if (m > 1 && dh <= 64) {
+                // a superblock's keys and values shared in LDS by four query tiles
+                int64_t qpt = 16 / (heads / kh);
+                // (then every row's superblocks are combined by a kernel of their own: many
+                // rows, each a wave, rather than one workgroup per tile group at the end)
+                int64_t groups = ((m + qpt - 1) / qpt + ATTN_QG_HOST - 1) / ATTN_QG_HOST;
+                out.push_back(mk(k.attn_pq[dti], (uint32_t)groups, (uint32_t)kh, (uint32_t)nsb,
+                                 64 * SLM_SB_SEGS * ATTN_QG_HOST, (uint32_t)(2 * SLM_SB_KEYS * 64 * 4),
+                                 c->ws, p[1], p[2], p[3], (const long long*)o.dyn, (long long)n[0],
+                                 (int)m, (long long)n[2], (long long)n[3], (long long)n[4],
+                                 (int)heads, (int)kh, (int)dh, o.f[0]));
+                out.push_back(mk(k.combine, (uint32_t)((m * heads + 3) / 4), 1, 1, 256, 0, p[0],
+                                 (const float*)c->ws, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
                 return SLM_OK;
             }
             // LDS: wpp segment partials being folded, then each wave's tile of values
@@ -520,14 +537,14 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int64_t qtiles = (m + qpt - 1) / qpt;
             // the last workgroup of each (query tile, key head) combines the superblocks itself
             // when its counter fits; otherwise slm_attn_combine runs after
-            bool self = qtiles * kh <= ATTN_CTR_MAX;
+            bool self = m == 1 && qtiles * kh <= ATTN_CTR_MAX;
             out.push_back(mk(k.attn[dti], (uint32_t)qtiles, (uint32_t)kh, (uint32_t)nsb,
                              64 * SLM_SB_SEGS, (uint32_t)shm(wpp), c->ws, p[1], p[2], p[3],
                              (const long long*)o.dyn, (long long)n[0], (int)m, (long long)n[2],
                              (long long)n[3], (long long)n[4], (int)heads, (int)kh, (int)dh, o.f[0],
                              (int)wpp, self ? p[0] : (float*)nullptr, self ? c->attn_ctr : (int*)nullptr));
             if (!self)
-                out.push_back(mk(k.combine, blocks_for(m * heads * dh), 1, 1, 256, 0, p[0],
+                out.push_back(mk(k.combine, (uint32_t)((m * heads + 3) / 4), 1, 1, 256, 0, p[0],
                                  (const float*)c->ws, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
             return SLM_OK;
         }
@@ -1889,7 +1906,9 @@ int load_kernels(slm_hip* c) {
                {&k.attn[2], "slm_attn_part_4"}, {&k.attn[3], "slm_attn_part_8"},
                {&k.attn[4], "slm_attn_part_16"},
                {&k.attn_dec[0], "slm_attn_dec_1"}, {&k.attn_dec[1], "slm_attn_dec_2"},
-               {&k.attn_dec[2], "slm_attn_dec_4"}, {&k.rows, "slm_rows"}};
+               {&k.attn_dec[2], "slm_attn_dec_4"}, {&k.rows, "slm_rows"},
+               {&k.attn_pq[0], "slm_attn_pq_1"}, {&k.attn_pq[1], "slm_attn_pq_2"},
+               {&k.attn_pq[2], "slm_attn_pq_4"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;
