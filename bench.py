@@ -243,7 +243,7 @@ def main():
     hip.set_timing(True)
     se.decode_greedy(a.timed_steps)
     se.logits()
-    kern = {n: hip.kernel_stat(n) for n in ("slm_fg", "slm_attn_part_4", "slm_gla1_4")}
+    kern = {n: hip.kernel_stat(n) for n in ("slm_fg", "slm_attn_dec_4", "slm_gla1_4")}
     hip.set_timing(False)
     hip.set_graphs(not a.no_graphs)
     fg = kern["slm_fg"]
