@@ -179,13 +179,14 @@ def test_a86_short_prompt_against_oracle(pkg, hip):
     assert worst < TOL
 
 
-def test_a86_chunked_ring_state_equals_step(pkg, hip):
+@pytest.mark.parametrize("loops", [4, 8, 16])
+def test_a86_chunked_ring_state_equals_step(pkg, hip, loops):
     """Config 3's check at full size: a 4096-token prompt in 256-token chunks leaves the
-    same ring state, bit for bit, as the same prompt token by token (R = 4)."""
+    same ring state, bit for bit, as the same prompt token by token (R = 4, 8 and 16)."""
     folder = model_dir("a86", 2)
     g = pkg.Model(hip, folder)
     toks = synth.tokens(4096, 32000, seed=4)
-    a, b = g.session(4), g.session(4)
+    a, b = g.session(loops), g.session(loops)
     a.feed(toks, 256)
     b.feed(toks, 1)
     assert np.array_equal(a.logits(), b.logits())
@@ -221,3 +222,46 @@ def test_fused_steps_match_per_op_kernels(pkg, hip, tiny_dir, name):
     for x, y in zip(la, lb):
         assert np.array_equal(x, y)
     _kept_equal(a, b)
+
+
+def test_g86_prompt_against_oracle(pkg, hip):
+    """Config 4's model (g86: global G layers with 4 key heads, logn / kshift / emb / far on)
+    at R = 4: a 700-token prompt in 256-token chunks with global caches that start at 256
+    slots and double twice, then 4 greedy steps, against the oracle."""
+    folder = model_dir("g86", 5)
+    g, c = _both(pkg, hip, folder, 4, global_cap=256)
+    toks = synth.tokens(700, 32000, seed=21)
+    gs, cs = g.session(4), c.session(4)
+    gs.feed(toks, 256)
+    cs.feed(toks, 256)
+    worst = rel(gs.logits(), cs.logits())
+    ids = []
+    for _ in range(4):
+        lg, lc = gs.logits(), cs.logits()
+        worst = max(worst, rel(lg, lc))
+        assert greedy(lg) == greedy(lc)
+        ids.append(greedy(lg))
+        gs.step(ids[-1])
+        cs.step(ids[-1])
+    print(f"g86: max rel {worst:.3g}; ids {ids}")
+    assert worst < TOL
+
+
+def test_g86_long_prompt_chunked_equals_step(pkg, hip):
+    """Config 4's prefill at full size: a 16384-token prompt in 256-token chunks (global caches
+    grow to 32768 slots; global attention spans up to 65 superblocks) leaves the same state, bit
+    for bit, as the same prompt token by token; then 16 greedy steps agree."""
+    folder = model_dir("g86", 5)
+    g = pkg.Model(hip, folder)
+    toks = synth.tokens(16384, 32000, seed=22)
+    a, b = g.session(4), g.session(4)
+    a.feed(toks, 256)
+    b.feed(toks, 1)
+    assert np.array_equal(a.logits(), b.logits())
+    _kept_equal(a, b)
+    for _ in range(16):
+        t = greedy(a.logits())
+        assert t == greedy(b.logits())
+        a.step(t)
+        b.step(t)
+    assert np.array_equal(a.logits(), b.logits())
