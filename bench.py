@@ -254,6 +254,30 @@ def main():
         f"{bpl / 1e6:.2f} MB/launch, {gemv_bw / 1e9:.0f} GB/s")
     share = {n: round(v["us"] / max(a.timed_steps, 1), 1) for n, v in kern.items()}
 
+    # the same workload in fp16 mode (the --fp16 analogue: linears with fp16 operands at
+    # fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)
+    hip.set_fp16(True)
+    s16 = model.session(a.loops)
+    s16.feed(prompt[:16], 256)
+    s16.logits()
+    t = time.perf_counter()
+    s16.feed(prompt, 256)
+    s16.logits()
+    fill16_s = time.perf_counter() - t
+    if a.warmup:
+        s16.decode_greedy(a.warmup)
+    s16.logits()
+    t = time.perf_counter()
+    s16.decode_greedy(a.steps)
+    s16.logits()
+    dec16_s = time.perf_counter() - t
+    hip.set_fp16(False)
+    fp16 = {"decode_tok_s": round(a.steps / dec16_s, 2), "prefill_tok_s": round(len(prompt) / fill16_s, 1),
+            "prefill_tflops": round(fl / fill16_s / 1e12, 2),
+            "note": "linears round operands to fp16 at v_mfma_f32_16x16x16f16 (fp32 sums); attention, "
+                    "GLA, norms and states fp32; checked at 2e-2 vs the fp32 oracle (config C5)"}
+    log(f"fp16 mode: prefill {fp16['prefill_tok_s']} tok/s, decode {fp16['decode_tok_s']} tok/s")
+
     cpu = None
     if not a.no_cpu:
         n = min(a.cpu_steps, a.steps)
@@ -296,6 +320,7 @@ def main():
                     "peak_tflops": FP32_MFMA_PEAK / 1e12,
                     "frac": round(fl / fill_s / FP32_MFMA_PEAK, 4)},
         "graphs": stats,
+        "fp16_mode": fp16,
         "cpu_baseline": cpu,
         "reference_published": {"decode_tok_s_r4_rtx5080": 209, "prefill_tok_s_r4_rtx5080": 2819,
                                 "note": "README.md:143-147; different GPU and model dims"},

@@ -136,6 +136,12 @@ int slm_hip_attend(slm_hip* ctx, float* y, float* scores, const float* q, const 
  * or upload inside a step runs what was recorded so far and finishes the step eagerly.
  * Results are identical in every mode: the same arithmetic runs. */
 int slm_hip_set_graphs(slm_hip* ctx, int on);
+/* fp16 mode (off by default), the analogue of the reference's --fp16 (mlx.rs:19-23,
+ * main.rs:421-423, where it selects Float16 for every MLX buffer): from this call on, every
+ * linear rounds both operands to fp16 (to nearest even) at fp16 MFMAs and sums in fp32;
+ * attention, GLA, norms and states stay fp32. A linear then needs a multiple of 64 columns
+ * and 16-byte aligned weights and input (else SLM_E_UNSUPPORTED). */
+int slm_hip_set_fp16(slm_hip* ctx, int on);
 /* Fusion (on by default): the planner lowers a recorded one-token step into fused
  * kernels (prologue vector ops + GEMV + epilogue) that compute the same values with the
  * same arithmetic as the per-op kernels. Off: one launch per operation. */

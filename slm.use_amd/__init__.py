@@ -88,6 +88,7 @@ _SIGS = {
     "slm_hip_attend": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_set_graphs": (_i, [_p, _i]),
     "slm_hip_set_fusion": (_i, [_p, _i]),
+    "slm_hip_set_fp16": (_i, [_p, _i]),
     "slm_hip_graph_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                  C.POINTER(C.c_uint64)]),
     "slm_hip_last_plan": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
@@ -222,6 +223,10 @@ class Hip:
 
     def set_fusion(self, on: bool):
         self.check(lib.slm_hip_set_fusion(self.ctx, int(on)))
+
+    def set_fp16(self, on: bool):
+        """fp16 mode: every linear rounds its operands to fp16 at fp16 MFMAs (sums in fp32)."""
+        self.check(lib.slm_hip_set_fp16(self.ctx, int(on)))
 
     def graph_stats(self):
         a, b, c = C.c_uint64(), C.c_uint64(), C.c_uint64()

@@ -96,7 +96,7 @@ typedef struct {
 typedef struct __attribute__((aligned(16))) {
     int32_t npf, nvp, cols, nsl;    // nsl: canonical slices of `cols`
     int32_t W, xin, nseg, units;    // W: GEMV waves (slices per split); xin: LDS offset of x
-    int32_t lds_vp, fold_off, pf4, pad;  // pf4: float4s the prologue loads
+    int32_t lds_vp, fold_off, pf4, f16;  // pf4: float4s the prologue loads; f16: fp16 mode MFMAs
     PfOp pf[SLM_PF_MAX];
     VpOp vp[SLM_VP_MAX];
     FgSeg seg[SLM_SEG_MAX];

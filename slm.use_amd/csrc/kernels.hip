@@ -52,6 +52,18 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// fp16 mode (the --fp16 analogue, mlx.rs:19-23): a 16-column block of a linear's chain is one
+// v_mfma_f32_16x16x16f16 instead of four 16x16x4 f32 MFMAs. Its operands are the same
+// registers (lane (i, g) holds columns 4g .. 4g + 3 of row / token i), rounded to fp16 to
+// nearest even; the sums stay fp32.
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ h4 to_h4(f4 v) {
+    return h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+}
+__device__ __forceinline__ f4 block16h(f4 a, f4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(to_h4(a), to_h4(b), c, 0, 0, 0);
+}
+
 // ---------------------------------------------------------------------------------------
 // element-wise operations (src/cpu.rs:66-185, 209-268, 331-350)
 // ---------------------------------------------------------------------------------------
@@ -418,7 +430,7 @@ __device__ __forceinline__ f4 ld4(const float* __restrict__ p, long long row, lo
 // m <= 16: one workgroup per 16 rows; wave w takes slices w, w+W, w+2W, ... four at a
 // time, loading them before their chains start (four independent chains interleave);
 // slice partials meet in LDS and one pass adds them in order.
-template <bool VEC>
+template <bool VEC, bool H>
 __device__ void linear_small_body(float* __restrict__ y, const float* __restrict__ w,
                                   const float* __restrict__ x, int rows, int cols, int m) {
     extern __shared__ float part[];  // [slices][16 rows][16 tokens]
@@ -446,15 +458,25 @@ __device__ void linear_small_body(float* __restrict__ y, const float* __restrict
         f4 acc[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (H) {
 #pragma unroll
-        for (int u = 0; u < SLM_KS; u++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
+            for (int u = 0; u < SLM_KS; u++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     int s = s0 + j * waves;
-                    if (s < nsl && s * SLM_KS + u < kblocks) acc[j] = mfma4(wa[j][u][e], xb[j][u][e], acc[j]);
+                    if (s < nsl && s * SLM_KS + u < kblocks) acc[j] = block16h(wa[j][u], xb[j][u], acc[j]);
                 }
+        } else {
+#pragma unroll
+            for (int u = 0; u < SLM_KS; u++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        int s = s0 + j * waves;
+                        if (s < nsl && s * SLM_KS + u < kblocks) acc[j] = mfma4(wa[j][u][e], xb[j][u][e], acc[j]);
+                    }
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             int s = s0 + j * waves;
@@ -480,11 +502,15 @@ __device__ void linear_small_body(float* __restrict__ y, const float* __restrict
 
 KERNEL void __launch_bounds__(512) slm_linear_small_v(float* y, const float* w, const float* x,
                                                       int rows, int cols, int m) {
-    linear_small_body<true>(y, w, x, rows, cols, m);
+    linear_small_body<true, false>(y, w, x, rows, cols, m);
 }
 KERNEL void __launch_bounds__(512) slm_linear_small_s(float* y, const float* w, const float* x,
                                                       int rows, int cols, int m) {
-    linear_small_body<false>(y, w, x, rows, cols, m);
+    linear_small_body<false, false>(y, w, x, rows, cols, m);
+}
+KERNEL void __launch_bounds__(512) slm_linear_small_vh(float* y, const float* w, const float* x,
+                                                       int rows, int cols, int m) {
+    linear_small_body<true, true>(y, w, x, rows, cols, m);
 }
 
 // m > 16: a 64-row × 64-token tile per workgroup, 32 × 32 per wave (2 × 2 MFMA tiles).
@@ -671,7 +697,7 @@ __device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N), other counte
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM, int WAVES>
+template <int BM, int WAVES, bool H>
 __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                            const float* __restrict__ w, const float* __restrict__ x, int rows,
                            int cols, int m) {
@@ -746,14 +772,23 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
             for (int v = 0; v < NV; v++) bb[q][v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
         }
+        if constexpr (H) {
 #pragma unroll
-        for (int q = 0; q < SLM_KS; q++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
+            for (int q = 0; q < SLM_KS; q++)
 #pragma unroll
                 for (int u = 0; u < MU; u++)
 #pragma unroll
-                    for (int v = 0; v < NV; v++) acc[u][v] = mfma4(a[q][u][e], bb[q][v][e], acc[u][v]);
+                    for (int v = 0; v < NV; v++) acc[u][v] = block16h(a[q][u], bb[q][v], acc[u][v]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < SLM_KS; q++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int u = 0; u < MU; u++)
+#pragma unroll
+                        for (int v = 0; v < NV; v++) acc[u][v] = mfma4(a[q][u][e], bb[q][v][e], acc[u][v]);
+        }
         // slice sums in order within the split
 #pragma unroll
         for (int u = 0; u < MU; u++)
@@ -781,7 +816,11 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #define GEMM2(BM, WAVES)                                                                  \
     KERNEL void __launch_bounds__(64 * WAVES) slm_gemm2_##BM(float* y, float* part, const float* w, \
                                                            const float* x, int rows, int cols, int m) { \
-        gemm2_body<BM, WAVES>(y, part, w, x, rows, cols, m);                              \
+        gemm2_body<BM, WAVES, false>(y, part, w, x, rows, cols, m);                       \
+    }                                                                                     \
+    KERNEL void __launch_bounds__(64 * WAVES) slm_gemm2h_##BM(float* y, float* part, const float* w, \
+                                                            const float* x, int rows, int cols, int m) { \
+        gemm2_body<BM, WAVES, true>(y, part, w, x, rows, cols, m);                        \
     }
 GEMM2(32, 4)
 GEMM2(64, 16)
@@ -1919,6 +1958,7 @@ __device__ __forceinline__ void fg_load(const FgLane& p, f4 (&wa)[SLM_KS]) {
 }
 
 // The canonical chain of the lane's slice; lanes of row 0 of B hold the token.
+template <bool H>
 __device__ __forceinline__ void fg_chain(const FgLane& p, int i, int g, const f4 (&wa)[SLM_KS],
                                          const float* xin, float* out) {
     if (p.nkb <= 0) return;
@@ -1928,8 +1968,12 @@ __device__ __forceinline__ void fg_chain(const FgLane& p, int i, int g, const f4
         if (q < p.nkb) {
             f4 xb = {0.0f, 0.0f, 0.0f, 0.0f};
             if (i == 0) xb = *(const f4*)(xin + (p.kb0 + q) * 16 + 4 * g);
+            if constexpr (H) {
+                acc = block16h(wa[q], xb, acc);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc = mfma4(wa[q][e], xb[e], acc);
+                for (int e = 0; e < 4; e++) acc = mfma4(wa[q][e], xb[e], acc);
+            }
         }
     }
     if (i == 0) {
@@ -1938,198 +1982,17 @@ __device__ __forceinline__ void fg_chain(const FgLane& p, int i, int g, const f4
     }
 }
 
-KERNEL void __launch_bounds__(1024) slm_fg(const FgDesc dk) {
-    // The descriptor is copied into LDS with one wide load per thread, so the many fields
-    // the kernel reads (some at indices only known per lane) cost one memory round trip.
-    __shared__ FgDesc d;
-    extern __shared__ float lds[];
-    static_assert(sizeof(FgDesc) % 16 == 0, "descriptor copy in float4s");
-    for (int q = threadIdx.x; q < (int)(sizeof(FgDesc) / 16); q += blockDim.x)
-        ((f4*)&d)[q] = ((const f4*)&dk)[q];
-    if (threadIdx.x < 4) ((int*)(lds + dk.lds_vp + 28))[threadIdx.x] = 0;
-    __syncthreads();
-    float* misc = lds + d.lds_vp;   // 32 floats, then the prefetch table (SLM_FG_MISC)
-    float* foldb = lds + d.fold_off;  // [2 rounds][2 units][W][16]
-    int* sync_ctr = (int*)(misc + 28);  // the prologue waves' barrier; +1: their loads are issued; +2: x is ready
-    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int W = d.W;
-    bool first = blockIdx.x == 0;
-    if (wave < W) {
-        // GEMV wave: slice `wave` of the split of every unit of this workgroup, two units
-        // (u and u + grid) per round, eight loads in flight. The prologue's loads go out
-        // first, so they do not queue behind the weights.
-        int i = lane & 15, g = lane >> 4, G = gridDim.x;
-        if (d.pf4 > 0) {
-            for (int it = 0; it < (1 << 24); it++) {
-                if (__hip_atomic_load(sync_ctr + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >=
-                    SLM_FG_EPI_WAVES)
-                    break;
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        f4 wa[SLM_KS], wb[SLM_KS];
-        int u = blockIdx.x;
-        FgLane pa = fg_lane(d, u, wave, i, g), pb = fg_lane(d, u + G, wave, i, g);
-        fg_load(pa, wa);
-        if (u + G < d.units) fg_load(pb, wb);  // (a second unit only if any)
-        // x is in LDS once the prologue waves say so (they ran the prologue meanwhile)
-        for (int it = 0; it < (1 << 24); it++) {
-            if (__hip_atomic_load(sync_ctr + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > 0) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        const float* xin = lds + d.xin;
-        for (int par = 0;; par ^= 1) {  // rounds alternate between two halves of foldb
-            float* fb = foldb + par * 2 * W * 16;
-            fg_chain(pa, i, g, wa, xin, fb + wave * 16);
-            fg_chain(pb, i, g, wb, xin, fb + (W + wave) * 16);
-            __syncthreads();
-            u += 2 * G;
-            if (u >= d.units) break;
-            pa = fg_lane(d, u, wave, i, g);
-            pb = fg_lane(d, u + G, wave, i, g);
-            fg_load(pa, wa);
-            if (u + G < d.units) fg_load(pb, wb);
-        }
-        return;
-    }
-    // The prologue / epilogue waves: the prefetches go straight into LDS, wave ew taking
-    // 64-float4 chunks ew, ew + 4, ... of each; then the prologue ops.
-    int ew = wave - W, ptid = tid - 64 * W, pnt = 64 * SLM_FG_EPI_WAVES;
-    ESync sync{sync_ctr, 0, SLM_FG_EPI_WAVES};
-    int npf = uni(d.npf), nvp = uni(d.nvp);
-    const float* src[SLM_PF_MAX];  // where each prefetch comes from this step
-#pragma unroll
-    for (int j = 0; j < SLM_PF_MAX; j++) {
-        src[j] = nullptr;
-        if (j < npf) {
-            const PfOp& p = d.pf[j];
-            src[j] = p.src + (p.dyn ? gld(p.dyn) * p.stride : 0);
-        }
-    }
-    float sf = 0.0f;  // lane k of each wave: the dynamic factor of a VP_SCALE op k
-    if (lane < nvp && d.vp[lane].kind == VP_SCALE && d.vp[lane].dyn)
-        sf = gld((const float*)d.vp[lane].dyn);
-#pragma unroll
-    for (int j = 0; j < SLM_PF_MAX; j++) {
-        if (j >= npf) break;
-        int n4 = uni(d.pf[j].n) >> 2, at = uni(d.pf[j].lds);
-        for (int c0 = 64 * ew; c0 < n4; c0 += pnt)
-            if (c0 + lane < n4)
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src[j] + 4 * (c0 + lane)),
-                                                 (__attribute__((address_space(3))) void*)(lds + at + 4 * c0), 16, 0, 0);
-    }
-    if (lane == 0)  // this wave's loads are out: the weights may go
-        __hip_atomic_fetch_add(sync_ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's prefetches are in LDS
-    sync();                         // and every wave's
-    bool prev_v4 = true;
-    for (int k = 0; k < nvp; k++) {
-        const VpOp o = vp_load(d.vp[k]);
-        if (!first && o.wg0) continue;
-        bool v4 = vp_v4(o);
-        // a barrier when this op reads elements other threads wrote: an offset read, rms,
-        // or a change between float4 and element layout
-        if (o.sync || o.kind == VP_RMS || v4 != prev_v4) sync();
-        prev_v4 = v4;
-        float f = o.f;
-        if (o.kind == VP_SCALE && o.dyn)
-            f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sf), k));
-        vp_run(o, lds, f, ptid, pnt);
-    }
-    sync();  // x is complete: the GEMV waves may go
-    if (ptid == 0) __hip_atomic_fetch_add(sync_ctr + 2, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (first) {  // workgroup 0 writes out what the prologue made that later ops read
-        for (int k = 0; k < nvp; k++) {
-            const VpOp o = vp_load(d.vp[k]);
-            if (!d.vp[k].gout) continue;
-            const float* v = lds + (o.out >= 0 ? o.out : o.in0);
-            for (int c = ptid; c < o.n; c += pnt) gst(d.vp[k].gout + c, v[c]);
-        }
-    }
-    if (ew > 0) return;  // the epilogue is wave 0's (a wave that has ended leaves barriers)
-    // The epilogue, per round of (up to) two units: lanes 0..15 hold rows 0..15 of a tile.
-    // Everything but the partials is worked out before the GEMV waves are waited for.
-    int r = lane & 15;
-    for (int u0 = blockIdx.x, par = 0; u0 < d.units; u0 += 2 * gridDim.x, par ^= 1) {
-        // the GEMV waves write the next round's partials into the other half of foldb
-        // while this round's are read here
-        const float* fb = foldb + par * 2 * W * 16;
-        FgSeg sg[2];
-        FgUnit cur[2];
-        int R[2] = {0, 0}, nsl[2] = {0, 0};
-        bool live[2] = {false, false};
-        float res[2] = {0.0f, 0.0f};
-        long long slot[2] = {0, 0};
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int u = u0 + h * gridDim.x;
-            if (u >= d.units) continue;
-            cur[h] = fg_unit(d, u);
-            sg[h] = d.seg[cur[h].seg];
-            R[h] = (int)fg_row(sg[h], cur[h].tile, r);
-            nsl[h] = min(SLM_SPLIT, d.nsl - cur[h].split * SLM_SPLIT);
-            live[h] = lane < 16 && R[h] < sg[h].rows;
-            if (!live[h] || sg[h].nsplit > 1) continue;
-            if (sg[h].epi == EPI_RESID) res[h] = gld(sg[h].res + R[h]);
-            if (sg[h].epi == EPI_ROPE) {
-                int part = R[h] / sg[h].d;
-                if (part == 1) slot[h] = (sg[h].dyn ? gld(sg[h].dyn) : sg[h].imm) % sg[h].cap;
-                if (part == 2) slot[h] = (sg[h].dyn2 ? gld(sg[h].dyn2) : sg[h].imm2) % sg[h].cap;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int u = u0 + h * gridDim.x;
-            if (u >= d.units) break;
-            float pv[SLM_SPLIT];  // the split's slice partials, read at once, added in order
-#pragma unroll
-            for (int q = 0; q < SLM_SPLIT; q++) pv[q] = fb[(h * W + min(q, nsl[h] - 1)) * 16 + r];
-            float v = pv[0];
-#pragma unroll
-            for (int q = 1; q < SLM_SPLIT; q++)
-                if (q < nsl[h]) v = v + pv[q];
-            float partner = __shfl_xor(v, 8);
-            if (!live[h]) continue;
-            const FgSeg& g = sg[h];
-            int Rh = R[h];
-            if (g.nsplit > 1) {
-                gst(g.part + (long long)cur[h].split * g.rows + Rh, v);
-                continue;
-            }
-            gst(g.y + Rh, v);
-            switch (g.epi) {
-                case EPI_RESID:
-                    gst(g.o1 + Rh, res[h] + v);
-                    break;
-                case EPI_SILU:
-                    if (r < 8) gst(g.o1 + cur[h].tile * 8 + r, partner * v / (1.0f + expf(-v)));
-                    break;
-                case EPI_ROPE: {
-                    int part = Rh / g.d, j = Rh % g.d;
-                    int e = j % g.dh, half = g.dh / 2, head = j / g.dh;
-                    if (part < 2) {
-                        int ie = e < half ? e : e - half;
-                        float cs = lds[g.cs_lds + ie], sn = lds[g.sn_lds + ie];
-                        float o = e < half ? v * cs - partner * sn : partner * sn + v * cs;
-                        if (part == 0) {
-                            gst(g.o1 + j, o);
-                        } else {
-                            gst(g.o2 + j, o);
-                            gst(g.o3 + ((long long)head * g.cap + slot[h]) * g.dh + e, o);
-                        }
-                    } else {
-                        gst(g.o4 + ((long long)head * g.cap + slot[h]) * g.dh + e, v);
-                    }
-                    break;
-                }
-                default:
-                    break;
-            }
-        }
-    }
-}
+// The fused GEMV, fp32 (slm_fg) and fp16 mode (slm_fgh): one kernel text, expanded twice.
+#define FG_NAME slm_fg
+#define FG_H false
+#include "fg_body.inc"
+#undef FG_NAME
+#undef FG_H
+#define FG_NAME slm_fgh
+#define FG_H true
+#include "fg_body.inc"
+#undef FG_NAME
+#undef FG_H
 
 // The splits of a linear added in order: y[c] = ((P0[c] + P1[c]) + P2[c]) + ...
 KERNEL void slm_fold(float* __restrict__ y, const float* __restrict__ part, long long n, int nsplit) {

@@ -103,7 +103,8 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 struct Kernels {
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
         store, rope, rope_table, rms, l2norm, rms_wave, l2norm_wave, fill, combine, probe, fg, fold,
-        gemm, gemm2_32, gemm2_64, gemm2_96, gemm2_128;
+        gemm, gemm2_32, gemm2_64, gemm2_96, gemm2_128, gemm2h_32, gemm2h_64, gemm2h_96, gemm2h_128,
+        lin_small_h, fgh;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
@@ -139,6 +140,7 @@ struct slm_hip {
     float* bounce = nullptr;
     std::map<uintptr_t, Table> tables;
     bool graphs_on = true, fusion_on = true, plan_trace = false;
+    bool fp16 = false;                   // linears with fp16 operands (slm_hip_set_fp16)
     bool timing = false, capturing = false;
     std::vector<Timed> timed;             // launches whose events are not read yet
     std::vector<hipEvent_t> ev_pool;
@@ -350,6 +352,17 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
     int vec = (cols % 4 == 0 && aligned16(p[1]) && aligned16(p[2])) ? 1 : 0;
     int64_t kblocks = (cols + 15) / 16, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
     double ab = 4.0 * (double)(rows * cols + m * cols + m * rows);
+    bool h = n[3] != 0;  // fp16 mode: 64-column multiples, aligned (checked when recorded)
+    if (h && m <= 16 && nsl <= 64) {
+        uint32_t waves = (uint32_t)std::min<int64_t>(nsl, 8);
+        out.push_back(mk(k.lin_small_h, (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
+                         (uint32_t)(nsl * 1024), p[0], p[1], p[2], (int)rows, (int)cols, (int)m));
+        out.back().abytes = ab;
+        return SLM_OK;
+    }
+    if (h && (m <= 16 || !vec || cols % 64))
+        return fail(c, SLM_E_UNSUPPORTED, "linear: fp16 mode has no kernel for %lld x %lld x %lld",
+                    (long long)rows, (long long)cols, (long long)m);
     if (m <= 16 && nsl <= 64) {
         uint32_t waves = (uint32_t)std::min<int64_t>(nsl, 8);
         out.push_back(mk(k.lin_small[vec], (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
@@ -377,6 +390,7 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
             }
             uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
             hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
+            if (h) f = bm == 32 ? k.gemm2h_32 : bm == 64 ? k.gemm2h_64 : bm == 96 ? k.gemm2h_96 : k.gemm2h_128;
             out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
                              (uint32_t)ns, bm == 32 ? 256 : bm == 96 ? 512 : 1024, shmem, p[0], c->gpart,
                              p[1], p[2], (int)rows, (int)cols, (int)m));
@@ -1279,7 +1293,7 @@ struct Planner {
             int64_t heads = lq.n[0], dh = lq.n[1], dd = heads * dh;
             bool ok = lk.n[0] == heads && lk.n[1] == dh && rows == 4 * dd && lq.p[1] == y &&
                       lk.p[1] == y + dd && D.n[2] == 1 && D.p[2] == x && D.n[1] == cols &&
-                      aligned16(D.p[1]);
+                      aligned16(D.p[1]) && D.n[3] == L.n[3];
             // the l2norm outputs are untouched until the GLA kernel writes them
             ok = ok && !overlap(rng(lq.p[0], dd), rng(D.p[0], D.n[0])) &&
                  !overlap(rng(lk.p[0], dd), rng(D.p[0], D.n[0])) &&
@@ -1467,6 +1481,7 @@ struct Planner {
         d.nseg = nseg;
         d.units = units;
         d.pf4 = b.pf4;
+        d.f16 = (int32_t)L.n[3];
         d.lds_vp = (b.lds + 3) & ~3;
         d.fold_off = d.lds_vp + SLM_FG_MISC;
         int total = d.fold_off + 4 * W * 16;
@@ -1474,7 +1489,7 @@ struct Planner {
         for (int k = 0; k < nseg; k++) d.seg[k] = seg[k];
         int threads = 64 * (W + SLM_FG_EPI_WAVES);
         uint32_t grid = (uint32_t)std::min(units, FG_GRID_MAX);
-        out.push_back(mk_desc(c->k.fg, grid, (uint32_t)threads, (uint32_t)(total * 4), d));
+        out.push_back(mk_desc(d.f16 ? c->k.fgh : c->k.fg, grid, (uint32_t)threads, (uint32_t)(total * 4), d));
         double ab = 16.0 * d.pf4;  // prologue vectors, then weights and outputs
         for (int k = 0; k < nseg; k++) ab += 4.0 * ((double)seg[k].rows * cols + seg[k].rows);
         out.back().abytes = ab;
@@ -1663,7 +1678,7 @@ int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fus
         for (size_t k = before; k < out.size(); k++) {
             const char* nm = "?";
             const Kernels& K = c->k;
-            if (out[k].f == K.fg) {
+            if (out[k].f == K.fg || out[k].f == K.fgh) {
                 const FgDesc* d = (const FgDesc*)out[k].blob;
                 fprintf(stderr, " fg[%dx%d vp", d->seg[0].rows, d->cols);
                 for (int q = 0; q < d->nvp; q++)
@@ -1897,6 +1912,9 @@ int load_kernels(slm_hip* c) {
                {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
                {&k.gemm2_32, "slm_gemm2_32"},   {&k.gemm2_64, "slm_gemm2_64"},
                {&k.gemm2_96, "slm_gemm2_96"},   {&k.gemm2_128, "slm_gemm2_128"},
+               {&k.gemm2h_32, "slm_gemm2h_32"}, {&k.gemm2h_64, "slm_gemm2h_64"},
+               {&k.gemm2h_96, "slm_gemm2h_96"}, {&k.gemm2h_128, "slm_gemm2h_128"},
+               {&k.lin_small_h, "slm_linear_small_vh"}, {&k.fgh, "slm_fgh"},
                {&k.lin_small[0], "slm_linear_small_s"}, {&k.lin_small[1], "slm_linear_small_v"},
                {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
                {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
@@ -2102,6 +2120,13 @@ int slm_hip_set_graphs(slm_hip* c, int on) {
     if (c->recording) TRY(finish_step(c));
     if (!on) drop_graphs(c);
     c->graphs_on = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_set_fp16(slm_hip* c, int on) {
+    if (!c) return SLM_E_INVALID;
+    if (c->recording) TRY(finish_step(c));
+    c->fp16 = on != 0;
     return SLM_OK;
 }
 
@@ -2442,6 +2467,10 @@ int slm_hip_linear(slm_hip* c, float* y, const float* w, size_t rows, size_t col
     o.n[0] = (int64_t)rows;
     o.n[1] = (int64_t)cols;
     o.n[2] = (int64_t)m;
+    o.n[3] = c->fp16 ? 1 : 0;
+    if (c->fp16 && (cols % 64 || !aligned16(w) || !aligned16(x)))
+        return fail(c, SLM_E_UNSUPPORTED,
+                    "linear: fp16 mode needs a multiple of 64 columns and 16-byte aligned w and x (%zu)", cols);
     return submit(c, o);
 }
 

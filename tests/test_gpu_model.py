@@ -265,3 +265,52 @@ def test_g86_long_prompt_chunked_equals_step(pkg, hip):
         a.step(t)
         b.step(t)
     assert np.array_equal(a.logits(), b.logits())
+
+
+def _arith_prompt(n, seed):
+    """Config 5's prompt: seeded random nested arithmetic over 0-9 + - ( ) of depth at most
+    10, cut to n characters and mapped through the character vocabulary (digits 17-26,
+    ( 9, ) 10, + 12, - 14)."""
+    rng = np.random.default_rng(seed)
+
+    def expr(depth):
+        if depth >= 10 or rng.random() < 0.3:
+            return str(int(rng.integers(0, 100)))
+        a, b = expr(depth + 1), expr(depth + 1)
+        return "(" + a + "+-"[int(rng.integers(0, 2))] + b + ")"
+
+    text = ""
+    while len(text) < n:
+        text += expr(0) + "+"
+    ids = {str(d): 17 + d for d in range(10)}
+    ids.update({"(": 9, ")": 10, "+": 12, "-": 14})
+    return [ids[ch] for ch in text[:n]]
+
+
+def test_c5_fp16_against_fp32_oracle(pkg, hip):
+    """Config 5: the 86M model at R = 16 in fp16 mode, a 512-character arithmetic prompt, one
+    greedy token: logits within 2e-2 relative of the fp32 oracle. fp16 mode keeps the
+    chunked-equals-step invariant (bitwise)."""
+    folder = model_dir("a86", 2)
+    toks = _arith_prompt(512, 5)
+    c = O.Model(folder)
+    cs = c.session(16)
+    cs.feed(toks, 256)
+    want = cs.logits()
+    hip.set_fp16(True)
+    try:
+        g = pkg.Model(hip, folder)
+        a, b = g.session(16), g.session(16)
+        a.feed(toks, 256)
+        b.feed(toks, 1)
+        got = a.logits()
+        assert np.array_equal(got, b.logits())
+        _kept_equal(a, b)
+        err = rel(got, want)
+        top = np.sort(want)[-2:]
+        print(f"C5 fp16: rel {err:.3g}; greedy {greedy(got)} vs {greedy(want)} (oracle top-2 margin {top[1] - top[0]:.3g})")
+        assert err < 2e-2
+        if top[1] - top[0] > 4 * err * np.abs(want).max():
+            assert greedy(got) == greedy(want)
+    finally:
+        hip.set_fp16(False)

@@ -284,8 +284,9 @@ FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "comb
                 "split_fold", "split_flush", "gla_l2", "rounds", "row_offset"]
 
 
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
 @pytest.mark.parametrize("case", FUSION_CASES)
-def test_fusion_pattern(hip, case):
+def test_fusion_pattern(hip, case, fp16):
     d, heads, dh, hid, cap = 768, 12, 64, 3072, 4352
     inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
     cs, sn = hip.alloc(32), hip.alloc(32)
@@ -373,11 +374,15 @@ def test_fusion_pattern(hip, case):
             hip.silu_mul(o["z"].ptr, o["y"].at(3 * d), o["y2"].ptr, d)
 
     got = []
-    for fuse in (False, True):
-        o = outs()
-        hip.write(o["S"], s0)
-        plan = _step(hip, lambda: body(o), inv, cs, sn, fuse)
-        got.append(({k: b.read() for k, b in o.items()}, plan))
+    hip.set_fp16(fp16)
+    try:
+        for fuse in (False, True):
+            o = outs()
+            hip.write(o["S"], s0)
+            plan = _step(hip, lambda: body(o), inv, cs, sn, fuse)
+            got.append(({k: b.read() for k, b in o.items()}, plan))
+    finally:
+        hip.set_fp16(False)
     (a, pa), (b, pb) = got
     print(case, "unfused", pa, "fused", pb)
     assert pb["kernels"] <= pa["kernels"]
@@ -477,3 +482,48 @@ def test_row_chain(hip, case, m):
     assert pb["kernels"] < pa["kernels"]
     for k in a:
         assert np.array_equal(a[k], b[k]), (case, m, k, float(np.abs(a[k] - b[k]).max()))
+
+
+# ---------------------------------------------------------------------------------------
+# fp16 mode: linears round their operands to fp16 at fp16 MFMAs and sum in fp32
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols", [(768, 768), (2304, 768), (768, 3072), (40, 128)])
+def test_linear_fp16(hip, rows, cols):
+    """Every m (the small-m GEMV and the GEMM) against float64 sums of the fp16-rounded
+    operands (their products are exact in fp32, so only the fp32 sums differ), and the same
+    bits for a row whatever m is."""
+    w = rnd(rows, cols, scale=0.05)
+    x = rnd(256, cols)
+    dw, dx = hip.upload(w), hip.upload(x)
+    w16 = w.astype(np.float16).astype(np.float64)
+    x16 = x.astype(np.float16).astype(np.float64)
+    want = x16 @ w16.T
+    hip.set_fp16(True)
+    try:
+        got = {}
+        for m in (1, 5, 37, 256):
+            dy = hip.alloc(m * rows)
+            hip.linear(dy.ptr, dw.ptr, rows, cols, dx.ptr, m)
+            got[m] = dy.read().reshape(m, rows)
+            err = np.abs(got[m] - want[:m]).max() / np.abs(want[:m]).max()
+            assert err < 1e-5, (m, err)
+        for m in (1, 5, 37):
+            assert np.array_equal(got[m], got[256][:m]), m
+        # fp16 rounding is visible: the fp32 path gives other values
+        dy = hip.alloc(rows)
+        hip.set_fp16(False)
+        hip.linear(dy.ptr, dw.ptr, rows, cols, dx.ptr, 1)
+        assert not np.array_equal(dy.read(), got[1][0])
+    finally:
+        hip.set_fp16(False)
+
+
+def test_linear_fp16_rejects_ragged_columns(hip):
+    dw, dx, dy = hip.alloc(16 * 40), hip.alloc(40), hip.alloc(16)
+    hip.set_fp16(True)
+    try:
+        with pytest.raises(Exception):
+            hip.linear(dy.ptr, dw.ptr, 16, 40, dx.ptr, 1)
+    finally:
+        hip.set_fp16(False)
