@@ -297,6 +297,17 @@ __device__ __forceinline__ float gla_colsum(float p) {
     return p;
 }
 
+// The same total in the column's first lane only (what the prompt kernel stores): distance
+// 4 and 8 through DPP row shifts (lane 16c + i reads lane 16c + i + n), so lane 16c adds the
+// same pairs in the same order as gla_colsum.
+__device__ __forceinline__ float gla_colsum0(float p) {
+    p = p + dpp_xor1(p);
+    p = p + dpp_xor2(p);
+    p = p + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x104, 0xF, 0xF, false));
+    p = p + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x108, 0xF, 0xF, false));
+    return p;
+}
+
 // One lane's rows for one token: st = d·st + k·v, and the lane's sum of q·st in order.
 template <int RPL>
 __device__ __forceinline__ float gla_rows(float (&st)[RPL], const float* kk, const float* qq,
@@ -366,12 +377,25 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
         for (int tt = tid; tt < nt_tok; tt += nt)
             dcs[tt] = 1.0f / (1.0f + expf(decay[(long long)(i0 + tt) * heads + h] + bh));
         __syncthreads();
-        for (int tt = 0; tt < nt_tok; tt++) {
-            const float* row = lds + tt * rowl;
-            float vb = live ? row[2 * dh + (b - c0)] : 0.0f;
-            float part = live ? gla_rows<RPL>(st, row + dh, row, dcs[tt], vb, j, dh) : 0.0f;
-            float tot = gla_colsum(part);
-            if (live && j == 0) y[((long long)(i0 + tt) * heads + h) * dh + b] = tot;
+        // eight tokens at a time: their state updates in order, then their eight column
+        // sums side by side (no token's sum waits for the next token's update)
+        for (int t0 = 0; t0 < nt_tok; t0 += 8) {
+            int nu = min(8, nt_tok - t0);
+            float part[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                part[u] = 0.0f;
+                if (u < nu && live) {
+                    const float* row = lds + (t0 + u) * rowl;
+                    part[u] = gla_rows<RPL>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j, dh);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) part[u] = gla_colsum0(part[u]);
+            if (live && j == 0)
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (u < nu) y[((long long)(i0 + t0 + u) * heads + h) * dh + b] = part[u];
         }
         __syncthreads();
     }
