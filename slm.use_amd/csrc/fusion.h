@@ -38,6 +38,8 @@ enum {
     VP_RMS,         // out = rms(in0) · lds[w], eps f
     VP_SILU,        // out = in1 · in0 / (1 + e^−in0)   (silu_mul with g = in0, u = in1)
     VP_FOLD,        // out = ((P0 + P1) + P2) + ...: the splits of a linear, lds[w] [nsb][n]
+    VP_COMB,        // out[head][dim] = the weight-max combine of one-token attention's nsb
+                    // superblock partials, lds[w] [nsb][heads][dp + 2]
 };
 
 enum {
@@ -97,6 +99,12 @@ typedef struct __attribute__((aligned(16))) {
     int32_t npf, nvp, cols, nsl;    // nsl: canonical slices of `cols`
     int32_t W, xin, nseg, units;    // W: GEMV waves (slices per split); xin: LDS offset of x
     int32_t lds_vp, fold_off, pf4, f16;  // pf4: float4s the prologue loads; f16: fp16 mode MFMAs
+    // cw ≥ 0: x is one-token attention's output, combined by the GEMV waves themselves:
+    // wave w (one 64-column slice) combines head w (64 dims) from the superblock partials
+    // in lds[cw] [cnsb][W][cdp + 2], and workgroup 0 writes the result to cgout
+    int32_t cw, cdp, cnsb, cpad;
+    float* cgout;
+    long long cpad2;
     PfOp pf[SLM_PF_MAX];
     VpOp vp[SLM_VP_MAX];
     FgSeg seg[SLM_SEG_MAX];

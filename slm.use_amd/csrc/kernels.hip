@@ -1865,6 +1865,75 @@ __device__ __forceinline__ void vp_fold(const float* part, float* out, int n, in
     }
 }
 
+// slm_attn_combine for one token in LDS, part [nsb][heads][dp + 2] (m, l, o per superblock
+// and head) into out [heads][dh], in two passes with a barrier between them (the same
+// expressions, so the same bits). First, one thread per (head, superblock z): M = the
+// largest m of the head's superblocks that saw a key, w_z = e^(m_z − M), and the pair
+// (w_z, l_z·w_z) into wl [heads][nsb] (w_z = −1: superblock z saw no key, it is skipped).
+__device__ void vp_comb_w(const float* part, float2* wl, int heads, int dp, int nsb, int tid, int nt) {
+    int sr = heads * (dp + 2);
+    for (int p = tid; p < heads * nsb; p += nt) {
+        int h = p / nsb, z = p - h * nsb;
+        const float* P = part + h * (dp + 2);
+        float M = NEG_INF;
+        for (int z0 = 0; z0 < nsb; z0 += 8) {
+            float2 ml[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) ml[u] = *(const float2*)(P + min(z0 + u, nsb - 1) * sr);
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (z0 + u < nsb && ml[u].y > 0.0f) M = fmaxf(M, ml[u].x);
+        }
+        float2 me = *(const float2*)(P + z * sr);
+        float w = expf(me.x - M);
+        wl[p] = me.y > 0.0f ? float2{w, me.y * w} : float2{-1.0f, 0.0f};
+    }
+}
+
+// Then DW dims per thread: L = Σ l_z·w_z and O = Σ o_z·w_z in superblock order,
+// out = O / L (0 when no superblock saw a key).
+template <int DW>
+__device__ void vp_comb_o(const float* part, const float2* wl, float* out, int heads, int dh,
+                          int dp, int nsb, int tid, int nt) {
+    int nq = dh / DW, sr = heads * (dp + 2);
+    for (int q = tid; q < heads * nq; q += nt) {
+        int h = q / nq, d0 = (q - h * nq) * DW;
+        const float* P = part + h * (dp + 2) + 2 + d0;
+        const float2* WL = wl + h * nsb;
+        float L = 0.0f, O[DW];
+#pragma unroll
+        for (int e = 0; e < DW; e++) O[e] = 0.0f;
+        for (int z0 = 0; z0 < nsb; z0 += 8) {
+            float2 wz[8];
+            float oz[8][DW];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {  // past the last superblock: reads the last again
+                int z = min(z0 + u, nsb - 1);
+                wz[u] = WL[z];
+                if (DW == 4) {
+                    float2 a = *(const float2*)(P + z * sr), b = *(const float2*)(P + z * sr + 2);
+                    oz[u][0] = a.x;
+                    oz[u][1] = a.y;
+                    oz[u][DW > 2 ? 2 : 0] = b.x;
+                    oz[u][DW > 3 ? 3 : 0] = b.y;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < DW; e++) oz[u][e] = P[z * sr + e];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (z0 + u < nsb && wz[u].x >= 0.0f) {
+                    L = L + wz[u].y;
+#pragma unroll
+                    for (int e = 0; e < DW; e++) O[e] = O[e] + oz[u][e] * wz[u].x;
+                }
+        }
+#pragma unroll
+        for (int e = 0; e < DW; e++) out[h * dh + d0 + e] = L > 0.0f ? O[e] / L : 0.0f;
+    }
+}
+
 // Whether an op runs on float4s: its length and every vector offset a multiple of four.
 __device__ __forceinline__ bool vp_v4(const VpOp& o) {
     return ((o.in0 | (o.in1 >= 0 ? o.in1 : 0) | (o.out >= 0 ? o.out : 0) | (o.w >= 0 ? o.w : 0) |
@@ -1885,6 +1954,9 @@ __device__ __forceinline__ VpOp vp_load(const VpOp& src) {
     o.in1 = uni(o.in1);
     o.w = uni(o.w);
     o.nsb = uni(o.nsb);
+    o.heads = uni(o.heads);
+    o.dh = uni(o.dh);
+    o.dp = uni(o.dp);
     o.sync = uni(o.sync);
     o.f = __int_as_float(uni(__float_as_int(o.f)));
     return o;
@@ -1911,6 +1983,10 @@ __device__ void vp_run(const VpOp& o, float* lds, float f, int tid, int nt) {
         case VP_SCALE: vp_map<VP_SCALE>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
         case VP_SILU: vp_map<VP_SILU>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
         case VP_FOLD: vp_fold(lds + o.w, out, n, o.nsb, v4, tid, nt); break;
+        case VP_COMB:  // the second pass (the caller ran vp_comb_w and a barrier)
+            if (o.dh % 4 == 0) vp_comb_o<4>(lds + o.w, (const float2*)(lds + o.in1), out, o.heads, o.dh, o.dp, o.nsb, tid, nt);
+            else vp_comb_o<1>(lds + o.w, (const float2*)(lds + o.in1), out, o.heads, o.dh, o.dp, o.nsb, tid, nt);
+            break;
         case VP_RMS: {  // rms (cpu.rs:187-207) of one group: out = a·r·w
             float dsum = dot16_wave(a, n, tid & 63);
             float r = 1.0f / sqrtf(dsum / (float)n + o.f);
@@ -1979,6 +2055,54 @@ __device__ __forceinline__ void fg_load(const FgLane& p, f4 (&wa)[SLM_KS]) {
         const float* src = ok && q < p.nkb ? p.base + (p.kb0 + q) * 16 : slm_zero16;
         wa[q] = gld((const f4*)src);
     }
+}
+
+// slm_attn_combine's expressions for head h of one token, run by one wave: every lane
+// finds M (the largest m of the superblocks that saw a key) from the (m, l) pairs, lane z
+// holds superblock z's weight w_z = e^(m_z − M) and l_z·w_z, lane d sums dim d in
+// superblock order; x[64h + d] = O / L (0 when no superblock saw a key). nsb ≤ 64.
+__device__ __forceinline__ void fg_comb_wave(const float* part, float* x, int heads, int dp,
+                                             int nsb, int h, int lane, float* gout) {
+    int sr = heads * (dp + 2);
+    const float* P = part + h * (dp + 2);
+    float M = NEG_INF;
+    for (int z0 = 0; z0 < nsb; z0 += 8) {
+        float2 ml[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) ml[u] = *(const float2*)(P + min(z0 + u, nsb - 1) * sr);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (z0 + u < nsb && ml[u].y > 0.0f) M = fmaxf(M, ml[u].x);
+    }
+    float wz = -1.0f, lwz = 0.0f;
+    if (lane < nsb) {
+        float2 me = *(const float2*)(P + lane * sr);
+        float w = expf(me.x - M);
+        if (me.y > 0.0f) {
+            wz = w;
+            lwz = me.y * w;
+        }
+    }
+    float L = 0.0f, O = 0.0f;
+    for (int z0 = 0; z0 < nsb; z0 += 8) {
+        float oz[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) oz[u] = P[min(z0 + u, nsb - 1) * sr + 2 + lane];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (z0 + u >= nsb) break;
+            float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wz), z0 + u));
+            float lw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lwz), z0 + u));
+            if (w >= 0.0f) {
+                L = L + lw;
+                O = O + oz[u] * w;
+            }
+        }
+    }
+    float v = L > 0.0f ? O / L : 0.0f;
+    x[64 * h + lane] = v;
+    if (gout) gout[64 * h + lane] = v;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
 }
 
 // The canonical chain of the lane's slice; lanes of row 0 of B hold the token.

@@ -42,6 +42,7 @@ constexpr size_t STAGE_CAP = 4 << 20;     // bytes of eager staging
 constexpr size_t BOUNCE_CAP = 4 << 20;    // pinned bounce buffer for reads
 constexpr size_t MAX_GRAPHS = 8;
 constexpr int VP_LEN_MAX = 4096;          // longest vector a fused prologue holds
+constexpr int64_t COMB_PART_MAX = 16384;  // attention partials (floats) a fused prologue combines
 constexpr int LDS_MAX = 163840;            // gfx950: 160 KB of LDS per workgroup
 constexpr int FG_GRID_MAX = 256;           // workgroups of a fused GEMV: one per compute unit
 constexpr int64_t ATTN_CTR_MAX = 65536;   // (query tile, key head) pairs one attention launch combines itself
@@ -411,6 +412,40 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
     return SLM_OK;
 }
 
+// One-token attention on the vector-ALU kernel (the same arithmetic as the MFMA kernels; its
+// ring offsets step four slots at a time and are 32-bit).
+bool attn_dec_ok(const Op& o) {
+    const int64_t* n = o.n;
+    return n[1] == 1 && n[7] <= 64 && n[4] >= 64 && n[4] * n[7] * 4 < ((int64_t)1 << 32);
+}
+
+int64_t attn_dp(int64_t dh) { return (int64_t)16 << pow2_index((dh + 15) / 16, 4); }
+
+// The superblock partials of a one-token attention, [nsb][heads][dp + 2] floats at c->ws.
+int64_t attn_dec_part_floats(const Op& o) { return o.n[8] * o.n[5] * (attn_dp(o.n[7]) + 2); }
+
+// With `defer` the kernel only writes its superblock partials (a later fused prologue, or
+// slm_attn_combine, combines them); otherwise it combines them itself when every partial
+// of a key head fits in its LDS, else slm_attn_combine runs after it.
+int lower_attn_dec(slm_hip* c, const Op& o, std::vector<Rec>& out, bool defer) {
+    const Kernels& k = c->k;
+    const float* const* p = o.p;
+    const int64_t* n = o.n;
+    int64_t heads = n[5], kh = n[6], dh = n[7], nsb = n[8];
+    int dti = pow2_index((dh + 15) / 16, 4);
+    int64_t dp = attn_dp(dh);
+    bool self = !defer && kh <= ATTN_CTR_MAX && nsb * (heads / kh) * (dp + 2) <= ATTN_DEC_LDS / 4;
+    out.push_back(mk(k.attn_dec[dti], (uint32_t)kh, (uint32_t)nsb, 1, 64 * SLM_SB_SEGS,
+                     (uint32_t)ATTN_DEC_LDS, c->ws, p[1], p[2], p[3], (const long long*)o.dyn,
+                     (long long)n[0], (long long)n[2], (long long)n[3], (long long)n[4], (int)heads,
+                     (int)kh, (int)dh, o.f[0], self ? p[0] : (float*)nullptr,
+                     self ? c->attn_ctr : (int*)nullptr));
+    if (!self && !defer)
+        out.push_back(mk(k.combine, (uint32_t)((heads + 3) / 4), 1, 1, 256, 0, p[0], (const float*)c->ws,
+                         1, (int)heads, (int)dh, (int)dp, (int)nsb));
+    return SLM_OK;
+}
+
 int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
     const Kernels& k = c->k;
     const float* const* p = o.p;
@@ -512,22 +547,7 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int64_t m = n[1], heads = n[5], kh = n[6], dh = n[7], nsb = n[8];
             int dti = pow2_index((dh + 15) / 16, 4);
             int64_t dp = (int64_t)16 << dti;
-            if (m == 1 && dh <= 64 && n[4] >= 64 && n[4] * dh * 4 < ((int64_t)1 << 32)) {
-                // one token: the vector-ALU kernel (the same arithmetic; its ring offsets step
-                // four slots at a time and are 32-bit). It combines the superblocks itself when
-                // every partial of a key head fits in its LDS
-                bool self = kh <= ATTN_CTR_MAX && nsb * (heads / kh) * (dp + 2) <= ATTN_DEC_LDS / 4;
-                out.push_back(mk(k.attn_dec[dti], (uint32_t)kh, (uint32_t)nsb, 1, 64 * SLM_SB_SEGS,
-                                 (uint32_t)ATTN_DEC_LDS, c->ws, p[1], p[2], p[3],
-                                 (const long long*)o.dyn, (long long)n[0], (long long)n[2],
-                                 (long long)n[3], (long long)n[4], (int)heads, (int)kh, (int)dh,
-                                 o.f[0], self ? p[0] : (float*)nullptr,
-                                 self ? c->attn_ctr : (int*)nullptr));
-                if (!self)
-                    out.push_back(mk(k.combine, (uint32_t)((heads + 3) / 4), 1, 1, 256, 0, p[0],
-                                     (const float*)c->ws, 1, (int)heads, (int)dh, (int)dp, (int)nsb));
-                return SLM_OK;
-            }
+            if (attn_dec_ok(o)) return lower_attn_dec(c, o, out, false);
             if (m > 1 && dh <= 64) {
                 // a superblock's keys and values shared in LDS by four query tiles
                 int64_t qpt = 16 / (heads / kh);
@@ -580,11 +600,12 @@ bool overlap(const Range& x, const Range& y) { return x.a < y.b && y.a < x.b; }
 
 // An element-wise one-token op as prologue material: what it reads and writes.
 enum { SRC_COPY = 1, SRC_ADD, SRC_MIX, SRC_SCALE, SRC_GATHER, SRC_RMS, SRC_ROPE_TABLE, SRC_SILU,
-       SRC_FOLD };
+       SRC_FOLD, SRC_COMB };
 struct VpSrc {
     int kind = 0;
     int n = 0;
-    int nsplit = 0;  // SRC_FOLD: partials [nsplit][n] at in[0]
+    int nsplit = 0;  // SRC_FOLD: partials [nsplit][n] at in[0]; SRC_COMB: superblocks
+    int heads = 0, dh = 0, dp = 0;  // SRC_COMB: partials [nsplit][heads][dp + 2] at in[0]
     const float* in[2] = {nullptr, nullptr};
     const float* out[2] = {nullptr, nullptr};
     const Op* op = nullptr;
@@ -1111,6 +1132,9 @@ struct Planner {
             if (v.kind == SRC_FOLD) {
                 out.push_back(mk(c->k.fold, blocks_for(v.n), 1, 1, 256, 0, v.out[0], v.in[0],
                                  (long long)v.n, v.nsplit));
+            } else if (v.kind == SRC_COMB) {
+                out.push_back(mk(c->k.combine, (uint32_t)((v.heads + 3) / 4), 1, 1, 256, 0, v.out[0],
+                                 v.in[0], 1, v.heads, v.dh, v.dp, v.nsplit));
             } else {
                 TRY(lower_one(c, *v.op, out));
             }
@@ -1180,6 +1204,19 @@ struct Planner {
                 o.nsb = v.nsplit;
                 b.reads.push_back(rng(v.in[0], (int64_t)v.nsplit * v.n));
                 if (!b.prefetch(v.in[0], v.nsplit * v.n, nullptr, 0, &o.w)) return false;
+                break;
+            }
+            case SRC_COMB: {  // the attention partials, combined in LDS
+                int np = v.nsplit * v.heads * (v.dp + 2);
+                o.kind = VP_COMB;
+                o.nsb = v.nsplit;
+                o.heads = v.heads;
+                o.dh = v.dh;
+                o.dp = v.dp;
+                b.reads.push_back(rng(v.in[0], np));
+                if (!b.prefetch(v.in[0], np, nullptr, 0, &o.w)) return false;
+                o.in0 = o.w;
+                o.in1 = b.alloc(2 * v.heads * v.nsplit);  // the superblock weights
                 break;
             }
             default: {
@@ -1474,6 +1511,17 @@ struct Planner {
                 if (overlap(b.writes[a], b.writes[q]) && !(b.writes[a].wg0 && b.writes[q].wg0))
                     return nofuse(i, "two writes meet");
         FgDesc& d = b.d;
+        d.cw = -1;
+        if (nsplit == 1 && d.nvp == 1 && d.vp[0].kind == VP_COMB && d.vp[0].dh == 64 &&
+            (int64_t)d.vp[0].heads * 64 == cols && d.vp[0].nsb <= 64 && xin == d.vp[0].out &&
+            std::count(want.begin(), want.end(), xin) == 1) {
+            // the attention output is only the GEMV's input: wave w combines head w itself
+            d.cw = d.vp[0].w;
+            d.cdp = d.vp[0].dp;
+            d.cnsb = d.vp[0].nsb;
+            d.cgout = d.vp[0].gout;
+            d.nvp = 0;
+        }
         d.cols = (int32_t)cols;
         d.nsl = (int32_t)nsl;
         d.W = W;
@@ -1590,6 +1638,27 @@ struct Planner {
         while (i < ops.size()) {
             const Op& o = ops[i];
             VpSrc v;
+            // one-token attention: its partials wait for the next fused prologue to combine
+            if (fuse && o.kind == OP_ATTEND && attn_dec_ok(o) && !l2q && pend.size() < SLM_VP_MAX &&
+                o.n[5] * o.n[7] <= VP_LEN_MAX && (o.n[5] * o.n[7]) % 4 == 0 &&
+                attn_dec_part_floats(o) <= COMB_PART_MAX && aligned16(c->ws) &&
+                (int64_t)c->ws_bytes >= 4 * ((attn_dec_part_floats(o) + 3) & ~(int64_t)3)) {
+                TRY(row_flush());
+                TRY(flush_pending());
+                TRY(lower_attn_dec(c, o, out, true));
+                v.kind = SRC_COMB;
+                v.n = (int)(o.n[5] * o.n[7]);
+                v.nsplit = (int)o.n[8];
+                v.heads = (int)o.n[5];
+                v.dh = (int)o.n[7];
+                v.dp = (int)attn_dp(o.n[7]);
+                v.in[0] = c->ws;
+                v.out[0] = o.p[0];
+                v.op = &o;
+                pend.push_back(v);
+                i++;
+                continue;
+            }
             if (fuse && pend.size() < SLM_VP_MAX && vp_of(o, &v)) {
                 TRY(row_flush());
                 // a held l2norm's output may not be touched before the GLA kernel
