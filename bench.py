@@ -166,6 +166,33 @@ def traffic():
     return None
 
 
+def fp16_leg(hip, model, a, prompt, fl):
+    """The same workload in fp16 mode (the --fp16 analogue: linears with fp16 operands at
+    fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)."""
+    hip.set_fp16(True)
+    s16 = model.session(a.loops)
+    s16.feed(prompt[:16], 256)
+    s16.logits()
+    t = time.perf_counter()
+    s16.feed(prompt, 256)
+    s16.logits()
+    fill16_s = time.perf_counter() - t
+    if a.warmup:
+        s16.decode_greedy(a.warmup)
+    s16.logits()
+    t = time.perf_counter()
+    s16.decode_greedy(a.steps)
+    s16.logits()
+    dec16_s = time.perf_counter() - t
+    hip.set_fp16(False)
+    fp16 = {"decode_tok_s": round(a.steps / dec16_s, 2), "prefill_tok_s": round(len(prompt) / fill16_s, 1),
+            "prefill_tflops": round(fl / fill16_s / 1e12, 2),
+            "note": "linears round operands to fp16 at v_mfma_f32_16x16x16f16 (fp32 sums); attention, "
+                    "GLA, norms and states fp32; checked at 2e-2 vs the fp32 oracle (config C5)"}
+    log(f"fp16 mode: prefill {fp16['prefill_tok_s']} tok/s, decode {fp16['decode_tok_s']} tok/s")
+    return fp16
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,6 +203,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--no-graphs", action="store_true")
+    ap.add_argument("--no-fp16", action="store_true", help="skip the fp16-mode leg")
     ap.add_argument("--timed-steps", type=int, default=16,
                     help="decode steps whose kernels are timed one by one for the roofline")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -256,27 +284,9 @@ def main():
 
     # the same workload in fp16 mode (the --fp16 analogue: linears with fp16 operands at
     # fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)
-    hip.set_fp16(True)
-    s16 = model.session(a.loops)
-    s16.feed(prompt[:16], 256)
-    s16.logits()
-    t = time.perf_counter()
-    s16.feed(prompt, 256)
-    s16.logits()
-    fill16_s = time.perf_counter() - t
-    if a.warmup:
-        s16.decode_greedy(a.warmup)
-    s16.logits()
-    t = time.perf_counter()
-    s16.decode_greedy(a.steps)
-    s16.logits()
-    dec16_s = time.perf_counter() - t
-    hip.set_fp16(False)
-    fp16 = {"decode_tok_s": round(a.steps / dec16_s, 2), "prefill_tok_s": round(len(prompt) / fill16_s, 1),
-            "prefill_tflops": round(fl / fill16_s / 1e12, 2),
-            "note": "linears round operands to fp16 at v_mfma_f32_16x16x16f16 (fp32 sums); attention, "
-                    "GLA, norms and states fp32; checked at 2e-2 vs the fp32 oracle (config C5)"}
-    log(f"fp16 mode: prefill {fp16['prefill_tok_s']} tok/s, decode {fp16['decode_tok_s']} tok/s")
+    fp16 = None
+    if not a.no_fp16:
+        fp16 = fp16_leg(hip, model, a, prompt, fl)
 
     cpu = None
     if not a.no_cpu:
