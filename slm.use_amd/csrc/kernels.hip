@@ -333,6 +333,37 @@ __device__ __forceinline__ float gla_rows(float (&st)[RPL], const float* kk, con
     return part;
 }
 
+// gla_rows when every lane's RPL rows are inside the head: the rows' k and q read as float4s.
+template <int RPL>
+__device__ __forceinline__ float gla_rows_full(float (&st)[RPL], const float* kk, const float* qq,
+                                               float dc, float vb, int j) {
+    float kv[RPL], qv[RPL];
+    if constexpr (RPL % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < RPL / 4; c++) {
+            f4 a = *(const f4*)(kk + j * RPL + 4 * c), b = *(const f4*)(qq + j * RPL + 4 * c);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                kv[4 * c + e] = a[e];
+                qv[4 * c + e] = b[e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < RPL; rr++) {
+            kv[rr] = kk[j * RPL + rr];
+            qv[rr] = qq[j * RPL + rr];
+        }
+    }
+    float part = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPL; rr++) {
+        st[rr] = dc * st[rr] + kv[rr] * vb;
+        part = part + qv[rr] * st[rr];
+    }
+    return part;
+}
+
 // The prompt kernel: grid (heads, column groups of 16); each workgroup stages q and k of
 // its head and v of its columns for SLM_GLA_T tokens at a time in LDS.
 template <int RPL>
@@ -340,7 +371,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                          const float* __restrict__ q, const float* __restrict__ k,
                          const float* __restrict__ v, const float* __restrict__ decay,
                          const float* __restrict__ bias, int m, int heads, int dh, int vec) {
-    extern __shared__ float lds[];  // [SLM_GLA_T][q (dh) | k (dh) | v (16)], then [SLM_GLA_T] d
+    extern __shared__ float lds[];  // 2 x ([SLM_GLA_T][q (dh) | k (dh) | v (16)], then [SLM_GLA_T] d)
     int h = blockIdx.x, c0 = blockIdx.y * 16, tid = threadIdx.x, nt = blockDim.x;
     int b = c0 + (tid >> 4), j = tid & 15;
     bool live = b < dh;
@@ -352,42 +383,70 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
         st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
     }
     float bh = bias[h];
-    int rowl = 2 * dh + 16;
-    float* dcs = lds + SLM_GLA_T * rowl;
-    // staging: piece pc (of `vec` floats) of tokens tt0, tt0 + tpar, ...
+    bool full = 16 * RPL == dh && c0 + 16 <= dh;  // uniform
+    int rowl = 2 * dh + 16, bufl = SLM_GLA_T * (rowl + 1);
+    // Two LDS buffers of SLM_GLA_T token rows (then their decays): the next group's rows are
+    // copied straight into one (and its decay inputs loaded into registers) while the
+    // tokens of the other run. Thread tid copies piece pc (of `vec` floats) of tokens
+    // tt0, tt0 + tpar, ...: piece tid·vec of the buffer, so a wave's copies are contiguous.
     int lpt = rowl / vec, tpar = max(1, nt / lpt);
     int tt0 = tid / lpt, pc = (tid % lpt) * vec;
-    const float* src0 = nullptr;
+    bool loader = tid < tpar * lpt;
+    const float* src0 = q + (long long)h * dh;  // (a piece past the head's columns copies q)
     if (pc < dh) src0 = q + (long long)h * dh + pc;
     else if (pc < 2 * dh) src0 = k + (long long)h * dh + pc - dh;
     else if (c0 + pc - 2 * dh < dh) src0 = v + (long long)h * dh + c0 + pc - 2 * dh;
-    bool loader = tid < tpar * lpt;
-    for (int i0 = 0; i0 < m; i0 += SLM_GLA_T) {
+    int wbase = (tid & ~63) * vec;  // this wave's first piece
+    auto issue = [&](int i0, int buf) {
         int nt_tok = min(SLM_GLA_T, m - i0);
-        for (int tt = tt0; loader && tt < nt_tok; tt += tpar) {
-            float* dst = lds + tt * rowl + pc;
-            if (!src0) {
-                for (int e = 0; e < vec; e++) dst[e] = 0.0f;
-                continue;
-            }
+        float* base = lds + buf * bufl + wbase;
+        for (int kk = 0; kk * tpar < SLM_GLA_T; kk++) {
+            int tt = tt0 + kk * tpar;
+            if (!loader || tt >= nt_tok) continue;
             const float* src = src0 + (long long)(i0 + tt) * heads * dh;
-            if (vec == 4) *(f4*)dst = *(const f4*)src;
-            else *dst = *src;
+            if (vec == 4)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                                 (__attribute__((address_space(3))) void*)(base + kk * tpar * rowl), 16, 0, 0);
+            else
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                                 (__attribute__((address_space(3))) void*)(base + kk * tpar * rowl), 4, 0, 0);
         }
-        for (int tt = tid; tt < nt_tok; tt += nt)
-            dcs[tt] = 1.0f / (1.0f + expf(decay[(long long)(i0 + tt) * heads + h] + bh));
+    };
+    float dnext = 0.0f;  // thread tt: the decay input of token tt of the next group
+    issue(0, 0);
+    if (tid < min(SLM_GLA_T, m)) dnext = decay[(long long)tid * heads + h];
+    for (int i0 = 0, buf = 0; i0 < m; i0 += SLM_GLA_T, buf ^= 1) {
+        int nt_tok = min(SLM_GLA_T, m - i0);
+        const float* rows = lds + buf * bufl;
+        float* dcs = lds + buf * bufl + SLM_GLA_T * rowl;
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's copies of the group are in
+        if (tid < nt_tok) dcs[tid] = 1.0f / (1.0f + expf(dnext + bh));
+        // every thread's copies and decays are in, and every thread is done with the group
+        // before (whose buffer the next copies overwrite)
         __syncthreads();
+        if (i0 + SLM_GLA_T < m) {
+            issue(i0 + SLM_GLA_T, buf ^ 1);
+            if (tid < min(SLM_GLA_T, m - i0 - SLM_GLA_T)) dnext = decay[(long long)(i0 + SLM_GLA_T + tid) * heads + h];
+        }
         // eight tokens at a time: their state updates in order, then their eight column
         // sums side by side (no token's sum waits for the next token's update)
         for (int t0 = 0; t0 < nt_tok; t0 += 8) {
             int nu = min(8, nt_tok - t0);
             float part[8];
+            if (full && nu == 8) {  // (every lane's rows inside the head, every column live)
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                part[u] = 0.0f;
-                if (u < nu && live) {
-                    const float* row = lds + (t0 + u) * rowl;
-                    part[u] = gla_rows<RPL>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j, dh);
+                for (int u = 0; u < 8; u++) {
+                    const float* row = rows + (t0 + u) * rowl;
+                    part[u] = gla_rows_full<RPL>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    part[u] = 0.0f;
+                    if (u < nu && live) {
+                        const float* row = rows + (t0 + u) * rowl;
+                        part[u] = gla_rows<RPL>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j, dh);
+                    }
                 }
             }
 #pragma unroll
@@ -397,7 +456,6 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                 for (int u = 0; u < 8; u++)
                     if (u < nu) y[((long long)(i0 + t0 + u) * heads + h) * dh + b] = part[u];
         }
-        __syncthreads();
     }
 #pragma unroll
     for (int rr = 0; rr < RPL; rr++) {
