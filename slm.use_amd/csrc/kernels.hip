@@ -779,7 +779,11 @@ __device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N), other counte
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int BM, int WAVES, bool H>
+// With SILU the weight rows are the two halves of a gate|amp matrix (rows = 2·half): tile
+// rows 0 .. BM/2 − 1 are gate rows r0h + j and rows BM/2 .. BM − 1 the amp rows half + r0h + j
+// (r0h = blockIdx.x·BM/2), and the tile writes amp·gate / (1 + e^−gate) (slm_silu_mul's
+// expression) for its BM/2 output columns of y [m][half]; one split only.
+template <int BM, int WAVES, bool H, bool SILU>
 __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                            const float* __restrict__ w, const float* __restrict__ x, int rows,
                            int cols, int m) {
@@ -795,6 +799,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     // waves: RG groups of the rows times (64 / 16NV) groups of tokens
     int wr = (wave % RG) * (BM / RG), wt = (wave / RG) * 16 * NV;
     long long r0 = (long long)blockIdx.x * BM, t0 = (long long)blockIdx.y * 64;
+    long long r0h = (long long)blockIdx.x * (BM / 2), half = rows / 2;  // (SILU)
     int nsl = cols >> 6;
     int s_first = blockIdx.z * SLM_SPLIT, s_end = min(nsl, s_first + SLM_SPLIT), ns = s_end - s_first;
     // Stage copy: instruction k of this wave covers rows 4k' .. 4k'+3 of the stage's (BM + 64)
@@ -808,8 +813,14 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
             int chunk = pos ^ (rl & 15);
             const float* src;
             if (rr < BM) {
-                bool ok = r0 + rl < rows;
-                src = w + (ok ? (r0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
+                long long wr_ = r0 + rl;
+                bool ok = wr_ < rows;
+                if constexpr (SILU) {
+                    long long j = r0h + (rl < BM / 2 ? rl : rl - BM / 2);
+                    ok = j < half;
+                    wr_ = rl < BM / 2 ? j : half + j;
+                }
+                src = w + (ok ? wr_ * cols : 0) + (long long)sl * 64 + 4 * chunk;
             } else {
                 bool ok = t0 + rl < m;
                 src = x + (ok ? (t0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
@@ -888,6 +899,17 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
             for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
     __syncthreads();
+    if constexpr (SILU) {
+        constexpr int HB = BM / 2;
+        for (int e = tid; e < 64 * HB; e += 64 * WAVES) {
+            int tok = e / HB, j = e % HB;
+            if (t0 + tok < m && r0h + j < half) {
+                float gt = so[tok * (BM + 1) + j], up = so[tok * (BM + 1) + HB + j];
+                y[(t0 + tok) * half + r0h + j] = up * gt / (1.0f + expf(-gt));
+            }
+        }
+        return;
+    }
     float* out = gridDim.z > 1 ? part + (long long)blockIdx.z * m * rows : y;
     for (int e = tid; e < 64 * BM; e += 64 * WAVES) {
         int tok = e / BM, row = e % BM;
@@ -895,15 +917,16 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     }
 }
 
-#define GEMM2(BM, WAVES)                                                                  \
-    KERNEL void __launch_bounds__(64 * WAVES) slm_gemm2_##BM(float* y, float* part, const float* w, \
-                                                           const float* x, int rows, int cols, int m) { \
-        gemm2_body<BM, WAVES, false>(y, part, w, x, rows, cols, m);                       \
-    }                                                                                     \
-    KERNEL void __launch_bounds__(64 * WAVES) slm_gemm2h_##BM(float* y, float* part, const float* w, \
-                                                            const float* x, int rows, int cols, int m) { \
-        gemm2_body<BM, WAVES, true>(y, part, w, x, rows, cols, m);                        \
+#define GEMM2_K(NAME, BM, WAVES, H, S)                                                    \
+    KERNEL void __launch_bounds__(64 * WAVES) NAME(float* y, float* part, const float* w,  \
+                                                   const float* x, int rows, int cols, int m) { \
+        gemm2_body<BM, WAVES, H, S>(y, part, w, x, rows, cols, m);                         \
     }
+#define GEMM2(BM, WAVES)                                  \
+    GEMM2_K(slm_gemm2_##BM, BM, WAVES, false, false)      \
+    GEMM2_K(slm_gemm2h_##BM, BM, WAVES, true, false)      \
+    GEMM2_K(slm_gemm2s_##BM, BM, WAVES, false, true)      \
+    GEMM2_K(slm_gemm2hs_##BM, BM, WAVES, true, true)
 GEMM2(32, 4)
 GEMM2(64, 16)
 GEMM2(96, 8)

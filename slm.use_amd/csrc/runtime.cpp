@@ -110,6 +110,7 @@ struct Kernels {
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
     hipFunction_t attn_dec[3];               // one-token attention, dim tiles 1, 2, 4
+    hipFunction_t gemm2s[4], gemm2hs[4];     // prompt GEMM with the SiLU pair epilogue, BM 32..128
     hipFunction_t rows;                      // prompt row chains
     hipFunction_t attn_pq[3];                // prompt attention, superblock shared in LDS
 };
@@ -336,6 +337,25 @@ void drop_graphs(slm_hip* c) {
 // per-op lowering (the unfused kernels)
 // ---------------------------------------------------------------------------------------
 
+// The pipelined prompt GEMM's row tile: the one that leaves the busiest CU the least work —
+// rows per tile times the workgroups a CU runs (32-row tiles of four waves go two to a CU,
+// the others one) — the larger tile on a tie.
+int gemm2_bm(int64_t rows, int64_t m, int64_t ns) {
+    int bm = 32;
+    int64_t best = -1;
+    for (int t : {32, 64, 96, 128}) {
+        int64_t wgs = ((rows + t - 1) / t) * ((m + 63) / 64) * ns;
+        int64_t per_cu = t == 32 ? 2 : 1;
+        int64_t rounds = (wgs + per_cu * CU_COUNT - 1) / (per_cu * CU_COUNT);
+        int64_t sharing = std::min<int64_t>(per_cu, (wgs + CU_COUNT - 1) / CU_COUNT);
+        int64_t cost = rounds * t * sharing;
+        if (best < 0 || cost <= best) best = cost, bm = t;
+    }
+    return bm;
+}
+
+uint32_t gemm2_threads(int bm) { return bm == 32 ? 256 : bm == 96 ? 512 : 1024; }
+
 // A linear (p0 y, p1 w, p2 x; n0 rows, n1 cols, n2 m). With `fold_ns`, a split GEMM's
 // partials are left in c->gpart for the caller to add (*fold_ns: the split count, 1 when
 // the GEMM wrote y itself).
@@ -375,25 +395,12 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
         if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
             return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
         if (cols % 64 == 0) {
-            // the pipelined GEMM, with the row tile that leaves the busiest CU the
-            // least work: rows per tile times the workgroups a CU runs (32-row tiles
-            // of four waves go two to a CU, the others of eight waves one), the larger
-            // tile on a tie
-            int bm = 32;
-            int64_t best = -1;
-            for (int t : {32, 64, 96, 128}) {
-                int64_t wgs = ((rows + t - 1) / t) * ((m + 63) / 64) * ns;
-                int64_t per_cu = t == 32 ? 2 : 1;
-                int64_t rounds = (wgs + per_cu * CU_COUNT - 1) / (per_cu * CU_COUNT);
-                int64_t sharing = std::min<int64_t>(per_cu, (wgs + CU_COUNT - 1) / CU_COUNT);
-                int64_t cost = rounds * t * sharing;
-                if (best < 0 || cost <= best) best = cost, bm = t;
-            }
+            int bm = gemm2_bm(rows, m, ns);
             uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
             hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
             if (h) f = bm == 32 ? k.gemm2h_32 : bm == 64 ? k.gemm2h_64 : bm == 96 ? k.gemm2h_96 : k.gemm2h_128;
             out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
-                             (uint32_t)ns, bm == 32 ? 256 : bm == 96 ? 512 : 1024, shmem, p[0], c->gpart,
+                             (uint32_t)ns, gemm2_threads(bm), shmem, p[0], c->gpart,
                              p[1], p[2], (int)rows, (int)cols, (int)m));
         } else {
             out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
@@ -1633,6 +1640,38 @@ struct Planner {
         return used;
     }
 
+    // The prompt MLP's up projection (model.rs:552-555): up = linear(n) [m][2h], gate and amp
+    // its column halves, y = silu_mul(gate, amp). When up, gate and amp are read by nothing
+    // after, one GEMM writes y from paired gate/amp row tiles (slm_gemm2s_*).
+    size_t try_gemm_silu(size_t i) {
+        const Op& L = ops[i];
+        if (i + 3 >= ops.size()) return 0;
+        const Op &cg = ops[i + 1], &ca = ops[i + 2], &sm = ops[i + 3];
+        int64_t rows = L.n[0], cols = L.n[1], m = L.n[2], h = rows / 2;
+        if (m <= 16 || rows % 2 || cols % 64 || cols / 64 > SLM_SPLIT || !aligned16(L.p[1]) ||
+            !aligned16(L.p[2]))
+            return 0;
+        if (cg.kind != OP_COLUMNS || ca.kind != OP_COLUMNS || sm.kind != OP_SILU_MUL) return 0;
+        if (cg.p[1] != L.p[0] || ca.p[1] != L.p[0] || cg.n[0] != m || ca.n[0] != m || cg.n[1] != rows ||
+            ca.n[1] != rows || cg.n[2] != 0 || ca.n[2] != h || cg.n[3] != h || ca.n[3] != h)
+            return 0;
+        if (sm.p[1] != cg.p[0] || sm.p[2] != ca.p[0] || sm.n[0] != m * h) return 0;
+        if (!dead_after(ops, i + 4, rng(L.p[0], m * rows)) || !dead_after(ops, i + 4, rng(cg.p[0], m * h)) ||
+            !dead_after(ops, i + 4, rng(ca.p[0], m * h)))
+            return 0;
+        Range ry = rng(sm.p[0], m * h);
+        if (overlap(ry, rng(L.p[1], rows * cols)) || overlap(ry, rng(L.p[2], m * cols))) return 0;
+        int bm = gemm2_bm(rows, m, 1);
+        int q = bm == 32 ? 0 : bm == 64 ? 1 : bm == 96 ? 2 : 3;
+        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
+        out.push_back(mk(L.n[3] ? c->k.gemm2hs[q] : c->k.gemm2s[q], (uint32_t)((h + bm / 2 - 1) / (bm / 2)),
+                         (uint32_t)((m + 63) / 64), 1, gemm2_threads(bm), shmem, sm.p[0], c->gpart,
+                         L.p[1], L.p[2], (int)rows, (int)cols, (int)m));
+        out.back().abytes = 4.0 * (double)(rows * cols + m * cols + m * h);
+        last_m = m;
+        return 4;
+    }
+
     int run(bool fuse) {
         size_t i = 0;
         while (i < ops.size()) {
@@ -1695,6 +1734,10 @@ struct Planner {
             TRY(row_flush());
             TRY(flush_pending());
             if (fuse && o.kind == OP_LINEAR && o.n[2] > 1 && !l2q) {
+                if (size_t used = try_gemm_silu(i)) {
+                    i += used;
+                    continue;
+                }
                 int64_t ns = 1, rows = o.n[0], m = o.n[2];
                 TRY(lower_linear(c, o, out, &ns));
                 last_m = m;
@@ -1995,7 +2038,11 @@ int load_kernels(slm_hip* c) {
                {&k.attn_dec[0], "slm_attn_dec_1"}, {&k.attn_dec[1], "slm_attn_dec_2"},
                {&k.attn_dec[2], "slm_attn_dec_4"}, {&k.rows, "slm_rows"},
                {&k.attn_pq[0], "slm_attn_pq_1"}, {&k.attn_pq[1], "slm_attn_pq_2"},
-               {&k.attn_pq[2], "slm_attn_pq_4"}};
+               {&k.attn_pq[2], "slm_attn_pq_4"},
+               {&k.gemm2s[0], "slm_gemm2s_32"},   {&k.gemm2s[1], "slm_gemm2s_64"},
+               {&k.gemm2s[2], "slm_gemm2s_96"},   {&k.gemm2s[3], "slm_gemm2s_128"},
+               {&k.gemm2hs[0], "slm_gemm2hs_32"}, {&k.gemm2hs[1], "slm_gemm2hs_64"},
+               {&k.gemm2hs[2], "slm_gemm2hs_96"}, {&k.gemm2hs[3], "slm_gemm2hs_128"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;

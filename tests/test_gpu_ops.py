@@ -396,7 +396,7 @@ def test_fusion_pattern(hip, case, fp16):
 # prompt row chains: the element-wise ops between two GEMMs as one launch per chain
 # ---------------------------------------------------------------------------------------
 
-ROW_CASES = ["attn_in", "mlp", "inplace", "overlap"]
+ROW_CASES = ["attn_in", "mlp", "mlp_dead", "inplace", "overlap"]
 
 
 @pytest.mark.parametrize("m", [37, 256])
@@ -448,6 +448,16 @@ def test_row_chain(hip, case, m):
             hip.add(o["t"].ptr, res.ptr, o["dn"].ptr, m * d)
             hip.rms(o["n"].ptr, o["t"].ptr, nw.ptr, m, d, 1e-6)
             hip.linear(o["z"].ptr, wsq.ptr, d, d, o["n"].ptr, m)
+        elif case == "mlp_dead":  # up, gate and amp are overwritten before anything reads
+            # them: the up GEMM writes the SiLU pair's product itself
+            hip.linear(o["up"].ptr, wup.ptr, 2 * hid, d, x.ptr, m)
+            hip.columns(o["g"].ptr, o["up"].ptr, m, 2 * hid, 0, hid)
+            hip.columns(o["u"].ptr, o["up"].ptr, m, 2 * hid, hid, hid)
+            hip.silu_mul(o["h"].ptr, o["g"].ptr, o["u"].ptr, m * hid)
+            hip.linear(o["dn"].ptr, wdown.ptr, d, hid, o["h"].ptr, m)
+            hip.copy(o["g"].ptr, o["h"].ptr, m * hid)
+            hip.add(o["u"].ptr, o["h"].ptr, o["g"].ptr, m * hid)
+            hip.linear(o["up"].ptr, wup.ptr, 2 * hid, d, o["dn"].ptr, m)
         elif case == "inplace":
             hip.linear(o["t"].ptr, wsq.ptr, d, d, x.ptr, m)
             hip.add(o["t"].ptr, o["t"].ptr, res.ptr, m * d)
