@@ -949,6 +949,35 @@ GEMM2(128, 16)
 // Scores use the same 16x16x4 MFMA chain over dh as linear; P·V runs four MFMAs per tile
 // (MFMA r takes keys r, r+4, r+8, r+12).
 
+// v combined with lane l ^ 16 (or l ^ 32) through register lane swaps: v_permlane16_swap
+// gives every lane its row pair's even-row and odd-row values (v_permlane32_swap its half
+// pair's), so a symmetric op of the two is the lane's value with its partner's — the same bits
+// as op(v, shfl_xor(v, 16)) for the commutative max, + and |.
+__device__ __forceinline__ float xmax16(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xmax32(float v) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xsum16(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xsum32(float v) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ int xor16i(int v) {
+    auto p = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)(p[0] | p[1]);
+}
+__device__ __forceinline__ int xor32i(int v) {
+    auto p = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)(p[0] | p[1]);
+}
+
 // (M, L, O) ⊕= (mB, lB, oB); an empty partial (l = 0) changes nothing.
 __device__ __forceinline__ void fold(float& M, float& L, float& O, float mB, float lB,
                                      float oB) {
@@ -1059,19 +1088,19 @@ __device__ void attn_segment(const Col& col, const f4 (&qv)[DT], const float* __
             any = any || ok;
         }
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = xmax16(mx);
+        mx = xmax32(mx);
         int anyi = any ? 1 : 0;
-        anyi |= __shfl_xor(anyi, 16);
-        anyi |= __shfl_xor(anyi, 32);
+        anyi = xor16i(anyi);
+        anyi = xor32i(anyi);
         float mnew = fmaxf(mo, mx);
         float muse = mnew == NEG_INF ? 0.0f : mnew;
         float p[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) p[r] = sv[r] == NEG_INF ? 0.0f : expf(sv[r] - muse);
         float rs = ((p[0] + p[1]) + p[2]) + p[3];
-        rs = rs + __shfl_xor(rs, 16);
-        rs = rs + __shfl_xor(rs, 32);
+        rs = xsum16(rs);
+        rs = xsum32(rs);
         float alpha = expf(mo - muse);
         f4 on[DT];
 #pragma unroll
@@ -1320,19 +1349,19 @@ __device__ void attn_seg_lds(const Col& col, const f4 (&qv)[DT], const float* kt
             any = any || ok;
         }
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = xmax16(mx);
+        mx = xmax32(mx);
         int anyi = any ? 1 : 0;
-        anyi |= __shfl_xor(anyi, 16);
-        anyi |= __shfl_xor(anyi, 32);
+        anyi = xor16i(anyi);
+        anyi = xor32i(anyi);
         float mnew = fmaxf(mo, mx);
         float muse = mnew == NEG_INF ? 0.0f : mnew;
         float p[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) p[r] = sv[r] == NEG_INF ? 0.0f : expf(sv[r] - muse);
         float rs = ((p[0] + p[1]) + p[2]) + p[3];
-        rs = rs + __shfl_xor(rs, 16);
-        rs = rs + __shfl_xor(rs, 32);
+        rs = xsum16(rs);
+        rs = xsum32(rs);
         float alpha = expf(mo - muse);
         f4 on[DT];
 #pragma unroll
