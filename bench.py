@@ -259,6 +259,17 @@ def main():
     dec_s = time.perf_counter() - t
     tok_s = a.steps / dec_s
     log(f"decode: {tok_s:.1f} tok/s over {a.steps} steps at pos {pos0}..{se.pos - 1}")
+    # the same greedy loop with the pick on the device (the logits stay on the GPU; each step's
+    # embedding gather reads the previous step's pick there): the opt-in fast path
+    t = time.perf_counter()
+    se.decode_greedy_device(a.steps)
+    se.logits()
+    dev_s = time.perf_counter() - t
+    dev_pick = {"value": round(a.steps / dev_s, 1), "unit": "tok/s", "steps": a.steps,
+                "from_pos": se.pos - a.steps,
+                "note": "greedy decode with slm_hip_argmax on the device instead of the per-token "
+                        "logits read-back and host pick; the same ids (tests/test_gpu_model.py)"}
+    log(f"decode, device pick: {dev_pick['value']} tok/s")
     stats = hip.graph_stats()
 
     # whole-step roofline (decode) and MFMA utilisation (prefill)
@@ -329,6 +340,7 @@ def main():
                     "achieved_tflops": round(fl / fill_s / 1e12, 2),
                     "peak_tflops": FP32_MFMA_PEAK / 1e12,
                     "frac": round(fl / fill_s / FP32_MFMA_PEAK, 4)},
+        "decode_device_pick": dev_pick,
         "graphs": stats,
         "fp16_mode": fp16,
         "cpu_baseline": cpu,

@@ -77,6 +77,18 @@ int slm_hip_flush(slm_hip* ctx, const float* const* keep, size_t nkeep);
 /* y[i] = w[ids[i]], rows of d (ops.rs:93-94). `ids` is host memory. */
 int slm_hip_gather(slm_hip* ctx, float* y, const float* w, const uint32_t* ids, size_t m,
                    size_t d);
+/* One row of w at an index held in device memory (id[0], a long long below `rows`): the
+ * gather of ops.rs:93-94 for one token whose id a device-side pick wrote, so greedy decode
+ * steps follow each other with no host round trip (replaces the host ids of slm_hip_gather
+ * in that loop, main.rs:219-222). */
+int slm_hip_gather_dev(slm_hip* ctx, float* y, const float* w, const long long* id, size_t rows,
+                       size_t d);
+/* Greedy pick on the device: the index of the first maximum of x[0..n) under sample.rs:46-50
+ * (b = 0, b = i whenever x[i] > x[b]: NaNs never win; a NaN at 0 keeps 0), written to tok[0]
+ * and, when ids is not null, to ids[slot] (ids holds ids_cap uint32). Replaces the logits
+ * read-back and host scan of main.rs:219 and sample.rs:33-50 in the greedy loop. */
+int slm_hip_argmax(slm_hip* ctx, long long* tok, uint32_t* ids, size_t ids_cap, size_t slot,
+                   const float* x, size_t n);
 /* y = x (ops.rs:95). */
 int slm_hip_copy(slm_hip* ctx, float* y, const float* x, size_t n);
 /* y[0] = first, y[i] = x[i-1], rows of d (ops.rs:96-104). */

@@ -70,6 +70,8 @@ _SIGS = {
     "slm_hip_read": (_i, [_p, _f32p, _p, _sz]),
     "slm_hip_flush": (_i, [_p, C.POINTER(_p), _sz]),
     "slm_hip_gather": (_i, [_p, _p, _p, _u32p, _sz, _sz]),
+    "slm_hip_gather_dev": (_i, [_p, _p, _p, _p, _sz, _sz]),
+    "slm_hip_argmax": (_i, [_p, _p, _p, _sz, _sz, _p, _sz]),
     "slm_hip_copy": (_i, [_p, _p, _p, _sz]),
     "slm_hip_shift": (_i, [_p, _p, _p, _p, _sz, _sz]),
     "slm_hip_columns": (_i, [_p, _p, _p, _sz, _sz, _sz, _sz]),
@@ -115,6 +117,7 @@ _SIGS = {
     "slm_session_kept_len": (_sz, [_p, _sz]),
     "slm_session_kept_read": (_i, [_p, _sz, _f32p, _sz]),
     "slm_session_decode_greedy": (_i, [_p, _sz, _u32p]),
+    "slm_session_decode_greedy_device": (_i, [_p, _sz, _u32p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -241,6 +244,12 @@ class Hip:
     def gather(self, y, w, ids, d):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         self.check(lib.slm_hip_gather(self.ctx, y, w, _up(ids), ids.size, d))
+
+    def gather_dev(self, y, w, tok, rows, d):
+        self.check(lib.slm_hip_gather_dev(self.ctx, y, w, tok, rows, d))
+
+    def argmax(self, tok, ids, ids_cap, slot, x, n):
+        self.check(lib.slm_hip_argmax(self.ctx, tok, ids, ids_cap, slot, x, n))
 
     def copy(self, y, x, n):
         self.check(lib.slm_hip_copy(self.ctx, y, x, n))
@@ -388,6 +397,12 @@ class Session:
     def decode_greedy(self, n: int) -> np.ndarray:
         ids = np.empty(n, dtype=np.uint32)
         self.model.check(lib.slm_session_decode_greedy(self.h, n, _up(ids)))
+        return ids
+
+    def decode_greedy_device(self, n: int) -> np.ndarray:
+        """decode_greedy with the pick on the device: no logits read-back between steps."""
+        ids = np.empty(n, dtype=np.uint32)
+        self.model.check(lib.slm_session_decode_greedy_device(self.h, n, _up(ids)))
         return ids
 
 

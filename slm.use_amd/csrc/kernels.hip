@@ -123,6 +123,46 @@ KERNEL void slm_gather(float* __restrict__ y, const float* __restrict__ w,
     GRID_LOOP(i, n) y[i] = w[ids[i / d] * d + i % d];
 }
 
+// Greedy pick on the device (sample.rs:46-50: b = 0, then b = i whenever x[i] > x[b]): the
+// first index holding the largest value that is not a NaN, 0 when x[0] is a NaN or no value
+// compares. One workgroup: M = the maximum (fmaxf skips NaNs; the order of a maximum does not
+// matter), then the smallest index with x[i] == M. Writes the index to tok[0] (the next
+// step's gather reads it there) and to ids[slot] (slot from the device when `dslot`).
+KERNEL void __launch_bounds__(1024) slm_argmax(const float* __restrict__ x, long long n,
+                                               long long* __restrict__ tok, unsigned* __restrict__ ids,
+                                               const long long* __restrict__ dslot, long long slot_imm) {
+    __shared__ float wm[16];
+    __shared__ int wi[16];
+    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float M = NEG_INF;
+    for (long long i = tid; i < n; i += 1024) M = fmaxf(M, x[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) wm[wave] = M;
+    __syncthreads();
+    M = wm[0];
+#pragma unroll
+    for (int w = 1; w < 16; w++) M = fmaxf(M, wm[w]);
+    int b = 0x7fffffff;
+    for (long long i = tid; i < n; i += 1024)
+        if (x[i] == M) {
+            b = (int)i;
+            break;
+        }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) b = min(b, __shfl_xor(b, off));
+    if (lane == 0) wi[wave] = b;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++) b = min(b, wi[w]);
+        b = min(b, wi[0]);
+        long long r = b < n ? b : 0;
+        if (!(x[0] == x[0])) r = 0;  // a NaN first: nothing compares greater
+        tok[0] = r;
+        if (ids) ids[dslot ? dslot[0] : slot_imm] = (unsigned)r;
+    }
+}
+
 // Ring write: src [m][heads][dh] → cache [heads][cap][dh] at slots (pos+i) % cap.
 KERNEL void slm_store(float* __restrict__ cache, const float* __restrict__ src,
                       const long long* __restrict__ dyn, long long pos_imm, long long n,

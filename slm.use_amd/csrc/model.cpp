@@ -325,6 +325,13 @@ class Ops {
         ensure(y, m * d);
         ok(slm_hip_gather(c_, y.p, w.p, ids, m, d), "gather");
     }
+    void gather_dev(Buf& y, const Buf& w, const Buf& tok, size_t rows, size_t d) const {
+        ensure(y, d);
+        ok(slm_hip_gather_dev(c_, y.p, w.p, (const long long*)tok.p, rows, d), "gather_dev");
+    }
+    void argmax(Buf& tok, Buf& ids, size_t slot, const Buf& x, size_t n) const {
+        ok(slm_hip_argmax(c_, (long long*)tok.p, (uint32_t*)ids.p, ids.n, slot, x.p, n), "argmax");
+    }
     void copy(Buf& y, At x, size_t n) const {
         ensure(y, n);
         ok(slm_hip_copy(c_, y.p, view(x, n, "copy"), n), "copy");
@@ -470,6 +477,7 @@ struct slm_session {
     std::vector<State> coda;
     Scratch sc;
     Buf x, s, e0, e_proj, last, logits;
+    Buf tok, ids;  // device-side greedy decode: the next token (a long long), the picks (uint32)
 };
 
 namespace {
@@ -821,12 +829,18 @@ std::vector<const Buf*> kept(const Session& se) {  // model.rs:626-638
 }
 
 // model.rs:563-640
-void advance(Model& M, Session& se, const uint32_t* tokens, size_t m, bool want_logits) {
+// With `pick` >= 0 (one token, greedy decode on the device) the token comes from se.tok and
+// the step ends with the pick of the next one into se.tok and se.ids[pick].
+void advance(Model& M, Session& se, const uint32_t* tokens, size_t m, bool want_logits,
+             long pick = -1) {
     const Ops& ops = M.ops;
     size_t d = M.cfg.d_model, pos = se.pos;
     if (m == 0 || m > CHUNK) throw SlmError(SLM_E_INVALID, "advance takes 1 to 256 tokens");
     ops.rope_table(se.sc.cos, se.sc.sin, M.inv_freq, pos, m, M.cfg.head_dim() / 2);
-    ops.gather(se.e0, M.embed.w, tokens, m, d);
+    if (pick >= 0)
+        ops.gather_dev(se.e0, M.embed.w, se.tok, M.cfg.vocab_size, d);
+    else
+        ops.gather(se.e0, M.embed.w, tokens, m, d);
     ops.copy(se.x, at(se.e0, 0), m * d);
     for (size_t i = 0; i < M.prelude.size(); i++)
         block(M, M.prelude[i], se.prelude[i], se.x, se.e0, se.sc, pos, m);
@@ -853,6 +867,7 @@ void advance(Model& M, Session& se, const uint32_t* tokens, size_t m, bool want_
         ops.copy(se.last, at(se.x, (m - 1) * d), d);
         ops.rms(se.sc.n, at(se.last, 0), M.norm_f, 1, d, M.cfg.norm_eps);
         ops.linear(se.logits, M.embed.w, M.cfg.vocab_size, d, at(se.sc.n, 0), 1);
+        if (pick >= 0) ops.argmax(se.tok, se.ids, (size_t)pick, se.logits, M.cfg.vocab_size);
     }
     se.pos += m;
     ops.flush(kept(se));
@@ -990,7 +1005,7 @@ void slm_session_free(slm_session* s) {
     Scratch& sc = s->sc;
     for (Buf* p : {&sc.n, &sc.mix, &sc.q, &sc.k, &sc.v, &sc.g, &sc.y, &sc.y2, &sc.h, &sc.t, &sc.d,
                    &sc.shifted, &sc.prev_kv, &sc.up, &sc.gate, &sc.mid, &sc.scores, &sc.cos, &sc.sin,
-                   &s->x, &s->s, &s->e0, &s->e_proj, &s->last, &s->logits})
+                   &s->x, &s->s, &s->e0, &s->e_proj, &s->last, &s->logits, &s->tok, &s->ids})
         free_buf(ops, *p);
     delete s;
 }
@@ -1055,6 +1070,28 @@ int slm_session_decode_greedy(slm_session* s, size_t n, uint32_t* ids) {
             ids[t] = (uint32_t)b;
             advance(M, *s, &ids[t], 1, true);
         }
+    });
+}
+
+int slm_session_decode_greedy_device(slm_session* s, size_t n, uint32_t* ids) {
+    if (!s || (n && !ids)) return SLM_E_INVALID;
+    return guard(s->model, [&] {
+        Model& M = *s->model;
+        const Ops& ops = M.ops;
+        size_t V = M.cfg.vocab_size;
+        if (!n) return;
+        if (s->tok.n < 2) {
+            ops.release(s->tok);
+            s->tok = ops.zeros(2);
+        }
+        if (s->ids.n < n + 1) {
+            ops.release(s->ids);
+            s->ids = ops.zeros(n + 1);
+        }
+        ops.argmax(s->tok, s->ids, 0, s->logits, V);  // the first pick, from the current logits
+        for (size_t t = 0; t < n; t++) advance(M, *s, nullptr, 1, true, (long)(t + 1));
+        std::vector<float> got = ops.read(s->ids, n);  // uint32 ids in float-sized slots
+        std::memcpy(ids, got.data(), n * 4);
     });
 }
 

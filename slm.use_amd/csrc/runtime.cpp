@@ -54,7 +54,8 @@ constexpr int64_t CU_COUNT = 256;           // MI355X compute units
 
 enum OpKind : uint32_t {
     OP_GATHER = 1, OP_COPY, OP_SHIFT, OP_COLUMNS, OP_LINEAR, OP_ADD, OP_ADD_ROW, OP_SCALE_ROWS,
-    OP_MIX, OP_RMS, OP_SILU_MUL, OP_ROPE_TABLE, OP_ROPE, OP_L2NORM, OP_GLA, OP_STORE, OP_ATTEND
+    OP_MIX, OP_RMS, OP_SILU_MUL, OP_ROPE_TABLE, OP_ROPE, OP_L2NORM, OP_GLA, OP_STORE, OP_ATTEND,
+    OP_ARGMAX
 };
 
 // One operation, by value. p[] are device pointers (outputs first), n[] sizes, f[]
@@ -110,6 +111,7 @@ struct Kernels {
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
     hipFunction_t attn_dec[3];               // one-token attention, dim tiles 1, 2, 4
+    hipFunction_t argmax;                    // greedy pick on the device
     hipFunction_t gemm2s[4], gemm2hs[4];     // prompt GEMM with the SiLU pair epilogue, BM 32..128
     hipFunction_t rows;                      // prompt row chains
     hipFunction_t attn_pq[3];                // prompt attention, superblock shared in LDS
@@ -458,6 +460,10 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
     const float* const* p = o.p;
     const int64_t* n = o.n;
     switch (o.kind) {
+        case OP_ARGMAX:  // p0 tok (long long), p1 x, p2 ids (uint32); n0 n, n1 slot, n2 ids cap; dyn slot
+            out.push_back(mk(k.argmax, 1, 1, 1, 1024, 0, p[1], (long long)n[0], (long long*)p[0],
+                             (unsigned*)p[2], (const long long*)o.dyn, (long long)n[1]));
+            return SLM_OK;
         case OP_GATHER:  // p0 y, p1 w; n0 m, n1 d; dyn ids
             out.push_back(mk(k.gather, blocks_for(n[0] * n[1]), 1, 1, 256, 0, p[0], p[1],
                              (const long long*)o.dyn, (long long)(n[0] * n[1]), (long long)n[1]));
@@ -673,6 +679,11 @@ void op_ranges(const Op& o, std::vector<Range>& rd, std::vector<Range>& wr) {
     const int64_t* n = o.n;
     switch (o.kind) {
         case OP_GATHER: wr.push_back(rng(p[0], n[0] * n[1])); rd.push_back(rng(p[1], 1)); break;
+        case OP_ARGMAX:
+            wr.push_back(rng(p[0], 2));
+            if (p[2]) wr.push_back(rng(p[2], n[2]));
+            rd.push_back(rng(p[1], n[0]));
+            break;
         case OP_COPY: wr.push_back(rng(p[0], n[0])); rd.push_back(rng(p[1], n[0])); break;
         case OP_SHIFT:
             wr.push_back(rng(p[0], n[0] * n[1]));
@@ -2038,7 +2049,7 @@ int load_kernels(slm_hip* c) {
                {&k.attn_dec[0], "slm_attn_dec_1"}, {&k.attn_dec[1], "slm_attn_dec_2"},
                {&k.attn_dec[2], "slm_attn_dec_4"}, {&k.rows, "slm_rows"},
                {&k.attn_pq[0], "slm_attn_pq_1"}, {&k.attn_pq[1], "slm_attn_pq_2"},
-               {&k.attn_pq[2], "slm_attn_pq_4"},
+               {&k.attn_pq[2], "slm_attn_pq_4"},     {&k.argmax, "slm_argmax"},
                {&k.gemm2s[0], "slm_gemm2s_32"},   {&k.gemm2s[1], "slm_gemm2s_64"},
                {&k.gemm2s[2], "slm_gemm2s_96"},   {&k.gemm2s[3], "slm_gemm2s_128"},
                {&k.gemm2hs[0], "slm_gemm2hs_32"}, {&k.gemm2hs[1], "slm_gemm2hs_64"},
@@ -2429,6 +2440,37 @@ int slm_hip_gather(slm_hip* c, float* y, const float* w, const uint32_t* ids, si
     o.n[0] = (int64_t)m;
     o.n[1] = (int64_t)d;
     TRY(stage(c, v.data(), m * 8, &o.dyn));
+    return submit(c, o);
+}
+
+int slm_hip_gather_dev(slm_hip* c, float* y, const float* w, const long long* id, size_t rows, size_t d) {
+    if (!c || !id || !rows) return SLM_E_INVALID;
+    NEED(c, "gather_dev", y, d);
+    NEED(c, "gather_dev", w, rows * d);
+    NEED(c, "gather_dev", (const float*)id, 2);
+    if (!d) return SLM_OK;
+    Op o = op(OP_GATHER);
+    o.p[0] = y;
+    o.p[1] = w;
+    o.n[0] = 1;
+    o.n[1] = (int64_t)d;
+    o.dyn = id;  // read on the device when the op runs (slm_argmax writes an index below rows)
+    return submit(c, o);
+}
+
+int slm_hip_argmax(slm_hip* c, long long* tok, uint32_t* ids, size_t ids_cap, size_t slot,
+                   const float* x, size_t n) {
+    if (!c || !tok || !n || n > (size_t)INT32_MAX || (ids && slot >= ids_cap)) return SLM_E_INVALID;
+    NEED(c, "argmax", x, n);
+    NEED(c, "argmax", (const float*)tok, 2);
+    if (ids) NEED(c, "argmax", (const float*)ids, ids_cap);
+    Op o = op(OP_ARGMAX);
+    o.p[0] = (float*)tok;
+    o.p[1] = x;
+    o.p[2] = (float*)ids;
+    o.n[0] = (int64_t)n;
+    o.n[2] = (int64_t)ids_cap;
+    if (ids) TRY(stage_pos(c, slot, o, 1));  // the slot staged per step (graphs stay reusable)
     return submit(c, o);
 }
 

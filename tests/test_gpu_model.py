@@ -76,6 +76,28 @@ def test_c1_tiny_random_greedy(pkg, hip):
     assert gs2.decode_greedy(16).tolist() == ids_c
 
 
+@pytest.mark.parametrize("shape,loops,n", [("tiny", 2, 24), ("a86", 4, 12)])
+def test_decode_greedy_device_equals_host_pick(pkg, hip, shape, loops, n):
+    """Greedy decode with the pick on the device (the next step's gather reads it there)
+    gives the ids of the host loop, and leaves the same session: logits, position and every
+    kept buffer bit for bit."""
+    folder = model_dir(shape, 1)
+    m = pkg.Model(hip, folder)
+    prompt = synth.tokens(40, m.cfg.raw["vocab_size"], seed=5)
+    a, b = m.session(loops), m.session(loops)
+    a.feed(prompt, 256)
+    b.feed(prompt, 256)
+    ids_host = a.decode_greedy(n).tolist()
+    ids_dev = b.decode_greedy_device(n).tolist()
+    print(shape, ids_host)
+    assert ids_dev == ids_host
+    assert a.pos == b.pos
+    assert np.array_equal(a.logits(), b.logits())
+    _kept_equal(a, b)
+    # a second run continues from there (the device slot and ids buffer are reused)
+    assert b.decode_greedy_device(3).tolist() == a.decode_greedy(3).tolist()
+
+
 def _kept_equal(a, b):
     ka, kb = a.kept(), b.kept()
     assert len(ka) == len(kb)

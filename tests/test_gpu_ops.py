@@ -396,6 +396,47 @@ def test_fusion_pattern(hip, case, fp16):
 # prompt row chains: the element-wise ops between two GEMMs as one launch per chain
 # ---------------------------------------------------------------------------------------
 
+def _pick(x):
+    """sample.rs:46-50: b = 0, then b = i whenever x[i] > x[b]."""
+    b = 0
+    for i in range(1, len(x)):
+        if x[i] > x[b]:
+            b = i
+    return b
+
+
+@pytest.mark.parametrize("case", ["random", "ties", "nan_first", "nan_inside", "all_neg_inf",
+                                  "signed_zero", "short", "odd"])
+def test_argmax_picks_like_the_reference(hip, case):
+    """The device pick gives the reference's greedy index: the first maximum, NaNs never
+    chosen, a NaN at 0 keeping 0; written to the token slot and the ids slot."""
+    n = {"short": 1, "odd": 1025}.get(case, 32000)
+    x = rnd(n)
+    if case == "ties":
+        x[[7, 900, 31000]] = 9.0
+    if case == "nan_first":
+        x[0] = np.nan
+        x[5] = 50.0
+    if case == "nan_inside":
+        x[[3, 100, 20000]] = np.nan
+        x[4000] = 7.0
+    if case == "all_neg_inf":
+        x[:] = -np.inf
+    if case == "signed_zero":
+        x[:] = -1.0
+        x[10] = -0.0
+        x[20] = 0.0
+    want = _pick(x)
+    dx = hip.upload(x)
+    tok = hip.alloc(2)
+    ids = hip.alloc(4)
+    hip.argmax(tok.ptr, ids.ptr, 4, 2, dx.ptr, n)
+    hip.flush()
+    got_tok = int(tok.read(2).view(np.int64)[0])
+    got_id = int(ids.read(4).view(np.uint32)[2])
+    assert got_tok == want and got_id == want, (case, got_tok, got_id, want)
+
+
 ROW_CASES = ["attn_in", "mlp", "mlp_dead", "inplace", "overlap"]
 
 
