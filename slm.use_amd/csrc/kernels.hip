@@ -819,14 +819,31 @@ __device__ __forceinline__ void vm_wait() {  // s_waitcnt vmcnt(N), other counte
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// The attention-input epilogue (ROPE, BM = dh = 64, rows = 3·d): y [m][3d] is written as
+// usual, and tile r0 is one head of q, k or v: q and k are also written rotated (slm_rope's
+// expressions with the cos/sin rows of each token) into ep.q / ep.k [m][d], v as it is into
+// ep.v, and k and v into the rings at slot (pos + t) mod cap (slm_store).
+struct GemmEpi {
+    float* q;
+    float* k;
+    float* v;
+    float* kring;
+    float* vring;
+    const float* cs;  // [m][32]
+    const float* sn;
+    const long long* kdyn;  // each ring store's position on the device (or null: kpos, vpos)
+    const long long* vdyn;
+    long long kpos, vpos, cap;
+    int d, pad;
+};
 // With SILU the weight rows are the two halves of a gate|amp matrix (rows = 2·half): tile
 // rows 0 .. BM/2 − 1 are gate rows r0h + j and rows BM/2 .. BM − 1 the amp rows half + r0h + j
 // (r0h = blockIdx.x·BM/2), and the tile writes amp·gate / (1 + e^−gate) (slm_silu_mul's
 // expression) for its BM/2 output columns of y [m][half]; one split only.
-template <int BM, int WAVES, bool H, bool SILU>
+template <int BM, int WAVES, bool H, bool SILU, int ROPE = 0>
 __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                            const float* __restrict__ w, const float* __restrict__ x, int rows,
-                           int cols, int m) {
+                           int cols, int m, GemmEpi ep = GemmEpi{}) {
     constexpr int SW = BM * 64, SX = 64 * 64, STAGE = SW + SX;  // floats per stage
     constexpr int NV = WAVES == 4 ? 2 : 1;                      // 16-token MFMA tiles per wave
     constexpr int RG = WAVES == 16 ? 4 : 2;                     // groups of rows over the waves
@@ -939,6 +956,32 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
             for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
     __syncthreads();
+    if constexpr (ROPE != 0) {
+        static_assert(BM == 64, "one head of 64 dims per tile");
+        int region = (int)(r0 / ep.d), head = (int)((r0 % ep.d) >> 6);
+        long long pos = 0;
+        if (region == 1) pos = ep.kdyn ? ep.kdyn[0] : ep.kpos;
+        if (region == 2) pos = ep.vdyn ? ep.vdyn[0] : ep.vpos;
+        float* dst = region == 0 ? ep.q : region == 1 ? ep.k : ep.v;
+        float* ring = region == 1 ? ep.kring : ep.vring;
+        for (int e = tid; e < 64 * 64; e += 64 * WAVES) {
+            int tok = e >> 6, j = e & 63;
+            long long t = t0 + tok;
+            if (t >= m) continue;
+            const float* sr = so + tok * (BM + 1);
+            float v = sr[j];
+            y[t * rows + r0 + j] = v;
+            if (region < 2) {
+                int i = j & 31;
+                float c = ep.cs[t * 32 + i], sn = ep.sn[t * 32 + i];
+                float a = sr[i], b = sr[32 + i];
+                v = j < 32 ? a * c - b * sn : a * sn + b * c;
+            }
+            dst[t * ep.d + head * 64 + j] = v;
+            if (region > 0) ring[((long long)head * ep.cap + (pos + t) % ep.cap) * 64 + j] = v;
+        }
+        return;
+    }
     if constexpr (SILU) {
         constexpr int HB = BM / 2;
         for (int e = tid; e < 64 * HB; e += 64 * WAVES) {
@@ -967,6 +1010,18 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     GEMM2_K(slm_gemm2h_##BM, BM, WAVES, true, false)      \
     GEMM2_K(slm_gemm2s_##BM, BM, WAVES, false, true)      \
     GEMM2_K(slm_gemm2hs_##BM, BM, WAVES, true, true)
+// the QKV projection with the attention-input epilogue (fp32 and fp16 mode)
+#define GEMM2R_K(NAME, H)                                                                       \
+    KERNEL void __launch_bounds__(1024)                                                         \
+        NAME(float* y, float* part, const float* w, const float* x, int rows, int cols, int m,   \
+             float* q, float* k, float* v, float* kring, float* vring, const float* cs,          \
+             const float* sn, const long long* kdyn, const long long* vdyn, long long kpos,     \
+             long long vpos, long long cap, int d) {                                             \
+        gemm2_body<64, 16, H, false, 1>(y, part, w, x, rows, cols, m,                           \
+                                        GemmEpi{q, k, v, kring, vring, cs, sn, kdyn, vdyn, kpos, vpos, cap, d, 0}); \
+    }
+GEMM2R_K(slm_gemm2r_64, false)
+GEMM2R_K(slm_gemm2hr_64, true)
 GEMM2(32, 4)
 GEMM2(64, 16)
 GEMM2(96, 8)

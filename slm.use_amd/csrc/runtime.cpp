@@ -35,7 +35,7 @@ namespace {
 
 std::string g_open_error;
 
-constexpr int MAX_ARGS = 16;
+constexpr int MAX_ARGS = 24;
 constexpr size_t BLOB = 2048;             // bytes of kernel arguments per launch
 constexpr size_t DYN_CAP = 1 << 20;       // bytes of per-step dynamic values
 constexpr size_t STAGE_CAP = 4 << 20;     // bytes of eager staging
@@ -113,6 +113,7 @@ struct Kernels {
     hipFunction_t attn_dec[3];               // one-token attention, dim tiles 1, 2, 4
     hipFunction_t argmax;                    // greedy pick on the device
     hipFunction_t gemm2s[4], gemm2hs[4];     // prompt GEMM with the SiLU pair epilogue, BM 32..128
+    hipFunction_t gemm2r, gemm2hr;           // prompt QKV GEMM with the rope + ring-store epilogue
     hipFunction_t rows;                      // prompt row chains
     hipFunction_t attn_pq[3];                // prompt attention, superblock shared in LDS
 };
@@ -247,6 +248,7 @@ Rec rec(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uin
 template <typename... A>
 Rec mk(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t shmem,
        A... args) {
+    static_assert(sizeof...(A) <= MAX_ARGS, "more kernel arguments than a launch record holds");
     Rec r = rec(f, gx, gy, gz, bx, shmem);
     std::memset(r.blob, 0, 8 * MAX_ARGS);
     pack(r, args...);
@@ -1683,6 +1685,65 @@ struct Planner {
         return 4;
     }
 
+    // The prompt attention input (model.rs:417-432): mix = linear(n) [m][3d]; q = rope(mix
+    // columns 0..d), k = rope(columns d..2d), v = columns 2d..3d; k and v into the rings.
+    // With 64-dim heads each 64-row tile of the GEMM is one head of q, k or v, so one GEMM
+    // (slm_gemm2r_64) writes mix, q, k, v and both rings; only the column scratch that the
+    // chain passes through is left unwritten, so it must be read by nothing after.
+    size_t try_gemm_rope(size_t i) {
+        if (i + 7 >= ops.size()) return 0;
+        const Op &L = ops[i], &c1 = ops[i + 1], &r1 = ops[i + 2], &c2 = ops[i + 3], &r2 = ops[i + 4],
+                 &c3 = ops[i + 5], &s1 = ops[i + 6], &s2 = ops[i + 7];
+        if (c1.kind != OP_COLUMNS || r1.kind != OP_ROPE || c2.kind != OP_COLUMNS || r2.kind != OP_ROPE ||
+            c3.kind != OP_COLUMNS || s1.kind != OP_STORE || s2.kind != OP_STORE)
+            return 0;
+        int64_t rows = L.n[0], cols = L.n[1], m = L.n[2], d = rows / 3;
+        if (m <= 16 || rows % 3 || d % 64 || cols % 64 || cols / 64 > SLM_SPLIT || !aligned16(L.p[1]) ||
+            !aligned16(L.p[2]))
+            return 0;
+        const float* mix = L.p[0];
+        const float* cy = c1.p[0];  // the column scratch
+        auto col_ok = [&](const Op& c, int64_t off, const float* y) {
+            return c.p[0] == y && c.p[1] == mix && c.n[0] == m && c.n[1] == rows && c.n[2] == off &&
+                   c.n[3] == d;
+        };
+        if (!col_ok(c1, 0, cy) || !col_ok(c2, d, cy) || !col_ok(c3, 2 * d, c3.p[0])) return 0;
+        auto rope_ok = [&](const Op& r) {
+            return r.p[1] == cy && r.n[0] == m && r.n[2] == 64 && r.n[1] * 64 == d && r.p[2] == r1.p[2] &&
+                   r.p[3] == r1.p[3];
+        };
+        if (!rope_ok(r1) || !rope_ok(r2)) return 0;
+        const float *q = r1.p[0], *k = r2.p[0], *v = c3.p[0];
+        auto store_ok = [&](const Op& st, const float* src) {
+            return st.p[1] == src && st.n[0] == m && st.n[1] == s1.n[1] && st.n[2] * 64 == d &&
+                   st.n[3] == 64;
+        };
+        if (!store_ok(s1, k) || !store_ok(s2, v) || s1.p[0] == s2.p[0]) return 0;
+        int64_t cap = s1.n[1];
+        // what the chain writes, what it reads: pairwise apart, so the order of the writes
+        // does not matter
+        std::vector<Range> wr = {rng(mix, m * rows), rng(cy, m * d), rng(q, m * d), rng(k, m * d),
+                                 rng(v, m * d), rng(s1.p[0], d * cap), rng(s2.p[0], d * cap)};
+        std::vector<Range> rd = {rng(L.p[1], rows * cols), rng(L.p[2], m * cols), rng(r1.p[2], m * 32),
+                                 rng(r1.p[3], m * 32)};
+        for (size_t a = 0; a < wr.size(); a++) {
+            for (size_t b = a + 1; b < wr.size(); b++)
+                if (overlap(wr[a], wr[b])) return 0;
+            for (auto& x : rd)
+                if (overlap(wr[a], x)) return 0;
+        }
+        if (!dead_after(ops, i + 8, rng(cy, m * d))) return 0;
+        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (64 * 64 + 64 * 64) * 4);
+        out.push_back(mk(L.n[3] ? c->k.gemm2hr : c->k.gemm2r, (uint32_t)(rows / 64), (uint32_t)((m + 63) / 64),
+                         1, gemm2_threads(64), shmem, (float*)mix, c->gpart, L.p[1], L.p[2], (int)rows,
+                         (int)cols, (int)m, (float*)q, (float*)k, (float*)v, (float*)s1.p[0],
+                         (float*)s2.p[0], r1.p[2], r1.p[3], (const long long*)s1.dyn, (const long long*)s2.dyn,
+                         (long long)s1.n[4], (long long)s2.n[4], (long long)cap, (int)d));
+        out.back().abytes = 4.0 * (double)(rows * cols + m * cols + m * rows + 3 * m * d + 2 * m * d + 2 * m * 32);
+        last_m = m;
+        return 8;
+    }
+
     int run(bool fuse) {
         size_t i = 0;
         while (i < ops.size()) {
@@ -1746,6 +1807,10 @@ struct Planner {
             TRY(flush_pending());
             if (fuse && o.kind == OP_LINEAR && o.n[2] > 1 && !l2q) {
                 if (size_t used = try_gemm_silu(i)) {
+                    i += used;
+                    continue;
+                }
+                if (size_t used = try_gemm_rope(i)) {
                     i += used;
                     continue;
                 }
@@ -2053,7 +2118,8 @@ int load_kernels(slm_hip* c) {
                {&k.gemm2s[0], "slm_gemm2s_32"},   {&k.gemm2s[1], "slm_gemm2s_64"},
                {&k.gemm2s[2], "slm_gemm2s_96"},   {&k.gemm2s[3], "slm_gemm2s_128"},
                {&k.gemm2hs[0], "slm_gemm2hs_32"}, {&k.gemm2hs[1], "slm_gemm2hs_64"},
-               {&k.gemm2hs[2], "slm_gemm2hs_96"}, {&k.gemm2hs[3], "slm_gemm2hs_128"}};
+               {&k.gemm2hs[2], "slm_gemm2hs_96"}, {&k.gemm2hs[3], "slm_gemm2hs_128"},
+               {&k.gemm2r, "slm_gemm2r_64"},      {&k.gemm2hr, "slm_gemm2hr_64"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;

@@ -437,7 +437,7 @@ def test_argmax_picks_like_the_reference(hip, case):
     assert got_tok == want and got_id == want, (case, got_tok, got_id, want)
 
 
-ROW_CASES = ["attn_in", "mlp", "mlp_dead", "inplace", "overlap"]
+ROW_CASES = ["attn_in", "attn_in_dead", "mlp", "mlp_dead", "inplace", "overlap"]
 
 
 @pytest.mark.parametrize("m", [37, 256])
@@ -447,6 +447,8 @@ def test_row_chain(hip, case, m):
     per op, for in-place updates, operands read from an earlier op's output at an offset,
     a shared vector read by every row and outputs overwritten later in the chain."""
     d, heads, dh, hid, cap, pos = 768, 12, 64, 3072, 4352, 100
+    if case == "attn_in_dead":
+        pos = cap - 20  # the ring slots wrap inside the chunk
     inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
     cs, sn = hip.alloc(m * 32), hip.alloc(m * 32)
     wsq = hip.upload(rnd(d, d, scale=0.02))
@@ -480,6 +482,18 @@ def test_row_chain(hip, case, m):
             hip.store(o["kr"].ptr, o["k2"].ptr, pos, m, cap, heads, dh)
             hip.store(o["vr"].ptr, o["v"].ptr, pos, m, cap, heads, dh)
             hip.linear(o["t"].ptr, wsq.ptr, d, d, o["q"].ptr, m)
+        elif case == "attn_in_dead":  # model.rs:417-432 as the model issues it: the column
+            # scratch k is overwritten before anything reads it, so the QKV GEMM rotates q and k
+            # and writes the rings itself
+            hip.linear(o["y"].ptr, wqkv.ptr, 3 * d, d, x.ptr, m)
+            hip.columns(o["k"].ptr, o["y"].ptr, m, 3 * d, 0, d)
+            hip.rope(o["q"].ptr, o["k"].ptr, cs.ptr, sn.ptr, m, heads, dh)
+            hip.columns(o["k"].ptr, o["y"].ptr, m, 3 * d, d, d)
+            hip.rope(o["k2"].ptr, o["k"].ptr, cs.ptr, sn.ptr, m, heads, dh)
+            hip.columns(o["v"].ptr, o["y"].ptr, m, 3 * d, 2 * d, d)
+            hip.store(o["kr"].ptr, o["k2"].ptr, pos, m, cap, heads, dh)
+            hip.store(o["vr"].ptr, o["v"].ptr, pos - 7, m, cap, heads, dh)  # its own slots
+            hip.linear(o["k"].ptr, wsq.ptr, d, d, o["q"].ptr, m)
         elif case == "mlp":  # a split GEMM's fold opens the second chain
             hip.linear(o["up"].ptr, wup.ptr, 2 * hid, d, x.ptr, m)
             hip.columns(o["g"].ptr, o["up"].ptr, m, 2 * hid, 0, hid)
