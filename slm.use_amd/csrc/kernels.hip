@@ -831,6 +831,7 @@ struct GemmEpi {
     float* vring;
     const float* cs;  // [m][32]
     const float* sn;
+    float* g;  // (L2: the gate columns)
     const long long* kdyn;  // each ring store's position on the device (or null: kpos, vpos)
     const long long* vdyn;
     long long kpos, vpos, cap;
@@ -956,7 +957,28 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
             for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
     __syncthreads();
-    if constexpr (ROPE != 0) {
+    if constexpr (ROPE == 2) {
+        // The linear-attention input (rows = 4·d): q and k leave L2-normalised per head (the
+        // sum of slm_l2norm, dot16_wave, over the tile's 64 values of a token), v and the gate
+        // as they are; one wave per token, so the sums' lanes are all active.
+        static_assert(BM == 64, "one head of 64 dims per tile");
+        int region = (int)(r0 / ep.d), head = (int)((r0 % ep.d) >> 6);
+        float* dst = region == 0 ? ep.q : region == 1 ? ep.k : region == 2 ? ep.v : ep.g;
+        for (int tok = wave; tok < 64; tok += WAVES) {
+            long long t = t0 + tok;
+            if (t >= m) break;
+            const float* sr = so + tok * (BM + 1);
+            float v = sr[lane];
+            y[t * rows + r0 + lane] = v;
+            if (region < 2) {
+                float dd = dot16_wave(sr, 64, lane);
+                v = v * (1.0f / fmaxf(sqrtf(dd), 1e-12f));
+            }
+            dst[t * ep.d + head * 64 + lane] = v;
+        }
+        return;
+    }
+    if constexpr (ROPE == 1) {
         static_assert(BM == 64, "one head of 64 dims per tile");
         int region = (int)(r0 / ep.d), head = (int)((r0 % ep.d) >> 6);
         long long pos = 0;
@@ -1018,10 +1040,21 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
              const float* sn, const long long* kdyn, const long long* vdyn, long long kpos,     \
              long long vpos, long long cap, int d) {                                             \
         gemm2_body<64, 16, H, false, 1>(y, part, w, x, rows, cols, m,                           \
-                                        GemmEpi{q, k, v, kring, vring, cs, sn, kdyn, vdyn, kpos, vpos, cap, d, 0}); \
+                                        GemmEpi{q, k, v, kring, vring, cs, sn, nullptr, kdyn, vdyn, kpos, vpos, cap, d, 0}); \
     }
 GEMM2R_K(slm_gemm2r_64, false)
 GEMM2R_K(slm_gemm2hr_64, true)
+// the linear-attention QKVG projection with the per-head L2 epilogue (fp32 and fp16 mode)
+#define GEMM2N_K(NAME, H)                                                                        \
+    KERNEL void __launch_bounds__(1024)                                                          \
+        NAME(float* y, float* part, const float* w, const float* x, int rows, int cols, int m,    \
+             float* q, float* k, float* v, float* g, int d) {                                     \
+        gemm2_body<64, 16, H, false, 2>(                                                         \
+            y, part, w, x, rows, cols, m,                                                        \
+            GemmEpi{q, k, v, nullptr, nullptr, nullptr, nullptr, g, nullptr, nullptr, 0, 0, 0, d, 0}); \
+    }
+GEMM2N_K(slm_gemm2n_64, false)
+GEMM2N_K(slm_gemm2hn_64, true)
 GEMM2(32, 4)
 GEMM2(64, 16)
 GEMM2(96, 8)

@@ -114,6 +114,7 @@ struct Kernels {
     hipFunction_t argmax;                    // greedy pick on the device
     hipFunction_t gemm2s[4], gemm2hs[4];     // prompt GEMM with the SiLU pair epilogue, BM 32..128
     hipFunction_t gemm2r, gemm2hr;           // prompt QKV GEMM with the rope + ring-store epilogue
+    hipFunction_t gemm2n, gemm2hn;           // prompt QKVG GEMM with the per-head L2 epilogue
     hipFunction_t rows;                      // prompt row chains
     hipFunction_t attn_pq[3];                // prompt attention, superblock shared in LDS
 };
@@ -1744,6 +1745,52 @@ struct Planner {
         return 8;
     }
 
+    // The prompt linear-attention input (model.rs:434-440): mix = linear(n) [m][4d]; q and k
+    // = l2norm(mix columns 0..d, d..2d) per 64-dim head, v and the gate the columns 2d..3d,
+    // 3d..4d. One GEMM (slm_gemm2n_64) writes mix, q, k, v and the gate; the column scratch
+    // the chain passes through is left unwritten, so it must be read by nothing after.
+    size_t try_gemm_l2(size_t i) {
+        if (i + 6 >= ops.size()) return 0;
+        const Op &L = ops[i], &c1 = ops[i + 1], &n1 = ops[i + 2], &c2 = ops[i + 3], &n2 = ops[i + 4],
+                 &c3 = ops[i + 5], &c4 = ops[i + 6];
+        if (c1.kind != OP_COLUMNS || n1.kind != OP_L2NORM || c2.kind != OP_COLUMNS ||
+            n2.kind != OP_L2NORM || c3.kind != OP_COLUMNS || c4.kind != OP_COLUMNS)
+            return 0;
+        int64_t rows = L.n[0], cols = L.n[1], m = L.n[2], d = rows / 4;
+        if (m <= 16 || rows % 4 || d % 64 || cols % 64 || cols / 64 > SLM_SPLIT || !aligned16(L.p[1]) ||
+            !aligned16(L.p[2]))
+            return 0;
+        const float* mix = L.p[0];
+        const float* cy = c1.p[0];
+        auto col_ok = [&](const Op& c, int64_t off, const float* y) {
+            return c.p[0] == y && c.p[1] == mix && c.n[0] == m && c.n[1] == rows && c.n[2] == off &&
+                   c.n[3] == d;
+        };
+        if (!col_ok(c1, 0, cy) || !col_ok(c2, d, cy) || !col_ok(c3, 2 * d, c3.p[0]) ||
+            !col_ok(c4, 3 * d, c4.p[0]))
+            return 0;
+        auto norm_ok = [&](const Op& o) { return o.p[1] == cy && o.n[1] == 64 && o.n[0] * 64 == m * d; };
+        if (!norm_ok(n1) || !norm_ok(n2)) return 0;
+        const float *q = n1.p[0], *k = n2.p[0], *v = c3.p[0], *g = c4.p[0];
+        std::vector<Range> wr = {rng(mix, m * rows), rng(cy, m * d), rng(q, m * d), rng(k, m * d),
+                                 rng(v, m * d), rng(g, m * d)};
+        std::vector<Range> rd = {rng(L.p[1], rows * cols), rng(L.p[2], m * cols)};
+        for (size_t a = 0; a < wr.size(); a++) {
+            for (size_t b = a + 1; b < wr.size(); b++)
+                if (overlap(wr[a], wr[b])) return 0;
+            for (auto& x : rd)
+                if (overlap(wr[a], x)) return 0;
+        }
+        if (!dead_after(ops, i + 7, rng(cy, m * d))) return 0;
+        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (64 * 64 + 64 * 64) * 4);
+        out.push_back(mk(L.n[3] ? c->k.gemm2hn : c->k.gemm2n, (uint32_t)(rows / 64), (uint32_t)((m + 63) / 64),
+                         1, gemm2_threads(64), shmem, (float*)mix, c->gpart, L.p[1], L.p[2], (int)rows,
+                         (int)cols, (int)m, (float*)q, (float*)k, (float*)v, (float*)g, (int)d));
+        out.back().abytes = 4.0 * (double)(rows * cols + m * cols + m * rows + 4 * m * d);
+        last_m = m;
+        return 7;
+    }
+
     int run(bool fuse) {
         size_t i = 0;
         while (i < ops.size()) {
@@ -1811,6 +1858,10 @@ struct Planner {
                     continue;
                 }
                 if (size_t used = try_gemm_rope(i)) {
+                    i += used;
+                    continue;
+                }
+                if (size_t used = try_gemm_l2(i)) {
                     i += used;
                     continue;
                 }
@@ -2119,7 +2170,8 @@ int load_kernels(slm_hip* c) {
                {&k.gemm2s[2], "slm_gemm2s_96"},   {&k.gemm2s[3], "slm_gemm2s_128"},
                {&k.gemm2hs[0], "slm_gemm2hs_32"}, {&k.gemm2hs[1], "slm_gemm2hs_64"},
                {&k.gemm2hs[2], "slm_gemm2hs_96"}, {&k.gemm2hs[3], "slm_gemm2hs_128"},
-               {&k.gemm2r, "slm_gemm2r_64"},      {&k.gemm2hr, "slm_gemm2hr_64"}};
+               {&k.gemm2r, "slm_gemm2r_64"},      {&k.gemm2hr, "slm_gemm2hr_64"},
+               {&k.gemm2n, "slm_gemm2n_64"},      {&k.gemm2hn, "slm_gemm2hn_64"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;

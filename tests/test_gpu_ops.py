@@ -437,7 +437,7 @@ def test_argmax_picks_like_the_reference(hip, case):
     assert got_tok == want and got_id == want, (case, got_tok, got_id, want)
 
 
-ROW_CASES = ["attn_in", "attn_in_dead", "mlp", "mlp_dead", "inplace", "overlap"]
+ROW_CASES = ["attn_in", "attn_in_dead", "gla_in_dead", "mlp", "mlp_dead", "inplace", "overlap"]
 
 
 @pytest.mark.parametrize("m", [37, 256])
@@ -453,6 +453,7 @@ def test_row_chain(hip, case, m):
     cs, sn = hip.alloc(m * 32), hip.alloc(m * 32)
     wsq = hip.upload(rnd(d, d, scale=0.02))
     wqkv = hip.upload(rnd(3 * d, d, scale=0.02))
+    wqkvg = hip.upload(rnd(4 * d, d, scale=0.02))
     wup = hip.upload(rnd(2 * hid, d, scale=0.02))
     wdown = hip.upload(rnd(d, hid, scale=0.02))
     x = hip.upload(rnd(m, d))
@@ -463,7 +464,7 @@ def test_row_chain(hip, case, m):
 
     def outs():
         o = {k: hip.alloc(n) for k, n in
-             dict(y=m * 3 * d, q=m * d, k=m * d, k2=m * d, v=m * d, up=m * 2 * hid, g=m * hid,
+             dict(y=m * 3 * d, y4=m * 4 * d, gt=m * d, q=m * d, k=m * d, k2=m * d, v=m * d, up=m * 2 * hid, g=m * hid,
                   u=m * hid, h=m * hid, dn=m * d, t=m * d, n=m * d, z=m * d, s=m * d,
                   y2=m * d, a=m * d // 2, b=m * d, c2=m * d // 2,
                   kr=heads * cap * dh, vr=heads * cap * dh).items()}
@@ -493,6 +494,16 @@ def test_row_chain(hip, case, m):
             hip.columns(o["v"].ptr, o["y"].ptr, m, 3 * d, 2 * d, d)
             hip.store(o["kr"].ptr, o["k2"].ptr, pos, m, cap, heads, dh)
             hip.store(o["vr"].ptr, o["v"].ptr, pos - 7, m, cap, heads, dh)  # its own slots
+            hip.linear(o["k"].ptr, wsq.ptr, d, d, o["q"].ptr, m)
+        elif case == "gla_in_dead":  # model.rs:434-440: the QKVG GEMM normalises q and k per
+            # head and writes v and the gate itself (the column scratch k is dead)
+            hip.linear(o["y4"].ptr, wqkvg.ptr, 4 * d, d, x.ptr, m)
+            hip.columns(o["k"].ptr, o["y4"].ptr, m, 4 * d, 0, d)
+            hip.l2norm(o["q"].ptr, o["k"].ptr, m * heads, dh)
+            hip.columns(o["k"].ptr, o["y4"].ptr, m, 4 * d, d, d)
+            hip.l2norm(o["k2"].ptr, o["k"].ptr, m * heads, dh)
+            hip.columns(o["v"].ptr, o["y4"].ptr, m, 4 * d, 2 * d, d)
+            hip.columns(o["gt"].ptr, o["y4"].ptr, m, 4 * d, 3 * d, d)
             hip.linear(o["k"].ptr, wsq.ptr, d, d, o["q"].ptr, m)
         elif case == "mlp":  # a split GEMM's fold opens the second chain
             hip.linear(o["up"].ptr, wup.ptr, 2 * hid, d, x.ptr, m)
