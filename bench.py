@@ -1,22 +1,26 @@
 """Token-loop benchmark on one MI355X: the reference's `slm bench` sequence
-(src/main.rs:285-315) on the 86M-class synthetic model.
+(src/main.rs:285-315) on the 86M-class synthetic model, at R = 4, 8 and 16.
 
-    python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--loops 4] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--no-cpu] [--no-g86] [--no-fp16]
 
 Workload (one GPU): model "a86" (d 768, 12 x 64 heads, FFN 4x, vocab 32000, window 4096,
-prelude SS / core LS / coda SS, seeded N(0, 0.02) fp32 weights), R loops. A session reads
-16 warm-up tokens, then a 4096-token uniform-random prompt in 256-token chunks (timed:
-prefill tok/s, including the final logits read, main.rs:200-205) — which fills the
-sliding window — then decodes greedily, reading the logits back every token
-(main.rs:207-223): `--warmup` untimed tokens, then `--steps` timed ones. A "step" is one
-decoded token.
+prelude SS / core LS / coda SS, seeded N(0, 0.02) fp32 weights). For each R in 4, 8, 16 (the
+loop counts main.rs:134-135 bench over) a new session reads 16 warm-up tokens, then a
+4096-token uniform-random prompt in 256-token chunks (timed: prefill tok/s, including the
+final logits read, main.rs:200-205) — which fills the sliding window — then decodes greedily,
+reading the logits back every token (main.rs:207-223): `--warmup` untimed tokens, then
+`--steps` timed ones. With the defaults the positions run to 4384, past the 4352-slot ring
+(window + 256), so the rings overwrite as in the reference bench. A "step" is one decoded
+token; `value` is decode tok/s at R = 4, the headline configuration.
 
-Printed: one JSON line. `value` is decode tok/s. `roofline` is the dominant decode kernel
-(the fused one-token GEMV, slm_fg) against HBM: its launches over `--timed-steps` further
-decode steps, each bracketed by HIP events on the backend's stream, and the algorithmic
-bytes they move (weights, prologue vectors, outputs); `decode_roofline` is the whole step
-against HBM (algorithmic bytes per token); `prefill` is prefill against fp32 MFMA peak. `cpu_baseline` times the oracle (a C++ restatement of src/cpu.rs +
-src/model.rs, OpenMP over the host's cores) on a bounded sample of the same workload.
+Also printed, in the same JSON line: `r4`, `r8`, `r16` (decode and prefill tok/s with their
+HBM and MFMA roofline fractions), `g86` (the 16384-token prompt of the global-attention
+model, config C4, then 128 decode steps), `roofline` (the dominant decode kernel, the fused
+one-token GEMV slm_fg, against HBM: its launches over `--timed-steps` more decode steps, each
+timed by the start and stop events of hipExtModuleLaunchKernel on the backend's stream, which
+carry the dispatch's own begin and end timestamps), and `cpu_baseline` (the oracle, a C++
+restatement of src/cpu.rs + src/model.rs, OpenMP over the host's cores, on a bounded sample
+of the same workload).
 """
 
 from __future__ import annotations
@@ -166,6 +170,69 @@ def traffic():
     return None
 
 
+def cpu_model() -> str:
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run_loops(model, cfg, prompt, loops, warmup, steps):
+    """The reference bench sequence at one loop count: 16 warm-up tokens, the timed prompt,
+    untimed then timed greedy decode. Returns (prefill tok/s, decode tok/s, first timed
+    position, ids of the warm-up and timed steps, the session)."""
+    se = model.session(loops)
+    se.feed(prompt[:16], 256)  # main.rs:309
+    se.logits()
+    t = time.perf_counter()
+    se.feed(prompt, 256)
+    se.logits()
+    fill_s = time.perf_counter() - t
+    ids = se.decode_greedy(warmup).tolist() if warmup else []
+    se.logits()
+    pos0 = se.pos
+    t = time.perf_counter()
+    ids += se.decode_greedy(steps).tolist()
+    se.logits()  # waits for the last step
+    dec_s = time.perf_counter() - t
+    return len(prompt) / fill_s, steps / dec_s, pos0, ids, se
+
+
+def g86_leg(pkg, hip, synth):
+    """Config C4: the g86 model (global layers with logn, kshift, emb, far, 4 key heads), a
+    16384-token prompt at R = 4 in 256-token chunks (the global caches grow 8192 -> 16384 ->
+    32768), then 128 greedy decode steps."""
+    cache = Path(os.environ.get("SLM_MODEL_CACHE", "/tmp")) / "slm_models"
+    folder = synth.write_model(cache / "g86-4", "g86", 4)
+    cfg = synth.G86
+    prompt = synth.tokens(16384, cfg["vocab_size"], seed=6)
+    model = pkg.Model(hip, folder)
+    se = model.session(4)
+    t = time.perf_counter()
+    se.feed(prompt, 256)
+    se.logits()
+    fill_s = time.perf_counter() - t
+    pos0 = se.pos
+    t = time.perf_counter()
+    se.decode_greedy(128)
+    se.logits()
+    dec_s = time.perf_counter() - t
+    fl = prefill_flops(cfg, 4, 0, len(prompt))
+    bpt = np.mean([decode_bytes(cfg, 4, p) for p in range(pos0, pos0 + 128)])
+    out = {"prompt_tokens": len(prompt), "prefill_tok_s": round(len(prompt) / fill_s, 1),
+           "prefill_tflops": round(fl / fill_s / 1e12, 2),
+           "prefill_frac": round(fl / fill_s / FP32_MFMA_PEAK, 4),
+           "decode_tok_s": round(128 / dec_s, 1), "decode_from_pos": pos0,
+           "decode_bytes_per_token": round(bpt),
+           "decode_frac": round(bpt * 128 / dec_s / HBM_PEAK, 4),
+           "layers": "SG|LS|SG", "loops": 4}
+    del se, model
+    return out
+
+
 def fp16_leg(hip, model, a, prompt, fl):
     """The same workload in fp16 mode (the --fp16 analogue: linears with fp16 operands at
     fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)."""
@@ -198,12 +265,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--loops", type=int, default=4)
+    ap.add_argument("--loops", type=int, nargs="+", default=[4, 8, 16],
+                    help="loop counts to bench (the first is the headline)")
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--no-graphs", action="store_true")
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16-mode leg")
+    ap.add_argument("--no-g86", action="store_true", help="skip the g86 16K-prompt leg (config C4)")
     ap.add_argument("--timed-steps", type=int, default=16,
                     help="decode steps whose kernels are timed one by one for the roofline")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -241,24 +310,28 @@ def main():
         hip.set_graphs(False)
     log("device:", hip.name())
     model = pkg.Model(hip, folder)
-    se = model.session(a.loops)
-    se.feed(prompt[:16], 256)  # main.rs:309
-    se.logits()
-    t = time.perf_counter()
-    se.feed(prompt, 256)
-    se.logits()
-    fill_s = time.perf_counter() - t
-    prefill = len(prompt) / fill_s
-    log(f"prefill: {prefill:.1f} tok/s ({len(prompt)} tokens, R={a.loops})")
-    warm_ids = se.decode_greedy(a.warmup).tolist() if a.warmup else []
-    se.logits()
-    pos0 = se.pos
-    t = time.perf_counter()
-    ids = se.decode_greedy(a.steps)
-    se.logits()  # waits for the last step
-    dec_s = time.perf_counter() - t
-    tok_s = a.steps / dec_s
-    log(f"decode: {tok_s:.1f} tok/s over {a.steps} steps at pos {pos0}..{se.pos - 1}")
+    per_r = {}
+    head = a.loops[0]
+    for r in a.loops:
+        prefill, tok_s, pos0, ids, se = run_loops(model, cfg, prompt, r, a.warmup, a.steps)
+        bpt = np.mean([decode_bytes(cfg, r, p) for p in range(pos0, pos0 + a.steps)])
+        fl = prefill_flops(cfg, r, 16, len(prompt))
+        per_r[r] = {"decode_tok_s": round(tok_s, 2), "ms_per_token": round(1e3 / tok_s, 4),
+                    "decode_from_pos": pos0, "decode_to_pos": pos0 + a.steps - 1,
+                    "decode_bytes_per_token": round(bpt),
+                    "decode_hbm_frac": round(bpt * tok_s / HBM_PEAK, 4),
+                    "prefill_tok_s": round(prefill, 1), "prefill_flops_per_token": round(fl / len(prompt)),
+                    "prefill_tflops": round(fl * prefill / len(prompt) / 1e12, 2),
+                    "prefill_mfma_frac": round(fl * prefill / len(prompt) / FP32_MFMA_PEAK, 4),
+                    "state_bytes": se.state_bytes()}
+        log(f"R={r}: prefill {prefill:.1f} tok/s, decode {tok_s:.1f} tok/s "
+            f"(pos {pos0}..{pos0 + a.steps - 1})")
+        if r == head:
+            head_ids, head_se = ids, se
+        else:
+            del se
+    se = head_se
+    tok_s = per_r[head]["decode_tok_s"]
     # the same greedy loop with the pick on the device (the logits stay on the GPU; each step's
     # embedding gather reads the previous step's pick there): the opt-in fast path
     t = time.perf_counter()
@@ -271,13 +344,9 @@ def main():
                         "logits read-back and host pick; the same ids (tests/test_gpu_model.py)"}
     log(f"decode, device pick: {dev_pick['value']} tok/s")
     stats = hip.graph_stats()
-
-    # whole-step roofline (decode) and MFMA utilisation (prefill)
-    bpt = np.mean([decode_bytes(cfg, a.loops, p) for p in range(pos0, pos0 + a.steps)])
-    fl = prefill_flops(cfg, a.loops, 16, len(prompt))
     # dominant kernel: the fused decode GEMV (slm_fg), every launch of `--timed-steps` more
-    # decode steps bracketed by HIP events on the backend's stream (eager launches: the
-    # same kernels the step graph holds)
+    # decode steps timed by the dispatch's own timestamps (eager launches: the same kernels
+    # the step graph holds)
     hip.set_graphs(False)
     hip.set_timing(True)
     se.decode_greedy(a.timed_steps)
@@ -297,58 +366,74 @@ def main():
     # fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)
     fp16 = None
     if not a.no_fp16:
-        fp16 = fp16_leg(hip, model, a, prompt, fl)
+        fp16 = fp16_leg(hip, model, argparse.Namespace(loops=head, warmup=a.warmup, steps=a.steps),
+                        prompt, prefill_flops(cfg, head, 16, len(prompt)))
+    del se, head_se
+    g86 = None
+    if not a.no_g86:
+        log("g86: 16384-token prompt at R=4, then 128 decode steps ...")
+        g86 = g86_leg(pkg, hip, synth)
+        log(f"g86: prefill {g86['prefill_tok_s']} tok/s, decode {g86['decode_tok_s']} tok/s")
 
     cpu = None
     if not a.no_cpu:
         n = min(a.cpu_steps, a.steps)
-        log(f"CPU baseline: oracle prefill {len(prompt)} + decode {n} ...")
-        cpu = cpu_baseline(folder, cfg, a.loops, prompt, n)
-        same = cpu.pop("ids") == (warm_ids + ids.tolist())[:n]
+        log(f"CPU baseline: oracle prefill {len(prompt)} + decode {n} at R={head} ...")
+        cpu = cpu_baseline(folder, cfg, head, prompt, n)
+        same = cpu.pop("ids") == head_ids[:n]
         cpu["same_greedy_ids_as_gpu"] = bool(same)
+        cpu["cpu_model"] = cpu_model()
         log(f"CPU: prefill {cpu['prefill_tok_s']} tok/s, decode {cpu['value']} tok/s, "
             f"same ids: {same}")
 
+    h = per_r[head]
     line = {
-        "metric": f"decode tok/s @R={a.loops}, full {cfg['window']} window (86M fp32)",
-        "value": round(tok_s, 2),
+        "metric": "decode tok/s @R=4/8/16 full 4096 window; prefill tok/s; % HBM/MFMA peak",
+        "value": h["decode_tok_s"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(1e3 * dec_s / a.steps, 4),
+        "ms_per_step": h["ms_per_token"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: seeded N(0,0.02) fp32 weights, uniform random token ids",
-        "config": {"workload": "a86 decode after a 4096-token prompt (window full), greedy, "
-                               "logits read back every token",
-                   "loops": a.loops, "d_model": 768, "heads": 12, "head_dim": 64,
+        "config": {"workload": f"a86 decode at R={head} after 16 + {len(prompt)} prompt tokens "
+                               f"(window full, rings wrapping past position 4352), greedy, "
+                               f"logits read back every token",
+                   "loops": head, "d_model": 768, "heads": 12, "head_dim": 64,
                    "ffn": 3072, "vocab": 32000, "window": 4096, "layers": "SS|LS|SS",
-                   "prompt_tokens": len(prompt), "decode_from_pos": pos0},
+                   "prompt_tokens": len(prompt), "decode_from_pos": h["decode_from_pos"]},
         "roofline": {"bound": "hbm", "achieved": round(gemv_bw / 1e9, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(gemv_bw / HBM_PEAK, 4), "traffic": traffic(),
                      "kernel": "slm_fg", "launches": fg["launches"],
                      "bytes_per_launch": round(bpl), "us_per_launch": round(per_launch * 1e6, 3),
+                     "timing": "kernel begin/end timestamps (hipExtModuleLaunchKernel events), eager launches",
                      "us_per_step_by_kernel": share},
-        "decode_roofline": {"bound": "hbm", "bytes_per_token": round(bpt),
-                            "achieved": round(bpt * tok_s / 1e9, 1), "peak": 8000.0,
-                            "unit": "GB/s", "frac": round(bpt * tok_s / HBM_PEAK, 4)},
-        "prefill": {"value": round(prefill, 1), "unit": "tok/s", "prompt_tokens": len(prompt),
-                    "flops_per_token": round(fl / len(prompt)),
-                    "achieved_tflops": round(fl / fill_s / 1e12, 2),
-                    "peak_tflops": FP32_MFMA_PEAK / 1e12,
-                    "frac": round(fl / fill_s / FP32_MFMA_PEAK, 4)},
+        "decode_roofline": {"bound": "hbm", "bytes_per_token": h["decode_bytes_per_token"],
+                            "achieved": round(h["decode_bytes_per_token"] * h["decode_tok_s"] / 1e9, 1),
+                            "peak": 8000.0, "unit": "GB/s", "frac": h["decode_hbm_frac"]},
+        "prefill": {"value": h["prefill_tok_s"], "unit": "tok/s", "prompt_tokens": len(prompt),
+                    "flops_per_token": h["prefill_flops_per_token"],
+                    "achieved_tflops": h["prefill_tflops"], "peak_tflops": FP32_MFMA_PEAK / 1e12,
+                    "frac": h["prefill_mfma_frac"]},
+    }
+    for r in a.loops:
+        line[f"r{r}"] = per_r[r]
+    line.update({
+        "g86": g86,
         "decode_device_pick": dev_pick,
         "graphs": stats,
         "fp16_mode": fp16,
         "cpu_baseline": cpu,
-        "reference_published": {"decode_tok_s_r4_rtx5080": 209, "prefill_tok_s_r4_rtx5080": 2819,
-                                "note": "README.md:143-147; different GPU and model dims"},
-    }
+        "reference_published": {"decode_tok_s_rtx5080": {"r4": 209, "r8": 123, "r16": 67},
+                                "prefill_tok_s_rtx5080": {"r4": 2819, "r8": 1630, "r16": 884},
+                                "note": "README.md:143-149; different GPU and model dims"},
+    })
     print(json.dumps(line), flush=True)
-    del se, model
+    del model
     hip.close()
 
 

@@ -83,7 +83,7 @@ int slm_hip_gather(slm_hip* ctx, float* y, const float* w, const uint32_t* ids, 
  * in that loop, main.rs:219-222). */
 int slm_hip_gather_dev(slm_hip* ctx, float* y, const float* w, const long long* id, size_t rows,
                        size_t d);
-/* Greedy pick on the device: the index of the first maximum of x[0..n) under sample.rs:46-50
+/* Greedy pick on the device: the index of the first maximum of x[0..n) under sample.rs:48-53
  * (b = 0, b = i whenever x[i] > x[b]: NaNs never win; a NaN at 0 keeps 0), written to tok[0]
  * and, when ids is not null, to ids[slot] (ids holds ids_cap uint32). Replaces the logits
  * read-back and host scan of main.rs:219 and sample.rs:33-50 in the greedy loop. */
@@ -178,6 +178,13 @@ int slm_hip_kernel_stat(slm_hip* ctx, const char* name, long long* launches, dou
  * each) and writes the four result elements it holds to out[4l .. 4l+3] (256 floats).
  * Tests use it to pin the lane layout the kernels assume. */
 int slm_hip_probe_mfma(slm_hip* ctx, float* out, const float* a, const float* b);
+/* Bounded waits (no trait counterpart; a safety net). Fused kernels synchronise some of their
+ * waves through polls of LDS that give up after `polls` tries instead of waiting forever; a
+ * wait that gives up sets a fault word, and the next slm_hip_read or slm_hip_flush returns
+ * SLM_E_HIP (the results of the work since the previous check are not valid). The default is
+ * 2^24 polls; 0 makes every such wait give up at once (tests use it to exercise the error
+ * path: every kernel still runs to its end). Applies to steps recorded from this call on. */
+int slm_hip_set_spin_limit(slm_hip* ctx, long long polls);
 /* The context's hipStream_t, so a caller can time its work with HIP events. */
 int slm_hip_stream(slm_hip* ctx, void** out);
 

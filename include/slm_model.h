@@ -56,13 +56,13 @@ size_t slm_session_kept_count(const slm_session* s);
 size_t slm_session_kept_len(const slm_session* s, size_t i);
 int slm_session_kept_read(slm_session* s, size_t i, float* out, size_t n);
 /* The decode loop of src/main.rs:207-223: n times, read the logits, pick greedily
- * (src/sample.rs:179-184, first maximum wins) and step; ids[i] receives each pick. */
+ * (src/sample.rs:48-53, the first maximum wins) and step; ids[i] receives each pick. */
 int slm_session_decode_greedy(slm_session* s, size_t n, uint32_t* ids);
 /* The same loop with the pick on the device (replaces the per-token logits read-back and host
- * scan of main.rs:219-222 and sample.rs:46-50 for greedy decoding): each step's logits GEMV is
+ * scan of main.rs:219-222 and sample.rs:48-53 for greedy decoding): each step's logits GEMV is
  * followed by slm_hip_argmax into a device slot that the next step's embedding gather reads,
  * so the steps run back to back with no host round trip; the n ids are read once at the end.
- * The same ids as slm_session_decode_greedy (sample.rs:46-50 semantics). */
+ * The same ids as slm_session_decode_greedy (sample.rs:48-53 semantics). */
 int slm_session_decode_greedy_device(slm_session* s, size_t n, uint32_t* ids);
 
 #ifdef __cplusplus

@@ -98,6 +98,7 @@ _SIGS = {
     "slm_hip_kernel_stat": (_i, [_p, C.c_char_p, C.POINTER(C.c_longlong), C.POINTER(C.c_double),
                                  C.POINTER(C.c_double)]),
     "slm_hip_probe_mfma": (_i, [_p, _p, _p, _p]),
+    "slm_hip_set_spin_limit": (_i, [_p, C.c_longlong]),
     "slm_hip_stream": (_i, [_p, C.POINTER(_p)]),
     "slm_model_load": (_i, [_p, C.c_char_p, C.POINTER(_p)]),
     "slm_model_free": (None, [_p]),
@@ -305,6 +306,10 @@ class Hip:
         s = _p()
         self.check(lib.slm_hip_stream(self.ctx, C.byref(s)))
         return s.value or 0
+
+    def set_spin_limit(self, polls: int):
+        """Polls a fused kernel's bounded wait makes before it gives up (0: at once)."""
+        self.check(lib.slm_hip_set_spin_limit(self.ctx, polls))
 
     def probe_mfma(self, out, a, b):
         self.check(lib.slm_hip_probe_mfma(self.ctx, out, a, b))

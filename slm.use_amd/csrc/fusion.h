@@ -102,9 +102,9 @@ typedef struct __attribute__((aligned(16))) {
     // cw ≥ 0: x is one-token attention's output, combined by the GEMV waves themselves:
     // wave w (one 64-column slice) combines head w (64 dims) from the superblock partials
     // in lds[cw] [cnsb][W][cdp + 2], and workgroup 0 writes the result to cgout
-    int32_t cw, cdp, cnsb, cpad;
+    int32_t cw, cdp, cnsb, spin;    // spin: polls a bounded wait makes before it gives up
     float* cgout;
-    long long cpad2;
+    int* fault;                     // a wait that gives up ORs 1 in here (host memory)
     PfOp pf[SLM_PF_MAX];
     VpOp vp[SLM_VP_MAX];
     FgSeg seg[SLM_SEG_MAX];

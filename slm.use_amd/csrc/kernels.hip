@@ -1956,24 +1956,34 @@ KERNEL void slm_probe_mfma(float* out, const float* a, const float* b) {
 // fused decode kernels (one token), driven by the descriptors of fusion.h
 // ---------------------------------------------------------------------------------------
 
+// A bounded wait of a fused kernel that gave up: lane 0 ORs 1 into the fault word (host
+// memory), which the runtime reports at the next read or flush. The kernel goes on, so a
+// mistake cannot hang the GPU; its results are then not valid.
+__device__ __forceinline__ void wait_gave_up(int* fault, int lane) {
+    if (fault && lane == 0) __hip_atomic_fetch_or(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // The prologue waves' own barrier: a counter in LDS that each of the `nw` waves bumps once
 // per barrier, then waits for (the GEMV waves meanwhile wait for their weights, not for
-// this). Only LDS is ordered by it. The wait gives up after about a second, so a mistake
-// cannot hang the GPU.
-__device__ __forceinline__ void esync(int* ctr, int& target, int nw) {
+// this). Only LDS is ordered by it. The wait gives up after `spin` polls (about a second at
+// the default), so a mistake cannot hang the GPU.
+__device__ __forceinline__ void esync(int* ctr, int& target, int nw, int spin, int* fault) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     target += nw;
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    for (int it = 0; it < (1 << 24); it++) {
+    int it = 0;
+    for (; it < spin; it++) {
         if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
     }
+    if (it >= spin) wait_gave_up(fault, threadIdx.x & 63);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 struct ESync {
     int* ctr;
-    int target, nw;
-    __device__ __forceinline__ void operator()() { esync(ctr, target, nw); }
+    int target, nw, spin;
+    int* fault;
+    __device__ __forceinline__ void operator()() { esync(ctr, target, nw, spin, fault); }
 };
 
 // Sum of squares of in[0..size) in the order of dot16_self, run by one wave: lane l and

@@ -1064,7 +1064,7 @@ int slm_session_decode_greedy(slm_session* s, size_t n, uint32_t* ids) {
         std::vector<float> l(V);
         for (size_t t = 0; t < n; t++) {
             M.ops.ok(slm_hip_read(M.ops.ctx(), l.data(), s->logits.p, V), "read");
-            size_t b = 0;  // sample.rs:179-184: the first maximum wins
+            size_t b = 0;  // sample.rs:48-53: b = i whenever l[i] > l[b] (the first maximum; NaNs never win)
             for (size_t i = 0; i < V; i++)
                 if (l[i] > l[b]) b = i;
             ids[t] = (uint32_t)b;

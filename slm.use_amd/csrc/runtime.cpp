@@ -13,6 +13,7 @@
 // ids and factors live in a per-step block of device memory that is refreshed before
 // each replay, so a step's ops compare equal from one token to the next.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -152,6 +153,9 @@ struct slm_hip {
     std::vector<hipEvent_t> ev_pool;
     std::map<hipFunction_t, std::string> fname;
     std::map<std::string, KStat> kstats;
+    int* fault_host = nullptr;           // bounded waits that gave up OR 1 in here (pinned, mapped)
+    int* fault_dev = nullptr;            // ... its device address
+    int spin = 1 << 24;                  // polls a bounded wait makes before it gives up
     bool recording = false, tainted = false;
     std::vector<Op> ops;                 // the step being recorded
     std::vector<unsigned char> dyn;
@@ -302,20 +306,26 @@ int launch_now(slm_hip* c, const Rec& r) {
         for (uint32_t i = 0; i < r.nargs; i++) ptrs[i] = (void*)(r.blob + 8 * i);
     }
     bool timed = c->timing && !c->capturing;
-    Timed t{nullptr, nullptr, r.f, r.abytes};
-    if (timed) {
-        t.a = pool_event(c);
-        t.b = pool_event(c);
-        if (!t.a || !t.b) return fail(c, SLM_E_HIP, "hipEventCreate failed");
-        HIPC(c, hipEventRecord(t.a, c->stream));
+    if (!timed) {
+        hipError_t e = hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream,
+                                             ptrs, nullptr);
+        if (e != hipSuccess) {
+            // the attention counters are reset by the last workgroup of each launch; after a
+            // launch that failed, start them from zero again
+            if (!c->capturing) hipMemsetAsync(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int), c->stream);
+            return fail(c, SLM_E_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
+        }
+        return SLM_OK;
     }
-    HIPC(c, hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream, ptrs,
-                                  nullptr));
-    if (timed) {
-        HIPC(c, hipEventRecord(t.b, c->stream));
-        c->timed.push_back(t);
-        if (c->timed.size() >= 4096) TRY(collect_timing(c));
-    }
+    // The start and stop events of hipExtModuleLaunchKernel take the dispatch's own begin and
+    // end timestamps, so the duration is the kernel's alone (what a kernel trace reports),
+    // without the launch gap an event recorded around the call would add.
+    Timed t{pool_event(c), pool_event(c), r.f, r.abytes};
+    if (!t.a || !t.b) return fail(c, SLM_E_HIP, "hipEventCreate failed");
+    HIPC(c, hipExtModuleLaunchKernel(r.f, r.gx * r.bx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream,
+                                     ptrs, nullptr, t.a, t.b, 0));
+    c->timed.push_back(t);
+    if (c->timed.size() >= 4096) TRY(collect_timing(c));
     return SLM_OK;
 }
 
@@ -1551,6 +1561,8 @@ struct Planner {
         d.units = units;
         d.pf4 = b.pf4;
         d.f16 = (int32_t)L.n[3];
+        d.spin = c->spin;
+        d.fault = c->fault_dev;
         d.lds_vp = (b.lds + 3) & ~3;
         d.fold_off = d.lds_vp + SLM_FG_MISC;
         int total = d.fold_off + 4 * W * 16;
@@ -1970,6 +1982,16 @@ int taint(slm_hip* c) {
 
 bool recording(const slm_hip* c) { return c->recording && !c->tainted; }
 
+// A fused kernel's bounded wait that gave up leaves a bit in the fault word: the step it
+// belonged to did not compute what it should have. Reported (once) as SLM_E_HIP.
+int check_fault(slm_hip* c) {
+    int v = __atomic_load_n(c->fault_host, __ATOMIC_ACQUIRE);
+    if (!v) return SLM_OK;
+    __atomic_store_n(c->fault_host, 0, __ATOMIC_RELEASE);
+    return fail(c, SLM_E_HIP, "a fused kernel's bounded wait gave up (fault word %#x): the results "
+                "of the work since the last check are not valid", v);
+}
+
 // Queues an op: recorded inside a step, lowered and launched otherwise.
 int submit(slm_hip* c, const Op& o) {
     if (recording(c)) {
@@ -2228,6 +2250,9 @@ int slm_hip_open(int device, slm_hip** out) {
     }
     OPEN_HIP(hipMalloc((void**)&c->dyn_dev, DYN_CAP));
     OPEN_HIP(hipHostMalloc((void**)&c->bounce, BOUNCE_CAP, hipHostMallocDefault));
+    OPEN_HIP(hipHostMalloc((void**)&c->fault_host, 64, hipHostMallocMapped));
+    *c->fault_host = 0;
+    OPEN_HIP(hipHostGetDevicePointer((void**)&c->fault_dev, c->fault_host, 0));
     c->ws_bytes = 1 << 20;
     OPEN_HIP(hipMalloc((void**)&c->ws, c->ws_bytes));
     OPEN_HIP(hipMalloc((void**)&c->attn_ctr, ATTN_CTR_MAX * sizeof(int)));
@@ -2264,6 +2289,7 @@ void slm_hip_close(slm_hip* c) {
     if (c->dyn_dev) hipFree(c->dyn_dev);
     if (c->stage_host) hipHostFree(c->stage_host);
     if (c->bounce) hipHostFree(c->bounce);
+    if (c->fault_host) hipHostFree(c->fault_host);
     for (int i = 0; i < 2; i++) {
         if (c->dyn_pin[i]) hipHostFree(c->dyn_pin[i]);
         if (c->dyn_ev[i]) hipEventDestroy(c->dyn_ev[i]);
@@ -2349,14 +2375,23 @@ int slm_hip_read(slm_hip* c, float* host, const float* dev, size_t n) {
         done += part;
     }
     if (n == 0) HIPC(c, hipStreamSynchronize(c->stream));
-    return SLM_OK;
+    return check_fault(c);
 }
 
 int slm_hip_flush(slm_hip* c, const float* const* keep, size_t nkeep) {
     (void)keep;
     (void)nkeep;
     if (!c) return SLM_E_INVALID;
+    TRY(check_fault(c));  // (work already finished; the rest is reported by a later check)
     if (c->recording) return finish_step(c);
+    return SLM_OK;
+}
+
+int slm_hip_set_spin_limit(slm_hip* c, long long polls) {
+    if (!c || polls < 0) return SLM_E_INVALID;
+    TRY(taint(c));
+    drop_graphs(c);  // the graphs hold the old limit in their descriptors
+    c->spin = (int)std::min<long long>(polls, INT_MAX);
     return SLM_OK;
 }
 

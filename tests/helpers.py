@@ -27,8 +27,14 @@ def rel(a, b) -> float:
 
 
 def greedy(logits) -> int:
-    """src/sample.rs:179-184: the first maximum wins."""
-    return int(np.argmax(logits))
+    """src/sample.rs:48-53: fold(0, |b, (i, v)| if v > logits[b] { i } else { b }) — the
+    first maximum wins, a NaN never wins, and a NaN at index 0 keeps index 0."""
+    x = np.asarray(logits, np.float32)
+    b = 0
+    for i in np.flatnonzero(x > x[0]) if not np.isnan(x[0]) else ():
+        if x[i] > x[b]:
+            b = int(i)
+    return b
 
 
 def attend64(q, k, v, pos, m, reach, gap, cap, heads, key_heads, dh, scale):

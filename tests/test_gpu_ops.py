@@ -392,12 +392,44 @@ def test_fusion_pattern(hip, case, fp16):
         assert np.array_equal(a[k], b[k]), (case, k, float(np.abs(a[k] - b[k]).max()))
 
 
+def test_bounded_wait_that_gives_up_is_reported(hip, pkg):
+    """A fused kernel's bounded LDS wait that gives up sets the fault word; the next read
+    returns SLM_E_HIP once. Forced from the host with a spin limit of 0 (every such wait
+    gives up at once, and every kernel still runs to its end); with the default limit the
+    same step runs clean and gives the per-op kernels' bits."""
+    d = 768
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(32), hip.alloc(32)
+    w = hip.upload(rnd(d, d, scale=0.02))
+    x, nw, res = hip.upload(rnd(d)), hip.upload(rnd(d)), hip.upload(rnd(d))
+    n, y, t = hip.alloc(d), hip.alloc(d), hip.alloc(d)
+
+    def body():  # the block input chain: residual add, rms, GEMV (rms syncs the prologue)
+        hip.add(t.ptr, res.ptr, x.ptr, d)
+        hip.rms(n.ptr, t.ptr, nw.ptr, 1, d, 1e-6)
+        hip.linear(y.ptr, w.ptr, d, d, n.ptr, 1)
+
+    _step(hip, body, inv, cs, sn, False)
+    want = y.read()
+    hip.set_spin_limit(0)
+    try:
+        _step(hip, body, inv, cs, sn, True)
+        with pytest.raises(pkg.SlmError) as e:
+            y.read()
+        assert e.value.code == -2 and "gave up" in str(e.value)
+        y.read()  # reported once
+    finally:
+        hip.set_spin_limit(1 << 24)
+    _step(hip, body, inv, cs, sn, True)
+    assert np.array_equal(y.read(), want)
+
+
 # ---------------------------------------------------------------------------------------
 # prompt row chains: the element-wise ops between two GEMMs as one launch per chain
 # ---------------------------------------------------------------------------------------
 
 def _pick(x):
-    """sample.rs:46-50: b = 0, then b = i whenever x[i] > x[b]."""
+    """sample.rs:48-53: b = 0, then b = i whenever x[i] > x[b]."""
     b = 0
     for i in range(1, len(x)):
         if x[i] > x[b]:
