@@ -137,6 +137,17 @@ int slm_hip_store(slm_hip* ctx, float* cache, const float* src, size_t pos, size
  * `v` are [key_heads][cap][dh]. */
 int slm_hip_attend(slm_hip* ctx, float* y, float* scores, const float* q, const float* k,
                    const float* v, const slm_attn* a);
+/* slm_hip_attend without allocation. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under their own HIP graph capture of the context's
+ * stream, serving loops, harnesses that forbid hipMalloc). The superblock partials go to a
+ * fixed array of 16 MiB per GPU (static device memory, held until the process ends) instead of
+ * the context's workspace, and the call issues kernel launches only — no hipMalloc, hipFree,
+ * copy, fill or event. Results are bitwise those of slm_hip_attend. SLM_E_UNSUPPORTED when the
+ * partials, nsb · m · heads · (dp + 2) · 4 bytes (nsb: the 256-key superblocks the queries
+ * span; dp: 16 · 2^⌈log2 ⌈dh / 16⌉⌉), exceed 16 MiB, or when called inside a recorded step. Every call on one GPU shares that GPU's array: calls that overlap on
+ * one GPU (two streams or contexts at once) race. */
+int slm_hip_attend_noalloc(slm_hip* ctx, float* y, float* scores, const float* q, const float* k,
+                           const float* v, const slm_attn* a);
 
 /* ---- steps (no trait counterpart; backend settings like cuda.rs's one stream) ----
  * With step graphs or fusion on (both are by default), the operations of one advance —

@@ -88,6 +88,7 @@ _SIGS = {
     "slm_hip_gla": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _sz, _sz, _sz]),
     "slm_hip_store": (_i, [_p, _p, _p, _sz, _sz, _sz, _sz, _sz]),
     "slm_hip_attend": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
+    "slm_hip_attend_noalloc": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_set_graphs": (_i, [_p, _i]),
     "slm_hip_set_fusion": (_i, [_p, _i]),
     "slm_hip_set_fp16": (_i, [_p, _i]),
@@ -301,6 +302,11 @@ class Hip:
     def attend(self, y, q, k, v, **a):
         args = Attn(**a)
         self.check(lib.slm_hip_attend(self.ctx, y, None, q, k, v, C.byref(args)))
+
+    def attend_noalloc(self, y, q, k, v, **a):
+        """attend with its partials in the device's fixed scratch (no allocation)."""
+        args = Attn(**a)
+        self.check(lib.slm_hip_attend_noalloc(self.ctx, y, None, q, k, v, C.byref(args)))
 
     def stream(self) -> int:
         s = _p()

@@ -27,6 +27,7 @@
 #include <vector>
 
 #include "fusion.h"
+#include "scratch.h"
 #include "slm_hip.h"
 
 extern "C" const unsigned char slm_code_object[];
@@ -133,6 +134,7 @@ struct slm_hip {
     float* ws = nullptr;                 // attention partials
     size_t ws_bytes = 0;
     int* attn_ctr = nullptr;             // [ATTN_CTR_MAX] finished superblocks per (query tile, key head)
+    float* scratch = nullptr;            // this device's fixed scratch (scratch.hip), SLM_NOALLOC_SCRATCH_BYTES
     float* part = nullptr;               // split partials of fused one-token linears (two halves)
     size_t part_bytes = 0;
     float* gpart = nullptr;              // split partials of prompt GEMMs
@@ -446,9 +448,14 @@ int64_t attn_dp(int64_t dh) { return (int64_t)16 << pow2_index((dh + 15) / 16, 4
 // The superblock partials of a one-token attention, [nsb][heads][dp + 2] floats at c->ws.
 int64_t attn_dec_part_floats(const Op& o) { return o.n[8] * o.n[5] * (attn_dp(o.n[7]) + 2); }
 
+// Where an attention op's superblock partials go: the workspace, or (p4 set: the
+// allocation-free entry point) the buffer it names, and then no launch uses the counters.
+float* attn_part(slm_hip* c, const Op& o) { return o.p[4] ? (float*)o.p[4] : c->ws; }
+
 // With `defer` the kernel only writes its superblock partials (a later fused prologue, or
 // slm_attn_combine, combines them); otherwise it combines them itself when every partial
-// of a key head fits in its LDS, else slm_attn_combine runs after it.
+// of a key head fits in its LDS (and the op may use the counters), else slm_attn_combine
+// runs after it.
 int lower_attn_dec(slm_hip* c, const Op& o, std::vector<Rec>& out, bool defer) {
     const Kernels& k = c->k;
     const float* const* p = o.p;
@@ -456,14 +463,16 @@ int lower_attn_dec(slm_hip* c, const Op& o, std::vector<Rec>& out, bool defer) {
     int64_t heads = n[5], kh = n[6], dh = n[7], nsb = n[8];
     int dti = pow2_index((dh + 15) / 16, 4);
     int64_t dp = attn_dp(dh);
-    bool self = !defer && kh <= ATTN_CTR_MAX && nsb * (heads / kh) * (dp + 2) <= ATTN_DEC_LDS / 4;
+    float* part = attn_part(c, o);
+    bool self = !defer && !o.p[4] && kh <= ATTN_CTR_MAX &&
+                nsb * (heads / kh) * (dp + 2) <= ATTN_DEC_LDS / 4;
     out.push_back(mk(k.attn_dec[dti], (uint32_t)kh, (uint32_t)nsb, 1, 64 * SLM_SB_SEGS,
-                     (uint32_t)ATTN_DEC_LDS, c->ws, p[1], p[2], p[3], (const long long*)o.dyn,
+                     (uint32_t)ATTN_DEC_LDS, part, p[1], p[2], p[3], (const long long*)o.dyn,
                      (long long)n[0], (long long)n[2], (long long)n[3], (long long)n[4], (int)heads,
                      (int)kh, (int)dh, o.f[0], self ? p[0] : (float*)nullptr,
                      self ? c->attn_ctr : (int*)nullptr));
     if (!self && !defer)
-        out.push_back(mk(k.combine, (uint32_t)((heads + 3) / 4), 1, 1, 256, 0, p[0], (const float*)c->ws,
+        out.push_back(mk(k.combine, (uint32_t)((heads + 3) / 4), 1, 1, 256, 0, p[0], (const float*)part,
                          1, (int)heads, (int)dh, (int)dp, (int)nsb));
     return SLM_OK;
 }
@@ -574,6 +583,7 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int dti = pow2_index((dh + 15) / 16, 4);
             int64_t dp = (int64_t)16 << dti;
             if (attn_dec_ok(o)) return lower_attn_dec(c, o, out, false);
+            float* part = attn_part(c, o);
             if (m > 1 && dh <= 64) {
                 // a superblock's keys and values shared in LDS by four query tiles
                 int64_t qpt = 16 / (heads / kh);
@@ -582,11 +592,11 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                 int64_t groups = ((m + qpt - 1) / qpt + ATTN_QG_HOST - 1) / ATTN_QG_HOST;
                 out.push_back(mk(k.attn_pq[dti], (uint32_t)groups, (uint32_t)kh, (uint32_t)nsb,
                                  64 * SLM_SB_SEGS * ATTN_QG_HOST, (uint32_t)(2 * SLM_SB_KEYS * 64 * 4),
-                                 c->ws, p[1], p[2], p[3], (const long long*)o.dyn, (long long)n[0],
+                                 part, p[1], p[2], p[3], (const long long*)o.dyn, (long long)n[0],
                                  (int)m, (long long)n[2], (long long)n[3], (long long)n[4],
                                  (int)heads, (int)kh, (int)dh, o.f[0]));
                 out.push_back(mk(k.combine, (uint32_t)((m * heads + 3) / 4), 1, 1, 256, 0, p[0],
-                                 (const float*)c->ws, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
+                                 (const float*)part, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
                 return SLM_OK;
             }
             // LDS: wpp segment partials being folded, then each wave's tile of values
@@ -597,15 +607,15 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int64_t qtiles = (m + qpt - 1) / qpt;
             // the last workgroup of each (query tile, key head) combines the superblocks itself
             // when its counter fits; otherwise slm_attn_combine runs after
-            bool self = m == 1 && qtiles * kh <= ATTN_CTR_MAX;
+            bool self = m == 1 && !o.p[4] && qtiles * kh <= ATTN_CTR_MAX;
             out.push_back(mk(k.attn[dti], (uint32_t)qtiles, (uint32_t)kh, (uint32_t)nsb,
-                             64 * SLM_SB_SEGS, (uint32_t)shm(wpp), c->ws, p[1], p[2], p[3],
+                             64 * SLM_SB_SEGS, (uint32_t)shm(wpp), part, p[1], p[2], p[3],
                              (const long long*)o.dyn, (long long)n[0], (int)m, (long long)n[2],
                              (long long)n[3], (long long)n[4], (int)heads, (int)kh, (int)dh, o.f[0],
                              (int)wpp, self ? p[0] : (float*)nullptr, self ? c->attn_ctr : (int*)nullptr));
             if (!self)
                 out.push_back(mk(k.combine, (uint32_t)((m * heads + 3) / 4), 1, 1, 256, 0, p[0],
-                                 (const float*)c->ws, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
+                                 (const float*)part, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
             return SLM_OK;
         }
     }
@@ -2239,6 +2249,7 @@ int slm_hip_open(int device, slm_hip** out) {
         return bail(fail(c, SLM_E_UNSUPPORTED, "device %d is %s; this build is for gfx950",
                          device, prop.gcnArchName));
     OPEN_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    OPEN_HIP(slm_scratch_address((void**)&c->scratch));  // this device current (hipSetDevice above)
     OPEN_HIP(hipModuleLoadData(&c->mod, slm_code_object));
     int rc = load_kernels(c);
     if (rc) return bail(rc);
@@ -2818,9 +2829,14 @@ int slm_hip_gla(slm_hip* c, float* y, float* s, const float* q, const float* k, 
 
 // ---- attention ----
 
-int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const float* k,
-                   const float* v, const slm_attn* a) {
-    (void)scores;  // the trait's scratch: this backend keeps its own workspace
+}  // extern "C"
+
+namespace {
+
+// The checks and the op of an attention call; *part_bytes: the superblock partials it needs.
+int attend_op(slm_hip* c, float* y, const float* q, const float* k, const float* v,
+              const slm_attn* a, Op& o, size_t* part_bytes) {
+    *part_bytes = 0;
     if (!c || !a) return SLM_E_INVALID;
     size_t m = a->m, heads = a->heads, kh = a->key_heads, dh = a->dh, cap = a->cap;
     NEED(c, "attend", y, m * heads * dh);
@@ -2858,8 +2874,8 @@ int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const fl
     if (qtiles > UINT32_MAX || nsb > 65535)
         return fail(c, SLM_E_UNSUPPORTED, "attend: %zu query tiles x %zu superblocks", qtiles, nsb);
     size_t dp = (size_t)16 << pow2_index((dh + 15) / 16, 4);
-    TRY(need_ws(c, nsb * m * heads * (dp + 2) * 4));
-    Op o = op(OP_ATTEND);
+    *part_bytes = nsb * m * heads * (dp + 2) * 4;
+    o = op(OP_ATTEND);
     o.p[0] = y;
     o.p[1] = q;
     o.p[2] = k;
@@ -2873,8 +2889,58 @@ int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const fl
     o.n[7] = (int64_t)dh;
     o.n[8] = (int64_t)nsb;
     o.f[0] = a->scale;
+    return SLM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int slm_hip_attend(slm_hip* c, float* y, float* scores, const float* q, const float* k,
+                   const float* v, const slm_attn* a) {
+    (void)scores;  // the trait's scratch: this backend keeps its own workspace
+    Op o;
+    size_t part_bytes = 0;
+    int rc = attend_op(c, y, q, k, v, a, o, &part_bytes);
+    if (rc || !part_bytes) return rc;
+    TRY(need_ws(c, part_bytes));
     TRY(stage_pos(c, a->pos, o, 0));
     return submit(c, o);
+}
+
+// slm_hip_attend with the superblock partials in this device's fixed scratch: kernel launches
+// only, on the context's stream (no allocation, copy, fill or event), so that a caller may run
+// it under its own stream capture. Not inside a recorded step (the step's plan may allocate).
+int slm_hip_attend_noalloc(slm_hip* c, float* y, float* scores, const float* q, const float* k,
+                           const float* v, const slm_attn* a) {
+    (void)scores;
+    Op o;
+    size_t part_bytes = 0;
+    int rc = attend_op(c, y, q, k, v, a, o, &part_bytes);
+    if (rc || !part_bytes) return rc;
+    if (c->recording)
+        return fail(c, SLM_E_UNSUPPORTED, "attend_noalloc: called inside a recorded step (between "
+                    "rope_table and flush); call it outside a step");
+    if (part_bytes > SLM_NOALLOC_SCRATCH_BYTES)
+        return fail(c, SLM_E_UNSUPPORTED, "attend_noalloc: %zu bytes of superblock partials exceed the "
+                    "fixed scratch of %zu bytes (fewer queries per call, or slm_hip_attend)",
+                    part_bytes, (size_t)SLM_NOALLOC_SCRATCH_BYTES);
+    if (!c->scratch) return fail(c, SLM_E_HIP, "attend_noalloc: no device scratch");
+    o.p[4] = c->scratch;
+    o.n[0] = (int64_t)a->pos;  // an immediate position (outside a step: nothing is staged)
+    o.dyn = nullptr;
+    std::vector<Rec> recs;
+    TRY(lower_one(c, o, recs));
+    for (auto& r : recs) {
+        void* ptrs[MAX_ARGS];
+        for (uint32_t i = 0; i < r.nargs; i++) ptrs[i] = (void*)(r.blob + 8 * i);
+        if (r.bytes) return fail(c, SLM_E_HIP, "attend_noalloc: unexpected descriptor launch");
+        hipError_t e = hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream,
+                                             ptrs, nullptr);
+        if (e != hipSuccess)
+            return fail(c, SLM_E_HIP, "attend_noalloc: hipModuleLaunchKernel: %s", hipGetErrorString(e));
+    }
+    return SLM_OK;
 }
 
 // ---- diagnostics ----
