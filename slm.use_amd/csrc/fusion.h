@@ -47,6 +47,10 @@ enum {
     EPI_RESID = 1,  // y; o1 = res + y                       (add after the linear)
     EPI_ROPE = 2,   // y = [q|k|v]; o1 = rope(q), o2 = rope(k), o3[ring] = o2, o4[ring] = v
     EPI_SILU = 3,   // y = [gate|amp]; o1 = amp · gate / (1 + e^−gate)
+    EPI_PICK = 4,   // y; the greedy pick of y (the first maximum, sample.rs:48-53) to
+                    // ((long long*)o1)[0] and ((unsigned*)o2)[slot] (o2 may be null; slot:
+                    // dyn[0], else imm); o3: [0] the 64-bit key of the running maximum,
+                    // [2] the count of finished workgroups (both zero between launches)
 };
 
 // A global vector copied into LDS by the prologue waves: src + dyn[0]·stride (when dyn).

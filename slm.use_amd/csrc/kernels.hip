@@ -123,7 +123,7 @@ KERNEL void slm_gather(float* __restrict__ y, const float* __restrict__ w,
     GRID_LOOP(i, n) y[i] = w[ids[i / d] * d + i % d];
 }
 
-// Greedy pick on the device (sample.rs:46-50: b = 0, then b = i whenever x[i] > x[b]): the
+// Greedy pick on the device (sample.rs:48-53: b = 0, then b = i whenever x[i] > x[b]): the
 // first index holding the largest value that is not a NaN, 0 when x[0] is a NaN or no value
 // compares. One workgroup: M = the maximum (fmaxf skips NaNs; the order of a maximum does not
 // matter), then the smallest index with x[i] == M. Writes the index to tok[0] (the next
@@ -2376,6 +2376,43 @@ __device__ __forceinline__ void fg_chain(const FgLane& p, int i, int g, const f4
 #pragma unroll
         for (int r = 0; r < 4; r++) out[4 * g + r] = acc[r];
     }
+}
+
+// The greedy pick's order on (value, row): a larger value first, then a smaller row — the
+// first maximum of sample.rs:48-53 (b = 0, then b = i whenever x[i] > x[b]). −0 and +0 are
+// equal; a NaN never wins, except at row 0, where it wins outright (nothing compares greater
+// than the NaN that b starts on). Key 0: no row.
+__device__ __forceinline__ unsigned long long pick_key(float v, int row) {
+    if (v != v) return row == 0 ? ~0ull : 0ull;
+    unsigned u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    unsigned k = (u >> 31) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)k << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)row);
+}
+
+// The end of a fused GEMV with the greedy pick (EPI_PICK), run by the epilogue wave of every
+// workgroup: its rows' largest key goes into the launch's 64-bit atomic maximum, and the last
+// workgroup to count itself in writes the pick out and clears the key and the counter for
+// the next launch. (The release of the count orders the maximum before it; the acquire of
+// the last count sees every workgroup's.)
+__device__ void fg_pick_finish(const FgSeg& g, unsigned long long best, int lane) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        unsigned lo = __shfl_xor((unsigned)best, off), hi = __shfl_xor((unsigned)(best >> 32), off);
+        unsigned long long o = ((unsigned long long)hi << 32) | lo;
+        best = o > best ? o : best;
+    }
+    if (lane != 0) return;
+    unsigned long long* key = (unsigned long long*)g.o3;
+    int* ctr = (int*)g.o3 + 2;
+    if (best) __hip_atomic_fetch_max(key, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (before != (int)gridDim.x - 1) return;
+    unsigned long long k = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    long long r = k ? (long long)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)) : 0;
+    gst((long long*)g.o1, r);
+    if (g.o2) gst((unsigned*)g.o2 + (g.dyn ? gld(g.dyn) : g.imm), (unsigned)r);
+    __hip_atomic_store(key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The fused GEMV, fp32 (slm_fg) and fp16 mode (slm_fgh): one kernel text, expanded twice.

@@ -7,6 +7,10 @@
 
 #include <algorithm>
 #include <cmath>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -450,7 +454,7 @@ struct Scratch {
 
 struct Tensor {
     std::vector<size_t> shape;
-    const float* data;
+    const char* data;  // little-endian f32, possibly unaligned
     size_t count;
 };
 
@@ -489,19 +493,47 @@ using Session = slm_session;
 
 void free_buf(const Ops& ops, Buf& b) { ops.release(b); }
 
-// model.rs:36-54: f32-only safetensors.
+// model.rs:36-54: f32-only safetensors, read through a read-only memory map of the file: the
+// header is parsed from the mapping and each tensor is uploaded straight from it (through an
+// aligned copy only when its offset is not a multiple of 4 bytes), so loading neither reads
+// the file into a buffer first nor keeps more than the mapping.
 struct Weights {
-    std::string bytes;
+    const char* bytes = nullptr;
+    size_t size = 0;
     std::map<std::string, Tensor> tensors;
 
     explicit Weights(const std::string& dir) {
         std::string path = dir + "/model.safetensors";
-        bytes = read_file(path);
-        if (bytes.size() < 8) throw std::runtime_error(path + ": too short");
+        int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+        if (fd < 0) throw std::runtime_error("reading " + path + ": cannot open");
+        struct stat st;
+        if (::fstat(fd, &st) != 0 || st.st_size < 8) {
+            ::close(fd);
+            throw std::runtime_error(path + ": too short");
+        }
+        size = (size_t)st.st_size;
+        void* m = ::mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+        ::close(fd);
+        if (m == MAP_FAILED) throw std::runtime_error(path + ": cannot map");
+        bytes = (const char*)m;
+        try {
+            parse(path);
+        } catch (...) {
+            ::munmap(m, size);
+            throw;
+        }
+    }
+    ~Weights() {
+        if (bytes) ::munmap((void*)bytes, size);
+    }
+    Weights(const Weights&) = delete;
+    Weights& operator=(const Weights&) = delete;
+
+    void parse(const std::string& path) {
         uint64_t hl = 0;
-        std::memcpy(&hl, bytes.data(), 8);
-        if (8 + hl > bytes.size()) throw std::runtime_error(path + ": bad header length");
-        Json h = parse_json(bytes.substr(8, hl));
+        std::memcpy(&hl, bytes, 8);
+        if (hl > size - 8) throw std::runtime_error(path + ": bad header length");
+        Json h = parse_json(std::string(bytes + 8, hl));
         size_t base = 8 + hl;
         for (auto& kv : h.obj) {
             if (kv.first == "__metadata__") continue;
@@ -517,9 +549,9 @@ struct Weights {
                 count *= (size_t)d.num;
             }
             size_t a = (size_t)off->arr[0].num, b = (size_t)off->arr[1].num;
-            if (b < a || base + b > bytes.size() || b - a != count * 4)
+            if (b < a || b > size - base || b - a != count * 4)
                 throw std::runtime_error(kv.first + ": bad data offsets");
-            t.data = (const float*)(bytes.data() + base + a);
+            t.data = bytes + base + a;
             t.count = count;
             tensors[kv.first] = t;
         }
@@ -533,25 +565,26 @@ struct Weights {
     }
 };
 
-// model.rs:69-83. The f32 data is copied into aligned host memory first (safetensors
-// offsets need not be 4-byte aligned).
+// model.rs:69-83: one tensor to the device, from the mapping.
+Buf upload_tensor(const Ops& ops, const Tensor& t) {
+    if (((uintptr_t)t.data & 3) == 0) return ops.upload((const float*)t.data, t.count);
+    std::vector<float> host(t.count);
+    std::memcpy(host.data(), t.data, t.count * 4);
+    return ops.upload(host.data(), t.count);
+}
+
 Mat mat(const Ops& ops, Weights& w, const std::string& name) {
     Tensor t = w.take(name);
     if (t.shape.size() != 2) throw std::runtime_error(name + ": expected a matrix");
-    std::vector<float> host(t.count);
-    std::memcpy(host.data(), t.data, t.count * 4);
     Mat m;
-    m.w = ops.upload(host.data(), t.count);
+    m.w = upload_tensor(ops, t);
     m.rows = t.shape[0];
     m.cols = t.shape[1];
     return m;
 }
 
 Buf vec(const Ops& ops, Weights& w, const std::string& name) {
-    Tensor t = w.take(name);
-    std::vector<float> host(t.count);
-    std::memcpy(host.data(), t.data, t.count * 4);
-    return ops.upload(host.data(), t.count);
+    return upload_tensor(ops, w.take(name));
 }
 
 // model.rs:114-153
@@ -700,16 +733,17 @@ Session* new_session(Model& M, size_t loops_in) {
     return se;
 }
 
-// model.rs:383-398: doubles a global cache, moving every head's data through the host.
+// model.rs:383-398: doubles a global cache. The reference moves every head's data through
+// the host; here each head's `cap` rows go from the old buffer to the start of that head's
+// `2·cap` rows in a new zeroed one by a device copy on the stream (the same contents).
 void grow(const Model& M, Buf& k, Buf& v, size_t& cap) {
     size_t kh = M.cfg.global_kv_heads, dh = M.cfg.head_dim();
     size_t old = cap, nw = cap * 2;
     for (Buf* buf : {&k, &v}) {
-        std::vector<float> data = M.ops.read(*buf, kh * old * dh);
-        std::vector<float> out(kh * nw * dh, 0.0f);
+        Buf nb = M.ops.zeros(kh * nw * dh);
         for (size_t h = 0; h < kh; h++)
-            std::memcpy(&out[h * nw * dh], &data[h * old * dh], old * dh * 4);
-        Buf nb = M.ops.upload(out.data(), out.size());
+            M.ops.ok(slm_hip_copy(M.ops.ctx(), nb.p + h * nw * dh, buf->p + h * old * dh, old * dh),
+                     "grow");
         M.ops.release(*buf);
         *buf = nb;
     }

@@ -135,6 +135,7 @@ struct slm_hip {
     size_t ws_bytes = 0;
     int* attn_ctr = nullptr;             // [ATTN_CTR_MAX] finished superblocks per (query tile, key head)
     float* scratch = nullptr;            // this device's fixed scratch (scratch.hip), SLM_NOALLOC_SCRATCH_BYTES
+    float* pick = nullptr;               // [16] the fused greedy pick's key and counter (zero between launches)
     float* part = nullptr;               // split partials of fused one-token linears (two halves)
     size_t part_bytes = 0;
     float* gpart = nullptr;              // split partials of prompt GEMMs
@@ -314,7 +315,10 @@ int launch_now(slm_hip* c, const Rec& r) {
         if (e != hipSuccess) {
             // the attention counters are reset by the last workgroup of each launch; after a
             // launch that failed, start them from zero again
-            if (!c->capturing) hipMemsetAsync(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int), c->stream);
+            if (!c->capturing) {
+                hipMemsetAsync(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int), c->stream);
+                hipMemsetAsync(c->pick, 0, 16 * sizeof(float), c->stream);
+            }
             return fail(c, SLM_E_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
         }
         return SLM_OK;
@@ -1412,6 +1416,20 @@ struct Planner {
                 b.reads.push_back(rng(r, rows));
             }
         }
+        // the greedy pick of the logits (model twin's device-pick decode): each workgroup's
+        // first maximum goes into a 64-bit atomic maximum, and the last workgroup to finish
+        // writes the pick (sample.rs:48-53, the rule of slm_argmax)
+        if (s0.epi == EPI_PLAIN && nseg == 1 && nsplit == 1 && is(i + 1, OP_ARGMAX) &&
+            ops[i + 1].p[1] == y && ops[i + 1].n[0] == rows && rows <= INT32_MAX) {
+            const Op& a = ops[i + 1];
+            used = 2;
+            s0.epi = EPI_PICK;
+            s0.o1 = (float*)a.p[0];
+            s0.o2 = (float*)a.p[2];
+            s0.o3 = c->pick;
+            s0.dyn = (const long long*)a.dyn;
+            s0.imm = a.n[1];
+        }
         int64_t nsl = (cols / 16 + SLM_KS - 1) / SLM_KS;
         int W = (int)std::min<int64_t>(nsl, SLM_SPLIT);
         // what the segments read and write
@@ -1430,6 +1448,12 @@ struct Planner {
             switch (s.epi) {
                 case EPI_RESID: b.writes.push_back(rng(s.o1, s.rows)); break;
                 case EPI_SILU: b.writes.push_back(rng(s.o1, s.half)); break;
+                case EPI_PICK: {
+                    const Op& a = ops[i + 1];
+                    b.writes.push_back(rng(a.p[0], 2));
+                    if (a.p[2]) b.writes.push_back(rng(a.p[2], a.n[2]));
+                    break;
+                }
                 case EPI_ROPE: {
                     int64_t heads = s.d / s.dh;
                     b.writes.push_back(rng(s.o1, s.d));
@@ -2268,6 +2292,8 @@ int slm_hip_open(int device, slm_hip** out) {
     OPEN_HIP(hipMalloc((void**)&c->ws, c->ws_bytes));
     OPEN_HIP(hipMalloc((void**)&c->attn_ctr, ATTN_CTR_MAX * sizeof(int)));
     OPEN_HIP(hipMemset(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int)));
+    OPEN_HIP(hipMalloc((void**)&c->pick, 16 * sizeof(float)));
+    OPEN_HIP(hipMemset(c->pick, 0, 16 * sizeof(float)));
     c->dyn.reserve(DYN_CAP);
     c->ops.reserve(4096);
     c->plan_trace = getenv("SLM_HIP_PLAN_TRACE") != nullptr;
@@ -2292,6 +2318,7 @@ void slm_hip_close(slm_hip* c) {
     for (auto& a : c->allocs) hipFree((void*)a.first);
     if (c->ws) hipFree(c->ws);
     if (c->attn_ctr) hipFree(c->attn_ctr);
+    if (c->pick) hipFree(c->pick);
     if (c->part) hipFree(c->part);
     if (c->gpart) hipFree(c->gpart);
     collect_timing(c);

@@ -469,6 +469,83 @@ def test_argmax_picks_like_the_reference(hip, case):
     assert got_tok == want and got_id == want, (case, got_tok, got_id, want)
 
 
+def _pick_rows(case, rows, cols=64):
+    """Weights whose GEMV with x = e0 gives y = w[:, 0] exactly (the other columns meet zeros):
+    the pick cases of test_argmax_picks_like_the_reference, as logits of a linear."""
+    w = rnd(rows, cols)
+    c = w[:, 0]
+    if case == "ties":
+        c[[7, rows // 2, rows - 3]] = 9.0
+    if case == "nan_first":
+        c[0] = np.nan
+        c[5] = 50.0
+    if case == "nan_inside":
+        c[[3, rows // 3, rows - 1]] = np.nan
+        c[rows // 2] = 7.0
+    if case == "all_neg_inf":
+        c[:] = -np.inf
+    if case == "signed_zero":
+        c[:] = -1.0
+        c[10] = -0.0
+        c[20] = 0.0
+    return w
+
+
+@pytest.mark.parametrize("rows", [32000, 40])
+@pytest.mark.parametrize("case", ["random", "ties", "nan_first", "nan_inside", "all_neg_inf",
+                                  "signed_zero"])
+def test_pick_fused_into_the_logits_gemv(hip, case, rows):
+    """The greedy pick after a one-token linear, inside a step: fused into the GEMV's epilogue
+    (each workgroup's first maximum into a 64-bit atomic maximum, the last workgroup writes the
+    pick) it gives the standalone kernel's index, the reference's first maximum, with no
+    slm_argmax launch; and every replay of the step's graph picks afresh (the key and the
+    counter are cleared by the launch that used them)."""
+    cols = 64
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(32), hip.alloc(32)
+    x = np.zeros(cols, np.float32)
+    x[0] = 1.0
+    dx, dw = hip.upload(x), hip.upload(_pick_rows(case, rows))
+    y, tok, ids = hip.alloc(rows), hip.alloc(2), hip.alloc(4)
+
+    def body():
+        hip.linear(y.ptr, dw.ptr, rows, cols, dx.ptr, 1)
+        hip.argmax(tok.ptr, ids.ptr, 4, 2, y.ptr, rows)
+
+    def picked():
+        return int(tok.read(2).view(np.int64)[0]), int(ids.read(4).view(np.uint32)[2])
+
+    plans = {}
+    got = {}
+    for fuse in (False, True):
+        hip.write(tok, np.zeros(2, np.float32))
+        hip.write(ids, np.zeros(4, np.float32))
+        plans[fuse] = _step(hip, body, inv, cs, sn, fuse)
+        got[fuse] = picked()
+    yv = y.read()
+    want = _pick(yv)
+    assert got[True] == (want, want) and got[False] == (want, want), (case, got, want)
+    assert plans[True]["kernels"] < plans[False]["kernels"]
+    # eagerly, with the launches counted: no slm_argmax
+    hip.set_graphs(False)
+    hip.set_timing(True)
+    try:
+        _step(hip, body, inv, cs, sn, True)
+        assert hip.kernel_stat("slm_argmax")["launches"] == 0
+        assert hip.kernel_stat("slm_fg")["launches"] == 1
+    finally:
+        hip.set_timing(False)
+        hip.set_graphs(True)
+    assert picked() == (want, want)
+    # graph replays with new weights each time: each pick is fresh
+    for seed in range(4):
+        w = _pick_rows("random", rows)
+        w[(seed * 997) % rows, 0] = 20.0 + seed
+        hip.write(dw, w)
+        _step(hip, body, inv, cs, sn, True)
+        assert picked() == ((seed * 997) % rows,) * 2, seed
+
+
 ROW_CASES = ["attn_in", "attn_in_dead", "gla_in_dead", "mlp", "mlp_dead", "inplace", "overlap"]
 
 
