@@ -233,10 +233,12 @@ def g86_leg(pkg, hip, synth):
     return out
 
 
-def fp16_leg(hip, model, a, prompt, fl):
-    """The same workload in fp16 mode (the --fp16 analogue: linears with fp16 operands at
-    fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)."""
+def fp16_leg(pkg, hip, folder, a, prompt, fl):
+    """The same workload in fp16 mode (the --fp16 analogue): the model loaded with fp16 mode on
+    stores its linear weights as fp16 (half the bytes); linears run fp16 operands at fp16
+    MFMAs with fp32 sums; attention, GLA, norms and states fp32."""
     hip.set_fp16(True)
+    model = pkg.Model(hip, folder)
     s16 = model.session(a.loops)
     s16.feed(prompt[:16], 256)
     s16.logits()
@@ -251,11 +253,13 @@ def fp16_leg(hip, model, a, prompt, fl):
     s16.decode_greedy(a.steps)
     s16.logits()
     dec16_s = time.perf_counter() - t
+    del s16, model
     hip.set_fp16(False)
     fp16 = {"decode_tok_s": round(a.steps / dec16_s, 2), "prefill_tok_s": round(len(prompt) / fill16_s, 1),
             "prefill_tflops": round(fl / fill16_s / 1e12, 2),
-            "note": "linears round operands to fp16 at v_mfma_f32_16x16x16f16 (fp32 sums); attention, "
-                    "GLA, norms and states fp32; checked at 2e-2 vs the fp32 oracle (config C5)"}
+            "note": "linear weights stored as fp16 (slm_hip_alloc_half), operands at "
+                    "v_mfma_f32_16x16x16f16 (fp32 sums); attention, GLA, norms and states fp32; "
+                    "the bits of fp16 mode over fp32 weights; checked at 2e-2 vs the fp32 oracle (config C5)"}
     log(f"fp16 mode: prefill {fp16['prefill_tok_s']} tok/s, decode {fp16['decode_tok_s']} tok/s")
     return fp16
 
@@ -366,7 +370,7 @@ def main():
     # fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)
     fp16 = None
     if not a.no_fp16:
-        fp16 = fp16_leg(hip, model, argparse.Namespace(loops=head, warmup=a.warmup, steps=a.steps),
+        fp16 = fp16_leg(pkg, hip, folder, argparse.Namespace(loops=head, warmup=a.warmup, steps=a.steps),
                         prompt, prefill_flops(cfg, head, 16, len(prompt)))
     del se, head_se
     g86 = None

@@ -63,6 +63,14 @@ int slm_hip_name(slm_hip* ctx, char* out, size_t n);
 
 /* A zeroed buffer of max(n, 1) floats (ops.rs:72, cuda.rs:152-154). */
 int slm_hip_alloc(slm_hip* ctx, size_t n, float** out);
+/* A zeroed buffer of max(n, 1) fp16 values, for the weights of fp16 mode (mlx.rs:62 uploads
+ * in the backend's dtype; no counterpart in the f32 trait). The pointer is typed float* like
+ * every buffer but addresses halves: slm_hip_upload into it (at its start) rounds n floats to
+ * fp16, to nearest even; slm_hip_read from it widens them back; slm_hip_linear takes it as
+ * weights in fp16 mode only (SLM_E_UNSUPPORTED otherwise), with the bits of fp16 mode on the
+ * same weights in fp32 (the fp16 chain rounds them to the same halves) and half the bytes.
+ * No other operation takes it. Freed with slm_hip_free. */
+int slm_hip_alloc_half(slm_hip* ctx, size_t n, float** out);
 int slm_hip_free(slm_hip* ctx, float* buf);
 /* Copies n host floats into dst (Ops::upload, ops.rs:77). */
 int slm_hip_upload(slm_hip* ctx, float* dst, const float* src, size_t n);
@@ -165,6 +173,9 @@ int slm_hip_set_graphs(slm_hip* ctx, int on);
  * attention, GLA, norms and states stay fp32. A linear then needs a multiple of 64 columns
  * and 16-byte aligned weights and input (else SLM_E_UNSUPPORTED). */
 int slm_hip_set_fp16(slm_hip* ctx, int on);
+/* Whether fp16 mode is on (the model twin stores its linear weights as fp16 when it is on at
+ * load, as the reference's MLX backend stores every buffer in its dtype, mlx.rs:19-26). */
+int slm_hip_get_fp16(slm_hip* ctx, int* on);
 /* Fusion (on by default): the planner lowers a recorded one-token step into fused
  * kernels (prologue vector ops + GEMV + epilogue) that compute the same values with the
  * same arithmetic as the per-op kernels. Off: one launch per operation. */

@@ -65,6 +65,8 @@ _SIGS = {
     "slm_hip_last_error": (C.c_char_p, [_p]),
     "slm_hip_name": (_i, [_p, C.c_char_p, _sz]),
     "slm_hip_alloc": (_i, [_p, _sz, C.POINTER(_p)]),
+    "slm_hip_alloc_half": (_i, [_p, _sz, C.POINTER(_p)]),
+    "slm_hip_get_fp16": (_i, [_p, C.POINTER(_i)]),
     "slm_hip_free": (_i, [_p, _p]),
     "slm_hip_upload": (_i, [_p, _p, _f32p, _sz]),
     "slm_hip_read": (_i, [_p, _f32p, _p, _sz]),
@@ -197,6 +199,20 @@ class Hip:
         b = self.alloc(a.size)
         self.check(lib.slm_hip_upload(self.ctx, b.ptr, _fp(a), a.size))
         return b
+
+    def upload_half(self, data) -> Buffer:
+        """fp16 weights (slm_hip_alloc_half): `data` rounded to fp16; read() widens them back."""
+        a = _f32(data).reshape(-1)
+        p = _p()
+        self.check(lib.slm_hip_alloc_half(self.ctx, a.size, C.byref(p)))
+        b = Buffer(self, p.value, max(a.size, 1))
+        self.check(lib.slm_hip_upload(self.ctx, b.ptr, _fp(a), a.size))
+        return b
+
+    def get_fp16(self) -> bool:
+        on = C.c_int()
+        self.check(lib.slm_hip_get_fp16(self.ctx, C.byref(on)))
+        return bool(on.value)
 
     def write(self, buf: Buffer, data, offset: int = 0):
         a = _f32(data).reshape(-1)

@@ -63,6 +63,13 @@ __device__ __forceinline__ h4 to_h4(f4 v) {
 __device__ __forceinline__ f4 block16h(f4 a, f4 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(to_h4(a), to_h4(b), c, 0, 0, 0);
 }
+// The same block with the first operand already in fp16 (weights stored as halves): the
+// halves a rounding to nearest even of the fp32 weights gives, so the same MFMA inputs.
+__device__ __forceinline__ f4 block16hw(h4 a, f4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, to_h4(b), c, 0, 0, 0);
+}
+// Four fp16 weights widened to fp32 (exactly): what block16h rounds back to the same halves.
+__device__ __forceinline__ f4 wide4(h4 v) { return f4{(float)v.x, (float)v.y, (float)v.z, (float)v.w}; }
 
 // ---------------------------------------------------------------------------------------
 // element-wise operations (src/cpu.rs:66-185, 209-268, 331-350)
@@ -552,7 +559,16 @@ __device__ __forceinline__ f4 ld4(const float* __restrict__ p, long long row, lo
 // m <= 16: one workgroup per 16 rows; wave w takes slices w, w+W, w+2W, ... four at a
 // time, loading them before their chains start (four independent chains interleave);
 // slice partials meet in LDS and one pass adds them in order.
-template <bool VEC, bool H>
+// Row `row`, columns c .. c + 3 of fp16 weights (cols a multiple of 64), widened; zeros past
+// the last row.
+__device__ __forceinline__ f4 ld4w16(const float* __restrict__ p, long long row, long long nrows,
+                                     long long cols, long long c) {
+    f4 r = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (row < nrows && c < cols) r = wide4(*(const h4*)((const _Float16*)p + row * cols + c));
+    return r;
+}
+
+template <bool VEC, bool H, bool W16 = false>
 __device__ void linear_small_body(float* __restrict__ y, const float* __restrict__ w,
                                   const float* __restrict__ x, int rows, int cols, int m) {
     extern __shared__ float part[];  // [slices][16 rows][16 tokens]
@@ -572,7 +588,8 @@ __device__ void linear_small_body(float* __restrict__ y, const float* __restrict
                 xb[j][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
                 if (s < nsl && kb < kblocks) {
                     long long c = (long long)kb * 16 + g * 4;
-                    wa[j][u] = ld4<VEC>(w, r0 + i, rows, cols, c);
+                    if constexpr (W16) wa[j][u] = ld4w16(w, r0 + i, rows, cols, c);
+                    else wa[j][u] = ld4<VEC>(w, r0 + i, rows, cols, c);
                     xb[j][u] = ld4<VEC>(x, i, m, cols, c);
                 }
             }
@@ -633,6 +650,11 @@ KERNEL void __launch_bounds__(512) slm_linear_small_s(float* y, const float* w, 
 KERNEL void __launch_bounds__(512) slm_linear_small_vh(float* y, const float* w, const float* x,
                                                        int rows, int cols, int m) {
     linear_small_body<true, true>(y, w, x, rows, cols, m);
+}
+// fp16 mode with the weights stored as halves (w: rows x cols fp16)
+KERNEL void __launch_bounds__(512) slm_linear_small_vhw(float* y, const float* w, const float* x,
+                                                        int rows, int cols, int m) {
+    linear_small_body<true, true, true>(y, w, x, rows, cols, m);
 }
 
 // m > 16: a 64-row × 64-token tile per workgroup, 32 × 32 per wave (2 × 2 MFMA tiles).
@@ -841,16 +863,24 @@ struct GemmEpi {
 // rows 0 .. BM/2 − 1 are gate rows r0h + j and rows BM/2 .. BM − 1 the amp rows half + r0h + j
 // (r0h = blockIdx.x·BM/2), and the tile writes amp·gate / (1 + e^−gate) (slm_silu_mul's
 // expression) for its BM/2 output columns of y [m][half]; one split only.
-template <int BM, int WAVES, bool H, bool SILU, int ROPE = 0>
+// With W16 the weights are fp16 (rows x cols halves, H too): a stage holds the tile's BM rows of
+// 64 halves (128 bytes: eight 16-byte chunks, chunk c at position c ^ (row & 7)), eight rows
+// per copy instruction; copies past the stage's count repeat earlier ones (the same bytes to
+// the same place), so every wave issues the same number.
+template <int BM, int WAVES, bool H, bool SILU, int ROPE = 0, bool W16 = false>
 __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                            const float* __restrict__ w, const float* __restrict__ x, int rows,
                            int cols, int m, GemmEpi ep = GemmEpi{}) {
-    constexpr int SW = BM * 64, SX = 64 * 64, STAGE = SW + SX;  // floats per stage
+    static_assert(!W16 || H, "fp16 weights run the fp16 chain");
+    constexpr int SW = W16 ? BM * 32 : BM * 64, SX = 64 * 64, STAGE = SW + SX;  // floats per stage
     constexpr int NV = WAVES == 4 ? 2 : 1;                      // 16-token MFMA tiles per wave
     constexpr int RG = WAVES == 16 ? 4 : 2;                     // groups of rows over the waves
     constexpr int MU = BM / (16 * RG);                          // 16-row MFMA tiles per wave
-    constexpr int NDMA = (BM + 64) / (4 * WAVES);               // copies per wave per stage
-    static_assert((BM + 64) % (4 * WAVES) == 0 && MU >= 1, "copies per wave, rows per wave");
+    constexpr int NW = W16 ? BM / 8 : BM / 4;                   // copy instructions of the w tile
+    constexpr int NT = NW + 16;                                 // ... and of the x tile
+    constexpr int NDMA = (NT + WAVES - 1) / WAVES;              // copies per wave per stage
+    static_assert(W16 || (BM + 64) % (4 * WAVES) == 0, "copies per wave");
+    static_assert(MU >= 1 && NDMA * WAVES < 2 * NT && BM % 8 == 0, "rows per wave, repeated copies");
     extern __shared__ float lds[];  // [GEMM_STAGES][w: BM x 64 | x: 64 x 64]
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int i = lane & 15, g = lane >> 4;
@@ -864,6 +894,33 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     // rows (w rows first, then x rows), k' = wave + WAVES k; lane L takes row 4k' + L/16,
     // position L % 16, i.e. chunk (L % 16) ^ (row & 15) of that row.
     auto issue = [&](int sl, int buf) {
+        if constexpr (W16) {
+#pragma unroll
+            for (int k = 0; k < NDMA; k++) {
+                int kk = wave + WAVES * k;
+                if (kk >= NT) kk -= NT;
+                const void* src;
+                if (kk < NW) {  // eight weight rows of 64 halves
+                    int rl = 8 * kk + (lane >> 3), chunk = (lane & 7) ^ (rl & 7);
+                    long long wr_ = r0 + rl;
+                    bool ok = wr_ < rows;
+                    if constexpr (SILU) {
+                        long long j = r0h + (rl < BM / 2 ? rl : rl - BM / 2);
+                        ok = j < half;
+                        wr_ = rl < BM / 2 ? j : half + j;
+                    }
+                    src = (const _Float16*)w + (ok ? wr_ * cols : 0) + (long long)sl * 64 + 8 * chunk;
+                } else {  // four token rows of 64 floats
+                    int rl = 4 * (kk - NW) + (lane >> 4), chunk = (lane & 15) ^ (rl & 15);
+                    bool ok = t0 + rl < m;
+                    src = x + (ok ? (t0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
+                }
+                float* dst = lds + buf * STAGE + kk * 256;  // uniform: 1 KB per instruction
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                                 (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+            }
+            return;
+        }
 #pragma unroll
         for (int k = 0; k < NDMA; k++) {
             int rr = 4 * (wave + WAVES * k) + (lane >> 4), pos = lane & 15;
@@ -918,12 +975,31 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         f4 a[SLM_KS][MU], bb[SLM_KS][NV];
 #pragma unroll
         for (int q = 0; q < SLM_KS; q++) {
+            if constexpr (!W16) {
 #pragma unroll
-            for (int u = 0; u < MU; u++) a[q][u] = *(const f4*)(sw + gsw(wr + 16 * u + i, 4 * q + g));
+                for (int u = 0; u < MU; u++) a[q][u] = *(const f4*)(sw + gsw(wr + 16 * u + i, 4 * q + g));
+            }
 #pragma unroll
             for (int v = 0; v < NV; v++) bb[q][v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
         }
-        if constexpr (H) {
+        if constexpr (W16) {
+            // lane (i, g) of block q: halves 16q + 4g .. + 3 of its row, in chunk 2q + g / 2
+            h4 aw[SLM_KS][MU];
+#pragma unroll
+            for (int q = 0; q < SLM_KS; q++)
+#pragma unroll
+                for (int u = 0; u < MU; u++) {
+                    int row = wr + 16 * u + i;
+                    aw[q][u] = *(const h4*)((const char*)sw + row * 128 + 16 * ((2 * q + (g >> 1)) ^ (row & 7)) +
+                                            8 * (g & 1));
+                }
+#pragma unroll
+            for (int q = 0; q < SLM_KS; q++)
+#pragma unroll
+                for (int u = 0; u < MU; u++)
+#pragma unroll
+                    for (int v = 0; v < NV; v++) acc[u][v] = block16hw(aw[q][u], bb[q][v], acc[u][v]);
+        } else if constexpr (H) {
 #pragma unroll
             for (int q = 0; q < SLM_KS; q++)
 #pragma unroll
@@ -1022,39 +1098,44 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     }
 }
 
-#define GEMM2_K(NAME, BM, WAVES, H, S)                                                    \
+#define GEMM2_K(NAME, BM, WAVES, H, S, W16)                                               \
     KERNEL void __launch_bounds__(64 * WAVES) NAME(float* y, float* part, const float* w,  \
                                                    const float* x, int rows, int cols, int m) { \
-        gemm2_body<BM, WAVES, H, S>(y, part, w, x, rows, cols, m);                         \
+        gemm2_body<BM, WAVES, H, S, 0, W16>(y, part, w, x, rows, cols, m);                 \
     }
-#define GEMM2(BM, WAVES)                                  \
-    GEMM2_K(slm_gemm2_##BM, BM, WAVES, false, false)      \
-    GEMM2_K(slm_gemm2h_##BM, BM, WAVES, true, false)      \
-    GEMM2_K(slm_gemm2s_##BM, BM, WAVES, false, true)      \
-    GEMM2_K(slm_gemm2hs_##BM, BM, WAVES, true, true)
+// fp32, fp16 mode, fp16 mode with fp16 weights (..w); plain and with the SiLU pair (..s..)
+#define GEMM2(BM, WAVES)                                         \
+    GEMM2_K(slm_gemm2_##BM, BM, WAVES, false, false, false)      \
+    GEMM2_K(slm_gemm2h_##BM, BM, WAVES, true, false, false)      \
+    GEMM2_K(slm_gemm2hw_##BM, BM, WAVES, true, false, true)      \
+    GEMM2_K(slm_gemm2s_##BM, BM, WAVES, false, true, false)      \
+    GEMM2_K(slm_gemm2hs_##BM, BM, WAVES, true, true, false)      \
+    GEMM2_K(slm_gemm2hsw_##BM, BM, WAVES, true, true, true)
 // the QKV projection with the attention-input epilogue (fp32 and fp16 mode)
-#define GEMM2R_K(NAME, H)                                                                       \
+#define GEMM2R_K(NAME, H, W16)                                                                  \
     KERNEL void __launch_bounds__(1024)                                                         \
         NAME(float* y, float* part, const float* w, const float* x, int rows, int cols, int m,   \
              float* q, float* k, float* v, float* kring, float* vring, const float* cs,          \
              const float* sn, const long long* kdyn, const long long* vdyn, long long kpos,     \
              long long vpos, long long cap, int d) {                                             \
-        gemm2_body<64, 16, H, false, 1>(y, part, w, x, rows, cols, m,                           \
+        gemm2_body<64, 16, H, false, 1, W16>(y, part, w, x, rows, cols, m,                      \
                                         GemmEpi{q, k, v, kring, vring, cs, sn, nullptr, kdyn, vdyn, kpos, vpos, cap, d, 0}); \
     }
-GEMM2R_K(slm_gemm2r_64, false)
-GEMM2R_K(slm_gemm2hr_64, true)
+GEMM2R_K(slm_gemm2r_64, false, false)
+GEMM2R_K(slm_gemm2hr_64, true, false)
+GEMM2R_K(slm_gemm2hrw_64, true, true)
 // the linear-attention QKVG projection with the per-head L2 epilogue (fp32 and fp16 mode)
-#define GEMM2N_K(NAME, H)                                                                        \
+#define GEMM2N_K(NAME, H, W16)                                                                   \
     KERNEL void __launch_bounds__(1024)                                                          \
         NAME(float* y, float* part, const float* w, const float* x, int rows, int cols, int m,    \
              float* q, float* k, float* v, float* g, int d) {                                     \
-        gemm2_body<64, 16, H, false, 2>(                                                         \
+        gemm2_body<64, 16, H, false, 2, W16>(                                                    \
             y, part, w, x, rows, cols, m,                                                        \
             GemmEpi{q, k, v, nullptr, nullptr, nullptr, nullptr, g, nullptr, nullptr, 0, 0, 0, d, 0}); \
     }
-GEMM2N_K(slm_gemm2n_64, false)
-GEMM2N_K(slm_gemm2hn_64, true)
+GEMM2N_K(slm_gemm2n_64, false, false)
+GEMM2N_K(slm_gemm2hn_64, true, false)
+GEMM2N_K(slm_gemm2hnw_64, true, true)
 GEMM2(32, 4)
 GEMM2(64, 16)
 GEMM2(96, 8)
@@ -2278,6 +2359,8 @@ struct FgLane {
     int kb0, nkb;
 };
 
+// (W16: the matrices hold fp16 weights; `base` then addresses halves)
+template <bool W16>
 __device__ __forceinline__ FgLane fg_lane(const FgDesc& d, int u, int wave, int i, int g) {
     FgLane p{slm_zero16, 0, 0};
     if (u >= d.units) return p;
@@ -2289,19 +2372,30 @@ __device__ __forceinline__ FgLane fg_lane(const FgDesc& d, int u, int wave, int 
     p.kb0 = sl * SLM_KS;
     p.nkb = min(SLM_KS, kblocks - p.kb0);
     long long row = fg_row(s, un.tile, i);
-    if (row < s.rows) p.base = s.w + row * d.cols + 4 * g;
+    if (row < s.rows) {
+        if constexpr (W16) p.base = (const float*)((const _Float16*)s.w + row * d.cols + 4 * g);
+        else p.base = s.w + row * d.cols + 4 * g;
+    }
     return p;
 }
 
 // The weights of one unit's slice for this lane: four float4s. Lanes past the matrix load
 // zeros from slm_zero16, so the loads are always four and their results are used as they
 // arrive, without a select that would wait for them.
+// (W16: four halves per block, widened exactly; the zero page reads as zeros either way)
+template <bool W16>
 __device__ __forceinline__ void fg_load(const FgLane& p, f4 (&wa)[SLM_KS]) {
     bool ok = p.base != slm_zero16;
 #pragma unroll
     for (int q = 0; q < SLM_KS; q++) {
-        const float* src = ok && q < p.nkb ? p.base + (p.kb0 + q) * 16 : slm_zero16;
-        wa[q] = gld((const f4*)src);
+        if constexpr (W16) {
+            const h4* src = ok && q < p.nkb ? (const h4*)((const _Float16*)p.base + (p.kb0 + q) * 16)
+                                            : (const h4*)slm_zero16;
+            wa[q] = wide4(gld(src));
+        } else {
+            const float* src = ok && q < p.nkb ? p.base + (p.kb0 + q) * 16 : slm_zero16;
+            wa[q] = gld((const f4*)src);
+        }
     }
 }
 
@@ -2415,17 +2509,29 @@ __device__ void fg_pick_finish(const FgSeg& g, unsigned long long best, int lane
     __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The fused GEMV, fp32 (slm_fg) and fp16 mode (slm_fgh): one kernel text, expanded twice.
+// The fused GEMV, fp32 (slm_fg), fp16 mode (slm_fgh) and fp16 mode with fp16 weights
+// (slm_fghw): one kernel text, expanded three times.
 #define FG_NAME slm_fg
 #define FG_H false
+#define FG_W false
 #include "fg_body.inc"
 #undef FG_NAME
 #undef FG_H
+#undef FG_W
 #define FG_NAME slm_fgh
 #define FG_H true
+#define FG_W false
 #include "fg_body.inc"
 #undef FG_NAME
 #undef FG_H
+#undef FG_W
+#define FG_NAME slm_fghw
+#define FG_H true
+#define FG_W true
+#include "fg_body.inc"
+#undef FG_NAME
+#undef FG_H
+#undef FG_W
 
 // The splits of a linear added in order: y[c] = ((P0[c] + P1[c]) + P2[c]) + ...
 KERNEL void slm_fold(float* __restrict__ y, const float* __restrict__ part, long long n, int nsplit) {

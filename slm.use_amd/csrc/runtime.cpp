@@ -109,6 +109,8 @@ struct Kernels {
         store, rope, rope_table, rms, l2norm, rms_wave, l2norm_wave, fill, combine, probe, fg, fold,
         gemm, gemm2_32, gemm2_64, gemm2_96, gemm2_128, gemm2h_32, gemm2h_64, gemm2h_96, gemm2h_128,
         lin_small_h, fgh;
+    // fp16 mode over fp16 weights (allocated with slm_hip_alloc_half)
+    hipFunction_t lin_small_hw, fghw, gemm2hw[4], gemm2hsw[4], gemm2hrw, gemm2hnw;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
@@ -131,6 +133,7 @@ struct slm_hip {
     std::string err;
     char name[256] = {0};
     std::map<uintptr_t, size_t> allocs;  // live allocations: start -> bytes
+    std::map<uintptr_t, size_t> halves;  // the fp16 ones among them: start -> elements
     float* ws = nullptr;                 // attention partials
     size_t ws_bytes = 0;
     int* attn_ctr = nullptr;             // [ATTN_CTR_MAX] finished superblocks per (query tile, key head)
@@ -209,6 +212,55 @@ size_t room(const slm_hip* c, const void* p) {
     --it;
     if (a < it->first || a >= it->first + it->second) return 0;
     return it->first + it->second - a;
+}
+
+// fp32 -> fp16, rounding to nearest even (IEEE 754 binary16: overflow to infinity,
+// subnormals kept, NaNs stay NaNs with their sign) — the rounding of v_cvt_f16_f32.
+uint16_t f16_of(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));  // NaN
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // rounds to or past 2^16: inf
+    if (a < 0x38800000u) {  // below 2^-14: a subnormal half (or zero)
+        if (a < 0x33000000u) return sign;  // at most half the smallest subnormal: ±0
+        uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+        int shift = 126 - (int)(a >> 23);  // 14..24: bits dropped beyond the 13 of a normal
+        uint32_t q = mant >> shift, rem = mant & ((1u << shift) - 1), halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (q & 1))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = (a - 0x38000000u) >> 13, rem = a & 0x1fffu;  // rebias 127 -> 15
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;   // (a carry into the exponent is right)
+    return (uint16_t)(sign | q);
+}
+
+float f32_of(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu, u;
+    if (e == 0x1f) {
+        u = sign | 0x7f800000u | (m << 13);
+    } else if (e) {
+        u = sign | ((e + 112) << 23) | (m << 13);
+    } else if (!m) {
+        u = sign;
+    } else {  // subnormal: normalise
+        int k = 0;
+        while (!(m & 0x400u)) {
+            m <<= 1;
+            k++;
+        }
+        u = sign | ((uint32_t)(113 - k) << 23) | ((m & 0x3ffu) << 13);
+    }
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// The fp16 allocation that starts at p: its element count (0 if p starts none).
+size_t half_count(const slm_hip* c, const void* p) {
+    auto it = c->halves.find((uintptr_t)p);
+    return it == c->halves.end() ? 0 : it->second;
 }
 
 #define NEED(c, op, p, n)                                                            \
@@ -395,9 +447,11 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
     int64_t kblocks = (cols + 15) / 16, nsl = (kblocks + SLM_KS - 1) / SLM_KS;
     double ab = 4.0 * (double)(rows * cols + m * cols + m * rows);
     bool h = n[3] != 0;  // fp16 mode: 64-column multiples, aligned (checked when recorded)
+    bool w16 = n[4] != 0;  // fp16 weights (fp16 mode)
+    if (w16) ab = 2.0 * (double)(rows * cols) + 4.0 * (double)(m * cols + m * rows);
     if (h && m <= 16 && nsl <= 64) {
         uint32_t waves = (uint32_t)std::min<int64_t>(nsl, 8);
-        out.push_back(mk(k.lin_small_h, (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
+        out.push_back(mk(w16 ? k.lin_small_hw : k.lin_small_h, (uint32_t)((rows + 15) / 16), 1, 1, 64 * waves,
                          (uint32_t)(nsl * 1024), p[0], p[1], p[2], (int)rows, (int)cols, (int)m));
         out.back().abytes = ab;
         return SLM_OK;
@@ -417,9 +471,10 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
             return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
         if (cols % 64 == 0) {
             int bm = gemm2_bm(rows, m, ns);
-            uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
+            uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * (w16 ? 32 : 64) + 64 * 64) * 4);
             hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
             if (h) f = bm == 32 ? k.gemm2h_32 : bm == 64 ? k.gemm2h_64 : bm == 96 ? k.gemm2h_96 : k.gemm2h_128;
+            if (w16) f = k.gemm2hw[bm == 32 ? 0 : bm == 64 ? 1 : bm == 96 ? 2 : 3];
             out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
                              (uint32_t)ns, gemm2_threads(bm), shmem, p[0], c->gpart,
                              p[1], p[2], (int)rows, (int)cols, (int)m));
@@ -699,6 +754,9 @@ bool vp_of(const Op& o, VpSrc* v) {
 }
 
 
+// A linear's weights in floats of storage (fp16 weights take half).
+int64_t wfloats(const Op& o) { return o.n[4] ? (o.n[0] * o.n[1] + 1) / 2 : o.n[0] * o.n[1]; }
+
 // What an op reads and writes, in bytes of device memory (ring and state updates count as
 // both). The embedding table and the rope tables are only ever read.
 void op_ranges(const Op& o, std::vector<Range>& rd, std::vector<Range>& wr) {
@@ -720,7 +778,7 @@ void op_ranges(const Op& o, std::vector<Range>& rd, std::vector<Range>& wr) {
         case OP_COLUMNS: wr.push_back(rng(p[0], n[0] * n[3])); rd.push_back(rng(p[1], n[0] * n[1])); break;
         case OP_LINEAR:
             wr.push_back(rng(p[0], n[2] * n[0]));
-            rd.push_back(rng(p[1], n[0] * n[1]));
+            rd.push_back(rng(p[1], wfloats(o)));
             rd.push_back(rng(p[2], n[2] * n[1]));
             break;
         case OP_ADD:
@@ -1375,7 +1433,7 @@ struct Planner {
             int64_t heads = lq.n[0], dh = lq.n[1], dd = heads * dh;
             bool ok = lk.n[0] == heads && lk.n[1] == dh && rows == 4 * dd && lq.p[1] == y &&
                       lk.p[1] == y + dd && D.n[2] == 1 && D.p[2] == x && D.n[1] == cols &&
-                      aligned16(D.p[1]) && D.n[3] == L.n[3];
+                      aligned16(D.p[1]) && D.n[3] == L.n[3] && D.n[4] == L.n[4];
             // the l2norm outputs are untouched until the GLA kernel writes them
             ok = ok && !overlap(rng(lq.p[0], dd), rng(D.p[0], D.n[0])) &&
                  !overlap(rng(lk.p[0], dd), rng(D.p[0], D.n[0])) &&
@@ -1439,7 +1497,7 @@ struct Planner {
             s.units = s.tiles * s.nsplit;
             s.unit_first = units;
             units += s.units;
-            b.reads.push_back(rng(s.w, (int64_t)s.rows * cols));
+            b.reads.push_back(rng(s.w, L.n[4] ? ((int64_t)s.rows * cols + 1) / 2 : (int64_t)s.rows * cols));
             if (s.nsplit > 1) {
                 b.writes.push_back(rng(s.part, (int64_t)s.nsplit * s.rows));
                 continue;
@@ -1604,9 +1662,11 @@ struct Planner {
         for (int k = 0; k < nseg; k++) d.seg[k] = seg[k];
         int threads = 64 * (W + SLM_FG_EPI_WAVES);
         uint32_t grid = (uint32_t)std::min(units, FG_GRID_MAX);
-        out.push_back(mk_desc(d.f16 ? c->k.fgh : c->k.fg, grid, (uint32_t)threads, (uint32_t)(total * 4), d));
+        hipFunction_t fk = L.n[4] ? c->k.fghw : d.f16 ? c->k.fgh : c->k.fg;
+        out.push_back(mk_desc(fk, grid, (uint32_t)threads, (uint32_t)(total * 4), d));
         double ab = 16.0 * d.pf4;  // prologue vectors, then weights and outputs
-        for (int k = 0; k < nseg; k++) ab += 4.0 * ((double)seg[k].rows * cols + seg[k].rows);
+        double wb = L.n[4] ? 2.0 : 4.0;  // bytes per weight
+        for (int k = 0; k < nseg; k++) ab += wb * (double)seg[k].rows * cols + 4.0 * seg[k].rows;
         out.back().abytes = ab;
         if (nsplit > 1) {
             part_flip ^= 1;
@@ -1720,11 +1780,12 @@ struct Planner {
             !dead_after(ops, i + 4, rng(ca.p[0], m * h)))
             return 0;
         Range ry = rng(sm.p[0], m * h);
-        if (overlap(ry, rng(L.p[1], rows * cols)) || overlap(ry, rng(L.p[2], m * cols))) return 0;
+        if (overlap(ry, rng(L.p[1], wfloats(L))) || overlap(ry, rng(L.p[2], m * cols))) return 0;
         int bm = gemm2_bm(rows, m, 1);
         int q = bm == 32 ? 0 : bm == 64 ? 1 : bm == 96 ? 2 : 3;
-        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
-        out.push_back(mk(L.n[3] ? c->k.gemm2hs[q] : c->k.gemm2s[q], (uint32_t)((h + bm / 2 - 1) / (bm / 2)),
+        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * (L.n[4] ? 32 : 64) + 64 * 64) * 4);
+        hipFunction_t gf = L.n[4] ? c->k.gemm2hsw[q] : L.n[3] ? c->k.gemm2hs[q] : c->k.gemm2s[q];
+        out.push_back(mk(gf, (uint32_t)((h + bm / 2 - 1) / (bm / 2)),
                          (uint32_t)((m + 63) / 64), 1, gemm2_threads(bm), shmem, sm.p[0], c->gpart,
                          L.p[1], L.p[2], (int)rows, (int)cols, (int)m));
         out.back().abytes = 4.0 * (double)(rows * cols + m * cols + m * h);
@@ -1771,7 +1832,7 @@ struct Planner {
         // does not matter
         std::vector<Range> wr = {rng(mix, m * rows), rng(cy, m * d), rng(q, m * d), rng(k, m * d),
                                  rng(v, m * d), rng(s1.p[0], d * cap), rng(s2.p[0], d * cap)};
-        std::vector<Range> rd = {rng(L.p[1], rows * cols), rng(L.p[2], m * cols), rng(r1.p[2], m * 32),
+        std::vector<Range> rd = {rng(L.p[1], wfloats(L)), rng(L.p[2], m * cols), rng(r1.p[2], m * 32),
                                  rng(r1.p[3], m * 32)};
         for (size_t a = 0; a < wr.size(); a++) {
             for (size_t b = a + 1; b < wr.size(); b++)
@@ -1780,8 +1841,9 @@ struct Planner {
                 if (overlap(wr[a], x)) return 0;
         }
         if (!dead_after(ops, i + 8, rng(cy, m * d))) return 0;
-        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (64 * 64 + 64 * 64) * 4);
-        out.push_back(mk(L.n[3] ? c->k.gemm2hr : c->k.gemm2r, (uint32_t)(rows / 64), (uint32_t)((m + 63) / 64),
+        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (64 * (L.n[4] ? 32 : 64) + 64 * 64) * 4);
+        hipFunction_t gf = L.n[4] ? c->k.gemm2hrw : L.n[3] ? c->k.gemm2hr : c->k.gemm2r;
+        out.push_back(mk(gf, (uint32_t)(rows / 64), (uint32_t)((m + 63) / 64),
                          1, gemm2_threads(64), shmem, (float*)mix, c->gpart, L.p[1], L.p[2], (int)rows,
                          (int)cols, (int)m, (float*)q, (float*)k, (float*)v, (float*)s1.p[0],
                          (float*)s2.p[0], r1.p[2], r1.p[3], (const long long*)s1.dyn, (const long long*)s2.dyn,
@@ -1820,7 +1882,7 @@ struct Planner {
         const float *q = n1.p[0], *k = n2.p[0], *v = c3.p[0], *g = c4.p[0];
         std::vector<Range> wr = {rng(mix, m * rows), rng(cy, m * d), rng(q, m * d), rng(k, m * d),
                                  rng(v, m * d), rng(g, m * d)};
-        std::vector<Range> rd = {rng(L.p[1], rows * cols), rng(L.p[2], m * cols)};
+        std::vector<Range> rd = {rng(L.p[1], wfloats(L)), rng(L.p[2], m * cols)};
         for (size_t a = 0; a < wr.size(); a++) {
             for (size_t b = a + 1; b < wr.size(); b++)
                 if (overlap(wr[a], wr[b])) return 0;
@@ -1828,8 +1890,9 @@ struct Planner {
                 if (overlap(wr[a], x)) return 0;
         }
         if (!dead_after(ops, i + 7, rng(cy, m * d))) return 0;
-        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (64 * 64 + 64 * 64) * 4);
-        out.push_back(mk(L.n[3] ? c->k.gemm2hn : c->k.gemm2n, (uint32_t)(rows / 64), (uint32_t)((m + 63) / 64),
+        uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (64 * (L.n[4] ? 32 : 64) + 64 * 64) * 4);
+        hipFunction_t gf = L.n[4] ? c->k.gemm2hnw : L.n[3] ? c->k.gemm2hn : c->k.gemm2n;
+        out.push_back(mk(gf, (uint32_t)(rows / 64), (uint32_t)((m + 63) / 64),
                          1, gemm2_threads(64), shmem, (float*)mix, c->gpart, L.p[1], L.p[2], (int)rows,
                          (int)cols, (int)m, (float*)q, (float*)k, (float*)v, (float*)g, (int)d));
         out.back().abytes = 4.0 * (double)(rows * cols + m * cols + m * rows + 4 * m * d);
@@ -2227,7 +2290,13 @@ int load_kernels(slm_hip* c) {
                {&k.gemm2hs[0], "slm_gemm2hs_32"}, {&k.gemm2hs[1], "slm_gemm2hs_64"},
                {&k.gemm2hs[2], "slm_gemm2hs_96"}, {&k.gemm2hs[3], "slm_gemm2hs_128"},
                {&k.gemm2r, "slm_gemm2r_64"},      {&k.gemm2hr, "slm_gemm2hr_64"},
-               {&k.gemm2n, "slm_gemm2n_64"},      {&k.gemm2hn, "slm_gemm2hn_64"}};
+               {&k.gemm2n, "slm_gemm2n_64"},      {&k.gemm2hn, "slm_gemm2hn_64"},
+               {&k.lin_small_hw, "slm_linear_small_vhw"}, {&k.fghw, "slm_fghw"},
+               {&k.gemm2hw[0], "slm_gemm2hw_32"}, {&k.gemm2hw[1], "slm_gemm2hw_64"},
+               {&k.gemm2hw[2], "slm_gemm2hw_96"}, {&k.gemm2hw[3], "slm_gemm2hw_128"},
+               {&k.gemm2hsw[0], "slm_gemm2hsw_32"}, {&k.gemm2hsw[1], "slm_gemm2hsw_64"},
+               {&k.gemm2hsw[2], "slm_gemm2hsw_96"}, {&k.gemm2hsw[3], "slm_gemm2hsw_128"},
+               {&k.gemm2hrw, "slm_gemm2hrw_64"},  {&k.gemm2hnw, "slm_gemm2hnw_64"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;
@@ -2366,6 +2435,14 @@ int slm_hip_alloc(slm_hip* c, size_t n, float** out) {
     return SLM_OK;
 }
 
+int slm_hip_alloc_half(slm_hip* c, size_t n, float** out) {
+    if (!c || !out) return SLM_E_INVALID;
+    size_t nf = (std::max<size_t>(n, 1) + 1) / 2;  // floats of storage (zeroed: +0 halves)
+    TRY(slm_hip_alloc(c, nf, out));
+    c->halves[(uintptr_t)*out] = std::max<size_t>(n, 1);
+    return SLM_OK;
+}
+
 int slm_hip_free(slm_hip* c, float* p) {
     if (!c) return SLM_E_INVALID;
     if (!p) return SLM_OK;
@@ -2374,6 +2451,7 @@ int slm_hip_free(slm_hip* c, float* p) {
     TRY(taint(c));
     drop_graphs(c);
     c->allocs.erase(it);
+    c->halves.erase((uintptr_t)p);
     HIPC(c, hipStreamSynchronize(c->stream));
     HIPC(c, hipFree(p));
     return SLM_OK;
@@ -2381,6 +2459,20 @@ int slm_hip_free(slm_hip* c, float* p) {
 
 int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
     if (!c || (n && !src)) return SLM_E_INVALID;
+    if (size_t nh = half_count(c, dst)) {  // an fp16 allocation: n values rounded to fp16
+        if (n > nh) return fail(c, SLM_E_BOUNDS, "upload: %zu values into %zu halves", n, nh);
+        if (n == 0) return SLM_OK;
+        TRY(taint(c));
+        HIPC(c, hipStreamSynchronize(c->stream));
+        uint16_t* b = (uint16_t*)c->bounce;
+        for (size_t done = 0; done < n;) {
+            size_t part = std::min(n - done, BOUNCE_CAP / 2);
+            for (size_t i = 0; i < part; i++) b[i] = f16_of(src[done + i]);
+            HIPC(c, hipMemcpy((uint16_t*)dst + done, b, part * 2, hipMemcpyHostToDevice));
+            done += part;
+        }
+        return SLM_OK;
+    }
     NEED(c, "upload", dst, n);
     if (n == 0) return SLM_OK;
     TRY(taint(c));
@@ -2402,6 +2494,21 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
 
 int slm_hip_read(slm_hip* c, float* host, const float* dev, size_t n) {
     if (!c || (n && !host)) return SLM_E_INVALID;
+    if (size_t nh = half_count(c, dev)) {  // an fp16 allocation: n values widened to fp32
+        if (n > nh) return fail(c, SLM_E_BOUNDS, "read: %zu values from %zu halves", n, nh);
+        TRY(taint(c));
+        for (size_t done = 0; done < n;) {
+            size_t part = std::min(n - done, BOUNCE_CAP / 2);
+            HIPC(c, hipMemcpyAsync(c->bounce, (const uint16_t*)dev + done, part * 2,
+                                   hipMemcpyDeviceToHost, c->stream));
+            HIPC(c, hipStreamSynchronize(c->stream));
+            const uint16_t* b = (const uint16_t*)c->bounce;
+            for (size_t i = 0; i < part; i++) host[done + i] = f32_of(b[i]);
+            done += part;
+        }
+        if (n == 0) HIPC(c, hipStreamSynchronize(c->stream));
+        return check_fault(c);
+    }
     NEED(c, "read", dev, n);
     TRY(taint(c));
     size_t done = 0;
@@ -2445,6 +2552,12 @@ int slm_hip_set_fp16(slm_hip* c, int on) {
     if (!c) return SLM_E_INVALID;
     if (c->recording) TRY(finish_step(c));
     c->fp16 = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_get_fp16(slm_hip* c, int* on) {
+    if (!c || !on) return SLM_E_INVALID;
+    *on = c->fp16 ? 1 : 0;
     return SLM_OK;
 }
 
@@ -2796,7 +2909,14 @@ int slm_hip_linear(slm_hip* c, float* y, const float* w, size_t rows, size_t col
                    const float* x, size_t m) {
     if (!c) return SLM_E_INVALID;
     NEED(c, "linear", y, m * rows);
-    NEED(c, "linear", w, rows * cols);
+    size_t nh = half_count(c, w);
+    if (nh) {  // fp16 weights: fp16 mode only (the same halves the fp16 chain rounds to)
+        if (rows * cols > nh) return fail(c, SLM_E_BOUNDS, "linear: %zu x %zu weights in %zu halves", rows, cols, nh);
+        if (!c->fp16)
+            return fail(c, SLM_E_UNSUPPORTED, "linear: fp16 weights need fp16 mode (slm_hip_set_fp16)");
+    } else {
+        NEED(c, "linear", w, rows * cols);
+    }
     NEED(c, "linear", x, m * cols);
     if (!m || !rows) return SLM_OK;
     if (!fits_int(rows) || !fits_int(cols) || !fits_int(m))
@@ -2817,6 +2937,7 @@ int slm_hip_linear(slm_hip* c, float* y, const float* w, size_t rows, size_t col
     o.n[1] = (int64_t)cols;
     o.n[2] = (int64_t)m;
     o.n[3] = c->fp16 ? 1 : 0;
+    o.n[4] = nh ? 1 : 0;  // fp16 weights
     if (c->fp16 && (cols % 64 || !aligned16(w) || !aligned16(x)))
         return fail(c, SLM_E_UNSUPPORTED,
                     "linear: fp16 mode needs a multiple of 64 columns and 16-byte aligned w and x (%zu)", cols);

@@ -336,3 +336,46 @@ def test_c5_fp16_against_fp32_oracle(pkg, hip):
             assert greedy(got) == greedy(want)
     finally:
         hip.set_fp16(False)
+
+
+def test_a86_half_weights_equal_fp16_mode(pkg, hip):
+    """A model loaded in fp16 mode stores its linear weights as fp16 (half the bytes) and gives
+    the bits of fp16 mode over the same model's fp32 weights: a 300-token prompt (chunks of
+    256 + 44: the prompt GEMMs and their epilogues) and 8 greedy steps (the fused GEMV) at
+    R = 4, with the fp16-weight kernels the ones that ran."""
+    folder = model_dir("a86", 2)
+    g32 = pkg.Model(hip, folder)
+    hip.set_fp16(True)
+    try:
+        g16 = pkg.Model(hip, folder)
+        toks = synth.tokens(300, 32000, seed=3)
+        a, b = g32.session(4), g16.session(4)
+        a.feed(toks, 256)
+        hip.set_graphs(False)
+        hip.set_timing(True)
+        b.feed(toks, 256)
+        assert np.array_equal(a.logits(), b.logits())
+        assert hip.kernel_stat("slm_gemm2hrw_64")["launches"] > 0
+        assert hip.kernel_stat("slm_gemm2h_64")["launches"] == 0
+        hip.set_timing(False)
+        toks8, want = [], []
+        for t in range(8):
+            toks8.append(greedy(a.logits()))
+            a.step(toks8[-1])
+            want.append(a.logits())
+        hip.set_timing(True)  # (counts b's launches alone)
+        for t in range(8):
+            b.step(toks8[t])
+            assert np.array_equal(b.logits(), want[t]), t
+        assert hip.kernel_stat("slm_fghw")["launches"] > 0
+        assert hip.kernel_stat("slm_fgh")["launches"] == 0
+        hip.set_timing(False)
+        hip.set_graphs(True)
+        # with step graphs, and the pick on the device
+        ids_a, ids_b = a.decode_greedy(6).tolist(), b.decode_greedy_device(6).tolist()
+        assert ids_a == ids_b
+        assert np.array_equal(a.logits(), b.logits())
+    finally:
+        hip.set_timing(False)
+        hip.set_graphs(True)
+        hip.set_fp16(False)

@@ -712,3 +712,104 @@ def test_linear_fp16_rejects_ragged_columns(hip):
             hip.linear(dy.ptr, dw.ptr, 16, 40, dx.ptr, 1)
     finally:
         hip.set_fp16(False)
+
+
+# ---------------------------------------------------------------------------------------
+# fp16 weights (slm_hip_alloc_half): fp16 mode with half the weight bytes, the same bits
+# ---------------------------------------------------------------------------------------
+
+def test_half_upload_rounds_to_nearest_even(hip):
+    """Upload into an fp16 allocation rounds like numpy's float16 (IEEE binary16, ties to even:
+    subnormals, the overflow threshold, signed zeros, infinities, NaN); read widens back."""
+    tiny = np.float32(2.0 ** -24)
+    x = np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 - 2 ** -12, 65504, 65519.99, 65520, -65520,
+                  tiny, tiny / 2, tiny * 1.5, tiny * 2.5, 2 ** -14 - tiny / 2, -0.0, 0.0, np.inf,
+                  -np.inf, np.nan, 3.14159, -2.71828e-3, 1e-8, 6e4, 2 ** -15 * 1.25],
+                 dtype=np.float32)
+    x = np.concatenate([x, rnd(4099, scale=10.0), rnd(1000, scale=1e-5)])
+    b = hip.upload_half(x)
+    got = b.read(x.size)
+    with np.errstate(over="ignore"):  # (the values past 65504 round to infinity)
+        want = x.astype(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(768, 768), (2304, 768), (6144, 768), (768, 3072),
+                                       (12, 768), (2300, 768), (100, 1536), (8192, 768)])
+def test_linear_half_weights_equal_fp16_mode(hip, rows, cols):
+    """fp16 weights give fp16 mode's bits on the same weights in fp32, for every m (the
+    small-m GEMV and each GEMM row tile), eagerly; and refuse to run outside fp16 mode."""
+    w = rnd(rows, cols, scale=0.05)
+    x = rnd(256, cols)
+    dw, dh, dx = hip.upload(w), hip.upload_half(w), hip.upload(x)
+    hip.set_fp16(True)
+    try:
+        for m in (1, 5, 16, 17, 37, 256):
+            a, b = hip.alloc(m * rows), hip.alloc(m * rows)
+            hip.linear(a.ptr, dw.ptr, rows, cols, dx.ptr, m)
+            hip.linear(b.ptr, dh.ptr, rows, cols, dx.ptr, m)
+            assert np.array_equal(a.read(), b.read()), m
+    finally:
+        hip.set_fp16(False)
+    with pytest.raises(Exception):
+        hip.linear(hip.alloc(rows).ptr, dh.ptr, rows, cols, dx.ptr, 1)
+
+
+@pytest.mark.parametrize("case", ["plain", "rms", "resid", "silu", "rope_store", "split_fold", "rounds"])
+def test_fused_step_half_weights(hip, case):
+    """Inside a step (the fused GEMV slm_fghw): fp16 weights give the fused fp16-mode bits of the
+    same weights in fp32, and the unfused ones."""
+    d, hid, heads, dh, cap = 768, 3072, 12, 64, 4352
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(32), hip.alloc(32)
+    shapes = {"plain": (d, d), "rms": (3 * d, d), "resid": (d, d), "silu": (2 * hid, d),
+              "rope_store": (3 * d, d), "split_fold": (d, hid), "rounds": (32000, d)}
+    rows, cols = shapes[case]
+    w = rnd(rows, cols, scale=0.02)
+    dw, dh16 = hip.upload(w), hip.upload_half(w)
+    x, res, nw = hip.upload(rnd(cols)), hip.upload(rnd(rows)), hip.upload(rnd(cols))
+    xn, y, o1 = hip.alloc(cols), hip.alloc(rows), hip.alloc(rows)
+    kc, vc = hip.alloc(heads * cap * dh), hip.alloc(heads * cap * dh)
+    q, k, h = hip.alloc(d), hip.alloc(d), hip.alloc(hid)
+
+    def body(wp):
+        def run():
+            src = x.ptr
+            if case == "rms":
+                hip.rms(xn.ptr, x.ptr, nw.ptr, 1, cols, 1e-5)
+                src = xn.ptr
+            hip.linear(y.ptr, wp, rows, cols, src, 1)
+            if case == "resid":
+                hip.add(o1.ptr, res.ptr, y.ptr, rows)
+            if case == "silu":
+                hip.silu_mul(h.ptr, y.ptr, y.at(hid), hid)
+            if case == "rope_store":
+                hip.rope(q.ptr, y.ptr, cs.ptr, sn.ptr, 1, heads, dh)
+                hip.rope(k.ptr, y.at(d), cs.ptr, sn.ptr, 1, heads, dh)
+                hip.store(kc.ptr, k.ptr, 4300, 1, cap, heads, dh)
+                hip.store(vc.ptr, y.at(2 * d), 4300, 1, cap, heads, dh)
+        return run
+
+    def outs():
+        r = [y.read()]
+        if case == "resid":
+            r.append(o1.read())
+        if case == "silu":
+            r.append(h.read())
+        if case == "rope_store":
+            r += [q.read(), k.read(), kc.read()[:heads * dh], vc.read()[:heads * dh]]
+        return r
+
+    hip.set_fp16(True)
+    try:
+        got = {}
+        for name, wp, fuse in (("f32w", dw.ptr, True), ("half", dh16.ptr, True), ("half_unfused", dh16.ptr, False)):
+            _step(hip, body(wp), inv, cs, sn, fuse)
+            got[name] = outs()
+    finally:
+        hip.set_fp16(False)
+    for name in ("half", "half_unfused"):
+        for a, b in zip(got["f32w"], got[name]):
+            assert np.array_equal(a, b), (case, name)
