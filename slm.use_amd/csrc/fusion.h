@@ -29,6 +29,13 @@
 #define SLM_SB_KEYS (64 * SLM_SB_SEGS)
 #define SLM_GLA_T 32           // tokens per LDS stage of the prompt GLA kernel
 #define SLM_FG_MISC (32 + 4 * SLM_PF_MAX)  // LDS floats of slm_fg's scalars and prefetch table
+#define SLM_SIG_OPS 7          // prologue ops a signature can name
+// The signature of a prologue of kinds k0, k1, ...: what FgDesc.sig holds.
+#define SLM_SIG1(a) (1 | ((a) << 4))
+#define SLM_SIG2(a, b) (2 | ((a) << 4) | ((b) << 8))
+#define SLM_SIG3(a, b, c) (3 | ((a) << 4) | ((b) << 8) | ((c) << 12))
+#define SLM_SIG4(a, b, c, e) (4 | ((a) << 4) | ((b) << 8) | ((c) << 12) | ((e) << 16))
+#define SLM_SIG5(a, b, c, e, f) (5 | ((a) << 4) | ((b) << 8) | ((c) << 12) | ((e) << 16) | ((f) << 20))
 
 enum {
     VP_COPY = 1,    // out = in0
@@ -107,6 +114,10 @@ typedef struct __attribute__((aligned(16))) {
     // wave w (one 64-column slice) combines head w (64 dims) from the superblock partials
     // in lds[cw] [cnsb][W][cdp + 2], and workgroup 0 writes the result to cgout
     int32_t cw, cdp, cnsb, spin;    // spin: polls a bounded wait makes before it gives up
+    // sig: the prologue's op kinds when every op is a float4 op of at most one float4 per
+    // prologue thread (4 bits each from bit 4, the count in bits 0..3; 0: run the general
+    // loop); nsf: VP_SCALE ops whose factor lives on the device
+    int32_t sig, nsf, pad0, pad1;
     float* cgout;
     int* fault;                     // a wait that gives up ORs 1 in here (host memory)
     PfOp pf[SLM_PF_MAX];

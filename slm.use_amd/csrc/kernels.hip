@@ -2069,8 +2069,8 @@ struct ESync {
 
 // Sum of squares of in[0..size) in the order of dot16_self, run by one wave: lane l and
 // lane l + 16k keep the same running sum of elements l, l + 16, ... (sixteen loads in
-// flight), then the sixteen sums are added left to right through readlane, so every lane
-// returns the same value.
+// flight), then the sixteen sums are added left to right (a DPP scan along each row of
+// sixteen lanes), and every lane returns the total.
 __device__ float dot16_wave(const float* in, int size, int lane) {
     int l = lane & 15;
     int chunks = size / 16;
@@ -2087,10 +2087,17 @@ __device__ float dot16_wave(const float* in, int size, int lane) {
         float v = in[c * 16 + l];
         acc = acc + v * v;
     }
-    float s = -0.0f;
+    // ((-0.0 + acc_0) + acc_1) + ... + acc_15 as a scan along each row of sixteen lanes: at
+    // step k lane l adds its own sum to what lane l - 1 held, so after step k lanes 0..k
+    // hold their final prefix sums (lane 0 adds to the zero its missing neighbour reads,
+    // which equals -0.0 + acc_0 since acc_0 is never -0.0); lane 15 ends with the total.
+    float s = acc;
 #pragma unroll
-    for (int t = 0; t < 16; t++)
-        s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), t));
+    for (int k = 1; k < 16; k++) {
+        float prev = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x111, 0xf, 0xf, true));
+        s = prev + acc;
+    }
+    s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 15));
     float tail = -0.0f;
     for (int j = chunks * 16; j < size; j++) tail = tail + in[j] * in[j];
     return s + tail;
@@ -2298,6 +2305,126 @@ __device__ __forceinline__ VpOp vp_load(const VpOp& src) {
 // caller puts one before an op that reads other threads' elements. rms sums the whole
 // input in every wave (the same sum), so its factor needs no barrier either. `f` is the
 // op's factor (the dynamic one of a VP_SCALE already read).
+// The common case of vp_run, with fewer instructions on the critical path: a float4 op
+// whose vectors hold at most one float4 per thread (thread tid owns float4 tid, as in
+// vp_map4), so each thread reads its operands once, computes the expressions of vp_elem /
+// vp_fold / rms and writes once.
+template <int NSPLIT>
+__device__ __forceinline__ f4 vp_fold4(const f4* p, int n4, int c) {
+    f4 P[NSPLIT];
+#pragma unroll
+    for (int z = 0; z < NSPLIT; z++) P[z] = p[z * n4 + c];
+    f4 v = P[0];
+#pragma unroll
+    for (int z = 1; z < NSPLIT; z++) v = v + P[z];
+    return v;
+}
+
+// The fields of a prologue op that the float4 path reads, made wave-uniform.
+struct VpFast {
+    int n4, out, in0, in1, w, nsb, sync, wg0;
+    float f;
+};
+__device__ __forceinline__ VpFast vp_fast_load(const VpOp& src) {
+    VpFast o;
+    o.n4 = uni(src.n) >> 2;
+    o.out = uni(src.out);
+    o.in0 = uni(src.in0);
+    o.in1 = uni(src.in1 >= 0 ? src.in1 : src.w >= 0 ? src.w : src.in0);
+    o.w = uni(src.w);
+    o.nsb = uni(src.nsb);
+    o.sync = uni(src.sync);
+    o.wg0 = uni(src.wg0);
+    o.f = __int_as_float(uni(__float_as_int(src.f)));
+    return o;
+}
+
+template <int KIND>
+__device__ __forceinline__ void vp_fast(const VpFast& o, float* lds, float f, int tid) {
+    if (o.out < 0) return;  // a copy whose source slot is written out as it is
+    int n4 = o.n4, c = tid;
+    const f4* A = (const f4*)(lds + o.in0);
+    const f4* B = (const f4*)(lds + o.in1);
+    f4* O = (f4*)(lds + o.out);
+    if (KIND == VP_RMS) {  // rms (cpu.rs:187-207): out = a·r·w, summed by the waves that own elements
+        if (64 * (tid >> 6) >= n4) return;
+        float dsum = dot16_wave(lds + o.in0, 4 * n4, tid & 63);
+        float r = 1.0f / sqrtf(dsum / (float)(4 * n4) + o.f);
+        if (c < n4) {
+            f4 a = A[c], w = B[c], v;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = a[e] * r * w[e];
+            O[c] = v;
+        }
+        return;
+    }
+    if (c >= n4) return;
+    if (KIND == VP_FOLD) {
+        const f4* P = (const f4*)(lds + o.w);
+        switch (o.nsb) {
+            case 1: O[c] = vp_fold4<1>(P, n4, c); return;
+            case 2: O[c] = vp_fold4<2>(P, n4, c); return;
+            case 3: O[c] = vp_fold4<3>(P, n4, c); return;
+            case 4: O[c] = vp_fold4<4>(P, n4, c); return;
+            case 5: O[c] = vp_fold4<5>(P, n4, c); return;
+            case 6: O[c] = vp_fold4<6>(P, n4, c); return;
+            case 7: O[c] = vp_fold4<7>(P, n4, c); return;
+            default: O[c] = vp_fold4<8>(P, n4, c); return;
+        }
+    }
+    f4 a = A[c], b = KIND == VP_COPY || KIND == VP_SCALE ? a : B[c], v;
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = vp_elem<KIND>(a[e], b[e], f, 0.0f);
+    O[c] = v;
+}
+
+// A prologue of compile-time kinds K... (every op on the float4 path), run by the prologue
+// waves with `sync` (their barrier) before an op that reads what other threads wrote.
+template <int... K>
+struct VpSeq {
+    template <typename Sync>
+    __device__ __forceinline__ static void run(const VpOp* vp, float* lds, const float* sfac,
+                                               Sync& sync, int tid, bool first) {
+        int k = 0;
+        (step<K>(vp, lds, sfac, sync, tid, first, k++), ...);
+    }
+    template <int KIND, typename Sync>
+    __device__ __forceinline__ static void step(const VpOp* vp, float* lds, const float* sfac,
+                                                Sync& sync, int tid, bool first, int k) {
+        VpFast o = vp_fast_load(vp[k]);
+        if (!first && o.wg0) return;
+        if (k > 0 && (o.sync || KIND == VP_RMS)) sync();
+        float f = o.f;
+        if (KIND == VP_SCALE && vp[k].dyn) f = sfac[k];
+        vp_fast<KIND>(o, lds, f, tid);
+    }
+};
+
+// The prologue through its straight-line code when its signature is one of these; false
+// when it is not (the caller then runs the general loop).
+template <typename Sync>
+__device__ __forceinline__ bool vp_seq(int sig, const VpOp* vp, float* lds, const float* sfac,
+                                       Sync& sync, int tid, bool first) {
+    switch (sig) {
+        case SLM_SIG1(VP_RMS):
+            VpSeq<VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+        case SLM_SIG3(VP_FOLD, VP_ADD, VP_RMS):
+            VpSeq<VP_FOLD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+        case SLM_SIG5(VP_FOLD, VP_ADD, VP_ADD, VP_ADD, VP_RMS):
+            VpSeq<VP_FOLD, VP_ADD, VP_ADD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+        case SLM_SIG3(VP_ADD, VP_ADD, VP_RMS):
+            VpSeq<VP_ADD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+        case SLM_SIG3(VP_FOLD, VP_ADD, VP_COPY):
+            VpSeq<VP_FOLD, VP_ADD, VP_COPY>::run(vp, lds, sfac, sync, tid, first); return true;
+        case SLM_SIG4(VP_FOLD, VP_ADD, VP_COPY, VP_RMS):
+            VpSeq<VP_FOLD, VP_ADD, VP_COPY, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+        case SLM_SIG5(VP_COPY, VP_COPY, VP_COPY, VP_COPY, VP_RMS):
+            VpSeq<VP_COPY, VP_COPY, VP_COPY, VP_COPY, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+        default:
+            return false;
+    }
+}
+
 __device__ void vp_run(const VpOp& o, float* lds, float f, int tid, int nt) {
     if (o.out < 0) return;  // a copy whose source slot is written out as it is
     int n = o.n;
@@ -2317,6 +2444,8 @@ __device__ void vp_run(const VpOp& o, float* lds, float f, int tid, int nt) {
             else vp_comb_o<1>(lds + o.w, (const float2*)(lds + o.in1), out, o.heads, o.dh, o.dp, o.nsb, tid, nt);
             break;
         case VP_RMS: {  // rms (cpu.rs:187-207) of one group: out = a·r·w
+            // (only the waves that own elements of the group sum it, each the same sum)
+            if (64 * (tid >> 6) >= (v4 ? n >> 2 : n)) break;
             float dsum = dot16_wave(a, n, tid & 63);
             float r = 1.0f / sqrtf(dsum / (float)n + o.f);
             vp_map<VP_RMS>(a, b, out, n, v4, f, r, tid, nt);
@@ -2358,6 +2487,64 @@ struct FgLane {
     const float* base;
     int kb0, nkb;
 };
+
+// Descriptor dwords [base, base + 128) of the kernel argument, one per lane in two VGPRs: the
+// whole region costs one memory round trip (each dependent scalar load of a cold scalar cache
+// costs one), and a field is then a readlane with an index known at compile time.
+struct KDw {
+    int v0, v1;
+    __device__ __forceinline__ int operator[](int q) const {
+        return __builtin_amdgcn_readlane(q < 64 ? v0 : v1, q & 63);
+    }
+    __device__ __forceinline__ long long q64(int q) const {
+        return (long long)(unsigned)(*this)[q] | ((long long)(*this)[q + 1] << 32);
+    }
+};
+__device__ __forceinline__ KDw kdw_load(int base, int lane) {
+    const int* k = (const int*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
+    return KDw{gld(k + base + lane), gld(k + base + 64 + lane)};
+}
+
+// fg_lane from the descriptor's dwords in registers (KDw: the header at dword 0, the segments
+// at the dword of FgDesc::seg), for the first round, before the descriptor is in LDS.
+template <bool W16>
+__device__ __forceinline__ FgLane fg_lane_k(const KDw& hd, const KDw& sd, int u, int wave, int i, int g) {
+    constexpr int SW = (int)(sizeof(FgSeg) / 4);
+    constexpr int HU = (int)(offsetof(FgDesc, units) / 4), HC = (int)(offsetof(FgDesc, cols) / 4);
+    constexpr int HN = (int)(offsetof(FgDesc, nsl) / 4), HS = (int)(offsetof(FgDesc, nseg) / 4);
+    constexpr int SF = (int)(offsetof(FgSeg, unit_first) / 4), ST = (int)(offsetof(FgSeg, tiles) / 4);
+    constexpr int SWT = (int)(offsetof(FgSeg, w) / 4), SR = (int)(offsetof(FgSeg, rows) / 4);
+    constexpr int SP = (int)(offsetof(FgSeg, pair_rows) / 4), SH = (int)(offsetof(FgSeg, half) / 4);
+    static_assert(sizeof(FgSeg) % 4 == 0 && SLM_SEG_MAX * sizeof(FgSeg) <= 512, "segment table layout");
+    FgLane p{slm_zero16, 0, 0};
+    if (u >= hd[HU]) return p;
+    int nseg = hd[HS], k = 0;
+#pragma unroll
+    for (int q = 1; q < SLM_SEG_MAX; q++)
+        if (q < nseg && u >= sd[q * SW + SF]) k = q;
+    int local = u - sd[k * SW + SF], tiles = sd[k * SW + ST];
+    int tile = local % tiles, split = local / tiles;
+    int sl = split * SLM_SPLIT + wave;
+    int cols = hd[HC];
+    int kblocks = (cols + 15) >> 4;
+    if (sl >= hd[HN]) return p;
+    p.kb0 = sl * SLM_KS;
+    p.nkb = min(SLM_KS, kblocks - p.kb0);
+    long long row;
+    int pair_rows = sd[k * SW + SP], half = sd[k * SW + SH];
+    if (tile * 16 < pair_rows) {
+        int P = tile * 8 + (i & 7);
+        row = (long long)(P / half) * 2 * half + P % half + ((i & 8) ? half : 0);
+    } else {
+        row = (long long)tile * 16 + i;
+    }
+    if (row < sd[k * SW + SR]) {
+        const float* w = (const float*)sd.q64(k * SW + SWT);
+        if constexpr (W16) p.base = (const float*)((const _Float16*)w + row * cols + 4 * g);
+        else p.base = w + row * cols + 4 * g;
+    }
+    return p;
+}
 
 // (W16: the matrices hold fp16 weights; `base` then addresses halves)
 template <bool W16>

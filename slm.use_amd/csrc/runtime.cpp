@@ -1655,6 +1655,20 @@ struct Planner {
         d.f16 = (int32_t)L.n[3];
         d.spin = c->spin;
         d.fault = c->fault_dev;
+        // the prologue's signature: every op a float4 op of at most one float4 per prologue
+        // thread (the straight-line code of the fused kernel), else 0 (its general loop)
+        d.sig = d.nvp > 0 && d.nvp <= SLM_SIG_OPS ? d.nvp : 0;
+        d.nsf = 0;
+        for (int k = 0; k < d.nvp; k++) {
+            const VpOp& o = d.vp[k];
+            if (o.kind == VP_SCALE && o.dyn) d.nsf++;
+            bool v4 = ((o.in0 | (o.in1 >= 0 ? o.in1 : 0) | (o.out >= 0 ? o.out : 0) |
+                        (o.w >= 0 ? o.w : 0) | o.n) & 3) == 0;
+            bool fast = v4 && o.n / 4 <= 64 * SLM_FG_EPI_WAVES && o.kind != VP_COMB &&
+                        (o.kind != VP_FOLD || o.nsb <= 8);
+            if (!fast) d.sig = 0;
+            if (d.sig && k < SLM_SIG_OPS) d.sig |= o.kind << (4 * (k + 1));
+        }
         d.lds_vp = (b.lds + 3) & ~3;
         d.fold_off = d.lds_vp + SLM_FG_MISC;
         int total = d.fold_off + 4 * W * 16;
