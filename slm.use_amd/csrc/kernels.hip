@@ -1503,52 +1503,88 @@ ATTN_PART(16)
 
 // Prompt attention with the keys and values of a superblock shared in LDS: a workgroup of
 // 16 waves takes ATTN_QG query tiles of one key head against one superblock. The waves
-// first copy the superblock's 256 keys and values into LDS (rows of 16 chunks of 16 bytes,
-// chunk c at c ^ (key & 15)); then wave w runs segment w % 4 for query tile w / 4 with the
-// arithmetic of attn_segment (operands from LDS instead of registers; dims at or past dh
-// read as zero, as there). The segments of each tile are folded in order into superblock
-// partials part[z][qidx][head][2 + 16·DT], which slm_attn_combine then combines. Grid
-// (query tile groups, key heads, superblock slots).
+// first copy the superblock's keys and values into LDS (rows of 16 chunks of 16 bytes, chunk
+// c at c ^ (key & 15)) — only the 16-key tiles some query of the workgroup sees, and nothing
+// at all for a superblock none sees (its partials are written empty); then wave w runs
+// segment w % 4 for query tile w / 4 with the arithmetic of attn_segment (operands from LDS
+// instead of registers; dims at or past dh read as zero, as there). The segments of each tile
+// are folded in order into superblock partials part[z][qidx][head][2 + 16·DT], which
+// slm_attn_combine then combines. Grid (query tile groups, key heads, superblock slots),
+// placed XCD-aware (pq_place).
 #define ATTN_QG 4
+
+// Output dim of o[dt][r] in lane (i, g) of a prompt-attention wave. With DT = 4 the P·V MFMA
+// of block dt takes dims 4i + dt (A row i), so that the four values a lane needs of one key
+// are one 16-byte chunk (one LDS read per key instead of four); the accumulator then holds
+// dims 4·(4g + r) + dt. Each dim's chain (keys in the same order) is unchanged. DT < 4 keeps
+// dims 16dt + i, as attn_segment.
 template <int DT>
-__device__ void attn_seg_lds(const Col& col, const f4 (&qv)[DT], const float* kt,
-                             const float* vt, long long seg_lo, int dh, float scale, float& mo,
-                             float& lo, f4 (&o)[DT]) {
+__device__ __forceinline__ int pq_dim(int dt, int r, int g) {
+    return DT == 4 ? 4 * (4 * g + r) + dt : 16 * dt + 4 * g + r;
+}
+
+// One 16-key tile (keys 16·st .. 16·st + 15 of the segment whose rows start at kt / vt) for
+// the wave's 16 columns; b0 is its first position; koff / voff are the lane's LDS offsets
+// (floats) of its key chunks (t) and value rows (r) in tile 0. FULL: dh = 16·DT (no dim
+// tests). A tile that every valid column sees whole takes no per-key test (the same values:
+// a valid column's keys all pass, an invalid column's none); when every column is valid too,
+// every lane's state updates. A rescale by α = 1 (the running maximum unchanged in every
+// lane) is skipped: o·1 = o.
+template <int DT, bool FULL>
+__device__ __forceinline__ void pq_tile(const Col& col, bool allvalid, const f4 (&qv)[DT],
+                                        const float* kt, const float* vt, const int (&koff)[DT],
+                                        const int (&voff)[4], int st, long long b0, int dh,
+                                        float scale, float& mo, float& lo, f4 (&o)[DT]) {
     int lane = threadIdx.x & 63;
     int i = lane & 15, g = lane >> 4;
-    mo = NEG_INF;
-    lo = 0.0f;
+    bool sees = col.valid && col.lo < b0 + 16 && col.hi > b0;
+    if (__ballot(sees) == 0) return;
+    bool whole = __ballot(col.valid && (col.lo > b0 || col.hi < b0 + 16)) == 0;
+    const float* kst = kt + 1024 * st;
+    const float* vst = vt + 1024 * st;
+    // scores' A operand: key 16st + i of the segment, dims 16t + 4g .. +3
+    f4 kr[DT];
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 1
-    for (int st = 0; st < 4; st++) {
-        long long b0 = seg_lo + 16 * st;
-        bool sees = col.valid && col.lo < b0 + 16 && col.hi > b0;
-        if (__ballot(sees) == 0) continue;
-        // scores: key 16st + i of the segment, dims 16t + 4g .. +3 as the A operand
-        int kk = 16 * st + i;
-        f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < DT; t++) {
+        kr[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (FULL || 16 * t + 4 * g < dh) kr[t] = *(const f4*)(kst + koff[t]);
+    }
+    // values: MFMA r of block dt takes value of key 16st + 4g + r, dim pq_dim's A row i
+    float vr[4][DT];
+    if (DT == 4) {
 #pragma unroll
-        for (int t = 0; t < DT; t++) {
-            f4 kr = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (16 * t + 4 * g < dh) kr = *(const f4*)(kt + 4 * (16 * kk + ((4 * t + g) ^ (kk & 15))));
-            s = mfma4(kr.x, qv[t].x, s);
-            s = mfma4(kr.y, qv[t].y, s);
-            s = mfma4(kr.z, qv[t].z, s);
-            s = mfma4(kr.w, qv[t].w, s);
+        for (int r = 0; r < 4; r++) {
+            f4 w = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (FULL || 4 * i < dh) w = *(const f4*)(vst + voff[r]);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vr[r][dt] = w[dt];
         }
-        // values: MFMA r takes value of key 16st + 4g + r, dim 16dt + i
-        float vr[4][DT];
+    } else {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             int kv = 16 * st + 4 * g + r;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++) {
                 int dd = 16 * dt + i;
-                vr[r][dt] = dd < dh ? vt[4 * (16 * kv + ((dd >> 2) ^ (kv & 15))) + (dd & 3)] : 0.0f;
+                vr[r][dt] = (FULL || dd < dh) ? vt[4 * (16 * kv + ((dd >> 2) ^ (kv & 15))) + (dd & 3)] : 0.0f;
             }
         }
-        float sv[4];
+    }
+    f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < DT; t++) {
+        s = mfma4(kr[t].x, qv[t].x, s);
+        s = mfma4(kr[t].y, qv[t].y, s);
+        s = mfma4(kr[t].z, qv[t].z, s);
+        s = mfma4(kr[t].w, qv[t].w, s);
+    }
+    float sv[4];
+    int anyi;
+    if (whole) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) sv[r] = col.valid ? s[r] * scale : NEG_INF;
+        anyi = col.valid ? 1 : 0;
+    } else {
         bool any = false;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -1557,78 +1593,108 @@ __device__ void attn_seg_lds(const Col& col, const f4 (&qv)[DT], const float* kt
             sv[r] = ok ? s[r] * scale : NEG_INF;
             any = any || ok;
         }
-        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mx = xmax16(mx);
-        mx = xmax32(mx);
-        int anyi = any ? 1 : 0;
+        anyi = any ? 1 : 0;
         anyi = xor16i(anyi);
         anyi = xor32i(anyi);
-        float mnew = fmaxf(mo, mx);
-        float muse = mnew == NEG_INF ? 0.0f : mnew;
-        float p[4];
+    }
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = xmax16(mx);
+    mx = xmax32(mx);
+    float mnew = fmaxf(mo, mx);
+    float muse = mnew == NEG_INF ? 0.0f : mnew;
+    float p[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) p[r] = sv[r] == NEG_INF ? 0.0f : expf(sv[r] - muse);
-        float rs = ((p[0] + p[1]) + p[2]) + p[3];
-        rs = xsum16(rs);
-        rs = xsum32(rs);
-        float alpha = expf(mo - muse);
-        f4 on[DT];
+    for (int r = 0; r < 4; r++) p[r] = sv[r] == NEG_INF ? 0.0f : expf(sv[r] - muse);
+    float rs = ((p[0] + p[1]) + p[2]) + p[3];
+    rs = xsum16(rs);
+    rs = xsum32(rs);
+    float alpha = expf(mo - muse);
+    if (whole && allvalid) {  // every lane updates
+        if (__ballot(alpha != 1.0f) != 0) {
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) on[dt] = o[dt] * alpha;
+            for (int dt = 0; dt < DT; dt++) o[dt] = o[dt] * alpha;
+        }
 #pragma unroll
         for (int r = 0; r < 4; r++)
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) on[dt] = mfma4(vr[r][dt], p[r], on[dt]);
-        if (anyi) {
-            lo = lo * alpha + rs;
-            mo = mnew;
+            for (int dt = 0; dt < DT; dt++) o[dt] = mfma4(vr[r][dt], p[r], o[dt]);
+        lo = lo * alpha + rs;
+        mo = mnew;
+        return;
+    }
+    f4 on[DT];
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) o[dt] = on[dt];
-        }
+    for (int dt = 0; dt < DT; dt++) on[dt] = o[dt] * alpha;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) on[dt] = mfma4(vr[r][dt], p[r], on[dt]);
+    if (anyi) {
+        lo = lo * alpha + rs;
+        mo = mnew;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt] = on[dt];
     }
 }
 
-template <int DT>
-__device__ void attn_pq_body(float* __restrict__ part, const float* __restrict__ q,
-                             const float* __restrict__ kc, const float* __restrict__ vc,
-                             const long long* __restrict__ dyn, long long pos_imm, int m,
-                             long long reach, long long gap, long long cap, int heads,
-                             int key_heads, int dh, float scale) {
-    static_assert(DT >= 1 && DT <= 4, "shared-superblock attention: head size at most 64");
+// Workgroups go round-robin to the eight XCDs in launch order, each XCD with its own L2: the
+// workgroups L, L + 8, L + 16, ... (one XCD) take the query tile groups of one (key head,
+// superblock) in turn, so those groups read its keys and values through one L2. A tail of
+// the grid that does not fill whole rounds of 8 x groups keeps the plain order. (The host
+// keeps the grid under 2^31 workgroups.)
+__device__ __forceinline__ void pq_place(int& gx, int& kvh, int& z) {
+    unsigned G = gridDim.x, Y = gridDim.y;
+    unsigned L = blockIdx.x + G * (blockIdx.y + Y * blockIdx.z);
+    unsigned total = G * Y * gridDim.z, full = total / (8 * G) * (8 * G), unit;
+    if (L < full) {
+        unsigned s = L >> 3;
+        gx = (int)(s % G);
+        unit = (s / G) * 8 + (L & 7);
+    } else {
+        gx = (int)(L % G);
+        unit = L / G;
+    }
+    kvh = (int)(unit % Y);
+    z = (int)(unit / Y);
+}
+
+// The 16-key tiles [ta, tb) of a segment starting at position sbase that meet [LO, HI).
+__device__ __forceinline__ void pq_tiles(long long sbase, long long LO, long long HI, int& ta, int& tb) {
+    long long a = LO <= sbase ? 0 : (LO - sbase) >> 4;
+    long long b = HI <= sbase ? 0 : (HI - sbase + 15) >> 4;
+    tb = (int)(b < 4 ? b : 4);
+    ta = (int)(a < tb ? a : tb);
+}
+
+template <int DT, bool FULL>
+__device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ q,
+                            const float* __restrict__ kc, const float* __restrict__ vc,
+                            long long pos, int m, long long reach, long long gap, long long cap,
+                            int heads, int key_heads, int dh, float scale) {
     constexpr int DP = 16 * DT;
     constexpr int NT = 64 * SLM_SB_SEGS * ATTN_QG;
+    constexpr int NC = ATTN_QG * 16;  // columns of the workgroup
     extern __shared__ float lds[];  // keys [256][64], values [256][64]; then the fold slots
     float* kt = lds;
     float* vt = lds + SLM_SB_KEYS * 64;
-    long long pos = dyn_or(dyn, pos_imm);
     int lane = threadIdx.x & 63;
     int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int seg = wave % SLM_SB_SEGS, qt = wave / SLM_SB_SEGS;
     int i = lane & 15, g = lane >> 4;
     int group = heads / key_heads, qpt = 16 / group;
-    int kvh = blockIdx.y;
-    long long qtile = (long long)blockIdx.x * ATTN_QG + qt;
+    int gx, kvh, z;
+    pq_place(gx, kvh, z);
     long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
-    long long sb = first / SLM_SB_KEYS + blockIdx.z;
-    // the superblock's keys and values: instruction kk of a tensor covers keys 4kk .. 4kk+3,
-    // lane L taking key 4kk + L/16, chunk (L % 16) ^ (key & 15) (a chunk at or past dh
-    // copies the row's last one; those dims read as zero below)
-    const float* kb = kc + (long long)kvh * cap * dh;
-    const float* vb = vc + (long long)kvh * cap * dh;
-    unsigned base = (unsigned)((sb * SLM_SB_KEYS) % cap), cap32 = (unsigned)cap;
-    int nch = dh >> 2;
-#pragma unroll
-    for (int u = 0; u < SLM_SB_KEYS / 4 / (SLM_SB_SEGS * ATTN_QG); u++) {
-        int kk = wave + SLM_SB_SEGS * ATTN_QG * u;
-        int key = 4 * kk + (lane >> 4);
-        int chunk = min((lane & 15) ^ (key & 15), nch - 1);
-        long long off = (long long)((base + (unsigned)key) % cap32) * dh + 4 * chunk;
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off),
-                                         (__attribute__((address_space(3))) void*)(kt + 256 * kk), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off),
-                                         (__attribute__((address_space(3))) void*)(vt + 256 * kk), 16, 0, 0);
-    }
-    Col col = column(i, qtile, pos, m, reach, gap, group, qpt, kvh);
+    long long k0 = (first / SLM_SB_KEYS + z) * SLM_SB_KEYS;  // the superblock's first position
+    // every position some query of the workgroup sees lies in [LO, HI)
+    long long q0 = (long long)gx * ATTN_QG * qpt;
+    long long q1 = ((long long)m < q0 + ATTN_QG * qpt ? (long long)m : q0 + ATTN_QG * qpt) - 1;
+    long long LO = (reach - 1 > pos + q0) ? 0 : pos + q0 - (reach - 1);
+    long long HI = (gap > pos + q1 + 1) ? 0 : pos + q1 + 1 - gap;
+    // a superblock no query of the workgroup sees: nothing to write (slm_attn_combine reads
+    // only the superblocks each row sees)
+    if (HI <= LO || HI <= k0 || LO >= k0 + SLM_SB_KEYS) return;
+    Col col = column(i, (long long)gx * ATTN_QG + qt, pos, m, reach, gap, group, qpt, kvh);
     // this lane's share of its column's query: B[k = g][j = i] for each 16-dim block
     f4 qv[DT];
     const float* qrow = q + (col.qidx * heads + col.head) * (long long)dh;
@@ -1636,44 +1702,112 @@ __device__ void attn_pq_body(float* __restrict__ part, const float* __restrict__
     for (int t = 0; t < DT; t++) {
         int c = 16 * t + 4 * g;
         qv[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (col.valid && c < dh) qv[t] = *(const f4*)(qrow + c);
+        if (col.valid && (FULL || c < dh)) qv[t] = *(const f4*)(qrow + c);
     }
+    // the copies: wave w takes segment w / 4, and of each tile it copies the four keys
+    // 4·(w % 4) .. +3 (one instruction, lane L: key + L/16, chunk (L % 16) ^ (key & 15); a
+    // chunk at or past dh copies the row's last one, read as zero below)
+    {
+        const float* kb = kc + (long long)kvh * cap * dh;
+        const float* vb = vc + (long long)kvh * cap * dh;
+        int cs = wave >> 2;
+        int ta, tb;
+        pq_tiles(k0 + 64 * cs, LO, HI, ta, tb);
+        unsigned cap32 = (unsigned)cap;
+        unsigned base = (k0 >> 32) == 0 ? (unsigned)k0 % cap32 : (unsigned)(k0 % cap);
+        bool wrap1 = cap >= SLM_SB_KEYS;  // base + key < 2·cap: one subtraction wraps it
+        int nch = dh >> 2;
+        for (int st = ta; st < tb; st++) {
+            int row = 64 * cs + 16 * st + 4 * (wave & 3);
+            int key = row + (lane >> 4);
+            int chunk = (lane & 15) ^ (key & 15);
+            if (!FULL || DT < 4) chunk = min(chunk, nch - 1);  // rows hold 16 chunks
+            unsigned slot = base + (unsigned)key;
+            slot = wrap1 ? (slot >= cap32 ? slot - cap32 : slot) : slot % cap32;
+            long long off = (long long)slot * dh + 4 * chunk;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off),
+                                             (__attribute__((address_space(3))) void*)(kt + 64 * row), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off),
+                                             (__attribute__((address_space(3))) void*)(vt + 64 * row), 16, 0, 0);
+        }
+    }
+    bool allvalid = __ballot(col.valid) == ~0ull;
+    int koff[DT], voff[4];
+#pragma unroll
+    for (int t = 0; t < DT; t++) koff[t] = 64 * i + 4 * ((4 * t + g) ^ i);
+#pragma unroll
+    for (int r = 0; r < 4; r++) voff[r] = 64 * (4 * g + r) + 4 * (i ^ (4 * g + r));
     vm_wait<0>();
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    float mo, lo;
+    float mo = NEG_INF, lo = 0.0f;
     f4 o[DT];
-    attn_seg_lds<DT>(col, qv, kt + seg * 64 * 64, vt + seg * 64 * 64,
-                     (sb * SLM_SB_SEGS + seg) * 64, dh, scale, mo, lo, o);
-    __syncthreads();  // every wave is done with the keys and values: their LDS holds the folds
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     {
-        float* L = lds + (wave * 16 + i) * (DP + 2);
+        long long sbase = k0 + 64 * seg;
+        int ta, tb;
+        pq_tiles(sbase, LO, HI, ta, tb);
+        const float* ks = kt + seg * 64 * 64;
+        const float* vs = vt + seg * 64 * 64;
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) L[2 + 16 * dt + 4 * g + r] = o[dt][r];
-        if (g == 0) {
-            L[0] = mo;
-            L[1] = lo;
+        for (int st = 0; st < 4; st++) {
+            if (st < ta || st >= tb) continue;
+            pq_tile<DT, FULL>(col, allvalid, qv, ks, vs, koff, voff, st, sbase + 16 * st, dh,
+                              scale, mo, lo, o);
         }
     }
-    __syncthreads();
-    // fold each tile's segments in order, one (tile, column, dim) per thread and pass
-    for (int t = threadIdx.x; t < ATTN_QG * 16 * DP; t += NT) {
-        int qq = t / (16 * DP), cc = (t / DP) % 16, dd = t % DP;
-        Col c2 = column(cc, (long long)blockIdx.x * ATTN_QG + qq, pos, m, reach, gap, group, qpt, kvh);
-        if (!c2.valid || dd >= dh) continue;
-        float FM = NEG_INF, FL = 0.0f, FO = 0.0f;
+    __syncthreads();  // every wave is done with the keys and values: their LDS holds the folds
+    // fold each tile's segments in order (fold()'s expressions): wave (tile, s) takes the
+    // accumulator registers r = s of the tile's four segment waves, lane for lane (lane i of
+    // every one of them holds column i), with the column's (m, l) of each segment
+    f4* X = (f4*)lds;                                       // [wave][r][lane]: o[0..3][r]
+    float2* Y = (float2*)(lds + 4 * 16 * 4 * 64);           // [wave][lane]: (m, l)
 #pragma unroll
-        for (int w = 0; w < SLM_SB_SEGS; w++) {
-            const float* F = lds + ((qq * SLM_SB_SEGS + w) * 16 + cc) * (DP + 2);
-            fold(FM, FL, FO, F[0], F[1], F[2 + dd]);
+    for (int r = 0; r < 4; r++) {
+        f4 v = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) v[dt] = o[dt][r];
+        X[(wave * 4 + r) * 64 + lane] = v;
+    }
+    Y[wave * 64 + lane] = float2{mo, lo};
+    __syncthreads();
+    f4 xv[SLM_SB_SEGS];
+    float2 ml[SLM_SB_SEGS];
+#pragma unroll
+    for (int w = 0; w < SLM_SB_SEGS; w++) {
+        xv[w] = X[((qt * SLM_SB_SEGS + w) * 4 + seg) * 64 + lane];
+        ml[w] = Y[(qt * SLM_SB_SEGS + w) * 64 + lane];
+    }
+    float FM = NEG_INF, FL = 0.0f;
+    f4 FO = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < SLM_SB_SEGS; w++) {
+        float mB = ml[w].x, lB = ml[w].y;
+        if (lB == 0.0f) continue;
+        if (FL == 0.0f) {
+            FM = mB;
+            FL = lB;
+            FO = xv[w];
+            continue;
         }
-        float* P = part + (((long long)blockIdx.z * m + c2.qidx) * heads + c2.head) * (long long)(DP + 2);
-        if (dd == 0) {
+        float mn = fmaxf(FM, mB);
+        float a = expf(FM - mn), b = expf(mB - mn);
+        FL = FL * a + lB * b;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) FO[dt] = FO[dt] * a + xv[w][dt] * b;
+        FM = mn;
+    }
+    if (col.valid) {
+        float* P = part + (((long long)z * m + col.qidx) * heads + col.head) * (long long)(DP + 2);
+        if (g == 0 && seg == 0) {
             P[0] = FM;
             P[1] = FL;
         }
-        P[2 + dd] = FO;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            int dd = pq_dim<DT>(dt, seg, g);
+            if (FULL || dd < dh) P[2 + dd] = FO[dt];
+        }
     }
 }
 
@@ -1682,8 +1816,13 @@ __device__ void attn_pq_body(float* __restrict__ part, const float* __restrict__
         float* part, const float* q, const float* kc, const float* vc,                   \
         const long long* dyn, long long pos_imm, int m, long long reach, long long gap,  \
         long long cap, int heads, int key_heads, int dh, float scale) {                  \
-        attn_pq_body<DT>(part, q, kc, vc, dyn, pos_imm, m, reach, gap, cap, heads,        \
-                         key_heads, dh, scale);                                          \
+        long long pos = dyn_or(dyn, pos_imm);                                            \
+        if (dh == 16 * DT)                                                               \
+            attn_pq_run<DT, true>(part, q, kc, vc, pos, m, reach, gap, cap, heads,        \
+                                  key_heads, dh, scale);                                 \
+        else                                                                             \
+            attn_pq_run<DT, false>(part, q, kc, vc, pos, m, reach, gap, cap, heads,       \
+                                   key_heads, dh, scale);                                \
     }
 ATTN_PQ(1)
 ATTN_PQ(2)
@@ -1974,18 +2113,31 @@ ATTN_DEC(4)
 // superblock order), y = O / L (0 when the query sees nothing, cpu.rs:378-382). The last
 // workgroup of an attention launch that combines itself computes the same expressions.
 KERNEL void __launch_bounds__(256) slm_attn_combine(float* __restrict__ y, const float* __restrict__ part, int m,
-                             int heads, int dh, int dp, int nsb) {
+                             int heads, int dh, int dp, int nsb, const long long* dyn,
+                             long long pos_imm, long long reach, long long gap) {
     // one wave per (query, head) row: lane z holds superblock z's m and l (64 at a time),
-    // lane d the o values of dim d of every superblock, all loads of a batch in flight
+    // lane d the o values of dim d of every superblock, all loads of a batch in flight.
+    // With reach > 0 only the superblocks the row's query sees are read (the others have
+    // l = 0, which the sums skip; the prompt attention does not write them).
     int lane = threadIdx.x & 63;
     long long rw = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (rw >= (long long)m * heads) return;
+    int zlo = 0, zhi = nsb;
+    if (reach > 0) {
+        long long pos = dyn_or(dyn, pos_imm), p = pos + rw / heads;
+        long long lo = reach - 1 > p ? 0 : p - (reach - 1), hi = gap > p + 1 ? 0 : p + 1 - gap;
+        long long fb = (reach - 1 > pos ? 0 : pos - (reach - 1)) / SLM_SB_KEYS;
+        long long a = lo / SLM_SB_KEYS - fb, b = hi > lo ? (hi - 1) / SLM_SB_KEYS - fb + 1 : 0;
+        zlo = (int)(a > 0 ? a : 0);
+        zhi = (int)(b < nsb ? b : nsb);
+        if (zhi < zlo) zhi = zlo;
+    }
     const float* P = part + rw * (dp + 2);
     long long stride = (long long)m * heads * (dp + 2);
     float M = NEG_INF;
-    for (int z0 = 0; z0 < nsb; z0 += 64) {
+    for (int z0 = zlo; z0 < zhi; z0 += 64) {
         int z = z0 + lane;
-        float mz = z < nsb ? P[z * stride] : NEG_INF, lz = z < nsb ? P[z * stride + 1] : 0.0f;
+        float mz = z < zhi ? P[z * stride] : NEG_INF, lz = z < zhi ? P[z * stride + 1] : 0.0f;
         float mm = lz > 0.0f ? mz : NEG_INF;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
@@ -1994,11 +2146,11 @@ KERNEL void __launch_bounds__(256) slm_attn_combine(float* __restrict__ y, const
     for (int d0 = 0; d0 < dh; d0 += 64) {
         int dd = d0 + lane;
         float L = 0.0f, O = 0.0f;
-        for (int z0 = 0; z0 < nsb; z0 += 64) {
+        for (int z0 = zlo; z0 < zhi; z0 += 64) {
             int z = z0 + lane;
-            float mz = z < nsb ? P[z * stride] : NEG_INF, lz = z < nsb ? P[z * stride + 1] : 0.0f;
+            float mz = z < zhi ? P[z * stride] : NEG_INF, lz = z < zhi ? P[z * stride + 1] : 0.0f;
             float wz = lz > 0.0f ? expf(mz - M) : 0.0f;  // lane z: superblock z's weight
-            int nz = min(64, nsb - z0);
+            int nz = min(64, zhi - z0);
             for (int u0 = 0; u0 < nz; u0 += 16) {
                 float oz[16];
 #pragma unroll

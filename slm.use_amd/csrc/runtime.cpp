@@ -532,7 +532,8 @@ int lower_attn_dec(slm_hip* c, const Op& o, std::vector<Rec>& out, bool defer) {
                      self ? c->attn_ctr : (int*)nullptr));
     if (!self && !defer)
         out.push_back(mk(k.combine, (uint32_t)((heads + 3) / 4), 1, 1, 256, 0, p[0], (const float*)part,
-                         1, (int)heads, (int)dh, (int)dp, (int)nsb));
+                         1, (int)heads, (int)dh, (int)dp, (int)nsb, (const long long*)nullptr,
+                         (long long)0, (long long)0, (long long)0));
     return SLM_OK;
 }
 
@@ -643,26 +644,27 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int64_t dp = (int64_t)16 << dti;
             if (attn_dec_ok(o)) return lower_attn_dec(c, o, out, false);
             float* part = attn_part(c, o);
-            if (m > 1 && dh <= 64) {
+            int64_t qpt = 16 / (heads / kh);
+            int64_t groups = ((m + qpt - 1) / qpt + ATTN_QG_HOST - 1) / ATTN_QG_HOST;
+            if (m > 1 && dh <= 64 && groups * kh * nsb <= (int64_t)INT_MAX) {
                 // a superblock's keys and values shared in LDS by four query tiles
-                int64_t qpt = 16 / (heads / kh);
                 // (then every row's superblocks are combined by a kernel of their own: many
                 // rows, each a wave, rather than one workgroup per tile group at the end)
-                int64_t groups = ((m + qpt - 1) / qpt + ATTN_QG_HOST - 1) / ATTN_QG_HOST;
                 out.push_back(mk(k.attn_pq[dti], (uint32_t)groups, (uint32_t)kh, (uint32_t)nsb,
                                  64 * SLM_SB_SEGS * ATTN_QG_HOST, (uint32_t)(2 * SLM_SB_KEYS * 64 * 4),
                                  part, p[1], p[2], p[3], (const long long*)o.dyn, (long long)n[0],
                                  (int)m, (long long)n[2], (long long)n[3], (long long)n[4],
                                  (int)heads, (int)kh, (int)dh, o.f[0]));
                 out.push_back(mk(k.combine, (uint32_t)((m * heads + 3) / 4), 1, 1, 256, 0, p[0],
-                                 (const float*)part, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
+                                 (const float*)part, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb,
+                                 (const long long*)o.dyn, (long long)n[0], (long long)n[2],
+                                 (long long)n[3]));
                 return SLM_OK;
             }
             // LDS: wpp segment partials being folded, then each wave's tile of values
             auto shm = [&](int64_t w) { return (w * 16 * (dp + 2) + SLM_SB_SEGS * 16 * (dp + 4)) * 4; };
             int64_t wpp = SLM_SB_SEGS;
             while (wpp > 1 && shm(wpp) > ATTN_LDS_MAX) wpp /= 2;
-            int64_t qpt = 16 / (heads / kh);
             int64_t qtiles = (m + qpt - 1) / qpt;
             // the last workgroup of each (query tile, key head) combines the superblocks itself
             // when its counter fits; otherwise slm_attn_combine runs after
@@ -674,7 +676,8 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                              (int)wpp, self ? p[0] : (float*)nullptr, self ? c->attn_ctr : (int*)nullptr));
             if (!self)
                 out.push_back(mk(k.combine, (uint32_t)((m * heads + 3) / 4), 1, 1, 256, 0, p[0],
-                                 (const float*)part, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb));
+                                 (const float*)part, (int)m, (int)heads, (int)dh, (int)dp, (int)nsb,
+                                 (const long long*)nullptr, (long long)0, (long long)0, (long long)0));
             return SLM_OK;
         }
     }
@@ -1237,7 +1240,8 @@ struct Planner {
                                  (long long)v.n, v.nsplit));
             } else if (v.kind == SRC_COMB) {
                 out.push_back(mk(c->k.combine, (uint32_t)((v.heads + 3) / 4), 1, 1, 256, 0, v.out[0],
-                                 v.in[0], 1, v.heads, v.dh, v.dp, v.nsplit));
+                                 v.in[0], 1, v.heads, v.dh, v.dp, v.nsplit, (const long long*)nullptr,
+                                 (long long)0, (long long)0, (long long)0));
             } else {
                 TRY(lower_one(c, *v.op, out));
             }

@@ -229,6 +229,9 @@ ATTN_CASES = [
     dict(pos=2, m=3, reach=O.USIZE_MAX, gap=8, cap=64, heads=4, key_heads=1, dh=8),
     dict(pos=4100, m=1, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
     dict(pos=5000, m=256, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
+    # a filling window: superblock slots no query sees yet, a diagonal cut inside a segment
+    dict(pos=272, m=256, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
+    dict(pos=100, m=50, reach=64, gap=0, cap=200, heads=4, key_heads=2, dh=16),
     dict(pos=9000, m=40, reach=O.USIZE_MAX, gap=4096, cap=16384, heads=12, key_heads=4, dh=64),
     dict(pos=600, m=33, reach=200, gap=0, cap=456, heads=6, key_heads=3, dh=32),
     dict(pos=700, m=20, reach=512, gap=0, cap=600, heads=4, key_heads=2, dh=128),
