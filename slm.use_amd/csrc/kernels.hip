@@ -952,60 +952,52 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     for (int u = 0; u < MU; u++)
 #pragma unroll
         for (int v = 0; v < NV; v++) sp[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int p = 0; p < GEMM_STAGES - 1; p++)
-        if (p < ns) issue(s_first + p, p);
-    for (int q0 = 0; q0 < ns; q0++) {
-        // this slice's copies are done (the later ones may still run), then everyone's are,
-        // and everyone has finished the previous slice, whose buffer the next copy reuses
-        if (q0 + 1 < ns) vm_wait<NDMA * (GEMM_STAGES - 2)>();
-        else vm_wait<0>();
-        // a barrier without the fence of __syncthreads, which would wait for every copy in
-        // flight; this wave's LDS reads of the previous slice are done (their values were used)
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (q0 + GEMM_STAGES - 1 < ns) issue(s_first + q0 + GEMM_STAGES - 1, (q0 + GEMM_STAGES - 1) % GEMM_STAGES);
-        const float* sw = lds + (q0 % GEMM_STAGES) * STAGE;
+    // A slice's operands go from LDS into registers one slice ahead: while the MFMAs of slice
+    // q run, the reads of slice q + 1 are in flight (the LDS reads of all waves take about half
+    // as long as their MFMAs), and the copies of slices q + 2 and q + 3.
+    struct Ops {
+        f4 a[SLM_KS][MU];
+        h4 aw[SLM_KS][MU];
+        f4 bb[SLM_KS][NV];
+    };
+    auto load_ops = [&](int buf, Ops& o) {
+        const float* sw = lds + buf * STAGE;
         const float* sx = sw + SW;
+#pragma unroll
+        for (int q = 0; q < SLM_KS; q++) {
+#pragma unroll
+            for (int u = 0; u < MU; u++) {
+                int row = wr + 16 * u + i;
+                if constexpr (W16)  // lane (i, g) of block q: halves 16q + 4g .. + 3 of its row, chunk 2q + g / 2
+                    o.aw[q][u] = *(const h4*)((const char*)sw + row * 128 + 16 * ((2 * q + (g >> 1)) ^ (row & 7)) +
+                                              8 * (g & 1));
+                else
+                    o.a[q][u] = *(const f4*)(sw + gsw(row, 4 * q + g));
+            }
+#pragma unroll
+            for (int v = 0; v < NV; v++) o.bb[q][v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
+        }
+    };
+    auto run_ops = [&](const Ops& o, int q0) {
         f4 acc[MU][NV];
 #pragma unroll
         for (int u = 0; u < MU; u++)
 #pragma unroll
             for (int v = 0; v < NV; v++) acc[u][v] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        // the whole slice's operands first (one LDS round trip), then its MFMAs back to back
-        f4 a[SLM_KS][MU], bb[SLM_KS][NV];
-#pragma unroll
-        for (int q = 0; q < SLM_KS; q++) {
-            if constexpr (!W16) {
-#pragma unroll
-                for (int u = 0; u < MU; u++) a[q][u] = *(const f4*)(sw + gsw(wr + 16 * u + i, 4 * q + g));
-            }
-#pragma unroll
-            for (int v = 0; v < NV; v++) bb[q][v] = *(const f4*)(sx + gsw(wt + 16 * v + i, 4 * q + g));
-        }
         if constexpr (W16) {
-            // lane (i, g) of block q: halves 16q + 4g .. + 3 of its row, in chunk 2q + g / 2
-            h4 aw[SLM_KS][MU];
-#pragma unroll
-            for (int q = 0; q < SLM_KS; q++)
-#pragma unroll
-                for (int u = 0; u < MU; u++) {
-                    int row = wr + 16 * u + i;
-                    aw[q][u] = *(const h4*)((const char*)sw + row * 128 + 16 * ((2 * q + (g >> 1)) ^ (row & 7)) +
-                                            8 * (g & 1));
-                }
 #pragma unroll
             for (int q = 0; q < SLM_KS; q++)
 #pragma unroll
                 for (int u = 0; u < MU; u++)
 #pragma unroll
-                    for (int v = 0; v < NV; v++) acc[u][v] = block16hw(aw[q][u], bb[q][v], acc[u][v]);
+                    for (int v = 0; v < NV; v++) acc[u][v] = block16hw(o.aw[q][u], o.bb[q][v], acc[u][v]);
         } else if constexpr (H) {
 #pragma unroll
             for (int q = 0; q < SLM_KS; q++)
 #pragma unroll
                 for (int u = 0; u < MU; u++)
 #pragma unroll
-                    for (int v = 0; v < NV; v++) acc[u][v] = block16h(a[q][u], bb[q][v], acc[u][v]);
+                    for (int v = 0; v < NV; v++) acc[u][v] = block16h(o.a[q][u], o.bb[q][v], acc[u][v]);
         } else {
 #pragma unroll
             for (int q = 0; q < SLM_KS; q++)
@@ -1014,13 +1006,80 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
                     for (int u = 0; u < MU; u++)
 #pragma unroll
-                        for (int v = 0; v < NV; v++) acc[u][v] = mfma4(a[q][u][e], bb[q][v][e], acc[u][v]);
+                        for (int v = 0; v < NV; v++) acc[u][v] = mfma4(o.a[q][u][e], o.bb[q][v][e], acc[u][v]);
         }
         // slice sums in order within the split
 #pragma unroll
         for (int u = 0; u < MU; u++)
 #pragma unroll
             for (int v = 0; v < NV; v++) sp[u][v] = q0 == 0 ? acc[u][v] : sp[u][v] + acc[u][v];
+    };
+    // a barrier without the fence of __syncthreads, which would wait for every copy in flight;
+    // this wave's LDS reads issued before it are done (the second wait, a no-op, tells the
+    // compiler so: it would otherwise count the reads of two slices in flight, more than the
+    // counter holds, and wait for all of them before the first MFMA)
+    auto barrier = [&]() {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt untouched
+    };
+    static_assert(GEMM_STAGES == 3, "the copy waits below count three buffers");
+    // (two slices of operands in registers do not fit 16 waves of 128-row tiles: those read
+    // each slice after its barrier)
+    constexpr bool PIPE = !(BM == 128 && WAVES == 16);
+    if constexpr (!PIPE) {
+#pragma unroll
+        for (int p = 0; p < GEMM_STAGES - 1; p++)
+            if (p < ns) issue(s_first + p, p);
+        for (int q0 = 0; q0 < ns; q0++) {
+            if (q0 + 1 < ns) vm_wait<NDMA * (GEMM_STAGES - 2)>();
+            else vm_wait<0>();
+            barrier();
+            if (q0 + GEMM_STAGES - 1 < ns)
+                issue(s_first + q0 + GEMM_STAGES - 1, (q0 + GEMM_STAGES - 1) % GEMM_STAGES);
+            Ops o;
+            load_ops(q0 % GEMM_STAGES, o);
+            run_ops(o, q0);
+        }
+    } else {
+        // Every step issues one slice's copies (past the last slice, the last one again into
+        // the free buffer), so every wait below counts the same: no branches, and the
+        // compiler's waits for the LDS reads stay exact.
+#pragma unroll
+        for (int p = 0; p < GEMM_STAGES; p++) issue(s_first + min(p, ns - 1), p);
+        // slice 0 is in (this wave's copies of slices 1 and 2 may still run), then everyone's is
+        vm_wait<2 * NDMA>();
+        barrier();
+        Ops R0, R1;
+        load_ops(0, R0);
+        // step q (q + 1 < ns): slice q + 1 is in (everyone's copies) and slice q's buffer is
+        // free (everyone's reads of it were waited for before the barrier): copy slice q + 3
+        // there, read slice q + 1, run slice q, whose operands the barrier waited for
+        auto step = [&](int q, Ops& cur, Ops& nxt) {
+            vm_wait<NDMA>();
+            barrier();
+            issue(s_first + min(q + GEMM_STAGES, ns - 1), q % GEMM_STAGES);
+            load_ops((q + 1) % GEMM_STAGES, nxt);
+            __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
+            run_ops(cur, q);
+        };
+        // unrolled over the split's slices (ns <= SLM_SPLIT), so that the two register sets
+        // alternate without copies
+#pragma unroll
+        for (int q0 = 0; q0 < SLM_SPLIT; q0 += 2) {
+            if (q0 + 1 < ns) {
+                step(q0, R0, R1);
+                if (q0 + 2 < ns) {
+                    step(q0 + 1, R1, R0);
+                } else {
+                    run_ops(R1, q0 + 1);
+                    break;
+                }
+            } else {
+                run_ops(R0, q0);
+                break;
+            }
+        }
+        vm_wait<0>();  // the repeated copies are in before the buffers are reused below
     }
     // out: D[4g + r][i] is row wr + 16u + 4g + r, token wt + 16v + i; through LDS so the
     // stores run along rows
