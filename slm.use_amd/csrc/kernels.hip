@@ -867,22 +867,32 @@ struct GemmEpi {
 // 64 halves (128 bytes: eight 16-byte chunks, chunk c at position c ^ (row & 7)), eight rows
 // per copy instruction; copies past the stage's count repeat earlier ones (the same bytes to
 // the same place), so every wave issues the same number.
-template <int BM, int WAVES, bool H, bool SILU, int ROPE = 0, bool W16 = false>
+// With KG = 2 the workgroup has two groups of WAVES waves: group 0 runs the first half of
+// the split's slices and group 1 the second half, each through LDS buffers of its own, side
+// by side (twice the MFMA chains per SIMD); group 1 hands its slice sums to group 0, which
+// adds them after its own, in slice order (the same sums as one group). Plain outputs only.
+// RGX (when not 0) sets the number of row groups of the waves (RG); the token groups are the
+// rest (WAVES / RG), each 64 / (WAVES / RG) tokens wide.
+template <int BM, int WAVES, bool H, bool SILU, int ROPE = 0, bool W16 = false, int KG = 1, int RGX = 0>
 __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                            const float* __restrict__ w, const float* __restrict__ x, int rows,
                            int cols, int m, GemmEpi ep = GemmEpi{}) {
     static_assert(!W16 || H, "fp16 weights run the fp16 chain");
     constexpr int SW = W16 ? BM * 32 : BM * 64, SX = 64 * 64, STAGE = SW + SX;  // floats per stage
-    constexpr int NV = WAVES == 4 ? 2 : 1;                      // 16-token MFMA tiles per wave
-    constexpr int RG = WAVES == 16 ? 4 : 2;                     // groups of rows over the waves
+    constexpr int RG = RGX ? RGX : WAVES == 16 ? 4 : 2;         // groups of rows over the waves
+    constexpr int NV = 4 / (WAVES / RG);                        // 16-token MFMA tiles per wave
+    static_assert(WAVES % RG == 0 && NV * (WAVES / RG) == 4, "waves over rows and tokens");
     constexpr int MU = BM / (16 * RG);                          // 16-row MFMA tiles per wave
     constexpr int NW = W16 ? BM / 8 : BM / 4;                   // copy instructions of the w tile
     constexpr int NT = NW + 16;                                 // ... and of the x tile
     constexpr int NDMA = (NT + WAVES - 1) / WAVES;              // copies per wave per stage
     static_assert(W16 || (BM + 64) % (4 * WAVES) == 0, "copies per wave");
     static_assert(MU >= 1 && NDMA * WAVES < 2 * NT && BM % 8 == 0, "rows per wave, repeated copies");
-    extern __shared__ float lds[];  // [GEMM_STAGES][w: BM x 64 | x: 64 x 64]
-    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    static_assert(KG == 1 || (KG == 2 && !SILU && ROPE == 0), "slice groups: plain outputs");
+    constexpr int NTH = 64 * WAVES * KG;                        // threads
+    extern __shared__ float lds[];  // [KG][GEMM_STAGES][w: BM x 64 | x: 64 x 64]
+    int tid = threadIdx.x, lane = tid & 63;
+    int kg = __builtin_amdgcn_readfirstlane((tid >> 6) / WAVES), wave = (tid >> 6) % WAVES;
     int i = lane & 15, g = lane >> 4;
     // waves: RG groups of the rows times (64 / 16NV) groups of tokens
     int wr = (wave % RG) * (BM / RG), wt = (wave / RG) * 16 * NV;
@@ -890,6 +900,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     long long r0h = (long long)blockIdx.x * (BM / 2), half = rows / 2;  // (SILU)
     int nsl = cols >> 6;
     int s_first = blockIdx.z * SLM_SPLIT, s_end = min(nsl, s_first + SLM_SPLIT), ns = s_end - s_first;
+    float* gl = lds + kg * GEMM_STAGES * STAGE;  // this group's buffers
     // Stage copy: instruction k of this wave covers rows 4k' .. 4k'+3 of the stage's (BM + 64)
     // rows (w rows first, then x rows), k' = wave + WAVES k; lane L takes row 4k' + L/16,
     // position L % 16, i.e. chunk (L % 16) ^ (row & 15) of that row.
@@ -915,7 +926,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                     bool ok = t0 + rl < m;
                     src = x + (ok ? (t0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
                 }
-                float* dst = lds + buf * STAGE + kk * 256;  // uniform: 1 KB per instruction
+                float* dst = gl + buf * STAGE + kk * 256;  // uniform: 1 KB per instruction
                 __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                                  (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
             }
@@ -940,7 +951,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                 bool ok = t0 + rl < m;
                 src = x + (ok ? (t0 + rl) * cols : 0) + (long long)sl * 64 + 4 * chunk;
             }
-            float* dst = lds + buf * STAGE + (4 * (wave + WAVES * k)) * 64;  // uniform: 4 rows
+            float* dst = gl + buf * STAGE + (4 * (wave + WAVES * k)) * 64;  // uniform: 4 rows
             // a row past the end copies row 0 instead (its outputs are never stored), so every
             // copy runs and the waits below count them exactly
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
@@ -955,13 +966,14 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     // A slice's operands go from LDS into registers one slice ahead: while the MFMAs of slice
     // q run, the reads of slice q + 1 are in flight (the LDS reads of all waves take about half
     // as long as their MFMAs), and the copies of slices q + 2 and q + 3.
+    f4 p1[KG == 2 ? SLM_SPLIT / 2 : 1][MU][NV];  // (group 1) its slice sums
     struct Ops {
         f4 a[SLM_KS][MU];
         h4 aw[SLM_KS][MU];
         f4 bb[SLM_KS][NV];
     };
     auto load_ops = [&](int buf, Ops& o) {
-        const float* sw = lds + buf * STAGE;
+        const float* sw = gl + buf * STAGE;
         const float* sx = sw + SW;
 #pragma unroll
         for (int q = 0; q < SLM_KS; q++) {
@@ -1008,11 +1020,21 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
                         for (int v = 0; v < NV; v++) acc[u][v] = mfma4(o.a[q][u][e], o.bb[q][v][e], acc[u][v]);
         }
-        // slice sums in order within the split
+        // slice sums in order within the split (group 1 keeps its own for group 0)
+        if (KG == 1 || kg == 0) {
 #pragma unroll
-        for (int u = 0; u < MU; u++)
+            for (int u = 0; u < MU; u++)
 #pragma unroll
-            for (int v = 0; v < NV; v++) sp[u][v] = q0 == 0 ? acc[u][v] : sp[u][v] + acc[u][v];
+                for (int v = 0; v < NV; v++) sp[u][v] = q0 == 0 ? acc[u][v] : sp[u][v] + acc[u][v];
+        } else {  // (constant indices only: p1 stays in registers)
+#pragma unroll
+            for (int j = 0; j < (KG == 2 ? SLM_SPLIT / 2 : 1); j++)
+                if (j == q0)
+#pragma unroll
+                    for (int u = 0; u < MU; u++)
+#pragma unroll
+                        for (int v = 0; v < NV; v++) p1[j][u][v] = acc[u][v];
+        }
     };
     // a barrier without the fence of __syncthreads, which would wait for every copy in flight;
     // this wave's LDS reads issued before it are done (the second wait, a no-op, tells the
@@ -1026,6 +1048,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     // (two slices of operands in registers do not fit 16 waves of 128-row tiles: those read
     // each slice after its barrier)
     constexpr bool PIPE = !(BM == 128 && WAVES == 16);
+    static_assert(PIPE || KG == 1, "slice groups run the pipelined loop");
     if constexpr (!PIPE) {
 #pragma unroll
         for (int p = 0; p < GEMM_STAGES - 1; p++)
@@ -1041,56 +1064,90 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
             run_ops(o, q0);
         }
     } else {
-        // Every step issues one slice's copies (past the last slice, the last one again into
-        // the free buffer), so every wait below counts the same: no branches, and the
+        // This group's slices: g_ns from g_first (group 0: the first nst of the split; group 1
+        // the rest, possibly none). Both groups run nst steps (the same barriers).
+        int nst = (ns + KG - 1) / KG;
+        int g_first = kg == 0 ? s_first : s_first + nst, g_ns = kg == 0 ? nst : ns - nst;
+        int c_first = g_ns > 0 ? g_first : s_first, c_last = (g_ns > 0 ? g_ns : 1) - 1;
+        // Every step issues one slice's copies (past the group's last slice, the last one again
+        // into the free buffer), so every wait below counts the same: no branches, and the
         // compiler's waits for the LDS reads stay exact.
 #pragma unroll
-        for (int p = 0; p < GEMM_STAGES; p++) issue(s_first + min(p, ns - 1), p);
+        for (int p = 0; p < GEMM_STAGES; p++) issue(c_first + min(p, c_last), p);
         // slice 0 is in (this wave's copies of slices 1 and 2 may still run), then everyone's is
         vm_wait<2 * NDMA>();
         barrier();
         Ops R0, R1;
         load_ops(0, R0);
-        // step q (q + 1 < ns): slice q + 1 is in (everyone's copies) and slice q's buffer is
+        // step q (q + 1 < nst): slice q + 1 is in (everyone's copies) and slice q's buffer is
         // free (everyone's reads of it were waited for before the barrier): copy slice q + 3
         // there, read slice q + 1, run slice q, whose operands the barrier waited for
         auto step = [&](int q, Ops& cur, Ops& nxt) {
             vm_wait<NDMA>();
             barrier();
-            issue(s_first + min(q + GEMM_STAGES, ns - 1), q % GEMM_STAGES);
+            issue(c_first + min(q + GEMM_STAGES, c_last), q % GEMM_STAGES);
             load_ops((q + 1) % GEMM_STAGES, nxt);
             __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
-            run_ops(cur, q);
+            if (q < g_ns) run_ops(cur, q);
         };
-        // unrolled over the split's slices (ns <= SLM_SPLIT), so that the two register sets
-        // alternate without copies
+        // unrolled over the group's slices (nst <= SLM_SPLIT / KG), so that the two register
+        // sets alternate without copies
 #pragma unroll
-        for (int q0 = 0; q0 < SLM_SPLIT; q0 += 2) {
-            if (q0 + 1 < ns) {
+        for (int q0 = 0; q0 < SLM_SPLIT / KG; q0 += 2) {
+            if (q0 + 1 < nst) {
                 step(q0, R0, R1);
-                if (q0 + 2 < ns) {
+                if (q0 + 2 < nst) {
                     step(q0 + 1, R1, R0);
                 } else {
-                    run_ops(R1, q0 + 1);
+                    if (q0 + 1 < g_ns) run_ops(R1, q0 + 1);
                     break;
                 }
             } else {
-                run_ops(R0, q0);
+                if (q0 < g_ns) run_ops(R0, q0);
                 break;
             }
         }
         vm_wait<0>();  // the repeated copies are in before the buffers are reused below
+        if constexpr (KG == 2) {
+            // group 1's slice sums through LDS to group 0, which adds them after its own
+            __syncthreads();
+            f4* xp = (f4*)lds;  // [slice][wave][u][v][lane]
+            if (kg == 1) {
+#pragma unroll
+                for (int j = 0; j < SLM_SPLIT / 2; j++)
+                    if (j < g_ns)
+#pragma unroll
+                        for (int u = 0; u < MU; u++)
+#pragma unroll
+                            for (int v = 0; v < NV; v++)
+                                xp[(((j * WAVES + wave) * MU + u) * NV + v) * 64 + lane] = p1[j][u][v];
+            }
+            __syncthreads();
+            if (kg == 0) {
+                int n1 = ns - nst;
+#pragma unroll
+                for (int j = 0; j < SLM_SPLIT / 2; j++)
+                    if (j < n1)
+#pragma unroll
+                        for (int u = 0; u < MU; u++)
+#pragma unroll
+                            for (int v = 0; v < NV; v++)
+                                sp[u][v] = sp[u][v] + xp[(((j * WAVES + wave) * MU + u) * NV + v) * 64 + lane];
+            }
+        }
     }
     // out: D[4g + r][i] is row wr + 16u + 4g + r, token wt + 16v + i; through LDS so the
     // stores run along rows
     __syncthreads();
     float* so = lds;  // [64 tokens][BM + 1]
+    if (KG == 1 || kg == 0) {
 #pragma unroll
-    for (int u = 0; u < MU; u++)
+        for (int u = 0; u < MU; u++)
 #pragma unroll
-        for (int v = 0; v < NV; v++)
+            for (int v = 0; v < NV; v++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
+                for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
+    }
     __syncthreads();
     if constexpr (ROPE == 2) {
         // The linear-attention input (rows = 4·d): q and k leave L2-normalised per head (the
@@ -1151,7 +1208,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         return;
     }
     float* out = gridDim.z > 1 ? part + (long long)blockIdx.z * m * rows : y;
-    for (int e = tid; e < 64 * BM; e += 64 * WAVES) {
+    for (int e = tid; e < 64 * BM; e += NTH) {
         int tok = e / BM, row = e % BM;
         if (t0 + tok < m && r0 + row < rows) out[(t0 + tok) * rows + r0 + row] = so[tok * (BM + 1) + row];
     }
@@ -1196,6 +1253,20 @@ GEMM2N_K(slm_gemm2n_64, false, false)
 GEMM2N_K(slm_gemm2hn_64, true, false)
 GEMM2N_K(slm_gemm2hnw_64, true, true)
 GEMM2(32, 4)
+// Plain fp32 tiles for skinny prompts (the host picks by the chip's fill): 32 and 16 rows
+// with two slice groups of four waves; 48 rows with four waves of three row blocks each.
+KERNEL void __launch_bounds__(512) slm_gemm2k_32(float* y, float* part, const float* w,
+                                                 const float* x, int rows, int cols, int m) {
+    gemm2_body<32, 4, false, false, 0, false, 2>(y, part, w, x, rows, cols, m);
+}
+KERNEL void __launch_bounds__(512) slm_gemm2k_16(float* y, float* part, const float* w,
+                                                 const float* x, int rows, int cols, int m) {
+    gemm2_body<16, 4, false, false, 0, false, 2, 1>(y, part, w, x, rows, cols, m);
+}
+KERNEL void __launch_bounds__(256) slm_gemm2_48(float* y, float* part, const float* w,
+                                                const float* x, int rows, int cols, int m) {
+    gemm2_body<48, 4, false, false, 0, false, 1, 1>(y, part, w, x, rows, cols, m);
+}
 GEMM2(64, 16)
 GEMM2(96, 8)
 GEMM2(128, 16)

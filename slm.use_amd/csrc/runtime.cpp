@@ -121,6 +121,8 @@ struct Kernels {
     hipFunction_t gemm2n, gemm2hn;           // prompt QKVG GEMM with the per-head L2 epilogue
     hipFunction_t rows;                      // prompt row chains
     hipFunction_t attn_pq[3];                // prompt attention, superblock shared in LDS
+    hipFunction_t gemm2k_32, gemm2k_16;      // 32- and 16-row tiles, two slice groups (fp32)
+    hipFunction_t gemm2_48;                  // 48-row tiles, four waves of three row blocks
 };
 
 }  // namespace
@@ -429,6 +431,22 @@ int gemm2_bm(int64_t rows, int64_t m, int64_t ns) {
 
 uint32_t gemm2_threads(int bm) { return bm == 32 ? 256 : bm == 96 ? 512 : 1024; }
 
+// The plain fp32 GEMM's tile rows (16 and 32: two slice groups, 48: four waves of three row
+// blocks; 64, 96, 128 as gemm2_bm): the fewest rounds of one workgroup per CU, each round
+// costing its tile rows (the per-SIMD MFMA work) plus a fixed 16 (launch, first copies,
+// epilogue).
+int gemm2_bm_plain(int64_t rows, int64_t m, int64_t ns) {
+    int bm = 64;
+    int64_t best = -1;
+    for (int t : {16, 32, 48, 64, 96, 128}) {
+        int64_t wgs = ((rows + t - 1) / t) * ((m + 63) / 64) * ns;
+        int64_t rounds = (wgs + CU_COUNT - 1) / CU_COUNT;
+        int64_t cost = rounds * (t + 16);
+        if (best < 0 || cost < best) best = cost, bm = t;
+    }
+    return bm;
+}
+
 // A linear (p0 y, p1 w, p2 x; n0 rows, n1 cols, n2 m). With `fold_ns`, a split GEMM's
 // partials are left in c->gpart for the caller to add (*fold_ns: the split count, 1 when
 // the GEMM wrote y itself).
@@ -472,11 +490,23 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
         if (cols % 64 == 0) {
             int bm = gemm2_bm(rows, m, ns);
             uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * (w16 ? 32 : 64) + 64 * 64) * 4);
+            uint32_t threads = gemm2_threads(bm);
             hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
             if (h) f = bm == 32 ? k.gemm2h_32 : bm == 64 ? k.gemm2h_64 : bm == 96 ? k.gemm2h_96 : k.gemm2h_128;
             if (w16) f = k.gemm2hw[bm == 32 ? 0 : bm == 64 ? 1 : bm == 96 ? 2 : 3];
+            if (!h && !w16) {  // fp32: the tile rows by the chip's fill
+                bm = gemm2_bm_plain(rows, m, ns);
+                shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
+                threads = bm == 48 ? 256 : gemm2_threads(bm);
+                f = bm == 48 ? k.gemm2_48 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
+                if (bm <= 32) {  // two slice groups: twice the MFMA chains per SIMD
+                    f = bm == 16 ? k.gemm2k_16 : k.gemm2k_32;
+                    shmem *= 2;
+                    threads = 512;
+                }
+            }
             out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
-                             (uint32_t)ns, gemm2_threads(bm), shmem, p[0], c->gpart,
+                             (uint32_t)ns, threads, shmem, p[0], c->gpart,
                              p[1], p[2], (int)rows, (int)cols, (int)m));
         } else {
             out.push_back(mk(k.gemm, (uint32_t)((rows + 63) / 64), (uint32_t)((m + 63) / 64),
@@ -2287,6 +2317,8 @@ int load_kernels(slm_hip* c) {
                {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
                {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
                {&k.gemm2_32, "slm_gemm2_32"},   {&k.gemm2_64, "slm_gemm2_64"},
+               {&k.gemm2k_32, "slm_gemm2k_32"}, {&k.gemm2k_16, "slm_gemm2k_16"},
+               {&k.gemm2_48, "slm_gemm2_48"},
                {&k.gemm2_96, "slm_gemm2_96"},   {&k.gemm2_128, "slm_gemm2_128"},
                {&k.gemm2h_32, "slm_gemm2h_32"}, {&k.gemm2h_64, "slm_gemm2h_64"},
                {&k.gemm2h_96, "slm_gemm2h_96"}, {&k.gemm2h_128, "slm_gemm2h_128"},
