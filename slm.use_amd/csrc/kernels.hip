@@ -418,7 +418,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                          const float* __restrict__ q, const float* __restrict__ k,
                          const float* __restrict__ v, const float* __restrict__ decay,
                          const float* __restrict__ bias, int m, int heads, int dh, int vec) {
-    extern __shared__ float lds[];  // 2 x ([SLM_GLA_T][q (dh) | k (dh) | v (16)], then [SLM_GLA_T] d)
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // 2 x ([SLM_GLA_T][q (dh) | k (dh) | v (16)], then [SLM_GLA_T] d)
     int h = blockIdx.x, c0 = blockIdx.y * 16, tid = threadIdx.x, nt = blockDim.x;
     int b = c0 + (tid >> 4), j = tid & 15;
     bool live = b < dh;
@@ -890,7 +890,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     static_assert(MU >= 1 && NDMA * WAVES < 2 * NT && BM % 8 == 0, "rows per wave, repeated copies");
     static_assert(KG == 1 || (KG == 2 && !SILU && ROPE == 0), "slice groups: plain outputs");
     constexpr int NTH = 64 * WAVES * KG;                        // threads
-    extern __shared__ float lds[];  // [KG][GEMM_STAGES][w: BM x 64 | x: 64 x 64]
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // [KG][GEMM_STAGES][w: BM x 64 | x: 64 x 64]
     int tid = threadIdx.x, lane = tid & 63;
     int kg = __builtin_amdgcn_readfirstlane((tid >> 6) / WAVES), wave = (tid >> 6) % WAVES;
     int i = lane & 15, g = lane >> 4;
@@ -1469,7 +1469,7 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
                                float* __restrict__ y, int* __restrict__ ctr) {
     constexpr int DP = 16 * DT;
     constexpr int NT = 64 * SLM_SB_SEGS;
-    extern __shared__ float lds[];  // [wpp][16][DP + 2] folds, then [waves][16][DP + 4] values
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // [wpp][16][DP + 2] folds, then [waves][16][DP + 4] values
     long long pos = dyn_or(dyn, pos_imm);
     int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int i = lane & 15, g = lane >> 4;
@@ -1804,7 +1804,7 @@ __device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ 
     constexpr int DP = 16 * DT;
     constexpr int NT = 64 * SLM_SB_SEGS * ATTN_QG;
     constexpr int NC = ATTN_QG * 16;  // columns of the workgroup
-    extern __shared__ float lds[];  // keys [256][64], values [256][64]; then the fold slots
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // keys [256][64], values [256][64]; then the fold slots
     float* kt = lds;
     float* vt = lds + SLM_SB_KEYS * 64;
     int lane = threadIdx.x & 63;
@@ -1982,7 +1982,7 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
                               int* __restrict__ ctr) {
     static_assert(DT >= 1 && DT <= 4, "one-token attention: head size at most 64");
     constexpr int DP = 16 * DT;
-    extern __shared__ float lds[];
+    extern __shared__ __attribute__((aligned(16))) float lds[];
     long long pos = dyn_or(dyn, pos_imm);
     int lane = threadIdx.x & 63;
     int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -3112,7 +3112,7 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
     for (int q = threadIdx.x; q < (int)(sizeof(RowDesc) / 16); q += blockDim.x)
         ((f4*)&d)[q] = ((const f4*)&dk)[q];
     __syncthreads();
-    extern __shared__ float lds[];
+    extern __shared__ __attribute__((aligned(16))) float lds[];
     long long r = blockIdx.x;
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int nops = uni(d.nops);
@@ -3271,7 +3271,7 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
 // SiLU gate of model.rs:483-484 follow, in the expressions of slm_rms and slm_silu_mul.
 template <int RPL>
 __device__ void gla1_body(const GlaDesc& g) {
-    extern __shared__ float lds[];  // [dh + 4] rms, [dh] q, [dh] k, 4 norms
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // [dh + 4] rms, [dh] q, [dh] k, 4 norms
     int h = blockIdx.x, tid = threadIdx.x, dh = g.dh;
     int b = tid >> 4, j = tid & 15;
     bool live = b < dh;
