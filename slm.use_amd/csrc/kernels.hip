@@ -3105,35 +3105,55 @@ __device__ __forceinline__ RowOp row_load(const RowOp& src) {
     return o;
 }
 KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
-    // the descriptor goes to LDS with one wide load per thread: its fields then cost one
-    // memory round trip, not one per op
+    // The header, the prefetch table and the first op come into registers with one dword per
+    // lane (one memory round trip, no LDS hop), so the operand prefetches — and, when the chain
+    // starts with a fold of split partials, those partials — are issued at once; the whole
+    // descriptor goes to LDS for the ops meanwhile (one wide load per thread).
     __shared__ RowDesc d;
-    static_assert(sizeof(RowDesc) % 16 == 0, "descriptor copy in float4s");
-    for (int q = threadIdx.x; q < (int)(sizeof(RowDesc) / 16); q += blockDim.x)
-        ((f4*)&d)[q] = ((const f4*)&dk)[q];
-    __syncthreads();
+    constexpr int ND4 = (int)(sizeof(RowDesc) / 16), PF0 = (int)(offsetof(RowDesc, pf) / 4);
+    constexpr int PFW = (int)(sizeof(RowPf) / 4), O0 = (int)(offsetof(RowDesc, op) / 4);
+    static_assert(sizeof(RowDesc) % 16 == 0 && ND4 <= 256, "descriptor copy: a float4 per thread");
+    static_assert(O0 + (int)(sizeof(RowOp) / 4) <= 128, "the first op in the registers' dwords");
     extern __shared__ __attribute__((aligned(16))) float lds[];
     long long r = blockIdx.x;
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int nops = uni(d.nops);
-    // the operand rows the chain reads from global memory, copied straight into LDS, all in
-    // flight at once (instruction j of an entry: float4s 64j .. 64j + 63, one per lane)
-    int npf = uni(d.npf);
-    if (npf > 0) {
-        for (int e = 0; e < npf; e++) {
-            const float* src = uni_ptr(d.pf[e].g) + r * uni_ll(d.pf[e].stride);
-            int n4 = uni(d.pf[e].n) >> 2, plds = uni(d.pf[e].lds);
-            for (int j = wave; 64 * j < n4; j += 4) {
-                int c = 64 * j + lane;
-                if (c < n4)
-                    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + 4 * c),
-                                                     (__attribute__((address_space(3))) void*)(lds + plds + 256 * j),
-                                                     16, 0, 0);
-            }
+    KDw hd = kdw_load(0, lane);
+    f4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (tid < ND4) dv = ((const f4*)(const void*)__builtin_amdgcn_kernarg_segment_ptr())[tid];
+    int nops = hd[0], npf = hd[1];
+#pragma unroll
+    for (int e = 0; e < SLM_ROW_PF; e++) {
+        if (e >= npf) break;
+        const float* src = (const float*)hd.q64(PF0 + PFW * e) + r * hd.q64(PF0 + PFW * e + 2);
+        int n4 = hd[PF0 + PFW * e + 4] >> 2, plds = hd[PF0 + PFW * e + 5];
+        for (int j = wave; 64 * j < n4; j += 4) {
+            int c = 64 * j + lane;
+            if (c < n4)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + 4 * c),
+                                                 (__attribute__((address_space(3))) void*)(lds + plds + 256 * j),
+                                                 16, 0, 0);
         }
-        vm_wait<0>();
-        lds_barrier();
     }
+    // a first op that folds at most 8 split partials of a row of at most 1024 floats (float4s):
+    // this thread's partials, in registers
+    constexpr int FOLD_PRE = 8;
+    constexpr int OK = O0 + (int)(offsetof(RowOp, kind) / 4), ON = O0 + (int)(offsetof(RowOp, n) / 4);
+    constexpr int OI0 = O0 + (int)(offsetof(RowOp, i0) / 4), OV = O0 + (int)(offsetof(RowOp, vec) / 4);
+    constexpr int OAG = O0 + (int)(offsetof(RowOp, a) / 4), OQ0 = O0 + (int)(offsetof(RowOp, q0) / 4);
+    static_assert(offsetof(RowIn, g) == 0 && offsetof(RowIn, stride) == 8, "RowIn layout");
+    f4 fpre[FOLD_PRE];
+    bool early = nops > 0 && hd[OK] == R_FOLD && hd[OV] && hd[ON] <= 1024 && hd[OI0] <= FOLD_PRE;
+    if (early) {
+        int nf = hd[ON], nz = hd[OI0], i = 4 * tid;
+        const float* pp = (const float*)hd.q64(OAG) + r * hd.q64(OAG + 2) + i;
+        long long q0 = hd.q64(OQ0);
+#pragma unroll
+        for (int z = 0; z < FOLD_PRE; z++)
+            if (z < nz && i < nf) fpre[z] = *(const f4*)(pp + z * q0);
+    }
+    if (tid < ND4) ((f4*)&d)[tid] = dv;
+    vm_wait<0>();
+    __syncthreads();
     for (int k = 0; k < nops; k++) {
         const RowOp o = row_load(d.op[k]);
         int kind = o.kind, n = o.n;
@@ -3233,7 +3253,18 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
                 }
             }
         } else if (kind == R_FOLD) {
-            if (o.vec) {
+            if (k == 0 && early) {  // the partials are in registers
+                int i = 4 * tid;
+                if (i < n) {
+                    f4 v = fpre[0];
+#pragma unroll
+                    for (int z = 1; z < FOLD_PRE; z++)
+                        if (z < o.i0)
+#pragma unroll
+                            for (int e = 0; e < 4; e++) v[e] = v[e] + fpre[z][e];
+                    row_put4(lds, o, yr, i, v);
+                }
+            } else if (o.vec) {
                 for (int b0 = 0; b0 < n; b0 += 4 * 256) {
                     int i = b0 + 4 * tid;
                     if (i >= n) continue;
