@@ -2082,6 +2082,14 @@ int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fus
                 fprintf(stderr, " pf%d]", d->npf);
                 continue;
             }
+            if (out[k].f == K.rows) {
+                const RowDesc* d = (const RowDesc*)out[k].blob;
+                fprintf(stderr, " rows[");
+                for (int q = 0; q < d->nops; q++)
+                    fprintf(stderr, "%s%d:%d%s", q ? "," : "", d->op[q].kind, d->op[q].n, d->op[q].y ? "w" : "");
+                fprintf(stderr, " pf%d]", d->npf);
+                continue;
+            }
             auto it = c->fname.find(out[k].f);
             if (it != c->fname.end()) nm = it->second.c_str() + (it->second.rfind("slm_", 0) == 0 ? 4 : 0);
             fprintf(stderr, " %s", nm);
