@@ -1891,7 +1891,7 @@ __device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ 
     // accumulator registers r = s of the tile's four segment waves, lane for lane (lane i of
     // every one of them holds column i), with the column's (m, l) of each segment
     f4* X = (f4*)lds;                                       // [wave][r][lane]: o[0..3][r]
-    float2* Y = (float2*)(lds + 4 * 16 * 4 * 64);           // [wave][lane]: (m, l)
+    float2* Y = (float2*)(lds + 4 * (SLM_SB_SEGS * ATTN_QG) * 4 * 64);  // [wave][lane]: (m, l)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         f4 v = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1901,42 +1901,47 @@ __device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ 
     }
     Y[wave * 64 + lane] = float2{mo, lo};
     __syncthreads();
-    f4 xv[SLM_SB_SEGS];
-    float2 ml[SLM_SB_SEGS];
+    // (with fewer than four segment waves a tile, each takes the registers r = s, s + SEGS, ..)
+    static_assert(4 % SLM_SB_SEGS == 0, "accumulator registers over the segment waves");
 #pragma unroll
-    for (int w = 0; w < SLM_SB_SEGS; w++) {
-        xv[w] = X[((qt * SLM_SB_SEGS + w) * 4 + seg) * 64 + lane];
-        ml[w] = Y[(qt * SLM_SB_SEGS + w) * 64 + lane];
-    }
-    float FM = NEG_INF, FL = 0.0f;
-    f4 FO = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int r = seg; r < 4; r += SLM_SB_SEGS) {
+        f4 xv[SLM_SB_SEGS];
+        float2 ml[SLM_SB_SEGS];
 #pragma unroll
-    for (int w = 0; w < SLM_SB_SEGS; w++) {
-        float mB = ml[w].x, lB = ml[w].y;
-        if (lB == 0.0f) continue;
-        if (FL == 0.0f) {
-            FM = mB;
-            FL = lB;
-            FO = xv[w];
-            continue;
+        for (int w = 0; w < SLM_SB_SEGS; w++) {
+            xv[w] = X[((qt * SLM_SB_SEGS + w) * 4 + r) * 64 + lane];
+            ml[w] = Y[(qt * SLM_SB_SEGS + w) * 64 + lane];
         }
-        float mn = fmaxf(FM, mB);
-        float a = expf(FM - mn), b = expf(mB - mn);
-        FL = FL * a + lB * b;
+        float FM = NEG_INF, FL = 0.0f;
+        f4 FO = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) FO[dt] = FO[dt] * a + xv[w][dt] * b;
-        FM = mn;
-    }
-    if (col.valid) {
-        float* P = part + (((long long)z * m + col.qidx) * heads + col.head) * (long long)(DP + 2);
-        if (g == 0 && seg == 0) {
-            P[0] = FM;
-            P[1] = FL;
+        for (int w = 0; w < SLM_SB_SEGS; w++) {
+            float mB = ml[w].x, lB = ml[w].y;
+            if (lB == 0.0f) continue;
+            if (FL == 0.0f) {
+                FM = mB;
+                FL = lB;
+                FO = xv[w];
+                continue;
+            }
+            float mn = fmaxf(FM, mB);
+            float a = expf(FM - mn), b = expf(mB - mn);
+            FL = FL * a + lB * b;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) FO[dt] = FO[dt] * a + xv[w][dt] * b;
+            FM = mn;
         }
+        if (col.valid) {
+            float* P = part + (((long long)z * m + col.qidx) * heads + col.head) * (long long)(DP + 2);
+            if (g == 0 && r == 0) {
+                P[0] = FM;
+                P[1] = FL;
+            }
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            int dd = pq_dim<DT>(dt, seg, g);
-            if (FULL || dd < dh) P[2 + dd] = FO[dt];
+            for (int dt = 0; dt < DT; dt++) {
+                int dd = pq_dim<DT>(dt, r, g);
+                if (FULL || dd < dh) P[2 + dd] = FO[dt];
+            }
         }
     }
 }
