@@ -1267,6 +1267,23 @@ KERNEL void __launch_bounds__(256) slm_gemm2_48(float* y, float* part, const flo
                                                 const float* x, int rows, int cols, int m) {
     gemm2_body<48, 4, false, false, 0, false, 1, 1>(y, part, w, x, rows, cols, m);
 }
+// the same tiles in fp16 mode (fp16 operands; ..w: fp16 weights)
+KERNEL void __launch_bounds__(512) slm_gemm2hk_16(float* y, float* part, const float* w,
+                                                  const float* x, int rows, int cols, int m) {
+    gemm2_body<16, 4, true, false, 0, false, 2, 1>(y, part, w, x, rows, cols, m);
+}
+KERNEL void __launch_bounds__(512) slm_gemm2hwk_16(float* y, float* part, const float* w,
+                                                   const float* x, int rows, int cols, int m) {
+    gemm2_body<16, 4, true, false, 0, true, 2, 1>(y, part, w, x, rows, cols, m);
+}
+KERNEL void __launch_bounds__(256) slm_gemm2h_48(float* y, float* part, const float* w,
+                                                 const float* x, int rows, int cols, int m) {
+    gemm2_body<48, 4, true, false, 0, false, 1, 1>(y, part, w, x, rows, cols, m);
+}
+KERNEL void __launch_bounds__(256) slm_gemm2hw_48(float* y, float* part, const float* w,
+                                                  const float* x, int rows, int cols, int m) {
+    gemm2_body<48, 4, true, false, 0, true, 1, 1>(y, part, w, x, rows, cols, m);
+}
 GEMM2(64, 16)
 GEMM2(96, 8)
 GEMM2(128, 16)

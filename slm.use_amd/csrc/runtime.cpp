@@ -123,6 +123,7 @@ struct Kernels {
     hipFunction_t attn_pq[3];                // prompt attention, superblock shared in LDS
     hipFunction_t gemm2k_32, gemm2k_16;      // 32- and 16-row tiles, two slice groups (fp32)
     hipFunction_t gemm2_48;                  // 48-row tiles, four waves of three row blocks
+    hipFunction_t gemm2hk_16, gemm2hwk_16, gemm2h_48, gemm2hw_48;  // the same in fp16 mode
 };
 
 }  // namespace
@@ -488,22 +489,21 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
         if (ns > 1 && (int64_t)c->gpart_bytes < ns * m * rows * 4)
             return fail(c, SLM_E_INVALID, "linear: no room for %lld split partials", (long long)ns);
         if (cols % 64 == 0) {
-            int bm = gemm2_bm(rows, m, ns);
+            // the tile rows by the chip's fill (in fp16 mode 32-row tiles run as 48: the slice
+            // groups of 32 rows are fp32 only)
+            int bm = gemm2_bm_plain(rows, m, ns);
+            if (bm == 32 && h) bm = 48;
             uint32_t shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * (w16 ? 32 : 64) + 64 * 64) * 4);
-            uint32_t threads = gemm2_threads(bm);
-            hipFunction_t f = bm == 32 ? k.gemm2_32 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
-            if (h) f = bm == 32 ? k.gemm2h_32 : bm == 64 ? k.gemm2h_64 : bm == 96 ? k.gemm2h_96 : k.gemm2h_128;
-            if (w16) f = k.gemm2hw[bm == 32 ? 0 : bm == 64 ? 1 : bm == 96 ? 2 : 3];
-            if (!h && !w16) {  // fp32: the tile rows by the chip's fill
-                bm = gemm2_bm_plain(rows, m, ns);
-                shmem = (uint32_t)(GEMM_STAGES_HOST * (bm * 64 + 64 * 64) * 4);
-                threads = bm == 48 ? 256 : gemm2_threads(bm);
-                f = bm == 48 ? k.gemm2_48 : bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
-                if (bm <= 32) {  // two slice groups: twice the MFMA chains per SIMD
-                    f = bm == 16 ? k.gemm2k_16 : k.gemm2k_32;
-                    shmem *= 2;
-                    threads = 512;
-                }
+            uint32_t threads = bm == 48 ? 256 : gemm2_threads(bm);
+            hipFunction_t f;
+            if (bm == 48) f = w16 ? k.gemm2hw_48 : h ? k.gemm2h_48 : k.gemm2_48;
+            else if (w16) f = k.gemm2hw[bm == 64 ? 1 : bm == 96 ? 2 : 3];
+            else if (h) f = bm == 64 ? k.gemm2h_64 : bm == 96 ? k.gemm2h_96 : k.gemm2h_128;
+            else f = bm == 64 ? k.gemm2_64 : bm == 96 ? k.gemm2_96 : k.gemm2_128;
+            if (bm <= 32) {  // two slice groups: twice the MFMA chains per SIMD
+                f = bm == 16 ? (w16 ? k.gemm2hwk_16 : h ? k.gemm2hk_16 : k.gemm2k_16) : k.gemm2k_32;
+                shmem *= 2;
+                threads = 512;
             }
             out.push_back(mk(f, (uint32_t)((rows + bm - 1) / bm), (uint32_t)((m + 63) / 64),
                              (uint32_t)ns, threads, shmem, p[0], c->gpart,
@@ -2326,7 +2326,9 @@ int load_kernels(slm_hip* c) {
                {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
                {&k.gemm2_32, "slm_gemm2_32"},   {&k.gemm2_64, "slm_gemm2_64"},
                {&k.gemm2k_32, "slm_gemm2k_32"}, {&k.gemm2k_16, "slm_gemm2k_16"},
-               {&k.gemm2_48, "slm_gemm2_48"},
+               {&k.gemm2_48, "slm_gemm2_48"},   {&k.gemm2hk_16, "slm_gemm2hk_16"},
+               {&k.gemm2hwk_16, "slm_gemm2hwk_16"}, {&k.gemm2h_48, "slm_gemm2h_48"},
+               {&k.gemm2hw_48, "slm_gemm2hw_48"},
                {&k.gemm2_96, "slm_gemm2_96"},   {&k.gemm2_128, "slm_gemm2_128"},
                {&k.gemm2h_32, "slm_gemm2h_32"}, {&k.gemm2h_64, "slm_gemm2h_64"},
                {&k.gemm2h_96, "slm_gemm2h_96"}, {&k.gemm2h_128, "slm_gemm2h_128"},
