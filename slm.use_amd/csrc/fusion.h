@@ -28,6 +28,7 @@
 #define SLM_SB_SEGS 4          // 64-key attention segments per superblock
 #define SLM_SB_KEYS (64 * SLM_SB_SEGS)
 #define SLM_GLA_T 32           // tokens per LDS stage of the prompt GLA kernel
+#define SLM_GLA_COLS 16        // state columns per workgroup of the prompt GLA kernel (16 lanes each)
 #define SLM_FG_MISC (32 + 4 * SLM_PF_MAX)  // LDS floats of slm_fg's scalars and prefetch table
 #define SLM_SIG_OPS 7          // prologue ops a signature can name
 // The signature of a prologue of kinds k0, k1, ...: what FgDesc.sig holds.

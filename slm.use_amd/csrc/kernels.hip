@@ -411,15 +411,35 @@ __device__ __forceinline__ float gla_rows_full(float (&st)[RPL], const float* kk
     return part;
 }
 
-// The prompt kernel: grid (heads, column groups of 16); each workgroup stages q and k of
-// its head and v of its columns for SLM_GLA_T tokens at a time in LDS.
+// One token's operands for a lane of the prompt kernel's pipelined path: its RPL rows of k
+// and q and the column's v.
+template <int RPL>
+struct GlaOps {
+    float k[RPL], q[RPL], v;
+};
+// gla_rows_full's expressions on operands already in registers.
+template <int RPL>
+__device__ __forceinline__ float gla_step(float (&st)[RPL], const GlaOps<RPL>& o, float dc) {
+    float part = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPL; rr++) {
+        st[rr] = dc * st[rr] + o.k[rr] * o.v;
+        part = part + o.q[rr] * st[rr];
+    }
+    return part;
+}
+
+// The prompt kernel: grid (heads, groups of SLM_GLA_COLS columns), one wave a workgroup (so a
+// CU's LDS serves one wave's reads); each workgroup stages q and k of its head and v of its
+// columns for SLM_GLA_T tokens at a time in LDS.
 template <int RPL>
 __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                          const float* __restrict__ q, const float* __restrict__ k,
                          const float* __restrict__ v, const float* __restrict__ decay,
                          const float* __restrict__ bias, int m, int heads, int dh, int vec) {
-    extern __shared__ __attribute__((aligned(16))) float lds[];  // 2 x ([SLM_GLA_T][q (dh) | k (dh) | v (16)], then [SLM_GLA_T] d)
-    int h = blockIdx.x, c0 = blockIdx.y * 16, tid = threadIdx.x, nt = blockDim.x;
+    extern __shared__ __attribute__((aligned(16))) float lds[];  // 2 x ([SLM_GLA_T][q (dh) | k (dh) | v (SLM_GLA_COLS)], then [SLM_GLA_T] d)
+    constexpr int NC = SLM_GLA_COLS;
+    int h = blockIdx.x, c0 = blockIdx.y * NC, tid = threadIdx.x, nt = blockDim.x;
     int b = c0 + (tid >> 4), j = tid & 15;
     bool live = b < dh;
     float* Sh = S + (long long)h * dh * dh;
@@ -430,38 +450,75 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
         st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
     }
     float bh = bias[h];
-    bool full = 16 * RPL == dh && c0 + 16 <= dh;  // uniform
-    int rowl = 2 * dh + 16, bufl = SLM_GLA_T * (rowl + 1);
+    bool full = 16 * RPL == dh && c0 + NC <= dh;  // uniform
+    int rowl = 2 * dh + NC, bufl = SLM_GLA_T * (rowl + 1);
     // Two LDS buffers of SLM_GLA_T token rows (then their decays): the next group's rows are
     // copied straight into one (and its decay inputs loaded into registers) while the
     // tokens of the other run. Thread tid copies piece pc (of `vec` floats) of tokens
     // tt0, tt0 + tpar, ...: piece tid·vec of the buffer, so a wave's copies are contiguous.
+    // (A row longer than the workgroup, lpt > nt: thread tid copies pieces tid, tid + nt, ...
+    // of every token instead.)
     int lpt = rowl / vec, tpar = max(1, nt / lpt);
     int tt0 = tid / lpt, pc = (tid % lpt) * vec;
     bool loader = tid < tpar * lpt;
-    const float* src0 = q + (long long)h * dh;  // (a piece past the head's columns copies q)
-    if (pc < dh) src0 = q + (long long)h * dh + pc;
-    else if (pc < 2 * dh) src0 = k + (long long)h * dh + pc - dh;
-    else if (c0 + pc - 2 * dh < dh) src0 = v + (long long)h * dh + c0 + pc - 2 * dh;
+    auto piece_src = [&](int pf) {  // token 0's source of the piece at float pf of a row
+        const float* sp = q + (long long)h * dh;  // (a piece past the head's columns copies q)
+        if (pf < dh) sp = q + (long long)h * dh + pf;
+        else if (pf < 2 * dh) sp = k + (long long)h * dh + pf - dh;
+        else if (c0 + pf - 2 * dh < dh) sp = v + (long long)h * dh + c0 + pf - 2 * dh;
+        return sp;
+    };
+    const float* src0 = piece_src(pc);
     int wbase = (tid & ~63) * vec;  // this wave's first piece
+    auto copy = [&](const float* src, float* dst) {
+        if (vec == 4)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                             (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                             (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+    };
     auto issue = [&](int i0, int buf) {
         int nt_tok = min(SLM_GLA_T, m - i0);
         float* base = lds + buf * bufl + wbase;
-        for (int kk = 0; kk * tpar < SLM_GLA_T; kk++) {
-            int tt = tt0 + kk * tpar;
-            if (!loader || tt >= nt_tok) continue;
-            const float* src = src0 + (long long)(i0 + tt) * heads * dh;
-            if (vec == 4)
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                                 (__attribute__((address_space(3))) void*)(base + kk * tpar * rowl), 16, 0, 0);
-            else
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                                 (__attribute__((address_space(3))) void*)(base + kk * tpar * rowl), 4, 0, 0);
+        if (lpt > nt) {
+            for (int tt = 0; tt < nt_tok; tt++)
+                for (int r = 0; r * nt < lpt; r++)
+                    if (r * nt + tid < lpt)
+                        copy(piece_src((r * nt + tid) * vec) + (long long)(i0 + tt) * heads * dh,
+                             base + tt * rowl + r * nt * vec);
+            return;
         }
+        if (!loader) return;
+        // tokens tt0, tt0 + tpar, ...: the source and destination advance by fixed strides
+        const float* src = src0 + (long long)(i0 + tt0) * heads * dh;
+        const long long sstep = (long long)tpar * heads * dh;
+        float* dst = base;
+        const int dstep = tpar * rowl;
+        if (vec == 4)
+            for (int tt = tt0; tt < nt_tok; tt += tpar, src += sstep, dst += dstep)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                                 (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        else
+            for (int tt = tt0; tt < nt_tok; tt += tpar, src += sstep, dst += dstep)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                                 (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
     };
     float dnext = 0.0f;  // thread tt: the decay input of token tt of the next group
     issue(0, 0);
     if (tid < min(SLM_GLA_T, m)) dnext = decay[(long long)tid * heads + h];
+    // The outputs of a pipelined group's last eight tokens are stored only after the next
+    // group's copies are issued, so that the wait for those copies does not also wait for
+    // stores issued just before it.
+    float pend[8];
+    float* pend_y = nullptr;  // (the first of the eight tokens' outputs of this lane's column)
+    const int ys = heads * dh;  // token stride of y
+    auto store_pend = [&]() {
+        if (pend_y && j == 0)
+#pragma unroll
+            for (int u = 0; u < 8; u++) pend_y[u * ys] = pend[u];
+        pend_y = nullptr;
+    };
     for (int i0 = 0, buf = 0; i0 < m; i0 += SLM_GLA_T, buf ^= 1) {
         int nt_tok = min(SLM_GLA_T, m - i0);
         const float* rows = lds + buf * bufl;
@@ -475,8 +532,100 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
             issue(i0 + SLM_GLA_T, buf ^ 1);
             if (tid < min(SLM_GLA_T, m - i0 - SLM_GLA_T)) dnext = decay[(long long)(i0 + SLM_GLA_T + tid) * heads + h];
         }
+        store_pend();
         // eight tokens at a time: their state updates in order, then their eight column
         // sums side by side (no token's sum waits for the next token's update)
+        if constexpr (RPL <= 8) if (full && nt_tok == SLM_GLA_T) {
+            // every lane's rows inside the head (dh = 16·RPL), every column live, a whole
+            // group: the operands of token t + 2 are read from LDS while token t runs (four
+            // register sets in turn), so no token waits for its reads; each read is a lane
+            // base plus a constant offset
+            constexpr int DH = 16 * RPL, ROWL = 2 * DH + NC;
+            const float* qb = rows + j * RPL;
+            const float* vb = rows + 2 * DH + (b - c0);
+            // LDS reads per token (k and q rows, v); a token's reads are in once at most the two
+            // later tokens' reads are pending
+            constexpr int GLA_NRD = (RPL % 4 == 0 ? RPL / 2 : 2 * RPL) + 1;
+            constexpr int GLA_WAIT = 2 * GLA_NRD < 15 ? 2 * GLA_NRD : 15;
+            GlaOps<RPL> ops[4];
+            auto load = [&](GlaOps<RPL>& o, int t) {
+                if constexpr (RPL % 4 == 0) {
+#pragma unroll
+                    for (int c = 0; c < RPL / 4; c++) {
+                        f4 ka = *(const f4*)(qb + t * ROWL + DH + 4 * c), qa = *(const f4*)(qb + t * ROWL + 4 * c);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            o.k[4 * c + e] = ka[e];
+                            o.q[4 * c + e] = qa[e];
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int rr = 0; rr < RPL; rr++) {
+                        o.k[rr] = qb[t * ROWL + DH + rr];
+                        o.q[rr] = qb[t * ROWL + rr];
+                    }
+                }
+                o.v = vb[t * ROWL];
+            };
+            // the group's decay factors, read once (four at a time: the decays start 16-byte
+            // aligned, as SLM_GLA_T is a multiple of 4)
+            static_assert(SLM_GLA_T % 8 == 0, "the prompt GLA runs whole blocks of eight tokens");
+            float dg[SLM_GLA_T];
+#pragma unroll
+            for (int t = 0; t < SLM_GLA_T; t += 4) {
+                f4 d4 = *(const f4*)(dcs + t);
+#pragma unroll
+                for (int e = 0; e < 4; e++) dg[t + e] = d4[e];
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // (nothing pending: the counts below are exact)
+#pragma unroll
+            for (int u = 0; u < 2; u++) load(ops[u], u);
+            // step t updates the state with token t and sums token t - 1 over the state that
+            // token left (the same expressions as gla_rows_full, in two halves that do not
+            // wait for each other)
+            float part[8];
+            float* yg = y + ((long long)i0 * heads + h) * dh + b;  // token i0's output, column b
+#pragma unroll
+            for (int t = 0; t <= SLM_GLA_T; t++) {
+                if (t < SLM_GLA_T) {
+                    // (past the group's last token the last row is read again, unused)
+                    load(ops[(t + 2) & 3], min(t + 2, SLM_GLA_T - 1));
+                    __builtin_amdgcn_s_waitcnt(0xC07F | (GLA_WAIT << 8));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                float sn[RPL];
+                if (t < SLM_GLA_T) {
+                    const GlaOps<RPL>& o = ops[t & 3];
+#pragma unroll
+                    for (int rr = 0; rr < RPL; rr++) sn[rr] = dg[t] * st[rr] + o.k[rr] * o.v;
+                }
+                if (t > 0) {
+                    const GlaOps<RPL>& o = ops[(t - 1) & 3];
+                    float pp = 0.0f;
+#pragma unroll
+                    for (int rr = 0; rr < RPL; rr++) pp = pp + o.q[rr] * st[rr];
+                    part[(t - 1) & 7] = pp;
+                }
+                if (t < SLM_GLA_T)
+#pragma unroll
+                    for (int rr = 0; rr < RPL; rr++) st[rr] = sn[rr];
+                __builtin_amdgcn_sched_barrier(0);
+                if (t > 0 && (t & 7) == 0) {
+#pragma unroll
+                    for (int u = 0; u < 8; u++) part[u] = gla_colsum0(part[u]);
+                    if (t == SLM_GLA_T) {
+#pragma unroll
+                        for (int u = 0; u < 8; u++) pend[u] = part[u];
+                        pend_y = yg + (t - 8) * ys;
+                    } else if (j == 0) {
+#pragma unroll
+                        for (int u = 0; u < 8; u++) yg[(t - 8 + u) * ys] = part[u];
+                    }
+                }
+            }
+            continue;
+        }
         for (int t0 = 0; t0 < nt_tok; t0 += 8) {
             int nu = min(8, nt_tok - t0);
             float part[8];
@@ -504,6 +653,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                     if (u < nu) y[((long long)(i0 + t0 + u) * heads + h) * dh + b] = part[u];
         }
     }
+    store_pend();
 #pragma unroll
     for (int rr = 0; rr < RPL; rr++) {
         int a = j * RPL + rr;
@@ -512,7 +662,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
 }
 
 #define GLA(R)                                                                          \
-    KERNEL void __launch_bounds__(256)                                                  \
+    KERNEL void __launch_bounds__(16 * SLM_GLA_COLS)                                    \
         slm_gla_##R(float* y, float* S, const float* q, const float* k, const float* v, \
                     const float* decay, const float* bias, int m, int heads, int dh,    \
                     int vec) {                                                          \

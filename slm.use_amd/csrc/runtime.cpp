@@ -652,11 +652,12 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                              p[2], p[3], (long long)n[0], (long long)n[1], (long long)n[2]));
             return SLM_OK;
         case OP_GLA: {  // p0 y, p1 s, p2 q, p3 k, p4 v, p5 decay, p6 bias; n0 m, n1 heads, n2 dh
-            // sixteen lanes per state column, sixteen columns per workgroup
+            // sixteen lanes per state column, SLM_GLA_COLS columns per workgroup
             int i = pow2_index((n[2] + 15) / 16, 4);
-            uint32_t shmem = (uint32_t)(2 * SLM_GLA_T * (2 * n[2] + 16 + 1) * 4);  // two token groups
+            uint32_t shmem = (uint32_t)(2 * SLM_GLA_T * (2 * n[2] + SLM_GLA_COLS + 1) * 4);  // two token groups
             int vec = (n[2] % 4 == 0 && aligned16(p[2]) && aligned16(p[3]) && aligned16(p[4])) ? 4 : 1;
-            out.push_back(mk(k.gla[i], (uint32_t)n[1], (uint32_t)((n[2] + 15) / 16), 1, 256, shmem,
+            out.push_back(mk(k.gla[i], (uint32_t)n[1], (uint32_t)((n[2] + SLM_GLA_COLS - 1) / SLM_GLA_COLS), 1,
+                             16 * SLM_GLA_COLS, shmem,
                              p[0], p[1], p[2], p[3], p[4], p[5], p[6], (int)n[0], (int)n[1],
                              (int)n[2], vec));
             return SLM_OK;

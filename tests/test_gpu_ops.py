@@ -195,7 +195,8 @@ def test_bounds_are_checked_before_launch(hip, pkg):
         hip.linear(dy.ptr, dw.ptr, 10, 4, dx.ptr, 3)  # x too short
 
 
-@pytest.mark.parametrize("m,heads,dh", [(1, 12, 64), (256, 12, 64), (37, 4, 8), (5, 2, 16)])
+@pytest.mark.parametrize("m,heads,dh", [(1, 12, 64), (256, 12, 64), (37, 4, 8), (5, 2, 16),
+                                        (300, 3, 16), (96, 2, 32), (70, 2, 128)])
 def test_gla(hip, m, heads, dh):
     q, k, v = rnd(m, heads, dh), rnd(m, heads, dh), rnd(m, heads, dh)
     q /= np.linalg.norm(q, axis=-1, keepdims=True)
@@ -220,6 +221,29 @@ def test_gla(hip, m, heads, dh):
         ys.append(dy1.read())
     assert np.array_equal(np.concatenate(ys), dy.read())
     assert np.array_equal(ds2.read(), ds.read())
+
+
+def test_gla_unaligned_inputs(hip):
+    """q, k and v one float past 16-byte alignment: the prompt kernel copies single floats,
+    more pieces per token row than the workgroup has threads."""
+    m, heads, dh = 45, 2, 64
+    q, k, v = rnd(m, heads, dh), rnd(m, heads, dh), rnd(m, heads, dh)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    dec, bias, s0 = rnd(m, heads), rnd(heads) - 3, rnd(heads, dh, dh, scale=0.1)
+    pads = [hip.upload(np.concatenate([np.zeros(1, np.float32), t.ravel()])) for t in (q, k, v)]
+    dd, db, ds = hip.upload(dec), hip.upload(bias), hip.upload(s0)
+    dy = hip.alloc(m * heads * dh)
+    hip.gla(dy.ptr, ds.ptr, pads[0].at(1), pads[1].at(1), pads[2].at(1), dd.ptr, db.ptr, m, heads, dh)
+    wy, wst = O.gla(s0, q, k, v, dec, bias, m, heads, dh)
+    assert rel(dy.read(), wy) < 2e-6
+    assert rel(ds.read(), wst) < 2e-6
+    # the same bits as from aligned inputs
+    al = [hip.upload(t) for t in (q, k, v)]
+    ds2, dy2 = hip.upload(s0), hip.alloc(m * heads * dh)
+    hip.gla(dy2.ptr, ds2.ptr, al[0].ptr, al[1].ptr, al[2].ptr, dd.ptr, db.ptr, m, heads, dh)
+    assert np.array_equal(dy.read(), dy2.read())
+    assert np.array_equal(ds.read(), ds2.read())
 
 
 ATTN_CASES = [
