@@ -146,6 +146,9 @@ struct slm_hip {
     size_t part_bytes = 0;
     float* gpart = nullptr;              // split partials of prompt GEMMs
     size_t gpart_bytes = 0;
+    std::vector<void*> retired;          // replaced internal buffers (launched work or cached
+                                         // graphs may still use them): freed at close
+    std::vector<void*> free_after_step;  // buffers freed while a step was recorded
     unsigned char* stage_host = nullptr; // eager staging: pinned ring copied into a device ring
     unsigned char* stage_dev = nullptr;
     size_t stage_head = 0;
@@ -2204,15 +2207,16 @@ int stage_pos(slm_hip* c, size_t pos, Op& o, int slot) {
     return SLM_OK;
 }
 
-// Reallocations of internal buffers happen between launches only: recorded work that
-// may point at the old buffer runs first, and graphs that do are dropped.
+// An internal buffer grows into a new allocation; the old one is kept until close, since
+// launched work and cached graphs may still use it (each for sizes it was big enough for),
+// so growing waits for nothing. A step being recorded keeps recording: its ops name these
+// buffers only when the step is planned, after every growth it asks for; an op lowered at
+// once lowers with its own partials' consumer (they share the buffer it saw).
 int internal_realloc(slm_hip* c, void** p, size_t bytes) {
-    TRY(taint(c));
-    drop_graphs(c);
-    HIPC(c, hipStreamSynchronize(c->stream));
-    if (*p) HIPC(c, hipFree(*p));
-    *p = nullptr;
-    HIPC(c, hipMalloc(p, bytes));
+    void* np = nullptr;
+    HIPC(c, hipMalloc(&np, bytes));
+    if (*p) c->retired.push_back(*p);
+    *p = np;
     return SLM_OK;
 }
 
@@ -2242,16 +2246,41 @@ int need_ws(slm_hip* c, size_t bytes) {
     return SLM_OK;
 }
 
+int finish_step_run(slm_hip* c);
+
+// Runs the recorded step, then frees what was freed while it was recorded (after its
+// kernels, and with the graphs that may name those buffers dropped).
+int finish_step(slm_hip* c) {
+    int rc = finish_step_run(c);
+    if (!c->free_after_step.empty()) {
+        drop_graphs(c);
+        hipError_t e = hipStreamSynchronize(c->stream);
+        for (void* p : c->free_after_step) {
+            c->halves.erase((uintptr_t)p);
+            hipFree(p);
+        }
+        c->free_after_step.clear();
+        if (!rc && e != hipSuccess) rc = fail(c, SLM_E_HIP, "free after step: %s", hipGetErrorString(e));
+    }
+    return rc;
+}
+
 // Captures the recorded step into a graph, or finds one that matches it; with graphs
 // off, plans the step and launches it directly.
-int finish_step(slm_hip* c) {
+int finish_step_run(slm_hip* c) {
     c->recording = false;
     if (c->tainted) {
         c->tainted = false;
         return SLM_OK;
     }
     TRY(upload_dyn(c));
-    if (!c->graphs_on) {
+    // Multi-token steps (prompt chunks) run planned but uncaptured: their kernels are long
+    // enough that replaying a graph saves nothing measurable, while capturing one (for each
+    // new buffer arrangement a chunk brings) costs about a millisecond.
+    bool multi = false;
+    for (const Op& o : c->ops)
+        if (o.kind == OP_LINEAR && o.n[2] > 1) { multi = true; break; }
+    if (!c->graphs_on || multi) {
         std::vector<Rec> recs;
         TRY(plan(c, c->ops, recs, c->fusion_on));
         return launch_all(c, recs);
@@ -2264,6 +2293,23 @@ int finish_step(slm_hip* c) {
             HIPC(c, hipGraphLaunch(g.exec, c->stream));
             c->n_launched++;
             return SLM_OK;
+        }
+    }
+    if (c->plan_trace) {  // what sets this step apart from a cached one of the same length
+        for (auto& g : c->cache) {
+            if (g.ops.size() != c->ops.size()) continue;
+            for (size_t i = 0; i < g.ops.size(); i++) {
+                const Op &a = g.ops[i], &b = c->ops[i];
+                if (std::memcmp(&a, &b, sizeof(Op)) == 0) continue;
+                int pi = -1, ni = -1;
+                for (int q = 0; q < 8 && pi < 0; q++) if (a.p[q] != b.p[q]) pi = q;
+                for (int q = 0; q < 10 && ni < 0; q++) if (a.n[q] != b.n[q]) ni = q;
+                fprintf(stderr, "slm graph miss: op %zu kind %u differs (p[%d] n[%d]: %lld vs %lld, dyn %s)\n",
+                        i, b.kind, pi, ni, ni >= 0 ? (long long)a.n[ni] : 0LL, ni >= 0 ? (long long)b.n[ni] : 0LL,
+                        a.dyn != b.dyn ? "differs" : "same");
+                break;
+            }
+            if (g.ndyn != c->dyn.size()) fprintf(stderr, "slm graph miss: dyn bytes %zu vs %zu\n", g.ndyn, c->dyn.size());
         }
     }
     std::vector<Rec> recs;
@@ -2451,6 +2497,8 @@ void slm_hip_close(slm_hip* c) {
     if (c->pick) hipFree(c->pick);
     if (c->part) hipFree(c->part);
     if (c->gpart) hipFree(c->gpart);
+    for (void* r : c->retired) hipFree(r);
+    for (void* r : c->free_after_step) hipFree(r);
     collect_timing(c);
     for (auto e : c->ev_pool) hipEventDestroy(e);
     if (c->stage_dev) hipFree(c->stage_dev);
@@ -2509,6 +2557,13 @@ int slm_hip_free(slm_hip* c, float* p) {
     if (!p) return SLM_OK;
     auto it = c->allocs.find((uintptr_t)p);
     if (it == c->allocs.end()) return fail(c, SLM_E_BOUNDS, "free: %p was not allocated here", (void*)p);
+    if (recording(c)) {
+        // (an output growing inside a step, cuda.rs:122-127) the step keeps recording: ops
+        // recorded before may still name the buffer, so it is freed once the step has run
+        c->allocs.erase(it);
+        c->free_after_step.push_back(p);  // (its fp16 mark, if any, goes with the free)
+        return SLM_OK;
+    }
     TRY(taint(c));
     drop_graphs(c);
     c->allocs.erase(it);
