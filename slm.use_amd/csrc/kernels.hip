@@ -346,12 +346,14 @@ __device__ __forceinline__ float gla_colsum(float p) {
 
 // The same total in the column's first lane only (what the prompt kernel stores): distance
 // 4 and 8 through DPP row shifts (lane 16c + i reads lane 16c + i + n), so lane 16c adds the
-// same pairs in the same order as gla_colsum.
+// same pairs in the same order as gla_colsum. (Lanes whose source is past the row read zero,
+// bound_ctrl, which lets each shift fuse into its add; only lane 16c's total is used, and its
+// sources are always inside the row.)
 __device__ __forceinline__ float gla_colsum0(float p) {
     p = p + dpp_xor1(p);
     p = p + dpp_xor2(p);
-    p = p + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x104, 0xF, 0xF, false));
-    p = p + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x108, 0xF, 0xF, false));
+    p = p + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x104, 0xF, 0xF, true));
+    p = p + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(p), 0x108, 0xF, 0xF, true));
     return p;
 }
 

@@ -574,14 +574,28 @@ def test_pick_fused_into_the_logits_gemv(hip, case, rows):
 
 
 ROW_CASES = ["attn_in", "attn_in_dead", "gla_in_dead", "mlp", "mlp_dead", "inplace", "overlap"]
+# the GEMM whose epilogue takes the dead ops over (fp16 mode: the same names with "2h")
+ROW_EPI_GEMM = {"attn_in_dead": ["slm_gemm2r_64"], "gla_in_dead": ["slm_gemm2n_64"],
+                "mlp_dead": [f"slm_gemm2s_{b}" for b in (32, 64, 96, 128)]}
 
 
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
 @pytest.mark.parametrize("m", [37, 256])
 @pytest.mark.parametrize("case", ROW_CASES)
-def test_row_chain(hip, case, m):
+def test_row_chain(hip, case, m, fp16):
     """A prompt chunk's element-wise ops fused into row chains give the bits of one launch
     per op, for in-place updates, operands read from an earlier op's output at an offset,
-    a shared vector read by every row and outputs overwritten later in the chain."""
+    a shared vector read by every row and outputs overwritten later in the chain; where the
+    ops after a GEMM are dead, that GEMM's epilogue kernel is the one that ran. In fp32 and
+    in fp16 mode."""
+    hip.set_fp16(fp16)
+    try:
+        _row_chain(hip, case, m, fp16)
+    finally:
+        hip.set_fp16(False)
+
+
+def _row_chain(hip, case, m, fp16):
     d, heads, dh, hid, cap, pos = 768, 12, 64, 3072, 4352, 100
     if case == "attn_in_dead":
         pos = cap - 20  # the ring slots wrap inside the chunk
@@ -680,18 +694,31 @@ def test_row_chain(hip, case, m):
             hip.copy(o["s"].ptr, o["y2"].ptr, m * d)
 
     got = []
-    for fuse in (True, False, True):  # the first pass grows the backend's buffers (a growth
-        o = outs()                     # ends the recorded step early)
+    for fuse in (True, False, True):  # (the first pass grows the backend's buffers)
+        o = outs()
         hip.set_fusion(fuse)
-        hip.rope_table(cs.ptr, sn.ptr, inv.ptr, pos, m, 32)
-        body(o)
-        hip.flush()
-        plan = hip.last_plan()
-        hip.set_fusion(True)
+        last = len(got) == 2
+        if last:  # eager launches, counted by kernel
+            hip.set_graphs(False)
+            hip.set_timing(True)
+        try:
+            hip.rope_table(cs.ptr, sn.ptr, inv.ptr, pos, m, 32)
+            body(o)
+            hip.flush()
+            plan = hip.last_plan()
+            epi = sum(hip.kernel_stat(n.replace("gemm2", "gemm2h") if fp16 else n)["launches"]
+                      for n in ROW_EPI_GEMM.get(case, [])) if last else 0
+        finally:
+            hip.set_fusion(True)
+            if last:
+                hip.set_timing(False)
+                hip.set_graphs(True)
         got.append(({k: b.read() for k, b in o.items()}, plan))
     _, (a, pa), (b, pb) = got
     print(case, m, "unfused", pa, "fused", pb)
     assert pb["kernels"] < pa["kernels"]
+    if case in ROW_EPI_GEMM:
+        assert epi == 1, (case, m, fp16, epi)
     for k in a:
         assert np.array_equal(a[k], b[k]), (case, m, k, float(np.abs(a[k] - b[k]).max()))
 
