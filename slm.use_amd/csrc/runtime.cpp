@@ -149,6 +149,11 @@ struct slm_hip {
     std::vector<void*> retired;          // replaced internal buffers (launched work or cached
                                          // graphs may still use them): freed at close
     std::vector<void*> free_after_step;  // buffers freed while a step was recorded
+    struct Deferred {
+        hipEvent_t done;                 // recorded after the step that last used them
+        std::vector<void*> bufs;
+    };
+    std::vector<Deferred> deferred;      // ... freed once their event has completed
     unsigned char* stage_host = nullptr; // eager staging: pinned ring copied into a device ring
     unsigned char* stage_dev = nullptr;
     size_t stage_head = 0;
@@ -2248,20 +2253,50 @@ int need_ws(slm_hip* c, size_t bytes) {
 
 int finish_step_run(slm_hip* c);
 
-// Runs the recorded step, then frees what was freed while it was recorded (after its
-// kernels, and with the graphs that may name those buffers dropped).
-int finish_step(slm_hip* c) {
-    int rc = finish_step_run(c);
-    if (!c->free_after_step.empty()) {
-        drop_graphs(c);
-        hipError_t e = hipStreamSynchronize(c->stream);
-        for (void* p : c->free_after_step) {
+// Frees deferred buffers whose step has run (all of them, after a wait, with `wait`).
+void free_deferred(slm_hip* c, bool wait) {
+    for (size_t i = 0; i < c->deferred.size();) {
+        auto& d = c->deferred[i];
+        bool done = wait ? hipEventSynchronize(d.done) == hipSuccess : hipEventQuery(d.done) == hipSuccess;
+        if (!done && !wait) {
+            i++;
+            continue;
+        }
+        for (void* p : d.bufs) {
             c->halves.erase((uintptr_t)p);
             hipFree(p);
         }
-        c->free_after_step.clear();
-        if (!rc && e != hipSuccess) rc = fail(c, SLM_E_HIP, "free after step: %s", hipGetErrorString(e));
+        hipEventDestroy(d.done);
+        c->deferred.erase(c->deferred.begin() + (long)i);
     }
+}
+
+// Runs the recorded step. What was freed while it was recorded is freed once the step's
+// kernels have run (an event after them; the host does not wait). A cached graph that names
+// such a buffer is kept: it runs again only for an identical op list, whose ops the bounds
+// checks have already found inside live allocations.
+int finish_step(slm_hip* c) {
+    int rc = finish_step_run(c);
+    if (!c->free_after_step.empty()) {
+        {
+            slm_hip::Deferred d{nullptr, std::move(c->free_after_step)};
+            c->free_after_step.clear();
+            hipError_t e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+            if (e == hipSuccess) e = hipEventRecord(d.done, c->stream);
+            if (e != hipSuccess) {  // no event: wait here instead
+                if (d.done) hipEventDestroy(d.done);
+                hipStreamSynchronize(c->stream);
+                for (void* p : d.bufs) {
+                    c->halves.erase((uintptr_t)p);
+                    hipFree(p);
+                }
+                if (!rc) rc = fail(c, SLM_E_HIP, "free after step: %s", hipGetErrorString(e));
+            } else {
+                c->deferred.push_back(std::move(d));
+            }
+        }
+    }
+    if (!c->deferred.empty()) free_deferred(c, false);
     return rc;
 }
 
@@ -2499,6 +2534,7 @@ void slm_hip_close(slm_hip* c) {
     if (c->gpart) hipFree(c->gpart);
     for (void* r : c->retired) hipFree(r);
     for (void* r : c->free_after_step) hipFree(r);
+    free_deferred(c, true);
     collect_timing(c);
     for (auto e : c->ev_pool) hipEventDestroy(e);
     if (c->stage_dev) hipFree(c->stage_dev);
