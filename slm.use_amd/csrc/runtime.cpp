@@ -136,6 +136,15 @@ struct slm_hip {
     std::string err;
     char name[256] = {0};
     std::map<uintptr_t, size_t> allocs;  // live allocations: start -> bytes
+    // The memory behind slm_hip_alloc: blocks up to POOL_BLOCK_MAX bytes come out of slabs of
+    // POOL_SLAB bytes (hipMalloc itself takes 0.02-0.3 ms for 1-13 MB here, which a model
+    // growing its outputs inside a prompt would otherwise pay) and go back to a free list of
+    // their rounded size; larger ones are allocated directly.
+    std::vector<void*> slabs;
+    char* slab_cur = nullptr;
+    size_t slab_left = 0;
+    std::map<size_t, std::vector<void*>> pool_free;  // rounded bytes -> free blocks
+    std::map<uintptr_t, size_t> pooled;              // live pooled blocks: start -> rounded bytes
     std::map<uintptr_t, size_t> halves;  // the fp16 ones among them: start -> elements
     float* ws = nullptr;                 // attention partials
     size_t ws_bytes = 0;
@@ -2212,6 +2221,43 @@ int stage_pos(slm_hip* c, size_t pos, Op& o, int slot) {
     return SLM_OK;
 }
 
+constexpr size_t POOL_SLAB = (size_t)128 << 20, POOL_BLOCK_MAX = (size_t)32 << 20;
+
+hipError_t dev_alloc(slm_hip* c, size_t bytes, void** out) {
+    size_t rb = (bytes + 255) & ~(size_t)255;
+    if (rb > POOL_BLOCK_MAX) return hipMalloc(out, bytes);
+    auto f = c->pool_free.find(rb);
+    if (f != c->pool_free.end() && !f->second.empty()) {
+        *out = f->second.back();
+        f->second.pop_back();
+    } else {
+        if (c->slab_left < rb) {  // (the last slab's tail stays unused)
+            void* sl = nullptr;
+            hipError_t e = hipMalloc(&sl, POOL_SLAB);
+            if (e != hipSuccess) return hipMalloc(out, bytes);
+            c->slabs.push_back(sl);
+            c->slab_cur = (char*)sl;
+            c->slab_left = POOL_SLAB;
+        }
+        *out = c->slab_cur;
+        c->slab_cur += rb;
+        c->slab_left -= rb;
+    }
+    c->pooled[(uintptr_t)*out] = rb;
+    return hipSuccess;
+}
+
+// Gives back a dev_alloc block (no work may still use it).
+void dev_free(slm_hip* c, void* p) {
+    auto it = c->pooled.find((uintptr_t)p);
+    if (it == c->pooled.end()) {
+        hipFree(p);
+        return;
+    }
+    c->pool_free[it->second].push_back(p);
+    c->pooled.erase(it);
+}
+
 // An internal buffer grows into a new allocation; the old one is kept until close, since
 // launched work and cached graphs may still use it (each for sizes it was big enough for),
 // so growing waits for nothing. A step being recorded keeps recording: its ops name these
@@ -2264,7 +2310,7 @@ void free_deferred(slm_hip* c, bool wait) {
         }
         for (void* p : d.bufs) {
             c->halves.erase((uintptr_t)p);
-            hipFree(p);
+            dev_free(c, p);
         }
         hipEventDestroy(d.done);
         c->deferred.erase(c->deferred.begin() + (long)i);
@@ -2288,7 +2334,7 @@ int finish_step(slm_hip* c) {
                 hipStreamSynchronize(c->stream);
                 for (void* p : d.bufs) {
                     c->halves.erase((uintptr_t)p);
-                    hipFree(p);
+                    dev_free(c, p);
                 }
                 if (!rc) rc = fail(c, SLM_E_HIP, "free after step: %s", hipGetErrorString(e));
             } else {
@@ -2526,15 +2572,18 @@ void slm_hip_close(slm_hip* c) {
         hipFree(t.second.cos);
         hipFree(t.second.sin);
     }
-    for (auto& a : c->allocs) hipFree((void*)a.first);
+    for (auto& a : c->allocs)
+        if (!c->pooled.count(a.first)) hipFree((void*)a.first);
     if (c->ws) hipFree(c->ws);
     if (c->attn_ctr) hipFree(c->attn_ctr);
     if (c->pick) hipFree(c->pick);
     if (c->part) hipFree(c->part);
     if (c->gpart) hipFree(c->gpart);
     for (void* r : c->retired) hipFree(r);
-    for (void* r : c->free_after_step) hipFree(r);
+    for (void* r : c->free_after_step)
+        if (!c->pooled.count((uintptr_t)r)) hipFree(r);
     free_deferred(c, true);
+    for (void* sl : c->slabs) hipFree(sl);
     collect_timing(c);
     for (auto e : c->ev_pool) hipEventDestroy(e);
     if (c->stage_dev) hipFree(c->stage_dev);
@@ -2565,14 +2614,14 @@ int slm_hip_alloc(slm_hip* c, size_t n, float** out) {
     if (!c || !out) return SLM_E_INVALID;
     size_t bytes = std::max<size_t>(n, 1) * 4;
     float* p = nullptr;
-    hipError_t e = hipMalloc((void**)&p, bytes);
+    hipError_t e = dev_alloc(c, bytes, (void**)&p);
     if (e != hipSuccess) return fail(c, SLM_E_MEMORY, "alloc %zu floats: %s", n, hipGetErrorString(e));
     // zeroed on the stream now, ordered before any later use of the buffer (also before
     // the launches of a step being recorded, which run at flush)
     int rc = launch_now(c, mk(c->k.fill, blocks_for(bytes / 4), 1, 1, 256, 0, p,
                               (long long)(bytes / 4), 0.0f));
     if (rc) {
-        hipFree(p);
+        dev_free(c, p);
         return rc;
     }
     c->allocs[(uintptr_t)p] = bytes;
@@ -2605,7 +2654,7 @@ int slm_hip_free(slm_hip* c, float* p) {
     c->allocs.erase(it);
     c->halves.erase((uintptr_t)p);
     HIPC(c, hipStreamSynchronize(c->stream));
-    HIPC(c, hipFree(p));
+    dev_free(c, p);
     return SLM_OK;
 }
 
