@@ -2265,7 +2265,7 @@ void dev_free(slm_hip* c, void* p) {
 // once lowers with its own partials' consumer (they share the buffer it saw).
 int internal_realloc(slm_hip* c, void** p, size_t bytes) {
     void* np = nullptr;
-    HIPC(c, hipMalloc(&np, bytes));
+    HIPC(c, dev_alloc(c, bytes, &np));
     if (*p) c->retired.push_back(*p);
     *p = np;
     return SLM_OK;
@@ -2568,20 +2568,21 @@ void slm_hip_close(slm_hip* c) {
     if (c->stream) hipStreamSynchronize(c->stream);
     for (auto& g : c->cache)
         if (g.exec) hipGraphExecDestroy(g.exec);
+    auto release = [&](void* p) {  // (pooled blocks go with their slabs)
+        if (p && !c->pooled.count((uintptr_t)p)) hipFree(p);
+    };
     for (auto& t : c->tables) {
-        hipFree(t.second.cos);
-        hipFree(t.second.sin);
+        release(t.second.cos);
+        release(t.second.sin);
     }
-    for (auto& a : c->allocs)
-        if (!c->pooled.count(a.first)) hipFree((void*)a.first);
-    if (c->ws) hipFree(c->ws);
+    for (auto& a : c->allocs) release((void*)a.first);
+    release(c->ws);
     if (c->attn_ctr) hipFree(c->attn_ctr);
     if (c->pick) hipFree(c->pick);
-    if (c->part) hipFree(c->part);
-    if (c->gpart) hipFree(c->gpart);
-    for (void* r : c->retired) hipFree(r);
-    for (void* r : c->free_after_step)
-        if (!c->pooled.count((uintptr_t)r)) hipFree(r);
+    release(c->part);
+    release(c->gpart);
+    for (void* r : c->retired) release(r);
+    for (void* r : c->free_after_step) release(r);
     free_deferred(c, true);
     for (void* sl : c->slabs) hipFree(sl);
     collect_timing(c);
@@ -2681,8 +2682,8 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
         if (it->first >= (uintptr_t)dst && it->first < (uintptr_t)(dst + n)) {
             drop_graphs(c);
             hipStreamSynchronize(c->stream);
-            hipFree(it->second.cos);
-            hipFree(it->second.sin);
+            dev_free(c, it->second.cos);
+            dev_free(c, it->second.sin);
             it = c->tables.erase(it);
         } else {
             ++it;
