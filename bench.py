@@ -180,6 +180,24 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def window_note(cfg, h):
+    """What the timed positions do to the sliding-window rings (cap = window + 256 slots)."""
+    cap = cfg["window"] + 256
+    first, last = h["decode_from_pos"], h["decode_to_pos"]
+    full = "window full" if first >= cfg["window"] else f"window filling ({first} of {cfg['window']})"
+    if last < cap:
+        return f"{full}; positions {first}..{last}, below the {cap}-slot ring's wrap"
+    if first >= cap:
+        return f"{full}; positions {first}..{last}, the rings overwriting"
+    return f"{full}; positions {first}..{last}, the rings wrapping at {cap}"
+
+
+def under_profiler() -> bool:
+    """Is this process running under rocprofv3 (its tool library preloaded)?"""
+    return ("rocprofiler" in os.environ.get("LD_PRELOAD", "")
+            or any(k.startswith("ROCPROF") for k in os.environ))
+
+
 def run_loops(model, cfg, prompt, loops, warmup, steps):
     """The reference bench sequence at one loop count: 16 warm-up tokens, the timed prompt,
     untimed then timed greedy decode. Returns (prefill tok/s, decode tok/s, first timed
@@ -201,15 +219,17 @@ def run_loops(model, cfg, prompt, loops, warmup, steps):
     return len(prompt) / fill_s, steps / dec_s, pos0, ids, se
 
 
-def g86_leg(pkg, hip, synth):
+def g86_leg(pkg, hip, synth, device_grow=False):
     """Config C4: the g86 model (global layers with logn, kshift, emb, far, 4 key heads), a
     16384-token prompt at R = 4 in 256-token chunks (the global caches grow 8192 -> 16384 ->
-    32768), then 128 greedy decode steps."""
+    32768), then 128 greedy decode steps. The caches grow by model.rs:383-398's own sequence
+    (read, host relayout, upload inside the advance) or, with `device_grow`, by device
+    copies (the optional grow_cache trait method)."""
     cache = Path(os.environ.get("SLM_MODEL_CACHE", "/tmp")) / "slm_models"
     folder = synth.write_model(cache / "g86-4", "g86", 4)
     cfg = synth.G86
     prompt = synth.tokens(16384, cfg["vocab_size"], seed=6)
-    model = pkg.Model(hip, folder)
+    model = pkg.Model(hip, folder, device_grow=device_grow)
     se = model.session(4)
     t = time.perf_counter()
     se.feed(prompt, 256)
@@ -228,15 +248,18 @@ def g86_leg(pkg, hip, synth):
            "decode_tok_s": round(128 / dec_s, 1), "decode_from_pos": pos0,
            "decode_bytes_per_token": round(bpt),
            "decode_frac": round(bpt * 128 / dec_s / HBM_PEAK, 4),
-           "layers": "SG|LS|SG", "loops": 4}
+           "layers": "SG|LS|SG", "loops": 4,
+           "grow": ("device copies (grow_cache, an optional trait method)" if device_grow else
+                    "model.rs:383-398 as written: read + host relayout + upload inside the advance")}
     del se, model
     return out
 
 
 def fp16_leg(pkg, hip, folder, a, prompt, fl):
-    """The same workload in fp16 mode (the --fp16 analogue): the model loaded with fp16 mode on
-    stores its linear weights as fp16 (half the bytes); linears run fp16 operands at fp16
-    MFMAs with fp32 sums; attention, GLA, norms and states fp32."""
+    """The same workload in fp16 mode (the --fp16 analogue, slm_hip_set_fp16): the model uploads
+    fp32 weights through the trait as model.rs does; the backend's linears read fp16 copies of
+    them (half the bytes) with fp16 operands at fp16 MFMAs and fp32 sums; attention, GLA,
+    norms and states fp32."""
     hip.set_fp16(True)
     model = pkg.Model(hip, folder)
     s16 = model.session(a.loops)
@@ -257,9 +280,11 @@ def fp16_leg(pkg, hip, folder, a, prompt, fl):
     hip.set_fp16(False)
     fp16 = {"decode_tok_s": round(a.steps / dec16_s, 2), "prefill_tok_s": round(len(prompt) / fill16_s, 1),
             "prefill_tflops": round(fl / fill16_s / 1e12, 2),
-            "note": "linear weights stored as fp16 (slm_hip_alloc_half), operands at "
-                    "v_mfma_f32_16x16x16f16 (fp32 sums); attention, GLA, norms and states fp32; "
-                    "the bits of fp16 mode over fp32 weights; checked at 2e-2 vs the fp32 oracle (config C5)"}
+            "path": "the trait's calls unchanged: fp32 uploads, then slm_hip_set_fp16(1)",
+            "note": "linears read fp16 copies of the fp32 weights the backend makes on first use, "
+                    "operands at v_mfma_f32_16x16x16f16 (fp32 sums); attention, GLA, norms and "
+                    "states fp32; the bits of fp16 mode over the fp32 weights; checked at 2e-2 vs "
+                    "the fp32 oracle (config C5)"}
     log(f"fp16 mode: prefill {fp16['prefill_tok_s']} tok/s, decode {fp16['decode_tok_s']} tok/s")
     return fp16
 
@@ -309,6 +334,11 @@ def main():
     cfg = synth.A86
     prompt = synth.tokens(a.prompt, cfg["vocab_size"], seed=3)
 
+    if under_profiler() and not a.no_graphs:
+        # rocprofv3's kernel tracing of step-graph launches has crashed inside the profiler's
+        # own library here (twice); profiled runs launch the same kernels eagerly
+        log("under rocprofv3: step graphs off (--no-graphs)")
+        a.no_graphs = True
     hip = pkg.Hip(0)
     if a.no_graphs:
         hip.set_graphs(False)
@@ -337,7 +367,11 @@ def main():
     se = head_se
     tok_s = per_r[head]["decode_tok_s"]
     # the same greedy loop with the pick on the device (the logits stay on the GPU; each step's
-    # embedding gather reads the previous step's pick there): the opt-in fast path
+    # embedding gather reads the previous step's pick there): the opt-in fast path, after
+    # untimed steps of its own (its step graph's capture and first-call set-up)
+    if a.warmup:
+        se.decode_greedy_device(a.warmup)
+    se.logits()
     t = time.perf_counter()
     se.decode_greedy_device(a.steps)
     se.logits()
@@ -378,6 +412,10 @@ def main():
         log("g86: 16384-token prompt at R=4, then 128 decode steps ...")
         g86 = g86_leg(pkg, hip, synth)
         log(f"g86: prefill {g86['prefill_tok_s']} tok/s, decode {g86['decode_tok_s']} tok/s")
+        dg = g86_leg(pkg, hip, synth, device_grow=True)
+        g86["with_device_grow"] = {k: dg[k] for k in ("prefill_tok_s", "prefill_frac", "decode_tok_s",
+                                                      "decode_frac", "grow")}
+        log(f"g86 (device grow): prefill {dg['prefill_tok_s']} tok/s, decode {dg['decode_tok_s']} tok/s")
 
     cpu = None
     if not a.no_cpu:
@@ -405,8 +443,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic: seeded N(0,0.02) fp32 weights, uniform random token ids",
         "config": {"workload": f"a86 decode at R={head} after 16 + {len(prompt)} prompt tokens "
-                               f"(window full, rings wrapping past position 4352), greedy, "
-                               f"logits read back every token",
+                               f"({window_note(cfg, h)}), greedy, logits read back every token",
                    "loops": head, "d_model": 768, "heads": 12, "head_dim": 64,
                    "ffn": 3072, "vocab": 32000, "window": 4096, "layers": "SS|LS|SS",
                    "prompt_tokens": len(prompt), "decode_from_pos": h["decode_from_pos"]},

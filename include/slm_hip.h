@@ -171,11 +171,18 @@ int slm_hip_set_graphs(slm_hip* ctx, int on);
  * main.rs:421-423, where it selects Float16 for every MLX buffer): from this call on, every
  * linear rounds both operands to fp16 (to nearest even) at fp16 MFMAs and sums in fp32;
  * attention, GLA, norms and states stay fp32. A linear then needs a multiple of 64 columns
- * and 16-byte aligned weights and input (else SLM_E_UNSUPPORTED). */
+ * and 16-byte aligned weights and input (else SLM_E_UNSUPPORTED). Weights stay as uploaded
+ * (fp32, ops.rs:77); the first linear that reads a weight buffer in this mode keeps an fp16
+ * copy of it (the halves the mode rounds it to, so the same bits), which later linears read
+ * instead: half the weight bytes, as mlx.rs:61-63 uploads every buffer in its dtype. The copy
+ * is dropped when the buffer is freed, uploaded into or written by an operation. */
 int slm_hip_set_fp16(slm_hip* ctx, int on);
-/* Whether fp16 mode is on (the model twin stores its linear weights as fp16 when it is on at
- * load, as the reference's MLX backend stores every buffer in its dtype, mlx.rs:19-26). */
+/* Whether fp16 mode is on. */
 int slm_hip_get_fp16(slm_hip* ctx, int* on);
+/* The fp16 weight copies of fp16 mode (on by default; no trait counterpart, a measurement and
+ * test switch): off, fp16-mode linears read the fp32 weights and round them themselves (the
+ * same bits, twice the bytes), and the copies are freed. */
+int slm_hip_set_half_shadows(slm_hip* ctx, int on);
 /* Fusion (on by default): the planner lowers a recorded one-token step into fused
  * kernels (prologue vector ops + GEMV + epilogue) that compute the same values with the
  * same arithmetic as the per-op kernels. Off: one launch per operation. */
@@ -209,6 +216,10 @@ int slm_hip_probe_mfma(slm_hip* ctx, float* out, const float* a, const float* b)
 int slm_hip_set_spin_limit(slm_hip* ctx, long long polls);
 /* The context's hipStream_t, so a caller can time its work with HIP events. */
 int slm_hip_stream(slm_hip* ctx, void** out);
+/* Device memory (no trait counterpart; a diagnostic): the device's free and total bytes
+ * (hipMemGetInfo) and the bytes this context holds from the device — its pool slabs, its
+ * direct allocations and its internal buffers. */
+int slm_hip_mem_info(slm_hip* ctx, size_t* free_bytes, size_t* total_bytes, size_t* held_bytes);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,11 @@ const char* slm_model_error(const slm_model* m);
 size_t slm_model_params(const slm_model* m);
 /* Initial slots of global-layer caches (model.rs:320 uses 8192); for tests of grow. */
 int slm_model_set_global_cap(slm_model* m, size_t cap);
+/* How a global cache doubles (model.rs:383-398). 0 (the default): model.rs's own sequence —
+ * slm_hip_read of each cache inside the advance, the per-head relayout on the host, a fresh
+ * upload, the old buffer freed. 1: the relayout as device copies on the stream (the same
+ * contents; no host round trip). */
+int slm_model_set_device_grow(slm_model* m, int on);
 
 /* Model::session (model.rs:333-381); loops 0 takes the model's default (config.rs:96-105). */
 int slm_session_new(slm_model* m, size_t loops, slm_session** out);

@@ -103,11 +103,14 @@ _SIGS = {
     "slm_hip_probe_mfma": (_i, [_p, _p, _p, _p]),
     "slm_hip_set_spin_limit": (_i, [_p, C.c_longlong]),
     "slm_hip_stream": (_i, [_p, C.POINTER(_p)]),
+    "slm_hip_set_half_shadows": (_i, [_p, _i]),
+    "slm_hip_mem_info": (_i, [_p, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
     "slm_model_load": (_i, [_p, C.c_char_p, C.POINTER(_p)]),
     "slm_model_free": (None, [_p]),
     "slm_model_error": (C.c_char_p, [_p]),
     "slm_model_params": (_sz, [_p]),
     "slm_model_set_global_cap": (_i, [_p, _sz]),
+    "slm_model_set_device_grow": (_i, [_p, _i]),
     "slm_session_new": (_i, [_p, _sz, C.POINTER(_p)]),
     "slm_session_free": (None, [_p]),
     "slm_session_pos": (_sz, [_p]),
@@ -199,6 +202,11 @@ class Hip:
         b = self.alloc(a.size)
         self.check(lib.slm_hip_upload(self.ctx, b.ptr, _fp(a), a.size))
         return b
+
+    def upload_into(self, buf: Buffer, data, offset: int = 0):
+        """slm_hip_upload into an existing buffer, at `offset` floats."""
+        a = _f32(data).reshape(-1)
+        self.check(lib.slm_hip_upload(self.ctx, buf.at(offset), _fp(a), a.size))
 
     def upload_half(self, data) -> Buffer:
         """fp16 weights (slm_hip_alloc_half): `data` rounded to fp16; read() widens them back."""
@@ -329,6 +337,16 @@ class Hip:
         self.check(lib.slm_hip_stream(self.ctx, C.byref(s)))
         return s.value or 0
 
+    def set_half_shadows(self, on: bool):
+        """fp16 mode's fp16 copies of the weights its linears read (on by default)."""
+        self.check(lib.slm_hip_set_half_shadows(self.ctx, int(on)))
+
+    def mem_info(self):
+        """(free, total) bytes of the device and the bytes this context holds."""
+        f, t, h = _sz(), _sz(), _sz()
+        self.check(lib.slm_hip_mem_info(self.ctx, C.byref(f), C.byref(t), C.byref(h)))
+        return f.value, t.value, h.value
+
     def set_spin_limit(self, polls: int):
         """Polls a fused kernel's bounded wait makes before it gives up (0: at once)."""
         self.check(lib.slm_hip_set_spin_limit(self.ctx, polls))
@@ -340,7 +358,8 @@ class Hip:
 class Model:
     """The model twin (include/slm_model.h) on a Hip context."""
 
-    def __init__(self, hip: Hip, folder, global_cap: int | None = None):
+    def __init__(self, hip: Hip, folder, global_cap: int | None = None,
+                 device_grow: bool = False):
         import json
 
         self.hip = hip
@@ -352,6 +371,9 @@ class Model:
         self.h = h.value
         if global_cap is not None:
             self.check(lib.slm_model_set_global_cap(self.h, global_cap))
+        # grow global caches as model.rs:383-398 does (read, host relayout, upload) unless
+        # device_grow asks for the device-copy relayout
+        self.check(lib.slm_model_set_device_grow(self.h, int(device_grow)))
 
     def check(self, rc: int):
         if rc != SLM_OK:

@@ -84,6 +84,12 @@ KERNEL void slm_fill(float* __restrict__ y, long long n, float v) {
     GRID_LOOP(i, n) y[i] = v;
 }
 
+// fp32 -> fp16 to nearest even: the halves fp16 mode's linears round their weights to, kept
+// as a shadow copy of a weight buffer so those linears stream half the bytes.
+KERNEL void slm_to_half(_Float16* __restrict__ y, const float* __restrict__ x, long long n) {
+    GRID_LOOP(i, n) y[i] = (_Float16)x[i];
+}
+
 KERNEL void slm_add(float* __restrict__ y, const float* __restrict__ a,
                     const float* __restrict__ b, long long n) {
     GRID_LOOP(i, n) y[i] = a[i] + b[i];
@@ -2504,7 +2510,8 @@ __device__ __forceinline__ void wait_gave_up(int* fault, int lane) {
 // per barrier, then waits for (the GEMV waves meanwhile wait for their weights, not for
 // this). Only LDS is ordered by it. The wait gives up after `spin` polls (about a second at
 // the default), so a mistake cannot hang the GPU.
-__device__ __forceinline__ void esync(int* ctr, int& target, int nw, int spin, int* fault) {
+// Returns whether the wait gave up.
+__device__ __forceinline__ bool esync(int* ctr, int& target, int nw, int spin, int* fault) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     target += nw;
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -2512,15 +2519,21 @@ __device__ __forceinline__ void esync(int* ctr, int& target, int nw, int spin, i
     for (; it < spin; it++) {
         if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
     }
-    if (it >= spin) wait_gave_up(fault, threadIdx.x & 63);
+    bool gave_up = it >= spin;
+    if (gave_up) wait_gave_up(fault, threadIdx.x & 63);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    return gave_up;
 }
 
+// `failed` records that one of this wave's waits gave up: from then on what other waves
+// should have written to LDS before the barrier (the descriptor copy among it) may be
+// missing, so the caller stops using it.
 struct ESync {
     int* ctr;
     int target, nw, spin;
     int* fault;
-    __device__ __forceinline__ void operator()() { esync(ctr, target, nw, spin, fault); }
+    bool failed = false;
+    __device__ __forceinline__ void operator()() { failed |= esync(ctr, target, nw, spin, fault); }
 };
 
 // Sum of squares of in[0..size) in the order of dot16_self, run by one wave: lane l and

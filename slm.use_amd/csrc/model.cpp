@@ -303,14 +303,6 @@ class Ops {
         ok(slm_hip_upload(c_, b.p, data, n), "upload");
         return b;
     }
-    // fp16 weights (mlx.rs:62: upload in the backend's dtype): n values rounded to fp16
-    Buf upload_half(const float* data, size_t n) const {
-        Buf b;
-        ok(slm_hip_alloc_half(c_, n, &b.p), "upload");
-        b.n = std::max<size_t>(n, 1);
-        ok(slm_hip_upload(c_, b.p, data, n), "upload");
-        return b;
-    }
     void release(Buf& b) const {
         if (b.p) slm_hip_free(c_, b.p);
         b = Buf{};
@@ -472,14 +464,13 @@ struct slm_model {
     Ops ops;
     Config cfg;
     std::string error;
-    bool half = false;  // linear weights stored as fp16 (fp16 mode on at load)
     Mat embed;
-    Buf embed_h;        // (half) the embedding as fp16 weights of the logits linear
     std::vector<Block> prelude, core, coda;
     bool looped = false;
     Mat inject, loop_embed;
     Buf norm_f, inv_freq;
     size_t global_cap0 = 1u << 13;  // model.rs:320
+    bool device_grow = false;       // grow by device copies instead of model.rs's read + upload
     explicit slm_model(slm_hip* c) : ops(c) {}
 };
 
@@ -575,20 +566,20 @@ struct Weights {
     }
 };
 
-// model.rs:69-83: one tensor to the device, from the mapping (as fp16 with `half`).
-Buf upload_tensor(const Ops& ops, const Tensor& t, bool half = false) {
-    if (((uintptr_t)t.data & 3) == 0)
-        return half ? ops.upload_half((const float*)t.data, t.count) : ops.upload((const float*)t.data, t.count);
+// model.rs:69-83: one tensor to the device, from the mapping. Always fp32, as model.rs
+// uploads it (in fp16 mode the backend keeps fp16 shadows of the weights its linears read).
+Buf upload_tensor(const Ops& ops, const Tensor& t) {
+    if (((uintptr_t)t.data & 3) == 0) return ops.upload((const float*)t.data, t.count);
     std::vector<float> host(t.count);
     std::memcpy(host.data(), t.data, t.count * 4);
-    return half ? ops.upload_half(host.data(), t.count) : ops.upload(host.data(), t.count);
+    return ops.upload(host.data(), t.count);
 }
 
-Mat mat(const Ops& ops, Weights& w, const std::string& name, bool half = false) {
+Mat mat(const Ops& ops, Weights& w, const std::string& name) {
     Tensor t = w.take(name);
     if (t.shape.size() != 2) throw std::runtime_error(name + ": expected a matrix");
     Mat m;
-    m.w = upload_tensor(ops, t, half);
+    m.w = upload_tensor(ops, t);
     m.rows = t.shape[0];
     m.cols = t.shape[1];
     return m;
@@ -606,22 +597,22 @@ Block load_block(const Model& M, Weights& w, const std::string& prefix, char kin
     switch (kind) {
         case 'S':
             b.kind = WINDOW;
-            b.qkv = mat(ops, w, n("mixer.qkv.weight"), M.half);
-            b.o = mat(ops, w, n("mixer.o.weight"), M.half);
+            b.qkv = mat(ops, w, n("mixer.qkv.weight"));
+            b.o = mat(ops, w, n("mixer.o.weight"));
             break;
         case 'L':
             b.kind = LINEAR;
-            b.qkvg = mat(ops, w, n("mixer.qkvg.weight"), M.half);
-            b.decay = mat(ops, w, n("mixer.decay.weight"), M.half);
+            b.qkvg = mat(ops, w, n("mixer.qkvg.weight"));
+            b.decay = mat(ops, w, n("mixer.decay.weight"));
             b.bias = vec(ops, w, n("mixer.decay.bias"));
             b.head_norm = vec(ops, w, n("mixer.head_norm.weight"));
-            b.o = mat(ops, w, n("mixer.o.weight"), M.half);
+            b.o = mat(ops, w, n("mixer.o.weight"));
             break;
         case 'G':
             b.kind = GLOBAL;
-            b.q = mat(ops, w, n("mixer.q.weight"), M.half);
-            b.kv = mat(ops, w, n("mixer.kv.weight"), M.half);
-            b.o = mat(ops, w, n("mixer.o.weight"), M.half);
+            b.q = mat(ops, w, n("mixer.q.weight"));
+            b.kv = mat(ops, w, n("mixer.kv.weight"));
+            b.o = mat(ops, w, n("mixer.o.weight"));
             if (M.cfg.global_emb != 0) {
                 b.has_norm_e = true;
                 b.norm_e = vec(ops, w, n("mixer.norm_e.weight"));
@@ -632,8 +623,8 @@ Block load_block(const Model& M, Weights& w, const std::string& prefix, char kin
     }
     b.norm1 = vec(ops, w, n("norm1.weight"));
     b.norm2 = vec(ops, w, n("norm2.weight"));
-    b.up = mat(ops, w, n("mlp.up.weight"), M.half);
-    b.down = mat(ops, w, n("mlp.down.weight"), M.half);
+    b.up = mat(ops, w, n("mlp.up.weight"));
+    b.down = mat(ops, w, n("mlp.down.weight"));
     return b;
 }
 
@@ -641,9 +632,6 @@ Block load_block(const Model& M, Weights& w, const std::string& prefix, char kin
 void load(Model& M, const std::string& dir) {
     M.cfg = Config::load(dir);
     Weights w(dir);
-    int fp16 = 0;  // fp16 mode at load: linear weights stored as fp16 (mlx.rs:19-26)
-    M.ops.ok(slm_hip_get_fp16(M.ops.ctx(), &fp16), "load");
-    M.half = fp16 != 0;
     auto blocks = [&](const char* name, const std::string& kinds, std::vector<Block>& out) {
         for (size_t i = 0; i < kinds.size(); i++)
             out.push_back(load_block(M, w, std::string(name) + "." + std::to_string(i), kinds[i]));
@@ -653,14 +641,10 @@ void load(Model& M, const std::string& dir) {
     blocks("coda", M.cfg.coda, M.coda);
     M.looped = !M.cfg.core.empty();
     if (M.looped) {
-        M.inject = mat(M.ops, w, "inject_e.weight", M.half);
+        M.inject = mat(M.ops, w, "inject_e.weight");
         M.loop_embed = mat(M.ops, w, "loop_embed.weight");
     }
-    M.embed = mat(M.ops, w, "embed.weight");  // fp32 rows for the gather
-    if (M.half) {  // and fp16 weights for the logits linear
-        std::vector<float> e = M.ops.read(M.embed.w, M.embed.rows * M.embed.cols);
-        M.embed_h = M.ops.upload_half(e.data(), e.size());
-    }
+    M.embed = mat(M.ops, w, "embed.weight");
     M.norm_f = vec(M.ops, w, "norm_f.weight");
     size_t dh = M.cfg.head_dim();
     std::vector<float> inv(dh / 2);
@@ -751,17 +735,32 @@ Session* new_session(Model& M, size_t loops_in) {
     return se;
 }
 
-// model.rs:383-398: doubles a global cache. The reference moves every head's data through
-// the host; here each head's `cap` rows go from the old buffer to the start of that head's
-// `2·cap` rows in a new zeroed one by a device copy on the stream (the same contents).
+// model.rs:383-398: doubles a global cache. By default the reference's own sequence, which a
+// Rust `impl Ops for Hip` under an unchanged model.rs issues: `read` each cache (inside the
+// advance: the backend runs what the step recorded so far), lay every head's `cap` rows out
+// at the start of its `2·cap` rows on the host, `upload_cache` the result and drop the old
+// buffer. With `device_grow` set (slm_model_set_device_grow) the same relayout is a device
+// copy per head into a new zeroed buffer on the stream instead (the same contents, no host
+// round trip).
 void grow(const Model& M, Buf& k, Buf& v, size_t& cap) {
     size_t kh = M.cfg.global_kv_heads, dh = M.cfg.head_dim();
     size_t old = cap, nw = cap * 2;
     for (Buf* buf : {&k, &v}) {
-        Buf nb = M.ops.zeros(kh * nw * dh);
-        for (size_t h = 0; h < kh; h++)
-            M.ops.ok(slm_hip_copy(M.ops.ctx(), nb.p + h * nw * dh, buf->p + h * old * dh, old * dh),
-                     "grow");
+        Buf nb;
+        if (M.device_grow) {
+            nb = M.ops.zeros(kh * nw * dh);
+            for (size_t h = 0; h < kh; h++)
+                M.ops.ok(slm_hip_copy(M.ops.ctx(), nb.p + h * nw * dh, buf->p + h * old * dh,
+                                      old * dh),
+                         "grow");
+        } else {
+            std::vector<float> data = M.ops.read(*buf, kh * old * dh);
+            std::vector<float> out(kh * nw * dh, 0.0f);
+            for (size_t h = 0; h < kh; h++)
+                std::copy(data.begin() + h * old * dh, data.begin() + (h + 1) * old * dh,
+                          out.begin() + h * nw * dh);
+            nb = M.ops.upload(out.data(), out.size());  // ops.rs:79-88 upload_cache
+        }
         M.ops.release(*buf);
         *buf = nb;
     }
@@ -918,7 +917,7 @@ void advance(Model& M, Session& se, const uint32_t* tokens, size_t m, bool want_
     if (want_logits) {
         ops.copy(se.last, at(se.x, (m - 1) * d), d);
         ops.rms(se.sc.n, at(se.last, 0), M.norm_f, 1, d, M.cfg.norm_eps);
-        ops.linear(se.logits, M.half ? M.embed_h : M.embed.w, M.cfg.vocab_size, d, at(se.sc.n, 0), 1);
+        ops.linear(se.logits, M.embed.w, M.cfg.vocab_size, d, at(se.sc.n, 0), 1);
         if (pick >= 0) ops.argmax(se.tok, se.ids, (size_t)pick, se.logits, M.cfg.vocab_size);
     }
     se.pos += m;
@@ -999,7 +998,7 @@ void free_model_bufs(Model& M) {
             for (Buf* p : {&b.norm1, &b.norm2, &b.up.w, &b.down.w, &b.qkv.w, &b.o.w, &b.qkvg.w,
                            &b.decay.w, &b.bias, &b.head_norm, &b.q.w, &b.kv.w, &b.norm_e})
                 free_buf(ops, *p);
-    for (Buf* p : {&M.embed.w, &M.embed_h, &M.inject.w, &M.loop_embed.w, &M.norm_f, &M.inv_freq}) free_buf(ops, *p);
+    for (Buf* p : {&M.embed.w, &M.inject.w, &M.loop_embed.w, &M.norm_f, &M.inv_freq}) free_buf(ops, *p);
 }
 
 }  // namespace
@@ -1038,6 +1037,12 @@ size_t slm_model_params(const slm_model* m) { return m ? params(*m) : 0; }
 int slm_model_set_global_cap(slm_model* m, size_t cap) {
     if (!m || cap == 0) return SLM_E_INVALID;
     m->global_cap0 = cap;
+    return SLM_OK;
+}
+
+int slm_model_set_device_grow(slm_model* m, int on) {
+    if (!m) return SLM_E_INVALID;
+    m->device_grow = on != 0;
     return SLM_OK;
 }
 

@@ -105,6 +105,7 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 };
 
 struct Kernels {
+    hipFunction_t to_half;                   // fp32 -> fp16 weight shadows
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
         store, rope, rope_table, rms, l2norm, rms_wave, l2norm_wave, fill, combine, probe, fg, fold,
         gemm, gemm2_32, gemm2_64, gemm2_96, gemm2_128, gemm2h_32, gemm2h_64, gemm2h_96, gemm2h_128,
@@ -146,6 +147,16 @@ struct slm_hip {
     std::map<size_t, std::vector<void*>> pool_free;  // rounded bytes -> free blocks
     std::map<uintptr_t, size_t> pooled;              // live pooled blocks: start -> rounded bytes
     std::map<uintptr_t, size_t> halves;  // the fp16 ones among them: start -> elements
+    // fp16 mode's weight shadows: the fp32 weights a linear read, as the fp16 values fp16 mode
+    // rounds them to (converted once on the device), so the linear streams half the bytes
+    // with the same bits. Keyed by the fp32 pointer; dropped when anything writes, uploads
+    // into or frees that range.
+    struct Shadow {
+        void* h;   // n halves
+        size_t n;  // floats of the fp32 range [key, key + 4n)
+    };
+    std::map<uintptr_t, Shadow> shadows;
+    bool shadows_on = true;
     float* ws = nullptr;                 // attention partials
     size_t ws_bytes = 0;
     int* attn_ctr = nullptr;             // [ATTN_CTR_MAX] finished superblocks per (query tile, key head)
@@ -216,12 +227,15 @@ int fail(slm_hip* c, int code, const char* fmt, ...) {
     } while (0)
 
 // Is [p, p + bytes) inside one live allocation?
+// Is [p, p + bytes) inside one live fp32 allocation? An fp16 allocation (slm_hip_alloc_half)
+// holds halves, not floats: only upload, read and linear take it, at its start, and they
+// check it before this.
 bool inside(const slm_hip* c, const void* p, size_t bytes) {
     uintptr_t a = (uintptr_t)p;
     auto it = c->allocs.upper_bound(a);
     if (it == c->allocs.begin()) return false;
     --it;
-    return a >= it->first && a - it->first + bytes <= it->second;
+    return a >= it->first && a - it->first + bytes <= it->second && !c->halves.count(it->first);
 }
 
 // Bytes from p to the end of its allocation (0 if p is in none).
@@ -373,6 +387,16 @@ int collect_timing(slm_hip* c) {
     return SLM_OK;
 }
 
+// The attention counters and the fused pick's key and counter are returned to zero by the
+// last workgroup of each launch that uses them. After a launch that failed, or one whose
+// bounded waits gave up (its workgroups may have ended early), they start from zero again.
+// Never inside a capture: a fill recorded into a graph is not replayed reliably.
+void reset_counters(slm_hip* c) {
+    if (c->capturing) return;
+    hipMemsetAsync(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int), c->stream);
+    hipMemsetAsync(c->pick, 0, 16 * sizeof(float), c->stream);
+}
+
 int launch_now(slm_hip* c, const Rec& r) {
     void* ptrs[MAX_ARGS];
     if (r.bytes) {
@@ -385,23 +409,29 @@ int launch_now(slm_hip* c, const Rec& r) {
         hipError_t e = hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream,
                                              ptrs, nullptr);
         if (e != hipSuccess) {
-            // the attention counters are reset by the last workgroup of each launch; after a
-            // launch that failed, start them from zero again
-            if (!c->capturing) {
-                hipMemsetAsync(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int), c->stream);
-                hipMemsetAsync(c->pick, 0, 16 * sizeof(float), c->stream);
-            }
+            reset_counters(c);
             return fail(c, SLM_E_HIP, "hipModuleLaunchKernel: %s", hipGetErrorString(e));
         }
         return SLM_OK;
     }
     // The start and stop events of hipExtModuleLaunchKernel take the dispatch's own begin and
     // end timestamps, so the duration is the kernel's alone (what a kernel trace reports),
-    // without the launch gap an event recorded around the call would add.
+    // without the launch gap an event recorded around the call would add. Its grid is given
+    // in work-items, a 32-bit count.
+    uint64_t items = (uint64_t)r.gx * r.bx;
+    if (items > UINT32_MAX)
+        return fail(c, SLM_E_UNSUPPORTED, "timed launch of %llu work-items along x",
+                    (unsigned long long)items);
     Timed t{pool_event(c), pool_event(c), r.f, r.abytes};
     if (!t.a || !t.b) return fail(c, SLM_E_HIP, "hipEventCreate failed");
-    HIPC(c, hipExtModuleLaunchKernel(r.f, r.gx * r.bx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream,
-                                     ptrs, nullptr, t.a, t.b, 0));
+    hipError_t e = hipExtModuleLaunchKernel(r.f, (uint32_t)items, r.gy, r.gz, r.bx, 1, 1, r.shmem,
+                                            c->stream, ptrs, nullptr, t.a, t.b, 0);
+    if (e != hipSuccess) {
+        c->ev_pool.push_back(t.a);
+        c->ev_pool.push_back(t.b);
+        reset_counters(c);
+        return fail(c, SLM_E_HIP, "hipExtModuleLaunchKernel: %s", hipGetErrorString(e));
+    }
     c->timed.push_back(t);
     if (c->timed.size() >= 4096) TRY(collect_timing(c));
     return SLM_OK;
@@ -2159,12 +2189,21 @@ int check_fault(slm_hip* c) {
     int v = __atomic_load_n(c->fault_host, __ATOMIC_ACQUIRE);
     if (!v) return SLM_OK;
     __atomic_store_n(c->fault_host, 0, __ATOMIC_RELEASE);
+    reset_counters(c);
     return fail(c, SLM_E_HIP, "a fused kernel's bounded wait gave up (fault word %#x): the results "
                 "of the work since the last check are not valid", v);
 }
 
-// Queues an op: recorded inside a step, lowered and launched otherwise.
+void drop_shadows(slm_hip* c, uintptr_t a, uintptr_t b);
+
+// Queues an op: recorded inside a step, lowered and launched otherwise. What it writes
+// loses its fp16 shadow.
 int submit(slm_hip* c, const Op& o) {
+    if (!c->shadows.empty()) {
+        std::vector<Range> rd, wr;
+        op_ranges(o, rd, wr);
+        for (const Range& r : wr) drop_shadows(c, r.a, r.b);
+    }
     if (recording(c)) {
         c->ops.push_back(o);
         return SLM_OK;
@@ -2223,9 +2262,39 @@ int stage_pos(slm_hip* c, size_t pos, Op& o, int slot) {
 
 constexpr size_t POOL_SLAB = (size_t)128 << 20, POOL_BLOCK_MAX = (size_t)32 << 20;
 
+// Gives the slabs none of whose blocks is in use back to the device (their blocks leave the
+// free lists; the slab being carved stays). Free blocks are kept by their exact size, so
+// alloc/free cycles over changing sizes leave free slabs behind: they go back when an
+// allocation would otherwise fail. Returns the bytes released.
+size_t reclaim_slabs(slm_hip* c) {
+    size_t freed = 0;
+    for (size_t i = 0; i + 1 < c->slabs.size();) {
+        uintptr_t a = (uintptr_t)c->slabs[i], b = a + POOL_SLAB;
+        auto lo = c->pooled.lower_bound(a);
+        if (lo != c->pooled.end() && lo->first < b) {
+            i++;
+            continue;
+        }
+        for (auto& f : c->pool_free) {
+            auto& v = f.second;
+            v.erase(std::remove_if(v.begin(), v.end(),
+                                   [&](void* p) { return (uintptr_t)p >= a && (uintptr_t)p < b; }),
+                    v.end());
+        }
+        hipFree(c->slabs[i]);
+        c->slabs.erase(c->slabs.begin() + (long)i);
+        freed += POOL_SLAB;
+    }
+    return freed;
+}
+
 hipError_t dev_alloc(slm_hip* c, size_t bytes, void** out) {
     size_t rb = (bytes + 255) & ~(size_t)255;
-    if (rb > POOL_BLOCK_MAX) return hipMalloc(out, bytes);
+    if (rb > POOL_BLOCK_MAX) {
+        hipError_t e = hipMalloc(out, bytes);
+        if (e != hipSuccess && reclaim_slabs(c)) e = hipMalloc(out, bytes);
+        return e;
+    }
     auto f = c->pool_free.find(rb);
     if (f != c->pool_free.end() && !f->second.empty()) {
         *out = f->second.back();
@@ -2234,6 +2303,7 @@ hipError_t dev_alloc(slm_hip* c, size_t bytes, void** out) {
         if (c->slab_left < rb) {  // (the last slab's tail stays unused)
             void* sl = nullptr;
             hipError_t e = hipMalloc(&sl, POOL_SLAB);
+            if (e != hipSuccess && reclaim_slabs(c)) e = hipMalloc(&sl, POOL_SLAB);
             if (e != hipSuccess) return hipMalloc(out, bytes);
             c->slabs.push_back(sl);
             c->slab_cur = (char*)sl;
@@ -2268,6 +2338,64 @@ int internal_realloc(slm_hip* c, void** p, size_t bytes) {
     HIPC(c, dev_alloc(c, bytes, &np));
     if (*p) c->retired.push_back(*p);
     *p = np;
+    return SLM_OK;
+}
+
+// Drops the fp16 shadows of fp32 ranges that overlap [a, b). Inside a step being recorded
+// the ops recorded so far may read a shadow, so it is freed after the step has run;
+// otherwise once the work queued so far is done.
+void drop_shadows(slm_hip* c, uintptr_t a, uintptr_t b) {
+    bool synced = false;
+    for (auto it = c->shadows.begin(); it != c->shadows.end();) {
+        uintptr_t k0 = it->first, k1 = k0 + it->second.n * 4;
+        if (!(k0 < b && a < k1)) {
+            ++it;
+            continue;
+        }
+        if (c->recording) {
+            c->free_after_step.push_back(it->second.h);
+        } else {
+            if (!synced) hipStreamSynchronize(c->stream);
+            synced = true;
+            dev_free(c, it->second.h);
+        }
+        it = c->shadows.erase(it);
+    }
+}
+
+// fp16 mode: the fp16 shadow of the n fp32 weights at w, made on first use by a conversion
+// queued now (ahead of the step being recorded, whose ops run later on the same stream), or
+// null when the weights are written inside the step being recorded before this linear reads
+// them (the linear then reads the fp32 weights and rounds them itself: the same bits).
+int shadow_of(slm_hip* c, const float* w, size_t n, const float** out) {
+    *out = nullptr;
+    auto it = c->shadows.find((uintptr_t)w);
+    if (it != c->shadows.end() && it->second.n >= n) {
+        *out = (const float*)it->second.h;
+        return SLM_OK;
+    }
+    if (recording(c)) {
+        std::vector<Range> rd, wr;
+        Range r = rng(w, (int64_t)n);
+        for (const Op& o : c->ops) {
+            rd.clear();
+            wr.clear();
+            op_ranges(o, rd, wr);
+            for (const Range& x : wr)
+                if (overlap(x, r)) return SLM_OK;
+        }
+    }
+    if (it != c->shadows.end()) drop_shadows(c, (uintptr_t)w, (uintptr_t)w + 1);  // too short
+    void* h = nullptr;
+    HIPC(c, dev_alloc(c, n * 2, &h));
+    int rc = launch_now(c, mk(c->k.to_half, blocks_for(n), 1, 1, 256, 0, h, w, (long long)n));
+    if (rc) {
+        hipStreamSynchronize(c->stream);
+        dev_free(c, h);
+        return rc;
+    }
+    c->shadows[(uintptr_t)w] = slm_hip::Shadow{h, n};
+    *out = (const float*)h;
     return SLM_OK;
 }
 
@@ -2450,6 +2578,7 @@ int load_kernels(slm_hip* c) {
                {&k.rms, "slm_rms"},             {&k.l2norm, "slm_l2norm"},
                {&k.rms_wave, "slm_rms_wave"},   {&k.l2norm_wave, "slm_l2norm_wave"},
                {&k.fill, "slm_fill"},           {&k.combine, "slm_attn_combine"},
+               {&k.to_half, "slm_to_half"},
                {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
                {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
                {&k.gemm2_32, "slm_gemm2_32"},   {&k.gemm2_64, "slm_gemm2_64"},
@@ -2576,6 +2705,7 @@ void slm_hip_close(slm_hip* c) {
         release(t.second.sin);
     }
     for (auto& a : c->allocs) release((void*)a.first);
+    for (auto& sh : c->shadows) release(sh.second.h);
     release(c->ws);
     if (c->attn_ctr) hipFree(c->attn_ctr);
     if (c->pick) hipFree(c->pick);
@@ -2643,11 +2773,13 @@ int slm_hip_free(slm_hip* c, float* p) {
     if (!p) return SLM_OK;
     auto it = c->allocs.find((uintptr_t)p);
     if (it == c->allocs.end()) return fail(c, SLM_E_BOUNDS, "free: %p was not allocated here", (void*)p);
+    drop_shadows(c, (uintptr_t)p, (uintptr_t)p + it->second);
     if (recording(c)) {
         // (an output growing inside a step, cuda.rs:122-127) the step keeps recording: ops
         // recorded before may still name the buffer, so it is freed once the step has run
         c->allocs.erase(it);
-        c->free_after_step.push_back(p);  // (its fp16 mark, if any, goes with the free)
+        c->halves.erase((uintptr_t)p);  // no later call may take it as fp16 weights
+        c->free_after_step.push_back(p);
         return SLM_OK;
     }
     TRY(taint(c));
@@ -2678,6 +2810,7 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
     NEED(c, "upload", dst, n);
     if (n == 0) return SLM_OK;
     TRY(taint(c));
+    drop_shadows(c, (uintptr_t)dst, (uintptr_t)(dst + n));
     for (auto it = c->tables.begin(); it != c->tables.end();) {  // inv_freq rewritten
         if (it->first >= (uintptr_t)dst && it->first < (uintptr_t)(dst + n)) {
             drop_graphs(c);
@@ -2754,6 +2887,15 @@ int slm_hip_set_fp16(slm_hip* c, int on) {
     if (!c) return SLM_E_INVALID;
     if (c->recording) TRY(finish_step(c));
     c->fp16 = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_set_half_shadows(slm_hip* c, int on) {
+    if (!c) return SLM_E_INVALID;
+    if (c->recording) TRY(finish_step(c));
+    if (c->shadows_on != (on != 0)) drop_graphs(c);
+    c->shadows_on = on != 0;
+    if (!c->shadows_on) drop_shadows(c, 0, UINTPTR_MAX);
     return SLM_OK;
 }
 
@@ -3121,6 +3263,14 @@ int slm_hip_linear(slm_hip* c, float* y, const float* w, size_t rows, size_t col
     }
     NEED(c, "linear", x, m * cols);
     if (!m || !rows) return SLM_OK;
+    if (!nh && c->fp16 && c->shadows_on && cols % 64 == 0 && aligned16(w) && aligned16(x)) {
+        const float* h = nullptr;
+        TRY(shadow_of(c, w, rows * cols, &h));
+        if (h) {
+            w = h;
+            nh = rows * cols;
+        }
+    }
     if (!fits_int(rows) || !fits_int(cols) || !fits_int(m))
         return fail(c, SLM_E_UNSUPPORTED, "linear: %zu x %zu x %zu", rows, cols, m);
     if (m == 1 && c->fusion_on && cols <= (size_t)VP_LEN_MAX) {
@@ -3298,6 +3448,24 @@ int slm_hip_attend_noalloc(slm_hip* c, float* y, float* scores, const float* q, 
 int slm_hip_stream(slm_hip* c, void** out) {
     if (!c || !out) return SLM_E_INVALID;
     *out = (void*)c->stream;
+    return SLM_OK;
+}
+
+int slm_hip_mem_info(slm_hip* c, size_t* free_bytes, size_t* total_bytes, size_t* held_bytes) {
+    if (!c || !free_bytes || !total_bytes || !held_bytes) return SLM_E_INVALID;
+    HIPC(c, hipSetDevice(c->device));
+    HIPC(c, hipMemGetInfo(free_bytes, total_bytes));
+    // pool slabs, plus what went to hipMalloc directly (blocks above the pool's largest)
+    size_t held = c->slabs.size() * POOL_SLAB;
+    auto direct = [&](const void* p, size_t bytes) {
+        if (p && !c->pooled.count((uintptr_t)p)) held += bytes;
+    };
+    for (auto& a : c->allocs) direct((const void*)a.first, a.second);
+    for (auto& sh : c->shadows) direct(sh.second.h, sh.second.n * 2);
+    direct(c->ws, c->ws_bytes);
+    direct(c->part, c->part_bytes);
+    direct(c->gpart, c->gpart_bytes);
+    *held_bytes = held;
     return SLM_OK;
 }
 

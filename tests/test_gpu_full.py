@@ -35,9 +35,9 @@ def hip(pkg):
     h.close()
 
 
-def run(pkg, hip, name, seed, loops, prompt, steps, warm=0):
+def run(pkg, hip, name, seed, loops, prompt, steps, warm=0, device_grow=False):
     folder = model_dir(name, seed)
-    g, c = pkg.Model(hip, folder), O.Model(folder)
+    g, c = pkg.Model(hip, folder, device_grow=device_grow), O.Model(folder)
     gs, cs = g.session(loops), c.session(loops)
     t0 = time.perf_counter()
     if warm:
@@ -79,6 +79,9 @@ def test_a86_r16_prompt_4096(pkg, hip):
     run(pkg, hip, "a86", 2, 16, prompt, 128)
 
 
-def test_g86_prompt_16384(pkg, hip):
+@pytest.mark.parametrize("device_grow", [False, True], ids=["read_upload", "device_copy"])
+def test_g86_prompt_16384(pkg, hip, device_grow):
+    """The global caches grow 8192 -> 16384 -> 32768 inside the prompt: through model.rs's own
+    sequence (read, host relayout, upload inside the advance) and through device copies."""
     prompt = synth.tokens(16384, 32000, seed=6)
-    run(pkg, hip, "g86", 4, 4, prompt, 128)
+    run(pkg, hip, "g86", 4, 4, prompt, 128, device_grow=device_grow)

@@ -41,8 +41,8 @@ def test_reference_fixture_split_matrix(tiny_hip, tiny_dir):
     assert max(r.max_rel for r in reports) < TOL
 
 
-def _both(pkg, hip, folder, loops, global_cap=None):
-    g = pkg.Model(hip, folder, global_cap=global_cap)
+def _both(pkg, hip, folder, loops, global_cap=None, device_grow=False):
+    g = pkg.Model(hip, folder, global_cap=global_cap, device_grow=device_grow)
     c = O.Model(folder, global_cap=global_cap)
     return g, c
 
@@ -131,11 +131,16 @@ def test_ring_overwrite_against_oracle(pkg, hip):
         assert greedy(gs.logits()) == greedy(cs.logits())
 
 
-def test_global_grow(pkg, hip):
+GROW = pytest.mark.parametrize("device_grow", [False, True], ids=["read_upload", "device_copy"])
+
+
+@GROW
+def test_global_grow(pkg, hip, device_grow):
     """Caches that start at 16 slots and double (model.rs:383-398) give the same bits as
-    caches that never grow, and match the oracle."""
+    caches that never grow, and match the oracle: through model.rs's own sequence (a read of
+    each cache inside the advance, host relayout, upload) and through the device copy."""
     folder = model_dir("tiny", 3)
-    small = pkg.Model(hip, folder, global_cap=16)
+    small = pkg.Model(hip, folder, global_cap=16, device_grow=device_grow)
     big = pkg.Model(hip, folder)
     c = O.Model(folder)
     toks = synth.tokens(90, 97, seed=8)
@@ -246,12 +251,13 @@ def test_fused_steps_match_per_op_kernels(pkg, hip, tiny_dir, name):
     _kept_equal(a, b)
 
 
-def test_g86_prompt_against_oracle(pkg, hip):
+@GROW
+def test_g86_prompt_against_oracle(pkg, hip, device_grow):
     """Config 4's model (g86: global G layers with 4 key heads, logn / kshift / emb / far on)
     at R = 4: a 700-token prompt in 256-token chunks with global caches that start at 256
-    slots and double twice, then 4 greedy steps, against the oracle."""
+    slots and double twice, then 4 greedy steps, against the oracle (both ways of growing)."""
     folder = model_dir("g86", 5)
-    g, c = _both(pkg, hip, folder, 4, global_cap=256)
+    g, c = _both(pkg, hip, folder, 4, global_cap=256, device_grow=device_grow)
     toks = synth.tokens(700, 32000, seed=21)
     gs, cs = g.session(4), c.session(4)
     gs.feed(toks, 256)
@@ -338,32 +344,35 @@ def test_c5_fp16_against_fp32_oracle(pkg, hip):
         hip.set_fp16(False)
 
 
-def test_a86_half_weights_equal_fp16_mode(pkg, hip):
-    """A model loaded in fp16 mode stores its linear weights as fp16 (half the bytes) and gives
-    the bits of fp16 mode over the same model's fp32 weights: a 300-token prompt (chunks of
-    256 + 44: the prompt GEMMs and their epilogues) and 8 greedy steps (the fused GEMV) at
-    R = 4, with the fp16-weight kernels the ones that ran."""
+def test_a86_fp16_mode_reads_half_weights(pkg, hip):
+    """fp16 mode through the unchanged trait: the model uploads fp32 weights (ops.rs:77, as
+    model.rs does), and the backend's linears read fp16 copies of them (half the bytes) with
+    the bits of fp16 mode over the fp32 weights: a 300-token prompt (chunks of 256 + 44: the
+    prompt GEMMs and their epilogues) and 8 greedy steps (the fused GEMV) at R = 4, with the
+    fp16-weight kernels the ones that ran; then with step graphs and the device pick."""
     folder = model_dir("a86", 2)
-    g32 = pkg.Model(hip, folder)
     hip.set_fp16(True)
     try:
-        g16 = pkg.Model(hip, folder)
+        g = pkg.Model(hip, folder)
         toks = synth.tokens(300, 32000, seed=3)
-        a, b = g32.session(4), g16.session(4)
+        a, b = g.session(4), g.session(4)
+        hip.set_half_shadows(False)  # a: fp32 weights, rounded by each linear
         a.feed(toks, 256)
-        hip.set_graphs(False)
-        hip.set_timing(True)
-        b.feed(toks, 256)
-        assert np.array_equal(a.logits(), b.logits())
-        assert hip.kernel_stat("slm_gemm2hrw_64")["launches"] > 0
-        assert hip.kernel_stat("slm_gemm2h_64")["launches"] == 0
-        hip.set_timing(False)
+        want0 = a.logits()
         toks8, want = [], []
         for t in range(8):
             toks8.append(greedy(a.logits()))
             a.step(toks8[-1])
             want.append(a.logits())
-        hip.set_timing(True)  # (counts b's launches alone)
+        hip.set_half_shadows(True)  # b: the fp16 copies
+        hip.set_graphs(False)
+        hip.set_timing(True)
+        b.feed(toks, 256)
+        assert np.array_equal(b.logits(), want0)
+        assert hip.kernel_stat("slm_gemm2hrw_64")["launches"] > 0
+        assert hip.kernel_stat("slm_gemm2hr_64")["launches"] == 0
+        hip.set_timing(False)
+        hip.set_timing(True)
         for t in range(8):
             b.step(toks8[t])
             assert np.array_equal(b.logits(), want[t]), t
@@ -371,11 +380,39 @@ def test_a86_half_weights_equal_fp16_mode(pkg, hip):
         assert hip.kernel_stat("slm_fgh")["launches"] == 0
         hip.set_timing(False)
         hip.set_graphs(True)
-        # with step graphs, and the pick on the device
-        ids_a, ids_b = a.decode_greedy(6).tolist(), b.decode_greedy_device(6).tolist()
+        ids_b = b.decode_greedy_device(6).tolist()
+        hip.set_half_shadows(False)
+        ids_a = a.decode_greedy(6).tolist()
         assert ids_a == ids_b
         assert np.array_equal(a.logits(), b.logits())
     finally:
+        hip.set_half_shadows(True)
         hip.set_timing(False)
         hip.set_graphs(True)
         hip.set_fp16(False)
+
+
+def test_dropped_sessions_give_their_memory_back(pkg, hip):
+    """A server makes a session per request and drops it (serve.rs:369, main.rs:308), and a Rust
+    `HipBuf` frees its buffer on drop as cuda.rs's `CudaSlice` does: 40 a86 sessions at R = 16
+    (about 538 MB of rings and state each), each fed a prompt and stepped, then freed, leave
+    the device's free memory and the context's holdings where the first such session left
+    them."""
+    g = pkg.Model(hip, model_dir("a86", 2))
+    toks = synth.tokens(40, 32000, seed=4)
+    s = g.session(16)
+    s.feed(toks, 256)
+    s.step(1)
+    del s
+    free0, total, held0 = hip.mem_info()
+    for i in range(40):
+        s = g.session(16)
+        assert s.state_bytes() > 500e6
+        s.feed(toks[:24], 256)
+        s.step(int(toks[i]))
+        del s
+    free1, _, held1 = hip.mem_info()
+    print(f"after 40 sessions: device free {free0 / 2**30:.2f} -> {free1 / 2**30:.2f} GiB of "
+          f"{total / 2**30:.0f}; held {held0 / 2**20:.0f} -> {held1 / 2**20:.0f} MiB")
+    assert held1 <= held0
+    assert free0 - free1 < 64 << 20

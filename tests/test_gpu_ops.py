@@ -579,6 +579,12 @@ ROW_EPI_GEMM = {"attn_in_dead": ["slm_gemm2r_64"], "gla_in_dead": ["slm_gemm2n_6
                 "mlp_dead": [f"slm_gemm2s_{b}" for b in (32, 64, 96, 128)]}
 
 
+def _fp16_weight_kernel(name):
+    """slm_gemm2r_64 -> slm_gemm2hrw_64: the fp16-mode GEMM over fp16 weights."""
+    head, tile = name.rsplit("_", 1)
+    return head.replace("gemm2", "gemm2h") + "w_" + tile
+
+
 @pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
 @pytest.mark.parametrize("m", [37, 256])
 @pytest.mark.parametrize("case", ROW_CASES)
@@ -706,7 +712,9 @@ def _row_chain(hip, case, m, fp16):
             body(o)
             hip.flush()
             plan = hip.last_plan()
-            epi = sum(hip.kernel_stat(n.replace("gemm2", "gemm2h") if fp16 else n)["launches"]
+            # (fp16 mode: the fp16-weight kernel, "...w_", reading the context's fp16 copy of
+            # the weights)
+            epi = sum(hip.kernel_stat(_fp16_weight_kernel(n) if fp16 else n)["launches"]
                       for n in ROW_EPI_GEMM.get(case, [])) if last else 0
         finally:
             hip.set_fusion(True)
@@ -801,11 +809,16 @@ def test_linear_half_weights_equal_fp16_mode(hip, rows, cols):
     hip.set_fp16(True)
     try:
         for m in (1, 5, 16, 17, 37, 256):
-            a, b = hip.alloc(m * rows), hip.alloc(m * rows)
+            a, b, c = hip.alloc(m * rows), hip.alloc(m * rows), hip.alloc(m * rows)
+            hip.set_half_shadows(False)  # fp32 weights rounded by the linear itself
             hip.linear(a.ptr, dw.ptr, rows, cols, dx.ptr, m)
+            hip.set_half_shadows(True)  # fp32 weights through the context's fp16 copy
+            hip.linear(c.ptr, dw.ptr, rows, cols, dx.ptr, m)
             hip.linear(b.ptr, dh.ptr, rows, cols, dx.ptr, m)
             assert np.array_equal(a.read(), b.read()), m
+            assert np.array_equal(a.read(), c.read()), m
     finally:
+        hip.set_half_shadows(True)
         hip.set_fp16(False)
     with pytest.raises(Exception):
         hip.linear(hip.alloc(rows).ptr, dh.ptr, rows, cols, dx.ptr, 1)
@@ -859,11 +872,64 @@ def test_fused_step_half_weights(hip, case):
     hip.set_fp16(True)
     try:
         got = {}
-        for name, wp, fuse in (("f32w", dw.ptr, True), ("half", dh16.ptr, True), ("half_unfused", dh16.ptr, False)):
+        for name, wp, fuse in (("f32w", dw.ptr, True), ("half", dh16.ptr, True),
+                               ("half_unfused", dh16.ptr, False), ("shadow", dw.ptr, True)):
+            hip.set_half_shadows(name == "shadow")
             _step(hip, body(wp), inv, cs, sn, fuse)
             got[name] = outs()
     finally:
+        hip.set_half_shadows(True)
         hip.set_fp16(False)
-    for name in ("half", "half_unfused"):
+    for name in ("half", "half_unfused", "shadow"):
         for a, b in zip(got["f32w"], got[name]):
             assert np.array_equal(a, b), (case, name)
+
+
+def test_half_shadow_follows_the_weights(hip):
+    """fp16 mode's fp16 copy of a weight buffer is dropped whenever the fp32 buffer changes: an
+    upload into it, an operation writing it (outside a step and inside one, before the linear
+    in the same step), and a free and a new buffer at the same address. Each result equals
+    fp16 mode over the fp32 weights with no copies."""
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(32), hip.alloc(32)
+    rows, cols = 768, 768
+    w1, w2 = rnd(rows, cols, scale=0.02), rnd(rows, cols, scale=0.02)
+    dw, src, dx = hip.upload(w1), hip.upload(w2), hip.upload(rnd(cols))
+    y = hip.alloc(rows)
+
+    def want(w):
+        hip.set_half_shadows(False)
+        t = hip.upload(w)
+        o = hip.alloc(rows)
+        hip.linear(o.ptr, t.ptr, rows, cols, dx.ptr, 1)
+        hip.set_half_shadows(True)
+        return o.read()
+
+    hip.set_fp16(True)
+    try:
+        r1, r2 = want(w1), want(w2)
+        hip.linear(y.ptr, dw.ptr, rows, cols, dx.ptr, 1)
+        assert np.array_equal(y.read(), r1)
+        hip.upload_into(dw, w2)  # an upload into the weights
+        hip.linear(y.ptr, dw.ptr, rows, cols, dx.ptr, 1)
+        assert np.array_equal(y.read(), r2)
+        hip.copy(dw.ptr, hip.upload(w1.ravel()).ptr, rows * cols)  # an operation writing them
+        hip.linear(y.ptr, dw.ptr, rows, cols, dx.ptr, 1)
+        assert np.array_equal(y.read(), r1)
+
+        def body():  # inside a step: the write comes before the linear that reads the weights
+            hip.copy(dw.ptr, src.ptr, rows * cols)
+            hip.linear(y.ptr, dw.ptr, rows, cols, dx.ptr, 1)
+        _step(hip, body, inv, cs, sn, True)
+        assert np.array_equal(y.read(), r2)
+        hip.upload_into(dw, w1)
+        hip.linear(y.ptr, dw.ptr, rows, cols, dx.ptr, 1)
+        assert np.array_equal(y.read(), r1)
+        addr = dw.ptr
+        dw.free()
+        dw2 = hip.upload(w2)  # (the pool may give the same address back)
+        print("same address again:", dw2.ptr == addr)
+        hip.linear(y.ptr, dw2.ptr, rows, cols, dx.ptr, 1)
+        assert np.array_equal(y.read(), r2)
+    finally:
+        hip.set_fp16(False)
