@@ -236,10 +236,12 @@ def g86_leg(pkg, hip, synth, device_grow=False):
     se.logits()
     fill_s = time.perf_counter() - t
     pos0 = se.pos
+    g0 = hip.graph_stats()
     t = time.perf_counter()
     se.decode_greedy(128)
     se.logits()
     dec_s = time.perf_counter() - t
+    g1 = hip.graph_stats()
     fl = prefill_flops(cfg, 4, 0, len(prompt))
     bpt = np.mean([decode_bytes(cfg, 4, p) for p in range(pos0, pos0 + 128)])
     out = {"prompt_tokens": len(prompt), "prefill_tok_s": round(len(prompt) / fill_s, 1),
@@ -249,6 +251,7 @@ def g86_leg(pkg, hip, synth, device_grow=False):
            "decode_bytes_per_token": round(bpt),
            "decode_frac": round(bpt * 128 / dec_s / HBM_PEAK, 4),
            "layers": "SG|LS|SG", "loops": 4,
+           "decode_graphs": {k: g1[k] - g0[k] for k in g1},
            "grow": ("device copies (grow_cache, an optional trait method)" if device_grow else
                     "model.rs:383-398 as written: read + host relayout + upload inside the advance")}
     del se, model
