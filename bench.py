@@ -303,6 +303,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--no-graphs", action="store_true")
+    ap.add_argument("--tile-rows", type=int, default=0,
+                    help="fused GEMV rows per tile (0: the planner's choice; 16, 8 or 4)")
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16-mode leg")
     ap.add_argument("--no-g86", action="store_true", help="skip the g86 16K-prompt leg (config C4)")
     ap.add_argument("--timed-steps", type=int, default=16,
@@ -345,6 +347,8 @@ def main():
     hip = pkg.Hip(0)
     if a.no_graphs:
         hip.set_graphs(False)
+    if a.tile_rows:
+        hip.set_tile_rows(a.tile_rows)
     log("device:", hip.name())
     model = pkg.Model(hip, folder)
     per_r = {}

@@ -187,6 +187,11 @@ int slm_hip_set_half_shadows(slm_hip* ctx, int on);
  * kernels (prologue vector ops + GEMV + epilogue) that compute the same values with the
  * same arithmetic as the per-op kernels. Off: one launch per operation. */
 int slm_hip_set_fusion(slm_hip* ctx, int on);
+/* Rows per tile of the fused one-token GEMV (no trait counterpart; a test and measurement
+ * switch): 0 (the default) lets the planner choose 16, 8 or 4 per linear (smaller tiles spread
+ * a short matrix over more compute units); 16, 8 or 4 forces that size wherever the linear's
+ * row pairs allow it. Results are the same bits at every size. */
+int slm_hip_set_tile_rows(slm_hip* ctx, int rows);
 /* Counters for tests and benchmarks: graphs launched, graphs captured, eager steps. */
 int slm_hip_graph_stats(slm_hip* ctx, uint64_t* launched, uint64_t* captured,
                         uint64_t* eager);

@@ -104,6 +104,7 @@ _SIGS = {
     "slm_hip_set_spin_limit": (_i, [_p, C.c_longlong]),
     "slm_hip_stream": (_i, [_p, C.POINTER(_p)]),
     "slm_hip_set_half_shadows": (_i, [_p, _i]),
+    "slm_hip_set_tile_rows": (_i, [_p, _i]),
     "slm_hip_mem_info": (_i, [_p, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
     "slm_model_load": (_i, [_p, C.c_char_p, C.POINTER(_p)]),
     "slm_model_free": (None, [_p]),
@@ -336,6 +337,10 @@ class Hip:
         s = _p()
         self.check(lib.slm_hip_stream(self.ctx, C.byref(s)))
         return s.value or 0
+
+    def set_tile_rows(self, rows: int):
+        """Fused GEMV rows per tile: 0 = the planner's choice, or 16, 8, 4."""
+        self.check(lib.slm_hip_set_tile_rows(self.ctx, int(rows)))
 
     def set_half_shadows(self, on: bool):
         """fp16 mode's fp16 copies of the weights its linears read (on by default)."""

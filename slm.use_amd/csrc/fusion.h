@@ -11,8 +11,8 @@
 //     fold of a split linear's partials, rope-table rows, the embedding row) that makes
 //     the GEMV input, then, per unit, add the slice partials in order and run the
 //     epilogue (residual add, rope + ring store, SiLU of the gate/amp pair).
-// A unit is one 16-row tile of one split of one weight matrix; units go round-robin over
-// the grid. Every value is computed with the same expression, in the same order, as the
+// A unit is one tile (16, 8 or 4 rows) of one split of one weight matrix; units go
+// round-robin over the grid. Every value is computed with the same expression, in the same order, as the
 // per-op kernels, so fused and unfused runs give the same bits.
 #ifndef SLM_FUSION_H
 #define SLM_FUSION_H
@@ -82,17 +82,19 @@ typedef struct {
     float pad2;
 } VpOp;
 
-// One weight matrix of a fused GEMV. Its rows are grouped into 16-row tiles: the first
-// pair_rows rows (a multiple of 16) in tiles of 8 (row, row + half) pairs, pair P at row
-// (P / half)·2·half + P % half (the rope halves of a head, or the gate and amp rows of a
-// SiLU pair), the rest in consecutive rows.
+// One weight matrix of a fused GEMV. Its rows are grouped into tiles of rpt rows (16, 8 or
+// 4; a tile fills rows 0..rpt-1 of the 16-row MFMA operand, the other rows are zeros): the
+// first pair_rows rows (a multiple of 16) in tiles of rpt/2 (row, row + half) pairs, pair P
+// at row (P / half)·2·half + P % half (the rope halves of a head, or the gate and amp rows of
+// a SiLU pair), the rest in consecutive rows. Each row's chain is the same whatever the
+// tile, so rpt only moves work between workgroups.
 typedef struct {
     const float* w;         // weights [rows][cols]
     float* y;               // the linear's output
     float* part;            // nsplit > 1: the split partials [nsplit][rows]
     int32_t rows, tiles, nsplit, units, unit_first;
     int32_t pair_rows, half;
-    int32_t epi;
+    int32_t epi, rpt, pad_r;
     int32_t d, dh;          // ROPE: part width, head size
     int32_t cs_lds, sn_lds; // ROPE: LDS offsets of the cos / sin row
     float* o1;

@@ -2937,13 +2937,20 @@ __device__ __forceinline__ FgUnit fg_unit(const FgDesc& d, int u) {
     return FgUnit{k, local % s.tiles, local / s.tiles};
 }
 
-// Row of lane row i (0..15) of tile t.
-__device__ __forceinline__ long long fg_row(const FgSeg& s, int t, int i) {
-    if (t * 16 < s.pair_rows) {
-        int P = t * 8 + (i & 7);
-        return (long long)(P / s.half) * 2 * s.half + P % s.half + ((i & 8) ? s.half : 0);
+// Row of lane row i (0..15) of tile t of a matrix of `rows` rows in tiles of rpt rows (lane
+// rows past rpt hold none: `rows` is returned, one past the last). In the first pair_rows
+// rows lane rows i and i + rpt/2 hold a (row, row + half) pair.
+__device__ __forceinline__ long long fg_row_of(int rpt, int pair_rows, int half, int rows, int t, int i) {
+    if (i >= rpt) return rows;
+    int hp = rpt >> 1;
+    if (t * rpt < pair_rows) {
+        int P = t * hp + (i & (hp - 1));
+        return (long long)(P / half) * 2 * half + P % half + ((i & hp) ? half : 0);
     }
-    return (long long)t * 16 + i;
+    return (long long)t * rpt + i;
+}
+__device__ __forceinline__ long long fg_row(const FgSeg& s, int t, int i) {
+    return fg_row_of(s.rpt, s.pair_rows, s.half, s.rows, t, i);
 }
 
 // Sixteen zero bytes: what a lane past the end of a weight matrix loads.
@@ -2984,6 +2991,7 @@ __device__ __forceinline__ FgLane fg_lane_k(const KDw& hd, const KDw& sd, int u,
     constexpr int SF = (int)(offsetof(FgSeg, unit_first) / 4), ST = (int)(offsetof(FgSeg, tiles) / 4);
     constexpr int SWT = (int)(offsetof(FgSeg, w) / 4), SR = (int)(offsetof(FgSeg, rows) / 4);
     constexpr int SP = (int)(offsetof(FgSeg, pair_rows) / 4), SH = (int)(offsetof(FgSeg, half) / 4);
+    constexpr int SRT = (int)(offsetof(FgSeg, rpt) / 4);
     static_assert(sizeof(FgSeg) % 4 == 0 && SLM_SEG_MAX * sizeof(FgSeg) <= 512, "segment table layout");
     FgLane p{slm_zero16, 0, 0};
     if (u >= hd[HU]) return p;
@@ -2999,15 +3007,9 @@ __device__ __forceinline__ FgLane fg_lane_k(const KDw& hd, const KDw& sd, int u,
     if (sl >= hd[HN]) return p;
     p.kb0 = sl * SLM_KS;
     p.nkb = min(SLM_KS, kblocks - p.kb0);
-    long long row;
-    int pair_rows = sd[k * SW + SP], half = sd[k * SW + SH];
-    if (tile * 16 < pair_rows) {
-        int P = tile * 8 + (i & 7);
-        row = (long long)(P / half) * 2 * half + P % half + ((i & 8) ? half : 0);
-    } else {
-        row = (long long)tile * 16 + i;
-    }
-    if (row < sd[k * SW + SR]) {
+    int rows = sd[k * SW + SR];
+    long long row = fg_row_of(sd[k * SW + SRT], sd[k * SW + SP], sd[k * SW + SH], rows, tile, i);
+    if (row < rows) {
         const float* w = (const float*)sd.q64(k * SW + SWT);
         if constexpr (W16) p.base = (const float*)((const _Float16*)w + row * cols + 4 * g);
         else p.base = w + row * cols + 4 * g;

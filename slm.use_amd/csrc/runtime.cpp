@@ -185,6 +185,7 @@ struct slm_hip {
     std::map<uintptr_t, Table> tables;
     bool graphs_on = true, fusion_on = true, plan_trace = false;
     bool fp16 = false;                   // linears with fp16 operands (slm_hip_set_fp16)
+    int fg_rpt = 0;                      // fused GEMV rows per tile: 0 = the planner's choice
     bool timing = false, capturing = false;
     std::vector<Timed> timed;             // launches whose events are not read yet
     std::vector<hipEvent_t> ev_pool;
@@ -1441,9 +1442,34 @@ struct Planner {
         s.w = L.p[1];
         s.y = (float*)L.p[0];
         s.rows = (int32_t)L.n[0];
+        s.rpt = 16;
         s.tiles = (int32_t)((L.n[0] + 15) / 16);
         s.nsplit = 1;
         s.epi = EPI_PLAIN;
+    }
+
+    // Rows per tile of a one-matrix fused GEMV: 16, 8 or 4, whichever gives the least
+    // estimated time per workgroup — rounds of two units (a load latency each, ≈1 us) plus
+    // the weight bytes of the busiest workgroup at ≈24 KB/us (a compute unit's share of HBM
+    // when every one streams); a smaller tile must gain a tenth. Smaller tiles spread a short
+    // matrix (768 rows: 48 tiles of 16) over more compute units; the MFMA rows past the tile
+    // are zeros. `forced` (slm_hip_set_tile_rows) picks one where the pairs allow it.
+    static int choose_rpt(const FgSeg& s, int64_t cols, double wbytes, int forced) {
+        int64_t split_cols = std::min<int64_t>(cols, (int64_t)SLM_SPLIT * SLM_KS * 16);
+        int best = 16;
+        double best_t = 0.0;
+        for (int rpt : {16, 8, 4}) {
+            if (s.pair_rows % rpt) continue;
+            int64_t units = (s.rows + rpt - 1) / rpt * s.nsplit;
+            int64_t grid = std::min<int64_t>(units, FG_GRID_MAX);
+            int64_t per = (units + grid - 1) / grid;
+            double t = (double)((per + 1) / 2) + (double)per * rpt * split_cols * wbytes / 24e3;
+            if (forced ? rpt == forced : (rpt == 16 || t < 0.9 * best_t)) {
+                best = rpt;
+                best_t = t;
+            }
+        }
+        return best;
     }
 
     // Tries to fuse pend + ops[i] (a one-token linear) + what follows. Returns the number of
@@ -1572,6 +1598,10 @@ struct Planner {
         }
         int64_t nsl = (cols / 16 + SLM_KS - 1) / SLM_KS;
         int W = (int)std::min<int64_t>(nsl, SLM_SPLIT);
+        if (nseg == 1) {
+            s0.rpt = choose_rpt(s0, cols, L.n[4] ? 2.0 : 4.0, c->fg_rpt);
+            s0.tiles = (s0.rows + s0.rpt - 1) / s0.rpt;
+        }
         // what the segments read and write
         int units = 0;
         for (int k = 0; k < nseg; k++) {
@@ -2887,6 +2917,14 @@ int slm_hip_set_fp16(slm_hip* c, int on) {
     if (!c) return SLM_E_INVALID;
     if (c->recording) TRY(finish_step(c));
     c->fp16 = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_set_tile_rows(slm_hip* c, int rows) {
+    if (!c || (rows != 0 && rows != 4 && rows != 8 && rows != 16)) return SLM_E_INVALID;
+    if (c->recording) TRY(finish_step(c));
+    if (c->fg_rpt != rows) drop_graphs(c);
+    c->fg_rpt = rows;
     return SLM_OK;
 }
 

@@ -311,9 +311,14 @@ FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "comb
                 "split_fold", "split_flush", "gla_l2", "rounds", "row_offset"]
 
 
+@pytest.mark.parametrize("tile", [0, 16, 8, 4], ids=["tile_auto", "tile16", "tile8", "tile4"])
 @pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
 @pytest.mark.parametrize("case", FUSION_CASES)
-def test_fusion_pattern(hip, case, fp16):
+def test_fusion_pattern(hip, case, fp16, tile):
+    """Every fused one-token pattern gives the bits of one launch per op, with the fused
+    GEMV's rows per tile chosen by the planner or forced to 16, 8 or 4 (each row's chain is
+    the same whatever the tile: the rope and SiLU row pairs, the residual, the split
+    partials and the pick follow their rows)."""
     d, heads, dh, hid, cap = 768, 12, 64, 3072, 4352
     inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
     cs, sn = hip.alloc(32), hip.alloc(32)
@@ -402,6 +407,7 @@ def test_fusion_pattern(hip, case, fp16):
 
     got = []
     hip.set_fp16(fp16)
+    hip.set_tile_rows(tile)
     try:
         for fuse in (False, True):
             o = outs()
@@ -409,6 +415,7 @@ def test_fusion_pattern(hip, case, fp16):
             plan = _step(hip, lambda: body(o), inv, cs, sn, fuse)
             got.append(({k: b.read() for k, b in o.items()}, plan))
     finally:
+        hip.set_tile_rows(0)
         hip.set_fp16(False)
     (a, pa), (b, pb) = got
     print(case, "unfused", pa, "fused", pb)
@@ -518,15 +525,17 @@ def _pick_rows(case, rows, cols=64):
     return w
 
 
+@pytest.mark.parametrize("tile", [0, 4], ids=["tile_auto", "tile4"])
 @pytest.mark.parametrize("rows", [32000, 40])
 @pytest.mark.parametrize("case", ["random", "ties", "nan_first", "nan_inside", "all_neg_inf",
                                   "signed_zero"])
-def test_pick_fused_into_the_logits_gemv(hip, case, rows):
+def test_pick_fused_into_the_logits_gemv(hip, case, rows, tile):
     """The greedy pick after a one-token linear, inside a step: fused into the GEMV's epilogue
     (each workgroup's first maximum into a 64-bit atomic maximum, the last workgroup writes the
     pick) it gives the standalone kernel's index, the reference's first maximum, with no
     slm_argmax launch; and every replay of the step's graph picks afresh (the key and the
-    counter are cleared by the launch that used them)."""
+    counter are cleared by the launch that used them). With the planner's tiles and 4-row
+    tiles."""
     cols = 64
     inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
     cs, sn = hip.alloc(32), hip.alloc(32)
@@ -542,35 +551,39 @@ def test_pick_fused_into_the_logits_gemv(hip, case, rows):
     def picked():
         return int(tok.read(2).view(np.int64)[0]), int(ids.read(4).view(np.uint32)[2])
 
-    plans = {}
-    got = {}
-    for fuse in (False, True):
-        hip.write(tok, np.zeros(2, np.float32))
-        hip.write(ids, np.zeros(4, np.float32))
-        plans[fuse] = _step(hip, body, inv, cs, sn, fuse)
-        got[fuse] = picked()
-    yv = y.read()
-    want = _pick(yv)
-    assert got[True] == (want, want) and got[False] == (want, want), (case, got, want)
-    assert plans[True]["kernels"] < plans[False]["kernels"]
-    # eagerly, with the launches counted: no slm_argmax
-    hip.set_graphs(False)
-    hip.set_timing(True)
+    hip.set_tile_rows(tile)
     try:
-        _step(hip, body, inv, cs, sn, True)
-        assert hip.kernel_stat("slm_argmax")["launches"] == 0
-        assert hip.kernel_stat("slm_fg")["launches"] == 1
+        plans = {}
+        got = {}
+        for fuse in (False, True):
+            hip.write(tok, np.zeros(2, np.float32))
+            hip.write(ids, np.zeros(4, np.float32))
+            plans[fuse] = _step(hip, body, inv, cs, sn, fuse)
+            got[fuse] = picked()
+        yv = y.read()
+        want = _pick(yv)
+        assert got[True] == (want, want) and got[False] == (want, want), (case, got, want)
+        assert plans[True]["kernels"] < plans[False]["kernels"]
+        # eagerly, with the launches counted: no slm_argmax
+        hip.set_graphs(False)
+        hip.set_timing(True)
+        try:
+            _step(hip, body, inv, cs, sn, True)
+            assert hip.kernel_stat("slm_argmax")["launches"] == 0
+            assert hip.kernel_stat("slm_fg")["launches"] == 1
+        finally:
+            hip.set_timing(False)
+            hip.set_graphs(True)
+        assert picked() == (want, want)
+        # graph replays with new weights each time: each pick is fresh
+        for seed in range(4):
+            w = _pick_rows("random", rows)
+            w[(seed * 997) % rows, 0] = 20.0 + seed
+            hip.write(dw, w)
+            _step(hip, body, inv, cs, sn, True)
+            assert picked() == ((seed * 997) % rows,) * 2, seed
     finally:
-        hip.set_timing(False)
-        hip.set_graphs(True)
-    assert picked() == (want, want)
-    # graph replays with new weights each time: each pick is fresh
-    for seed in range(4):
-        w = _pick_rows("random", rows)
-        w[(seed * 997) % rows, 0] = 20.0 + seed
-        hip.write(dw, w)
-        _step(hip, body, inv, cs, sn, True)
-        assert picked() == ((seed * 997) % rows,) * 2, seed
+        hip.set_tile_rows(0)
 
 
 ROW_CASES = ["attn_in", "attn_in_dead", "gla_in_dead", "mlp", "mlp_dead", "inplace", "overlap"]
