@@ -279,9 +279,21 @@ def fp16_leg(pkg, hip, folder, a, prompt, fl):
     s16.decode_greedy(a.steps)
     s16.logits()
     dec16_s = time.perf_counter() - t
+    # per-kernel time of a few more steps, launched eagerly with every launch timed
+    hip.set_graphs(False)
+    hip.set_timing(True)
+    s16.decode_greedy(a.timed_steps)
+    s16.logits()
+    names = ("slm_fghw", "slm_attn_dec16_4", "slm_gla1_4")
+    kern = {n: hip.kernel_stat(n) for n in names}
+    hip.set_timing(False)
+    hip.set_graphs(not a.no_graphs)
     del s16, model
     hip.set_fp16(False)
     fp16 = {"decode_tok_s": round(a.steps / dec16_s, 2), "prefill_tok_s": round(len(prompt) / fill16_s, 1),
+            "us_per_step_by_kernel": {n: round(v["us"] / max(a.timed_steps, 1), 1) for n, v in kern.items()},
+            "us_per_launch_by_kernel": {n: round(v["us"] / max(v["launches"], 1), 2) for n, v in kern.items()},
+            "rings": "fp16 (slm_hip_alloc_cache in fp16 mode): K/V bytes halved",
             "prefill_tflops": round(fl / fill16_s / 1e12, 2),
             "path": "the trait's calls unchanged: fp32 uploads, then slm_hip_set_fp16(1)",
             "note": "linears read fp16 copies of the fp32 weights the backend makes on first use, "
@@ -397,6 +409,7 @@ def main():
     se.decode_greedy(a.timed_steps)
     se.logits()
     kern = {n: hip.kernel_stat(n) for n in ("slm_fg", "slm_attn_dec_4", "slm_gla1_4")}
+    attn_launch_us = kern["slm_attn_dec_4"]["us"] / max(kern["slm_attn_dec_4"]["launches"], 1)
     hip.set_timing(False)
     hip.set_graphs(not a.no_graphs)
     fg = kern["slm_fg"]
@@ -411,7 +424,8 @@ def main():
     # fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)
     fp16 = None
     if not a.no_fp16:
-        fp16 = fp16_leg(pkg, hip, folder, argparse.Namespace(loops=head, warmup=a.warmup, steps=a.steps),
+        fp16 = fp16_leg(pkg, hip, folder, argparse.Namespace(loops=head, warmup=a.warmup, steps=a.steps,
+                                                            timed_steps=a.timed_steps, no_graphs=a.no_graphs),
                         prompt, prefill_flops(cfg, head, 16, len(prompt)))
     del se, head_se
     g86 = None
@@ -459,7 +473,8 @@ def main():
                      "kernel": "slm_fg", "launches": fg["launches"],
                      "bytes_per_launch": round(bpl), "us_per_launch": round(per_launch * 1e6, 3),
                      "timing": "kernel begin/end timestamps (hipExtModuleLaunchKernel events), eager launches",
-                     "us_per_step_by_kernel": share},
+                     "us_per_step_by_kernel": share,
+                     "attn_dec_us_per_launch": round(attn_launch_us, 2)},
         "decode_roofline": {"bound": "hbm", "bytes_per_token": h["decode_bytes_per_token"],
                             "achieved": round(h["decode_bytes_per_token"] * h["decode_tok_s"] / 1e9, 1),
                             "peak": 8000.0, "unit": "GB/s", "frac": h["decode_hbm_frac"]},

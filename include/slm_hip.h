@@ -71,6 +71,19 @@ int slm_hip_alloc(slm_hip* ctx, size_t n, float** out);
  * same weights in fp32 (the fp16 chain rounds them to the same halves) and half the bytes.
  * No other operation takes it. Freed with slm_hip_free. */
 int slm_hip_alloc_half(slm_hip* ctx, size_t n, float** out);
+/* Ops::zeros_cache (ops.rs:73-76): a zeroed [heads][cap][dh] cache. In fp16 mode, where the
+ * fp16 attention kernels take it (head size at most 64 and a multiple of 8, at least 64 slots),
+ * the cache holds fp16 values, as the reference's MLX backend keeps every cache in its dtype
+ * (mlx.rs:57-59): slm_hip_store rounds what it writes to fp16 (nearest even), slm_hip_attend
+ * reads the halves widened exactly, slm_hip_upload into it rounds and slm_hip_read widens;
+ * half the bytes of an fp32 ring. Otherwise an fp32 buffer, as slm_hip_alloc. */
+int slm_hip_alloc_cache(slm_hip* ctx, size_t heads, size_t cap, size_t dh, float** out);
+/* Doubles a cache (model.rs:383-398's relayout, on the device): head h's cap·dh values of src
+ * ([heads][cap][dh]) to the start of its 2·cap·dh in dst ([heads][2·cap][dh], from
+ * slm_hip_alloc_cache, zero past them). Both fp32 or both fp16. No counterpart in the trait:
+ * what a `grow_cache` trait method with model.rs's host round trip as its default would call
+ * (INTEGRATION.md). */
+int slm_hip_grow_cache(slm_hip* ctx, float* dst, const float* src, size_t heads, size_t cap, size_t dh);
 int slm_hip_free(slm_hip* ctx, float* buf);
 /* Copies n host floats into dst (Ops::upload, ops.rs:77). */
 int slm_hip_upload(slm_hip* ctx, float* dst, const float* src, size_t n);
@@ -137,12 +150,13 @@ int slm_hip_gla(slm_hip* ctx, float* y, float* s, const float* q, const float* k
                 const float* v, const float* decay, const float* bias, size_t m,
                 size_t heads, size_t dh);
 /* Writes m [heads][dh] rows into ring slots (pos+i) % cap of cache [heads][cap][dh]
- * (ops.rs:206-217). */
+ * (ops.rs:206-217); into an fp16 cache (slm_hip_alloc_cache in fp16 mode) rounded to fp16. */
 int slm_hip_store(slm_hip* ctx, float* cache, const float* src, size_t pos, size_t m,
                   size_t cap, size_t heads, size_t dh);
 /* Softmax attention of m queries over the ring (ops.rs:218-227). `scores` is the trait's
  * scratch; this backend keeps its own workspace and ignores it (it may be NULL). `k` and
- * `v` are [key_heads][cap][dh]. */
+ * `v` are [key_heads][cap][dh], both fp32 or both fp16 caches (slm_hip_alloc_cache); fp16
+ * values are widened exactly, so the result is that of fp32 rings holding the same values. */
 int slm_hip_attend(slm_hip* ctx, float* y, float* scores, const float* q, const float* k,
                    const float* v, const slm_attn* a);
 /* slm_hip_attend without allocation. No counterpart in the reference: it is for callers that

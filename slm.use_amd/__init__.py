@@ -105,6 +105,8 @@ _SIGS = {
     "slm_hip_stream": (_i, [_p, C.POINTER(_p)]),
     "slm_hip_set_half_shadows": (_i, [_p, _i]),
     "slm_hip_set_tile_rows": (_i, [_p, _i]),
+    "slm_hip_alloc_cache": (_i, [_p, _sz, _sz, _sz, C.POINTER(_p)]),
+    "slm_hip_grow_cache": (_i, [_p, _p, _p, _sz, _sz, _sz]),
     "slm_hip_mem_info": (_i, [_p, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)]),
     "slm_model_load": (_i, [_p, C.c_char_p, C.POINTER(_p)]),
     "slm_model_free": (None, [_p]),
@@ -217,6 +219,16 @@ class Hip:
         b = Buffer(self, p.value, max(a.size, 1))
         self.check(lib.slm_hip_upload(self.ctx, b.ptr, _fp(a), a.size))
         return b
+
+    def alloc_cache(self, heads: int, cap: int, dh: int) -> Buffer:
+        """Ops::zeros_cache (slm_hip_alloc_cache): fp16 values in fp16 mode where the fp16
+        attention kernels take the shape, else fp32. Its pointer is the cache's start only."""
+        p = _p()
+        self.check(lib.slm_hip_alloc_cache(self.ctx, heads, cap, dh, C.byref(p)))
+        return Buffer(self, p.value, max(heads * cap * dh, 1))
+
+    def grow_cache(self, dst: Buffer, src: Buffer, heads: int, cap: int, dh: int):
+        self.check(lib.slm_hip_grow_cache(self.ctx, dst.ptr, src.ptr, heads, cap, dh))
 
     def get_fp16(self) -> bool:
         on = C.c_int()

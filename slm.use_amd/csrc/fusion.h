@@ -94,7 +94,7 @@ typedef struct {
     float* part;            // nsplit > 1: the split partials [nsplit][rows]
     int32_t rows, tiles, nsplit, units, unit_first;
     int32_t pair_rows, half;
-    int32_t epi, rpt, pad_r;
+    int32_t epi, rpt, ring16;  // ring16 (ROPE): the rings hold fp16 values
     int32_t d, dh;          // ROPE: part width, head size
     int32_t cs_lds, sn_lds; // ROPE: LDS offsets of the cos / sin row
     float* o1;
@@ -164,7 +164,7 @@ enum {
     R_MIX,       // out = a + f0·(b − a)
     R_SILU,      // out = b · a / (1 + e^−a)                  (silu_mul, a = gate)
     R_ROPE,      // i0 heads of i1 dims: half-split rotation of a by cos c, sin d
-    R_STORE,     // ring y [i0 heads][q0 slots][i1] at slot (pos + r) mod q0 ← a
+    R_STORE,     // ring y [i0 heads][q0 slots][i1] at slot (pos + r) mod q0 ← a (h16: fp16 ring)
     R_RMS,       // groups of i0: a · (1/sqrt(dot/i0 + f0)) · b   (b: weights, stride 0)
     R_L2NORM,    // groups of i0: a · (1/max(sqrt(dot), 1e-12))
     R_FOLD,      // out = ((a + a[q0]) + a[2·q0]) + ...: i0 split partials, q0 apart
@@ -180,6 +180,7 @@ typedef struct {
     int32_t i0, i1;
     float f0;
     int32_t vec;                     // every operand, output and row length in float4s
+    int32_t h16, pad;                // R_STORE: the ring holds fp16 values
     RowIn a, b, c, d;
     float* y;                        // global output (row r at y + r·ystride), or null
     int64_t ystride;

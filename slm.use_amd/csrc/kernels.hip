@@ -47,6 +47,10 @@ template <typename T>
 __device__ __forceinline__ void gst(T* p, T v) {
     *(GAS T*)p = v;
 }
+// A value into an fp16 ring, rounded to nearest even.
+__device__ __forceinline__ void gst16(_Float16* p, float v) {
+    *(GAS _Float16*)p = (_Float16)v;
+}
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -185,6 +189,28 @@ KERNEL void slm_store(float* __restrict__ cache, const float* __restrict__ src,
         long long tok = t / (heads * dh), h = (t / dh) % heads, e = t % dh;
         long long slot = (pos + tok) % cap;
         cache[(h * cap + slot) * dh + e] = src[t];
+    }
+}
+
+// A cache [heads][cap][dh] laid out at twice the capacity (model.rs:383-398's relayout): head
+// h's cap·dh values to the start of its 2·cap·dh in y (zero after); fp32 and fp16 caches.
+template <typename T>
+__device__ __forceinline__ void grow_body(T* __restrict__ y, const T* __restrict__ x, long long heads,
+                                          long long n) {
+    GRID_LOOP(t, heads * n) y[(t / n) * 2 * n + t % n] = x[t];
+}
+KERNEL void slm_grow(float* y, const float* x, long long heads, long long n) { grow_body(y, x, heads, n); }
+KERNEL void slm_grow16(_Float16* y, const _Float16* x, long long heads, long long n) { grow_body(y, x, heads, n); }
+
+// slm_store into a ring of fp16 values (fp16 mode's caches): each value rounded to nearest even.
+KERNEL void slm_store16(_Float16* __restrict__ cache, const float* __restrict__ src,
+                        const long long* __restrict__ dyn, long long pos_imm, long long n,
+                        long long cap, long long heads, long long dh) {
+    long long pos = dyn_or(dyn, pos_imm);
+    GRID_LOOP(t, n) {
+        long long tok = t / (heads * dh), h = (t / dh) % heads, e = t % dh;
+        long long slot = (pos + tok) % cap;
+        cache[(h * cap + slot) * dh + e] = (_Float16)src[t];
     }
 }
 
@@ -1015,7 +1041,7 @@ struct GemmEpi {
     const long long* kdyn;  // each ring store's position on the device (or null: kpos, vpos)
     const long long* vdyn;
     long long kpos, vpos, cap;
-    int d, pad;
+    int d, ring16;  // ring16: the rings hold fp16 values
 };
 // With SILU the weight rows are the two halves of a gate|amp matrix (rows = 2·half): tile
 // rows 0 .. BM/2 − 1 are gate rows r0h + j and rows BM/2 .. BM − 1 the amp rows half + r0h + j
@@ -1350,7 +1376,11 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                 v = j < 32 ? a * c - b * sn : a * sn + b * c;
             }
             dst[t * ep.d + head * 64 + j] = v;
-            if (region > 0) ring[((long long)head * ep.cap + (pos + t) % ep.cap) * 64 + j] = v;
+            if (region > 0) {
+                long long at = ((long long)head * ep.cap + (pos + t) % ep.cap) * 64 + j;
+                if (ep.ring16) ((_Float16*)ring)[at] = (_Float16)v;  // an fp16 ring
+                else ring[at] = v;
+            }
         }
         return;
     }
@@ -1391,9 +1421,9 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         NAME(float* y, float* part, const float* w, const float* x, int rows, int cols, int m,   \
              float* q, float* k, float* v, float* kring, float* vring, const float* cs,          \
              const float* sn, const long long* kdyn, const long long* vdyn, long long kpos,     \
-             long long vpos, long long cap, int d) {                                             \
+             long long vpos, long long cap, int d, int ring16) {                                 \
         gemm2_body<64, 16, H, false, 1, W16>(y, part, w, x, rows, cols, m,                      \
-                                        GemmEpi{q, k, v, kring, vring, cs, sn, nullptr, kdyn, vdyn, kpos, vpos, cap, d, 0}); \
+                                        GemmEpi{q, k, v, kring, vring, cs, sn, nullptr, kdyn, vdyn, kpos, vpos, cap, d, ring16}); \
     }
 GEMM2R_K(slm_gemm2r_64, false, false)
 GEMM2R_K(slm_gemm2hr_64, true, false)
@@ -1971,7 +2001,9 @@ __device__ __forceinline__ void pq_tiles(long long sbase, long long LO, long lon
     ta = (int)(a < tb ? a : tb);
 }
 
-template <int DT, bool FULL>
+// With KH the rings hold fp16 values: the copies go through registers (four halves a lane,
+// widened exactly, written where the fp32 copy puts them); the rest is unchanged.
+template <int DT, bool FULL, bool KH = false>
 __device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ q,
                             const float* __restrict__ kc, const float* __restrict__ vc,
                             long long pos, int m, long long reach, long long gap, long long cap,
@@ -2012,28 +2044,45 @@ __device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ 
     // the copies: wave w takes segment w / 4, and of each tile it copies the four keys
     // 4·(w % 4) .. +3 (one instruction, lane L: key + L/16, chunk (L % 16) ^ (key & 15); a
     // chunk at or past dh copies the row's last one, read as zero below)
+    h4 hk[KH ? 4 : 1], hv[KH ? 4 : 1];
+    int cs = wave >> 2, cta, ctb;
+    pq_tiles(k0 + 64 * cs, LO, HI, cta, ctb);
     {
-        const float* kb = kc + (long long)kvh * cap * dh;
-        const float* vb = vc + (long long)kvh * cap * dh;
-        int cs = wave >> 2;
-        int ta, tb;
-        pq_tiles(k0 + 64 * cs, LO, HI, ta, tb);
+        int nch = dh >> 2;
         unsigned cap32 = (unsigned)cap;
         unsigned base = (k0 >> 32) == 0 ? (unsigned)k0 % cap32 : (unsigned)(k0 % cap);
         bool wrap1 = cap >= SLM_SB_KEYS;  // base + key < 2·cap: one subtraction wraps it
-        int nch = dh >> 2;
-        for (int st = ta; st < tb; st++) {
-            int row = 64 * cs + 16 * st + 4 * (wave & 3);
+        auto where = [&](int st, int& row) {  // the element offset of this lane's chunk of tile st
+            row = 64 * cs + 16 * st + 4 * (wave & 3);
             int key = row + (lane >> 4);
             int chunk = (lane & 15) ^ (key & 15);
             if (!FULL || DT < 4) chunk = min(chunk, nch - 1);  // rows hold 16 chunks
             unsigned slot = base + (unsigned)key;
             slot = wrap1 ? (slot >= cap32 ? slot - cap32 : slot) : slot % cap32;
-            long long off = (long long)slot * dh + 4 * chunk;
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off),
-                                             (__attribute__((address_space(3))) void*)(kt + 64 * row), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off),
-                                             (__attribute__((address_space(3))) void*)(vt + 64 * row), 16, 0, 0);
+            return (long long)slot * dh + 4 * chunk;
+        };
+        if constexpr (KH) {
+            const _Float16* kb = (const _Float16*)kc + (long long)kvh * cap * dh;
+            const _Float16* vb = (const _Float16*)vc + (long long)kvh * cap * dh;
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                if (st < cta || st >= ctb) continue;
+                int row;
+                long long off = where(st, row);
+                hk[st] = gld((const h4*)(kb + off));
+                hv[st] = gld((const h4*)(vb + off));
+            }
+        } else {
+            const float* kb = kc + (long long)kvh * cap * dh;
+            const float* vb = vc + (long long)kvh * cap * dh;
+            for (int st = cta; st < ctb; st++) {
+                int row;
+                long long off = where(st, row);
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off),
+                                                 (__attribute__((address_space(3))) void*)(kt + 64 * row), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off),
+                                                 (__attribute__((address_space(3))) void*)(vt + 64 * row), 16, 0, 0);
+            }
         }
     }
     bool allvalid = __ballot(col.valid) == ~0ull;
@@ -2043,6 +2092,15 @@ __device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ 
 #pragma unroll
     for (int r = 0; r < 4; r++) voff[r] = 64 * (4 * g + r) + 4 * (i ^ (4 * g + r));
     vm_wait<0>();
+    if constexpr (KH) {  // the widened halves where the fp32 copies put their rows
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            if (st < cta || st >= ctb) continue;
+            int row = 64 * cs + 16 * st + 4 * (wave & 3);
+            *(f4*)(kt + 64 * row + 4 * lane) = wide4(hk[st]);
+            *(f4*)(vt + 64 * row + 4 * lane) = wide4(hv[st]);
+        }
+    }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     float mo = NEG_INF, lo = 0.0f;
     f4 o[DT];
@@ -2121,22 +2179,26 @@ __device__ void attn_pq_run(float* __restrict__ part, const float* __restrict__ 
     }
 }
 
-#define ATTN_PQ(DT)                                                                      \
-    KERNEL void __launch_bounds__(64 * SLM_SB_SEGS * ATTN_QG) slm_attn_pq_##DT(           \
+#define ATTN_PQ(NAME, DT, KH)                                                            \
+    KERNEL void __launch_bounds__(64 * SLM_SB_SEGS * ATTN_QG) NAME(                       \
         float* part, const float* q, const float* kc, const float* vc,                   \
         const long long* dyn, long long pos_imm, int m, long long reach, long long gap,  \
         long long cap, int heads, int key_heads, int dh, float scale) {                  \
         long long pos = dyn_or(dyn, pos_imm);                                            \
         if (dh == 16 * DT)                                                               \
-            attn_pq_run<DT, true>(part, q, kc, vc, pos, m, reach, gap, cap, heads,        \
-                                  key_heads, dh, scale);                                 \
+            attn_pq_run<DT, true, KH>(part, q, kc, vc, pos, m, reach, gap, cap, heads,    \
+                                      key_heads, dh, scale);                             \
         else                                                                             \
-            attn_pq_run<DT, false>(part, q, kc, vc, pos, m, reach, gap, cap, heads,       \
-                                   key_heads, dh, scale);                                \
+            attn_pq_run<DT, false, KH>(part, q, kc, vc, pos, m, reach, gap, cap, heads,   \
+                                       key_heads, dh, scale);                            \
     }
-ATTN_PQ(1)
-ATTN_PQ(2)
-ATTN_PQ(4)
+ATTN_PQ(slm_attn_pq_1, 1, false)
+ATTN_PQ(slm_attn_pq_2, 2, false)
+ATTN_PQ(slm_attn_pq_4, 4, false)
+// over fp16 rings
+ATTN_PQ(slm_attn_pq16_1, 1, true)
+ATTN_PQ(slm_attn_pq16_2, 2, true)
+ATTN_PQ(slm_attn_pq16_4, 4, true)
 
 // One-token attention (m = 1) on the vector ALUs, with the arithmetic of slm_attn_part_*
 // element for element. A 16x16x4 f32 MFMA step is, bit for bit, fmaf over k = 0..3 in
@@ -2153,7 +2215,10 @@ ATTN_PQ(4)
 // Output: part[z][0][head][2 + 16·DT], as slm_attn_part_*; with `ctr` the last workgroup of
 // a key head combines the superblocks into y (its partials fit in LDS: the host checks).
 #define ADEC_WAVE_FLOATS (2 * 64 * 64 + 1024)  // a wave's LDS: keys [64][64], values [64][64], queries
-template <int DT>
+// With KH the rings hold fp16 values (fp16 mode's caches): each lane loads its four halves of
+// a chunk into registers and writes them, widened exactly, where the copy would have put the
+// floats; everything after the staging is the fp32 kernel's.
+template <int DT, bool KH = false>
 __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict__ q,
                               const float* __restrict__ kc, const float* __restrict__ vc,
                               const long long* __restrict__ dyn, long long pos_imm,
@@ -2171,8 +2236,9 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
     long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
     long long sb = first / SLM_SB_KEYS + blockIdx.y;
     long long seg_lo = (sb * SLM_SB_SEGS + wave) * 64;
-    const char* kb = (const char*)(kc + (long long)kvh * cap * dh);
-    const char* vb = (const char*)(vc + (long long)kvh * cap * dh);
+    constexpr unsigned ES = KH ? 2u : 4u;  // bytes per ring element
+    const char* kb = (const char*)kc + (long long)kvh * cap * dh * ES;
+    const char* vb = (const char*)vc + (long long)kvh * cap * dh * ES;
     float* kt = lds + wave * ADEC_WAVE_FLOATS;  // keys; then p and the fold slots
     float* vt = kt + 64 * 64;                    // values
     float* qt = vt + 64 * 64;                    // the key head's queries [group][dh]
@@ -2190,7 +2256,7 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
     // copies the row's last one: it is never read). Key 4k + g is ring slot (seg_lo + 4k + g)
     // mod cap; with cap >= 64 each step of four keys wraps at most once, and a key head's
     // ring is under 4 GB, so byte offsets are 32-bit (the host checks both).
-    unsigned rowb = (unsigned)dh * 4u, wrapb = (unsigned)cap * rowb;
+    unsigned rowb = (unsigned)dh * ES, wrapb = (unsigned)cap * rowb;
     unsigned slot = (unsigned)(seg_lo % cap) + (unsigned)(lane >> 4);
     if (slot >= (unsigned)cap) slot -= (unsigned)cap;
     unsigned roff = slot * rowb;
@@ -2198,22 +2264,34 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         int key = 4 * k + (lane >> 4);
-        off[k] = roff + 16u * (unsigned)min((lane & 15) ^ (key & 15), nch - 1);
+        off[k] = roff + 4u * ES * (unsigned)min((lane & 15) ^ (key & 15), nch - 1);
         roff += 4 * rowb;
         if (roff >= wrapb) roff -= wrapb;
     }
-    // (non-temporal: the keys and values are read once per token, and should not push this
-    // kernel's code and the partials out of L2)
+    h4 hk[KH ? 16 : 1], hv[KH ? 16 : 1];
+    if constexpr (KH) {  // four halves per lane per instruction, into registers
 #pragma unroll
-    for (int k = 0; k < 16; k++)
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off[k]),
-                                         (__attribute__((address_space(3))) void*)(kt + 256 * k), 16, 0, 2);
+        for (int k = 0; k < 16; k++) hk[k] = __builtin_nontemporal_load((const GAS h4*)(kb + off[k]));
 #pragma unroll
-    for (int k = 0; k < 16; k++)
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off[k]),
-                                         (__attribute__((address_space(3))) void*)(vt + 256 * k), 16, 0, 2);
+        for (int k = 0; k < 16; k++) hv[k] = __builtin_nontemporal_load((const GAS h4*)(vb + off[k]));
+    } else {
+        // (non-temporal: the keys and values are read once per token, and should not push
+        // this kernel's code and the partials out of L2)
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off[k]),
+                                             (__attribute__((address_space(3))) void*)(kt + 256 * k), 16, 0, 2);
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off[k]),
+                                             (__attribute__((address_space(3))) void*)(vt + 256 * k), 16, 0, 2);
+    }
     vm_wait<16>();  // the queries and keys are in (the values may still be on their way)
     asm volatile("" ::: "memory");
+    if constexpr (KH) {  // the keys, widened, where the copies put fp32 rows
+#pragma unroll
+        for (int k = 0; k < 16; k++) *(f4*)(kt + 256 * k + 4 * lane) = wide4(hk[k]);
+    }
     // this lane's key: dims 16t + 4g .. +3 as kr[t][g]
     int j = lane;
     f4 kr[DT][4];
@@ -2257,6 +2335,10 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
         if (vwait) {  // the values are in
             vm_wait<0>();
             asm volatile("" ::: "memory");
+            if constexpr (KH) {
+#pragma unroll
+                for (int k = 0; k < 16; k++) *(f4*)(vt + 256 * k + 4 * lane) = wide4(hv[k]);
+            }
             vwait = false;
         }
         // tile by tile: the running maximum and α of the MFMA path (uniform), this tile's p,
@@ -2405,18 +2487,22 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
     }
 }
 
-#define ATTN_DEC(DT)                                                                     \
-    KERNEL void __launch_bounds__(64 * SLM_SB_SEGS) slm_attn_dec_##DT(                    \
+#define ATTN_DEC(NAME, DT, KH)                                                           \
+    KERNEL void __launch_bounds__(64 * SLM_SB_SEGS) NAME(                                 \
         float* part, const float* q, const float* kc, const float* vc,                   \
         const long long* dyn, long long pos_imm, long long reach, long long gap,         \
         long long cap, int heads, int key_heads, int dh, float scale, float* y,          \
         int* ctr) {                                                                      \
-        attn_dec_body<DT>(part, q, kc, vc, dyn, pos_imm, reach, gap, cap, heads,          \
-                          key_heads, dh, scale, y, ctr);                                 \
+        attn_dec_body<DT, KH>(part, q, kc, vc, dyn, pos_imm, reach, gap, cap, heads,      \
+                              key_heads, dh, scale, y, ctr);                             \
     }
-ATTN_DEC(1)
-ATTN_DEC(2)
-ATTN_DEC(4)
+ATTN_DEC(slm_attn_dec_1, 1, false)
+ATTN_DEC(slm_attn_dec_2, 2, false)
+ATTN_DEC(slm_attn_dec_4, 4, false)
+// over fp16 rings
+ATTN_DEC(slm_attn_dec16_1, 1, true)
+ATTN_DEC(slm_attn_dec16_2, 2, true)
+ATTN_DEC(slm_attn_dec16_4, 4, true)
 
 // y[qidx][head][dim] from the nsb superblock partials: with M the largest m of the
 // superblocks that saw a key, w_z = e^(m_z − M), L = Σ l_z·w_z and O = Σ o_z·w_z (both in
@@ -3284,6 +3370,7 @@ __device__ __forceinline__ RowOp row_load(const RowOp& src) {
     o.kind = uni(o.kind); o.n = uni(o.n);
     o.la = uni(o.la); o.lb = uni(o.lb); o.lc = uni(o.lc); o.ld = uni(o.ld);
     o.out = uni(o.out); o.tmp = uni(o.tmp); o.i0 = uni(o.i0); o.i1 = uni(o.i1); o.vec = uni(o.vec);
+    o.h16 = uni(o.h16);
     o.f0 = __int_as_float(uni(__float_as_int(o.f0)));
     o.a.g = uni_ptr(o.a.g); o.b.g = uni_ptr(o.b.g); o.c.g = uni_ptr(o.c.g); o.d.g = uni_ptr(o.d.g);
     o.a.stride = uni_ll(o.a.stride); o.b.stride = uni_ll(o.b.stride);
@@ -3385,7 +3472,13 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
             int heads = o.i0, dh = o.i1;
             long long pos = dyn_or(o.dyn, o.q1);
             long long slot = (pos + r) % o.q0;
-            if (o.vec) {
+            if (o.h16) {  // an fp16 ring: each value rounded to nearest even
+                _Float16* ring = (_Float16*)o.y;
+                for (int t = tid; t < heads * dh; t += 256) {
+                    int h = t / dh, e = t % dh;
+                    ring[((long long)h * o.q0 + slot) * dh + e] = (_Float16)row_in(lds, o.la, o.a, r, t);
+                }
+            } else if (o.vec) {
                 int d4 = dh >> 2;
                 for (int t = tid; t < heads * d4; t += 256) {
                     int h = t / d4, e = 4 * (t % d4);

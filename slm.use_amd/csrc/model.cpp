@@ -303,6 +303,19 @@ class Ops {
         ok(slm_hip_upload(c_, b.p, data, n), "upload");
         return b;
     }
+    // ops.rs:73-76 zeros_cache (a [heads][cap][dh] cache; fp16 in fp16 mode, slm_hip.h)
+    Buf zeros_cache(size_t heads, size_t cap, size_t dh) const {
+        Buf b;
+        ok(slm_hip_alloc_cache(c_, heads, cap, dh, &b.p), "zeros_cache");
+        b.n = std::max<size_t>(heads * cap * dh, 1);
+        return b;
+    }
+    // ops.rs:79-88 upload_cache
+    Buf upload_cache(const float* data, size_t heads, size_t cap, size_t dh) const {
+        Buf b = zeros_cache(heads, cap, dh);
+        ok(slm_hip_upload(c_, b.p, data, heads * cap * dh), "upload_cache");
+        return b;
+    }
     void release(Buf& b) const {
         if (b.p) slm_hip_free(c_, b.p);
         b = Buf{};
@@ -662,16 +675,16 @@ State new_state(const Model& M, const Block& b) {  // model.rs:308-331
     st.kind = b.kind;
     switch (b.kind) {
         case WINDOW:
-            st.k = ops.zeros(h * ring_cap(M) * dh);
-            st.v = ops.zeros(h * ring_cap(M) * dh);
+            st.k = ops.zeros_cache(h, ring_cap(M), dh);
+            st.v = ops.zeros_cache(h, ring_cap(M), dh);
             break;
         case LINEAR:
             st.s = ops.zeros(h * dh * dh);
             break;
         case GLOBAL:
             st.cap = M.global_cap0;
-            st.k = ops.zeros(M.cfg.global_kv_heads * st.cap * dh);
-            st.v = ops.zeros(M.cfg.global_kv_heads * st.cap * dh);
+            st.k = ops.zeros_cache(M.cfg.global_kv_heads, st.cap, dh);
+            st.v = ops.zeros_cache(M.cfg.global_kv_heads, st.cap, dh);
             st.prev = ops.zeros(M.cfg.d_model);
             st.scores = ops.zeros(1);
             break;
@@ -739,27 +752,24 @@ Session* new_session(Model& M, size_t loops_in) {
 // Rust `impl Ops for Hip` under an unchanged model.rs issues: `read` each cache (inside the
 // advance: the backend runs what the step recorded so far), lay every head's `cap` rows out
 // at the start of its `2·cap` rows on the host, `upload_cache` the result and drop the old
-// buffer. With `device_grow` set (slm_model_set_device_grow) the same relayout is a device
-// copy per head into a new zeroed buffer on the stream instead (the same contents, no host
-// round trip).
+// buffer. With `device_grow` set (slm_model_set_device_grow) the same relayout runs on the
+// device into a new zeroed cache, queued on the stream (slm_hip_grow_cache: the same
+// contents, no host round trip).
 void grow(const Model& M, Buf& k, Buf& v, size_t& cap) {
     size_t kh = M.cfg.global_kv_heads, dh = M.cfg.head_dim();
     size_t old = cap, nw = cap * 2;
     for (Buf* buf : {&k, &v}) {
         Buf nb;
         if (M.device_grow) {
-            nb = M.ops.zeros(kh * nw * dh);
-            for (size_t h = 0; h < kh; h++)
-                M.ops.ok(slm_hip_copy(M.ops.ctx(), nb.p + h * nw * dh, buf->p + h * old * dh,
-                                      old * dh),
-                         "grow");
+            nb = M.ops.zeros_cache(kh, nw, dh);
+            M.ops.ok(slm_hip_grow_cache(M.ops.ctx(), nb.p, buf->p, kh, old, dh), "grow");
         } else {
             std::vector<float> data = M.ops.read(*buf, kh * old * dh);
             std::vector<float> out(kh * nw * dh, 0.0f);
             for (size_t h = 0; h < kh; h++)
                 std::copy(data.begin() + h * old * dh, data.begin() + (h + 1) * old * dh,
                           out.begin() + h * nw * dh);
-            nb = M.ops.upload(out.data(), out.size());  // ops.rs:79-88 upload_cache
+            nb = M.ops.upload_cache(out.data(), kh, nw, dh);
         }
         M.ops.release(*buf);
         *buf = nb;

@@ -57,7 +57,7 @@ constexpr int64_t CU_COUNT = 256;           // MI355X compute units
 enum OpKind : uint32_t {
     OP_GATHER = 1, OP_COPY, OP_SHIFT, OP_COLUMNS, OP_LINEAR, OP_ADD, OP_ADD_ROW, OP_SCALE_ROWS,
     OP_MIX, OP_RMS, OP_SILU_MUL, OP_ROPE_TABLE, OP_ROPE, OP_L2NORM, OP_GLA, OP_STORE, OP_ATTEND,
-    OP_ARGMAX
+    OP_ARGMAX, OP_GROW
 };
 
 // One operation, by value. p[] are device pointers (outputs first), n[] sizes, f[]
@@ -106,6 +106,8 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 
 struct Kernels {
     hipFunction_t to_half;                   // fp32 -> fp16 weight shadows
+    hipFunction_t store16, grow, grow16;     // fp16 rings; cache growth
+    hipFunction_t attn_dec16[3], attn_pq16[3];  // attention over fp16 rings
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
         store, rope, rope_table, rms, l2norm, rms_wave, l2norm_wave, fill, combine, probe, fg, fold,
         gemm, gemm2_32, gemm2_64, gemm2_96, gemm2_128, gemm2h_32, gemm2h_64, gemm2h_96, gemm2h_128,
@@ -575,6 +577,13 @@ int lower_linear(slm_hip* c, const Op& o, std::vector<Rec>& out, int64_t* fold_n
 
 // One-token attention on the vector-ALU kernel (the same arithmetic as the MFMA kernels; its
 // ring offsets step four slots at a time and are 32-bit).
+// Rings the fp16 attention kernels take (the one-token kernel and the shared-superblock prompt
+// kernel): head size at most 64 and a multiple of 8, at least 64 slots, a key head's ring
+// under 4 GB.
+bool half_ring_ok(size_t heads, size_t dh, size_t cap) {
+    return heads > 0 && dh > 0 && dh <= 64 && dh % 8 == 0 && cap >= 64 && cap * dh * 4 < ((size_t)1 << 32);
+}
+
 bool attn_dec_ok(const Op& o) {
     const int64_t* n = o.n;
     return n[1] == 1 && n[7] <= 64 && n[4] >= 64 && n[4] * n[7] * 4 < ((int64_t)1 << 32);
@@ -603,7 +612,7 @@ int lower_attn_dec(slm_hip* c, const Op& o, std::vector<Rec>& out, bool defer) {
     float* part = attn_part(c, o);
     bool self = !defer && !o.p[4] && kh <= ATTN_CTR_MAX &&
                 nsb * (heads / kh) * (dp + 2) <= ATTN_DEC_LDS / 4;
-    out.push_back(mk(k.attn_dec[dti], (uint32_t)kh, (uint32_t)nsb, 1, 64 * SLM_SB_SEGS,
+    out.push_back(mk(n[9] ? k.attn_dec16[dti] : k.attn_dec[dti], (uint32_t)kh, (uint32_t)nsb, 1, 64 * SLM_SB_SEGS,
                      (uint32_t)ATTN_DEC_LDS, part, p[1], p[2], p[3], (const long long*)o.dyn,
                      (long long)n[0], (long long)n[2], (long long)n[3], (long long)n[4], (int)heads,
                      (int)kh, (int)dh, o.f[0], self ? p[0] : (float*)nullptr,
@@ -710,14 +719,18 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                              (int)n[2], vec));
             return SLM_OK;
         }
-        case OP_STORE:  // p0 cache, p1 src; n0 m, n1 cap, n2 heads, n3 dh, n4 pos
-            out.push_back(mk(k.store, blocks_for(n[0] * n[2] * n[3]), 1, 1, 256, 0, p[0], p[1],
+        case OP_STORE:  // p0 cache, p1 src; n0 m, n1 cap, n2 heads, n3 dh, n4 pos, n5 fp16 ring
+            out.push_back(mk(n[5] ? k.store16 : k.store, blocks_for(n[0] * n[2] * n[3]), 1, 1, 256, 0, p[0], p[1],
                              (const long long*)o.dyn, (long long)n[4], (long long)(n[0] * n[2] * n[3]),
                              (long long)n[1], (long long)n[2], (long long)n[3]));
             return SLM_OK;
+        case OP_GROW:  // p0 new cache, p1 old; n0 heads, n1 old cap, n2 dh, n3 fp16
+            out.push_back(mk(n[3] ? k.grow16 : k.grow, blocks_for(n[0] * n[1] * n[2]), 1, 1, 256, 0,
+                             p[0], p[1], (long long)n[0], (long long)(n[1] * n[2])));
+            return SLM_OK;
         case OP_ATTEND: {
             // p0 y, p1 q, p2 k, p3 v; n0 pos, n1 m, n2 reach, n3 gap, n4 cap, n5 heads,
-            // n6 key_heads, n7 dh, n8 nsb; f0 scale
+            // n6 key_heads, n7 dh, n8 nsb, n9 fp16 rings; f0 scale
             int64_t m = n[1], heads = n[5], kh = n[6], dh = n[7], nsb = n[8];
             int dti = pow2_index((dh + 15) / 16, 4);
             int64_t dp = (int64_t)16 << dti;
@@ -729,7 +742,7 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                 // a superblock's keys and values shared in LDS by four query tiles
                 // (then every row's superblocks are combined by a kernel of their own: many
                 // rows, each a wave, rather than one workgroup per tile group at the end)
-                out.push_back(mk(k.attn_pq[dti], (uint32_t)groups, (uint32_t)kh, (uint32_t)nsb,
+                out.push_back(mk(n[9] ? k.attn_pq16[dti] : k.attn_pq[dti], (uint32_t)groups, (uint32_t)kh, (uint32_t)nsb,
                                  64 * SLM_SB_SEGS * ATTN_QG_HOST, (uint32_t)(2 * SLM_SB_KEYS * 64 * 4),
                                  part, p[1], p[2], p[3], (const long long*)o.dyn, (long long)n[0],
                                  (int)m, (long long)n[2], (long long)n[3], (long long)n[4],
@@ -740,6 +753,7 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
                                  (long long)n[3]));
                 return SLM_OK;
             }
+            if (n[9]) return fail(c, SLM_E_UNSUPPORTED, "attend: fp16 rings of this shape");
             // LDS: wpp segment partials being folded, then each wave's tile of values
             auto shm = [&](int64_t w) { return (w * 16 * (dp + 2) + SLM_SB_SEGS * 16 * (dp + 4)) * 4; };
             int64_t wpp = SLM_SB_SEGS;
@@ -836,6 +850,9 @@ bool vp_of(const Op& o, VpSrc* v) {
 }
 
 
+// A ring's elements in floats of storage (fp16 rings take half).
+int64_t ring_floats(int64_t n, int64_t h16) { return h16 ? (n + 1) / 2 : n; }
+
 // A linear's weights in floats of storage (fp16 weights take half).
 int64_t wfloats(const Op& o) { return o.n[4] ? (o.n[0] * o.n[1] + 1) / 2 : o.n[0] * o.n[1]; }
 
@@ -900,15 +917,19 @@ void op_ranges(const Op& o, std::vector<Range>& rd, std::vector<Range>& wr) {
             break;
         }
         case OP_STORE:
-            wr.push_back(rng(p[0], n[2] * n[1] * n[3]));
-            rd.push_back(rng(p[0], n[2] * n[1] * n[3]));
+            wr.push_back(rng(p[0], ring_floats(n[2] * n[1] * n[3], n[5])));
+            rd.push_back(rng(p[0], ring_floats(n[2] * n[1] * n[3], n[5])));
             rd.push_back(rng(p[1], n[0] * n[2] * n[3]));
+            break;
+        case OP_GROW:
+            wr.push_back(rng(p[0], ring_floats(2 * n[0] * n[1] * n[2], n[3])));
+            rd.push_back(rng(p[1], ring_floats(n[0] * n[1] * n[2], n[3])));
             break;
         case OP_ATTEND:
             wr.push_back(rng(p[0], n[1] * n[5] * n[7]));
             rd.push_back(rng(p[1], n[1] * n[5] * n[7]));
-            rd.push_back(rng(p[2], n[6] * n[4] * n[7]));
-            rd.push_back(rng(p[3], n[6] * n[4] * n[7]));
+            rd.push_back(rng(p[2], ring_floats(n[6] * n[4] * n[7], n[9])));
+            rd.push_back(rng(p[3], ring_floats(n[6] * n[4] * n[7], n[9])));
             break;
     }
 }
@@ -1084,10 +1105,11 @@ struct Planner {
                 len = n[2] * n[3];
                 ro->kind = R_STORE; ro->a = {p[1], len};
                 ro->i0 = (int32_t)n[2]; ro->i1 = (int32_t)n[3]; ro->q0 = n[1]; ro->q1 = n[4];
+                ro->h16 = (int32_t)n[5];
                 ro->dyn = (const long long*)o.dyn;
                 ro->n = (int32_t)len;
                 ro->y = (float*)p[0];
-                *foot = rng(p[0], n[2] * n[1] * n[3]);
+                *foot = rng(p[0], ring_floats(n[2] * n[1] * n[3], n[5]));
                 return true;
             case OP_RMS:
             case OP_L2NORM:  // n0 groups, n1 size; f0 eps
@@ -1512,7 +1534,7 @@ struct Planner {
                       rq.p[3] == rk.p[3] && sk.n[0] == 1 && sv.n[0] == 1 && sk.p[1] == rk.p[0] &&
                       sv.p[1] == y + 2 * dd && sk.n[1] == sv.n[1] && sk.n[2] == heads &&
                       sv.n[2] == heads && sk.n[3] == dh && sv.n[3] == dh && dh % 2 == 0 &&
-                      dd % 16 == 0;
+                      dd % 16 == 0 && sk.n[5] == sv.n[5];
             if (ok) {
                 used = 5;
                 s0.epi = EPI_ROPE;
@@ -1527,6 +1549,7 @@ struct Planner {
                 cs = rq.p[2];
                 sn = rq.p[3];
                 s0.cap = sk.n[1];
+                s0.ring16 = (int32_t)sk.n[5];
                 s0.dyn = (const long long*)sk.dyn;
                 s0.imm = sk.n[4];
                 s0.dyn2 = (const long long*)sv.dyn;
@@ -1628,8 +1651,8 @@ struct Planner {
                     int64_t heads = s.d / s.dh;
                     b.writes.push_back(rng(s.o1, s.d));
                     b.writes.push_back(rng(s.o2, s.d));
-                    b.writes.push_back(rng(s.o3, heads * s.cap * s.dh));
-                    b.writes.push_back(rng(s.o4, heads * s.cap * s.dh));
+                    b.writes.push_back(rng(s.o3, ring_floats(heads * s.cap * s.dh, s.ring16)));
+                    b.writes.push_back(rng(s.o4, ring_floats(heads * s.cap * s.dh, s.ring16)));
                     break;
                 }
             }
@@ -1950,14 +1973,15 @@ struct Planner {
         const float *q = r1.p[0], *k = r2.p[0], *v = c3.p[0];
         auto store_ok = [&](const Op& st, const float* src) {
             return st.p[1] == src && st.n[0] == m && st.n[1] == s1.n[1] && st.n[2] * 64 == d &&
-                   st.n[3] == 64;
+                   st.n[3] == 64 && st.n[5] == s1.n[5];
         };
         if (!store_ok(s1, k) || !store_ok(s2, v) || s1.p[0] == s2.p[0]) return 0;
         int64_t cap = s1.n[1];
         // what the chain writes, what it reads: pairwise apart, so the order of the writes
         // does not matter
         std::vector<Range> wr = {rng(mix, m * rows), rng(cy, m * d), rng(q, m * d), rng(k, m * d),
-                                 rng(v, m * d), rng(s1.p[0], d * cap), rng(s2.p[0], d * cap)};
+                                 rng(v, m * d), rng(s1.p[0], ring_floats(d * cap, s1.n[5])),
+                                 rng(s2.p[0], ring_floats(d * cap, s1.n[5]))};
         std::vector<Range> rd = {rng(L.p[1], wfloats(L)), rng(L.p[2], m * cols), rng(r1.p[2], m * 32),
                                  rng(r1.p[3], m * 32)};
         for (size_t a = 0; a < wr.size(); a++) {
@@ -1973,7 +1997,7 @@ struct Planner {
                          1, gemm2_threads(64), shmem, (float*)mix, c->gpart, L.p[1], L.p[2], (int)rows,
                          (int)cols, (int)m, (float*)q, (float*)k, (float*)v, (float*)s1.p[0],
                          (float*)s2.p[0], r1.p[2], r1.p[3], (const long long*)s1.dyn, (const long long*)s2.dyn,
-                         (long long)s1.n[4], (long long)s2.n[4], (long long)cap, (int)d));
+                         (long long)s1.n[4], (long long)s2.n[4], (long long)cap, (int)d, (int)s1.n[5]));
         out.back().abytes = 4.0 * (double)(rows * cols + m * cols + m * rows + 3 * m * d + 2 * m * d + 2 * m * 32);
         last_m = m;
         return 8;
@@ -2608,7 +2632,11 @@ int load_kernels(slm_hip* c) {
                {&k.rms, "slm_rms"},             {&k.l2norm, "slm_l2norm"},
                {&k.rms_wave, "slm_rms_wave"},   {&k.l2norm_wave, "slm_l2norm_wave"},
                {&k.fill, "slm_fill"},           {&k.combine, "slm_attn_combine"},
-               {&k.to_half, "slm_to_half"},
+               {&k.to_half, "slm_to_half"},     {&k.store16, "slm_store16"},
+               {&k.grow, "slm_grow"},           {&k.grow16, "slm_grow16"},
+               {&k.attn_dec16[0], "slm_attn_dec16_1"}, {&k.attn_dec16[1], "slm_attn_dec16_2"},
+               {&k.attn_dec16[2], "slm_attn_dec16_4"}, {&k.attn_pq16[0], "slm_attn_pq16_1"},
+               {&k.attn_pq16[1], "slm_attn_pq16_2"},   {&k.attn_pq16[2], "slm_attn_pq16_4"},
                {&k.probe, "slm_probe_mfma"},    {&k.fg, "slm_fg"},
                {&k.fold, "slm_fold"},           {&k.gemm, "slm_gemm"},
                {&k.gemm2_32, "slm_gemm2_32"},   {&k.gemm2_64, "slm_gemm2_64"},
@@ -2796,6 +2824,35 @@ int slm_hip_alloc_half(slm_hip* c, size_t n, float** out) {
     TRY(slm_hip_alloc(c, nf, out));
     c->halves[(uintptr_t)*out] = std::max<size_t>(n, 1);
     return SLM_OK;
+}
+
+int slm_hip_alloc_cache(slm_hip* c, size_t heads, size_t cap, size_t dh, float** out) {
+    if (!c || !out) return SLM_E_INVALID;
+    if (c->fp16 && half_ring_ok(heads, dh, cap)) return slm_hip_alloc_half(c, heads * cap * dh, out);
+    return slm_hip_alloc(c, heads * cap * dh, out);
+}
+
+int slm_hip_grow_cache(slm_hip* c, float* dst, const float* src, size_t heads, size_t cap, size_t dh) {
+    if (!c) return SLM_E_INVALID;
+    if (!heads || !cap || !dh) return SLM_OK;
+    size_t hd = half_count(c, dst), hs = half_count(c, src), n = heads * cap * dh;
+    if ((hd != 0) != (hs != 0))
+        return fail(c, SLM_E_INVALID, "grow_cache: one fp16 cache and one fp32 cache");
+    if (hd) {
+        if (hd < 2 * n || hs < n)
+            return fail(c, SLM_E_BOUNDS, "grow_cache: %zu x %zu x %zu into %zu halves from %zu", heads, cap, dh, hd, hs);
+    } else {
+        NEED(c, "grow_cache", dst, 2 * n);
+        NEED(c, "grow_cache", src, n);
+    }
+    Op o = op(OP_GROW);
+    o.p[0] = dst;
+    o.p[1] = src;
+    o.n[0] = (int64_t)heads;
+    o.n[1] = (int64_t)cap;
+    o.n[2] = (int64_t)dh;
+    o.n[3] = hd ? 1 : 0;
+    return submit(c, o);
 }
 
 int slm_hip_free(slm_hip* c, float* p) {
@@ -3165,7 +3222,13 @@ int slm_hip_store(slm_hip* c, float* cache, const float* src, size_t pos, size_t
     if (!c) return SLM_E_INVALID;
     if (!m || !heads || !dh) return SLM_OK;
     if (!cap) return fail(c, SLM_E_INVALID, "store: cap is 0");
-    NEED(c, "store", cache, heads * cap * dh);
+    size_t h16 = half_count(c, cache);  // an fp16 ring (slm_hip_alloc_cache in fp16 mode)
+    if (h16) {
+        if (h16 < heads * cap * dh)
+            return fail(c, SLM_E_BOUNDS, "store: %zu x %zu x %zu ring in %zu halves", heads, cap, dh, h16);
+    } else {
+        NEED(c, "store", cache, heads * cap * dh);
+    }
     NEED(c, "store", src, m * heads * dh);
     Op o = op(OP_STORE);
     o.p[0] = cache;
@@ -3174,6 +3237,7 @@ int slm_hip_store(slm_hip* c, float* cache, const float* src, size_t pos, size_t
     o.n[1] = (int64_t)cap;
     o.n[2] = (int64_t)heads;
     o.n[3] = (int64_t)dh;
+    o.n[5] = h16 ? 1 : 0;
     TRY(stage_pos(c, pos, o, 4));
     return submit(c, o);
 }
@@ -3386,8 +3450,18 @@ int attend_op(slm_hip* c, float* y, const float* q, const float* k, const float*
     if (group > 16) return fail(c, SLM_E_UNSUPPORTED, "attend: %zu query heads per key head", group);
     if (!cap || a->reach == 0) return fail(c, SLM_E_INVALID, "attend: cap or reach is 0");
     NEED(c, "attend", q, m * heads * dh);
-    NEED(c, "attend", k, kh * cap * dh);
-    NEED(c, "attend", v, kh * cap * dh);
+    size_t hk = half_count(c, k), hv = half_count(c, v);  // fp16 rings
+    if (hk || hv) {
+        if (!hk || !hv) return fail(c, SLM_E_INVALID, "attend: one fp16 ring and one fp32 ring");
+        if (hk < kh * cap * dh || hv < kh * cap * dh)
+            return fail(c, SLM_E_BOUNDS, "attend: %zu x %zu x %zu rings in %zu and %zu halves", kh, cap, dh, hk, hv);
+        if (!half_ring_ok(heads, dh, cap))
+            return fail(c, SLM_E_UNSUPPORTED, "attend: fp16 rings need head size <= 64, a multiple of 8, "
+                        "and at least 64 slots");
+    } else {
+        NEED(c, "attend", k, kh * cap * dh);
+        NEED(c, "attend", v, kh * cap * dh);
+    }
     if (!aligned16(q) || !aligned16(k) || !aligned16(v))
         return fail(c, SLM_E_UNSUPPORTED, "attend: q, k and v must be 16-byte aligned");
     if (!fits_int(m) || !fits_int(heads))
@@ -3426,7 +3500,10 @@ int attend_op(slm_hip* c, float* y, const float* q, const float* k, const float*
     o.n[6] = (int64_t)kh;
     o.n[7] = (int64_t)dh;
     o.n[8] = (int64_t)nsb;
+    o.n[9] = hk ? 1 : 0;
     o.f[0] = a->scale;
+    if (hk && m > 1 && (int64_t)((qtiles + ATTN_QG_HOST - 1) / ATTN_QG_HOST) * (int64_t)kh * (int64_t)nsb > (int64_t)INT_MAX)
+        return fail(c, SLM_E_UNSUPPORTED, "attend: fp16 rings: %zu query tiles", qtiles);
     return SLM_OK;
 }
 

@@ -635,8 +635,10 @@ def _row_chain(hip, case, m, fp16):
         o = {k: hip.alloc(n) for k, n in
              dict(y=m * 3 * d, y4=m * 4 * d, gt=m * d, q=m * d, k=m * d, k2=m * d, v=m * d, up=m * 2 * hid, g=m * hid,
                   u=m * hid, h=m * hid, dn=m * d, t=m * d, n=m * d, z=m * d, s=m * d,
-                  y2=m * d, a=m * d // 2, b=m * d, c2=m * d // 2,
-                  kr=heads * cap * dh, vr=heads * cap * dh).items()}
+                  y2=m * d, a=m * d // 2, b=m * d, c2=m * d // 2).items()}
+        # the rings: Ops::zeros_cache, fp16 values in fp16 mode (the QKV GEMM's epilogue and
+        # the row chain's stores then round what they write)
+        o["kr"], o["vr"] = hip.alloc_cache(heads, cap, dh), hip.alloc_cache(heads, cap, dh)
         hip.write(o["kr"], kr0)
         hip.write(o["vr"], vr0)
         return o
@@ -946,3 +948,157 @@ def test_half_shadow_follows_the_weights(hip):
         assert np.array_equal(y.read(), r2)
     finally:
         hip.set_fp16(False)
+
+
+# ---------------------------------------------------------------------------------------
+# fp16 rings (slm_hip_alloc_cache in fp16 mode): stores round to fp16, attention widens the
+# halves exactly, so everything equals fp32 rings holding the same values
+# ---------------------------------------------------------------------------------------
+
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+# the ATTN_CASES the fp16 kernels take (head size at most 64, a multiple of 8, 64+ slots)
+HALF_ATTN_CASES = [c for c in ATTN_CASES if c["dh"] <= 64 and c["dh"] % 8 == 0 and c["cap"] >= 64]
+
+
+@pytest.mark.parametrize("case", HALF_ATTN_CASES, ids=lambda c: f"p{c['pos']}m{c['m']}kh{c['key_heads']}d{c['dh']}")
+def test_half_rings_store_and_attend(hip, case):
+    """A ring from slm_hip_alloc_cache in fp16 mode holds halves: a store rounds to nearest
+    even, and attention over it (the one-token kernel at m = 1, the prompt kernel at m > 1,
+    and the allocation-free entry point) gives, bit for bit, attention over fp32 rings that
+    hold the same values."""
+    a = dict(case, scale=float(1 / np.sqrt(case["dh"])))
+    m, heads, kh, dh, cap = a["m"], a["heads"], a["key_heads"], a["dh"], a["cap"]
+    k, v = _f16(rnd(kh, cap, dh)), _f16(rnd(kh, cap, dh))
+    q = rnd(m, heads, dh)
+    new_k, new_v = rnd(m, kh, dh), rnd(m, kh, dh)
+    hip.set_fp16(True)
+    try:
+        hk, hv = hip.alloc_cache(kh, cap, dh), hip.alloc_cache(kh, cap, dh)
+    finally:
+        hip.set_fp16(False)
+    fk, fv = hip.alloc_cache(kh, cap, dh), hip.alloc_cache(kh, cap, dh)  # fp32 outside fp16 mode
+    hip.write(hk, k)
+    hip.write(hv, v)
+    hip.write(fk, k)
+    hip.write(fv, v)
+    assert np.array_equal(hk.read(), k.ravel())
+    # the new rows: rounded by the store into the fp16 ring, stored pre-rounded into the fp32 one
+    spos = a["pos"]
+    sk, sv = hip.upload(new_k), hip.upload(new_v)
+    sk16, sv16 = hip.upload(_f16(new_k)), hip.upload(_f16(new_v))
+    hip.store(hk.ptr, sk.ptr, spos, m, cap, kh, dh)
+    hip.store(hv.ptr, sv.ptr, spos, m, cap, kh, dh)
+    hip.store(fk.ptr, sk16.ptr, spos, m, cap, kh, dh)
+    hip.store(fv.ptr, sv16.ptr, spos, m, cap, kh, dh)
+    assert np.array_equal(hk.read(), fk.read())
+    assert np.array_equal(hv.read(), fv.read())
+    dq = hip.upload(q)
+    y16, y32, yna = (hip.alloc(m * heads * dh) for _ in range(3))
+    hip.attend(y16.ptr, dq.ptr, hk.ptr, hv.ptr, **a)
+    hip.attend(y32.ptr, dq.ptr, fk.ptr, fv.ptr, **a)
+    assert np.array_equal(y16.read(), y32.read())
+    hip.attend_noalloc(yna.ptr, dq.ptr, hk.ptr, hv.ptr, **a)
+    assert np.array_equal(yna.read(), y32.read())
+    # against the oracle on the rounded values
+    want = O.attend(q, fk.read().reshape(kh, cap, dh), fv.read().reshape(kh, cap, dh), **a)
+    assert rel(y16.read(), want) < 1e-5
+
+
+def test_half_ring_refusals(hip):
+    """fp16 rings only where the fp16 kernels run: other shapes get fp32 caches; a ring pair
+    of mixed kinds is refused."""
+    hip.set_fp16(True)
+    try:
+        small = hip.alloc_cache(2, 32, 8)     # fewer than 64 slots: fp32
+        wide = hip.alloc_cache(2, 128, 128)   # head size above 64: fp32
+        half = hip.alloc_cache(2, 128, 64)
+    finally:
+        hip.set_fp16(False)
+    hip.write(small, np.arange(2 * 32 * 8, dtype=np.float32) + 0.1)
+    assert np.array_equal(small.read(), np.arange(2 * 32 * 8, dtype=np.float32) + 0.1)  # fp32 kept
+    hip.write(wide, np.full(2 * 128 * 128, 0.1, np.float32))
+    assert np.array_equal(wide.read(), np.full(2 * 128 * 128, 0.1, np.float32))
+    hip.write(half, np.full(2 * 128 * 64, 0.1, np.float32))
+    assert np.array_equal(half.read(), _f16(np.full(2 * 128 * 64, 0.1, np.float32)))  # rounded
+    f32 = hip.alloc(2 * 128 * 64)
+    q, y = hip.upload(rnd(1, 4, 64)), hip.alloc(4 * 64)
+    with pytest.raises(pkg_error()):
+        hip.attend(y.ptr, q.ptr, half.ptr, f32.ptr, pos=10, m=1, reach=64, gap=0, cap=128, heads=4,
+                   key_heads=2, dh=64, scale=0.125)
+    with pytest.raises(pkg_error()):  # an fp16 ring is not an fp32 buffer
+        hip.copy(y.ptr, half.ptr, 4 * 64)
+
+
+def pkg_error():
+    import slm_use_amd
+    return slm_use_amd.SlmError
+
+
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
+def test_grow_cache(hip, fp16):
+    """slm_hip_grow_cache: every head's rows at the start of its doubled rows, zeros after, for
+    fp32 and fp16 caches (model.rs:383-398's relayout)."""
+    kh, cap, dh = 3, 96, 64
+    x = _f16(rnd(kh, cap, dh))
+    hip.set_fp16(fp16)
+    try:
+        old, new = hip.alloc_cache(kh, cap, dh), hip.alloc_cache(kh, 2 * cap, dh)
+    finally:
+        hip.set_fp16(False)
+    hip.write(old, x)
+    hip.grow_cache(new, old, kh, cap, dh)
+    want = np.zeros((kh, 2 * cap, dh), np.float32)
+    want[:, :cap] = x
+    assert np.array_equal(new.read(), want.ravel())
+
+
+@pytest.mark.parametrize("fuse", [True, False], ids=["fused", "per_op"])
+def test_half_rings_in_a_decode_step(hip, fuse):
+    """The one-token attention block with fp16 rings inside a step: the QKV linear's rope and
+    ring-store epilogue (fused) or the per-op store kernel writes rounded values, and the
+    attention after it reads them; the same bits as the same step over fp32 rings whose
+    contents are those halves."""
+    d, heads, dh, cap, pos = 768, 12, 64, 4352, 4400
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(32), hip.alloc(32)
+    wqkv = hip.upload(rnd(3 * d, d, scale=0.02))
+    x = hip.upload(rnd(d))
+    k0, v0 = _f16(rnd(heads, cap, dh)), _f16(rnd(heads, cap, dh))
+    hip.set_fp16(True)
+    try:
+        rings = {"h": (hip.alloc_cache(heads, cap, dh), hip.alloc_cache(heads, cap, dh))}
+        rings["f"] = (hip.alloc(heads * cap * dh), hip.alloc(heads * cap * dh))
+        got = {}
+        for name, (kr, vr) in rings.items():
+            hip.write(kr, k0)
+            hip.write(vr, v0)
+            y, q, k, att = hip.alloc(3 * d), hip.alloc(d), hip.alloc(d), hip.alloc(d)
+
+            def body():
+                hip.linear(y.ptr, wqkv.ptr, 3 * d, d, x.ptr, 1)
+                hip.rope(q.ptr, y.ptr, cs.ptr, sn.ptr, 1, heads, dh)
+                hip.rope(k.ptr, y.at(d), cs.ptr, sn.ptr, 1, heads, dh)
+                hip.store(kr.ptr, k.ptr, pos, 1, cap, heads, dh)
+                hip.store(vr.ptr, y.at(2 * d), pos, 1, cap, heads, dh)
+                hip.attend(att.ptr, q.ptr, kr.ptr, vr.ptr, pos=pos, m=1, reach=4096, gap=0,
+                           cap=cap, heads=heads, key_heads=heads, dh=dh, scale=0.125)
+            if name == "f":  # the fp32 rings get the rounded new rows: store them rounded
+                def body():  # noqa: F811
+                    hip.linear(y.ptr, wqkv.ptr, 3 * d, d, x.ptr, 1)
+                    hip.rope(q.ptr, y.ptr, cs.ptr, sn.ptr, 1, heads, dh)
+                    hip.rope(k.ptr, y.at(d), cs.ptr, sn.ptr, 1, heads, dh)
+            _step(hip, body, inv, cs, sn, fuse)
+            if name == "f":
+                kk, vv = _f16(k.read()), _f16(y.read()[2 * d:])
+                hip.store(kr.ptr, hip.upload(kk).ptr, pos, 1, cap, heads, dh)
+                hip.store(vr.ptr, hip.upload(vv).ptr, pos, 1, cap, heads, dh)
+                hip.attend(att.ptr, q.ptr, kr.ptr, vr.ptr, pos=pos, m=1, reach=4096, gap=0,
+                           cap=cap, heads=heads, key_heads=heads, dh=dh, scale=0.125)
+            got[name] = (kr.read(), vr.read(), att.read(), q.read())
+    finally:
+        hip.set_fp16(False)
+    for a, b in zip(got["h"], got["f"]):
+        assert np.array_equal(a, b)
