@@ -202,8 +202,8 @@ int slm_hip_set_half_shadows(slm_hip* ctx, int on);
  * same arithmetic as the per-op kernels. Off: one launch per operation. */
 int slm_hip_set_fusion(slm_hip* ctx, int on);
 /* Rows per tile of the fused one-token GEMV (no trait counterpart; a test and measurement
- * switch): 0 (the default) lets the planner choose 16, 8 or 4 per linear (smaller tiles spread
- * a short matrix over more compute units); 16, 8 or 4 forces that size wherever the linear's
+ * switch): 0 (the default) lets the planner choose 16, 12, 8 or 4 per linear (smaller tiles spread
+ * a short matrix over more compute units); 16, 12, 8 or 4 forces that size wherever the linear's
  * row pairs allow it. Results are the same bits at every size. */
 int slm_hip_set_tile_rows(slm_hip* ctx, int rows);
 /* Counters for tests and benchmarks: graphs launched, graphs captured, eager steps. */

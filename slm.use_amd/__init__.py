@@ -351,7 +351,7 @@ class Hip:
         return s.value or 0
 
     def set_tile_rows(self, rows: int):
-        """Fused GEMV rows per tile: 0 = the planner's choice, or 16, 8, 4."""
+        """Fused GEMV rows per tile: 0 = the planner's choice, or 16, 12, 8, 4."""
         self.check(lib.slm_hip_set_tile_rows(self.ctx, int(rows)))
 
     def set_half_shadows(self, on: bool):

@@ -11,7 +11,7 @@
 //     fold of a split linear's partials, rope-table rows, the embedding row) that makes
 //     the GEMV input, then, per unit, add the slice partials in order and run the
 //     epilogue (residual add, rope + ring store, SiLU of the gate/amp pair).
-// A unit is one tile (16, 8 or 4 rows) of one split of one weight matrix; units go
+// A unit is one tile (16, 12, 8 or 4 rows) of one split of one weight matrix; units go
 // round-robin over the grid. Every value is computed with the same expression, in the same order, as the
 // per-op kernels, so fused and unfused runs give the same bits.
 #ifndef SLM_FUSION_H
@@ -82,8 +82,8 @@ typedef struct {
     float pad2;
 } VpOp;
 
-// One weight matrix of a fused GEMV. Its rows are grouped into tiles of rpt rows (16, 8 or
-// 4; a tile fills rows 0..rpt-1 of the 16-row MFMA operand, the other rows are zeros): the
+// One weight matrix of a fused GEMV. Its rows are grouped into tiles of rpt rows (16, 12, 8
+// or 4; a tile fills rows 0..rpt-1 of the 16-row MFMA operand, the other rows are zeros): the
 // first pair_rows rows (a multiple of 16) in tiles of rpt/2 (row, row + half) pairs, pair P
 // at row (P / half)·2·half + P % half (the rope halves of a head, or the gate and amp rows of
 // a SiLU pair), the rest in consecutive rows. Each row's chain is the same whatever the

@@ -3023,15 +3023,16 @@ __device__ __forceinline__ FgUnit fg_unit(const FgDesc& d, int u) {
     return FgUnit{k, local % s.tiles, local / s.tiles};
 }
 
-// Row of lane row i (0..15) of tile t of a matrix of `rows` rows in tiles of rpt rows (lane
-// rows past rpt hold none: `rows` is returned, one past the last). In the first pair_rows
-// rows lane rows i and i + rpt/2 hold a (row, row + half) pair.
+// Row of lane row i (0..15) of tile t of a matrix of `rows` rows in tiles of rpt rows (16, 12,
+// 8 or 4; lane rows past rpt hold none: `rows` is returned, one past the last). In the first
+// pair_rows rows lane rows i and i + rpt/2 hold a (row, row + half) pair.
 __device__ __forceinline__ long long fg_row_of(int rpt, int pair_rows, int half, int rows, int t, int i) {
     if (i >= rpt) return rows;
     int hp = rpt >> 1;
     if (t * rpt < pair_rows) {
-        int P = t * hp + (i & (hp - 1));
-        return (long long)(P / half) * 2 * half + P % half + ((i & hp) ? half : 0);
+        bool second = i >= hp;
+        int P = t * hp + (second ? i - hp : i);
+        return (long long)(P / half) * 2 * half + P % half + (second ? half : 0);
     }
     return (long long)t * rpt + i;
 }

@@ -1470,7 +1470,7 @@ struct Planner {
         s.epi = EPI_PLAIN;
     }
 
-    // Rows per tile of a one-matrix fused GEMV: 16, 8 or 4, whichever gives the least
+    // Rows per tile of a one-matrix fused GEMV: 16, 12, 8 or 4, whichever gives the least
     // estimated time per workgroup — rounds of two units (a load latency each, ≈1 us) plus
     // the weight bytes of the busiest workgroup at ≈24 KB/us (a compute unit's share of HBM
     // when every one streams); a smaller tile must gain a tenth. Smaller tiles spread a short
@@ -1480,7 +1480,7 @@ struct Planner {
         int64_t split_cols = std::min<int64_t>(cols, (int64_t)SLM_SPLIT * SLM_KS * 16);
         int best = 16;
         double best_t = 0.0;
-        for (int rpt : {16, 8, 4}) {
+        for (int rpt : {16, 12, 8, 4}) {
             if (s.pair_rows % rpt) continue;
             int64_t units = (s.rows + rpt - 1) / rpt * s.nsplit;
             int64_t grid = std::min<int64_t>(units, FG_GRID_MAX);
@@ -2978,7 +2978,7 @@ int slm_hip_set_fp16(slm_hip* c, int on) {
 }
 
 int slm_hip_set_tile_rows(slm_hip* c, int rows) {
-    if (!c || (rows != 0 && rows != 4 && rows != 8 && rows != 16)) return SLM_E_INVALID;
+    if (!c || (rows != 0 && rows != 4 && rows != 8 && rows != 12 && rows != 16)) return SLM_E_INVALID;
     if (c->recording) TRY(finish_step(c));
     if (c->fg_rpt != rows) drop_graphs(c);
     c->fg_rpt = rows;

@@ -311,12 +311,12 @@ FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "comb
                 "split_fold", "split_flush", "gla_l2", "rounds", "row_offset"]
 
 
-@pytest.mark.parametrize("tile", [0, 16, 8, 4], ids=["tile_auto", "tile16", "tile8", "tile4"])
+@pytest.mark.parametrize("tile", [0, 16, 12, 8, 4], ids=["tile_auto", "tile16", "tile12", "tile8", "tile4"])
 @pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
 @pytest.mark.parametrize("case", FUSION_CASES)
 def test_fusion_pattern(hip, case, fp16, tile):
     """Every fused one-token pattern gives the bits of one launch per op, with the fused
-    GEMV's rows per tile chosen by the planner or forced to 16, 8 or 4 (each row's chain is
+    GEMV's rows per tile chosen by the planner or forced to 16, 12, 8 or 4 (each row's chain is
     the same whatever the tile: the rope and SiLU row pairs, the residual, the split
     partials and the pick follow their rows)."""
     d, heads, dh, hid, cap = 768, 12, 64, 3072, 4352
@@ -525,7 +525,7 @@ def _pick_rows(case, rows, cols=64):
     return w
 
 
-@pytest.mark.parametrize("tile", [0, 4], ids=["tile_auto", "tile4"])
+@pytest.mark.parametrize("tile", [0, 12, 4], ids=["tile_auto", "tile12", "tile4"])
 @pytest.mark.parametrize("rows", [32000, 40])
 @pytest.mark.parametrize("case", ["random", "ties", "nan_first", "nan_inside", "all_neg_inf",
                                   "signed_zero"])
