@@ -60,8 +60,12 @@ size_t slm_session_state_bytes(const slm_session* s);
 size_t slm_session_kept_count(const slm_session* s);
 size_t slm_session_kept_len(const slm_session* s, size_t i);
 int slm_session_kept_read(slm_session* s, size_t i, float* out, size_t n);
+/* sample.rs:48-53's greedy pick on the host: the index b that b = 0, b = i whenever l[i] >
+ * l[b] ends on (the first maximum; NaNs never win, a NaN at index 0 keeps 0). A host function:
+ * no context or device. */
+size_t slm_pick_greedy(const float* logits, size_t n);
 /* The decode loop of src/main.rs:207-223: n times, read the logits, pick greedily
- * (src/sample.rs:48-53, the first maximum wins) and step; ids[i] receives each pick. */
+ * (slm_pick_greedy) and step; ids[i] receives each pick. */
 int slm_session_decode_greedy(slm_session* s, size_t n, uint32_t* ids);
 /* The same loop with the pick on the device (replaces the per-token logits read-back and host
  * scan of main.rs:219-222 and sample.rs:48-53 for greedy decoding): each step's logits GEMV is

@@ -127,6 +127,7 @@ _SIGS = {
     "slm_session_kept_len": (_sz, [_p, _sz]),
     "slm_session_kept_read": (_i, [_p, _sz, _f32p, _sz]),
     "slm_session_decode_greedy": (_i, [_p, _sz, _u32p]),
+    "slm_pick_greedy": (_sz, [_f32p, _sz]),
     "slm_session_decode_greedy_device": (_i, [_p, _sz, _u32p]),
 }
 for _name, (_res, _args) in _SIGS.items():
@@ -494,3 +495,9 @@ def header_symbols() -> list:
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names += re.findall(r"^\s*[\w\s\*]+?\b(slm_\w+)\s*\(", text, flags=re.M)
     return sorted(set(names))
+
+
+def pick_greedy(logits) -> int:
+    """sample.rs:48-53's greedy pick, as the model twin's host decode loop runs it."""
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    return int(lib.slm_pick_greedy(_fp(a), a.size))

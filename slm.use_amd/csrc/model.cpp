@@ -14,6 +14,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <emmintrin.h>
 #include <limits>
 #include <map>
 #include <stdexcept>
@@ -1123,6 +1124,41 @@ int slm_session_kept_read(slm_session* s, size_t i, float* out, size_t n) {
     });
 }
 
+// sample.rs:48-53, the greedy pick: b = 0, then b = i whenever l[i] > l[b]. That is the first
+// index holding the largest value under `>` (NaNs never win; a NaN at 0 keeps 0, since nothing
+// compares greater than it; −0 and +0 are one value). Found in two passes that do not wait on
+// each other element by element: the largest value with eight running maxima (x > m ? x : m,
+// which skips NaNs), then the first index whose value equals it (== also takes −0 for +0).
+// (SSE2, part of every x86-64 host: _mm_max_ps(x, m) is x > m ? x : m lane by lane, so a NaN in
+// x leaves m; _mm_cmpeq_ps finds the lanes equal to the maximum.)
+size_t slm_pick_greedy(const float* l, size_t n) {
+    if (n == 0 || l[0] != l[0]) return 0;
+    __m128 a0 = _mm_set1_ps(l[0]), a1 = a0, a2 = a0, a3 = a0;
+    size_t i = 0;
+    for (; i + 16 <= n; i += 16) {
+        a0 = _mm_max_ps(_mm_loadu_ps(l + i), a0);
+        a1 = _mm_max_ps(_mm_loadu_ps(l + i + 4), a1);
+        a2 = _mm_max_ps(_mm_loadu_ps(l + i + 8), a2);
+        a3 = _mm_max_ps(_mm_loadu_ps(l + i + 12), a3);
+    }
+    float acc[16];
+    _mm_storeu_ps(acc, a0);
+    _mm_storeu_ps(acc + 4, a1);
+    _mm_storeu_ps(acc + 8, a2);
+    _mm_storeu_ps(acc + 12, a3);
+    float m = acc[0];
+    for (int k = 1; k < 16; k++) m = acc[k] > m ? acc[k] : m;
+    for (; i < n; i++) m = l[i] > m ? l[i] : m;
+    __m128 mv = _mm_set1_ps(m);
+    for (i = 0; i + 4 <= n; i += 4) {
+        int hit = _mm_movemask_ps(_mm_cmpeq_ps(_mm_loadu_ps(l + i), mv));
+        if (hit) return i + (size_t)__builtin_ctz((unsigned)hit);
+    }
+    for (; i < n; i++)
+        if (l[i] == m) return i;
+    return 0;
+}
+
 int slm_session_decode_greedy(slm_session* s, size_t n, uint32_t* ids) {
     if (!s || (n && !ids)) return SLM_E_INVALID;
     return guard(s->model, [&] {
@@ -1131,10 +1167,7 @@ int slm_session_decode_greedy(slm_session* s, size_t n, uint32_t* ids) {
         std::vector<float> l(V);
         for (size_t t = 0; t < n; t++) {
             M.ops.ok(slm_hip_read(M.ops.ctx(), l.data(), s->logits.p, V), "read");
-            size_t b = 0;  // sample.rs:48-53: b = i whenever l[i] > l[b] (the first maximum; NaNs never win)
-            for (size_t i = 0; i < V; i++)
-                if (l[i] > l[b]) b = i;
-            ids[t] = (uint32_t)b;
+            ids[t] = (uint32_t)slm_pick_greedy(l.data(), V);
             advance(M, *s, &ids[t], 1, true);
         }
     });

@@ -49,3 +49,37 @@ def test_no_device_is_not_an_error(pkg):
     with pytest.raises(pkg.NoDevice):
         pkg.Hip(0)
     assert pkg.lib.slm_hip_last_error(None) == b"no usable AMD GPU"
+
+
+def _ref_pick(l):
+    """sample.rs:48-53 as written: b = 0, b = i whenever l[i] > l[b]."""
+    b = 0
+    for i in range(len(l)):
+        if l[i] > l[b]:
+            b = i
+    return b
+
+
+def test_host_greedy_pick(pkg):
+    """The twin's host pick (slm_pick_greedy, two passes) against sample.rs's loop as written and
+    against the oracle's pick: ties (the first wins), NaN at 0 and inside, all -inf, +-0,
+    infinities, one and 1025 elements, and random logits of the vocabulary's size."""
+    import numpy as np
+    import oracle as O
+
+    nan, inf = float("nan"), float("inf")
+    cases = [[0.0], [1.0, 1.0, 0.5], [0.0, 3.0, 1.0], [nan, 5.0, 9.0], [1.0, nan, 2.0, nan],
+             [-inf, -inf, -inf], [-0.0, 0.0, -0.0], [0.0, -0.0], [-1.0, inf, inf], [-inf, nan, -inf],
+             [nan, nan], [3.0, 2.0, 3.0, 3.0], list(np.arange(1025, dtype=np.float32) % 7)]
+    rng = np.random.default_rng(5)
+    for _ in range(40):
+        x = rng.standard_normal(32000).astype(np.float32)
+        if rng.random() < 0.5:
+            x[rng.integers(0, 32000, 3)] = x.max()  # ties at the maximum
+        if rng.random() < 0.3:
+            x[rng.integers(0, 32000, 5)] = nan
+        cases.append(list(x))
+    for c in cases:
+        a = np.asarray(c, dtype=np.float32)
+        want = _ref_pick(a.tolist())
+        assert pkg.pick_greedy(a) == want == O.pick(a), c[:8]
