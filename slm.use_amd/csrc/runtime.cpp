@@ -2420,7 +2420,8 @@ void drop_shadows(slm_hip* c, uintptr_t a, uintptr_t b) {
 // fp16 mode: the fp16 shadow of the n fp32 weights at w, made on first use by a conversion
 // queued now (ahead of the step being recorded, whose ops run later on the same stream), or
 // null when the weights are written inside the step being recorded before this linear reads
-// them (the linear then reads the fp32 weights and rounds them itself: the same bits).
+// them, or when the copy cannot be allocated (the linear then reads the fp32 weights and
+// rounds them itself: the same bits).
 int shadow_of(slm_hip* c, const float* w, size_t n, const float** out) {
     *out = nullptr;
     auto it = c->shadows.find((uintptr_t)w);
@@ -2441,7 +2442,10 @@ int shadow_of(slm_hip* c, const float* w, size_t n, const float** out) {
     }
     if (it != c->shadows.end()) drop_shadows(c, (uintptr_t)w, (uintptr_t)w + 1);  // too short
     void* h = nullptr;
-    HIPC(c, dev_alloc(c, n * 2, &h));
+    if (dev_alloc(c, n * 2, &h) != hipSuccess) {  // no room for a copy: the fp32 weights serve
+        (void)hipGetLastError();
+        return SLM_OK;
+    }
     int rc = launch_now(c, mk(c->k.to_half, blocks_for(n), 1, 1, 256, 0, h, w, (long long)n));
     if (rc) {
         hipStreamSynchronize(c->stream);
