@@ -181,6 +181,21 @@ int slm_hip_attend_noalloc(slm_hip* ctx, float* y, float* scores, const float* q
  * or upload inside a step runs what was recorded so far and finishes the step eagerly.
  * Results are identical in every mode: the same arithmetic runs. */
 int slm_hip_set_graphs(slm_hip* ctx, int on);
+/* Prompt lanes (1 to 4; no trait counterpart, a backend setting): consecutive prompt steps
+ * (advances of more than one token, ended by a flush) run on up to n streams at once, so
+ * that chunk c + 1 starts while chunk c still runs. What a step writes and its flush does not
+ * keep is dead once the step is over (ops.rs:90-91): on lanes other than the first the step
+ * writes it into copies of the lane's own, and a lane waits for another only before its first
+ * kernel that may touch a kept buffer (a ring, a state, a cache) that the other used last.
+ * Anything else on the context (a read, an upload, a free, a one-token step) first waits for
+ * every lane. A step that reads scratch before writing it, frees or grows a buffer, or holds
+ * a one-token attention or a device pick runs on the context's stream as before. Results
+ * are identical for any n: the same kernels run on the same values. */
+int slm_hip_set_prompt_lanes(slm_hip* ctx, int n);
+/* The prompt lanes in use. */
+int slm_hip_get_prompt_lanes(slm_hip* ctx, int* n);
+/* Prompt steps run on a lane, and those that could not, since the context opened. */
+int slm_hip_prompt_lane_stats(slm_hip* ctx, uint64_t* steps, uint64_t* fallbacks);
 /* fp16 mode (off by default), the analogue of the reference's --fp16 (mlx.rs:19-23,
  * main.rs:421-423, where it selects Float16 for every MLX buffer): from this call on, every
  * linear rounds both operands to fp16 (to nearest even) at fp16 MFMAs and sums in fp32;

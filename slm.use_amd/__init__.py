@@ -92,6 +92,9 @@ _SIGS = {
     "slm_hip_attend": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_attend_noalloc": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_set_graphs": (_i, [_p, _i]),
+    "slm_hip_set_prompt_lanes": (_i, [_p, _i]),
+    "slm_hip_get_prompt_lanes": (_i, [_p, C.POINTER(C.c_int)]),
+    "slm_hip_prompt_lane_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "slm_hip_set_fusion": (_i, [_p, _i]),
     "slm_hip_set_fp16": (_i, [_p, _i]),
     "slm_hip_graph_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
@@ -248,6 +251,19 @@ class Hip:
 
     def set_graphs(self, on: bool):
         self.check(lib.slm_hip_set_graphs(self.ctx, int(on)))
+
+    def set_prompt_lanes(self, n: int):
+        self.check(lib.slm_hip_set_prompt_lanes(self.ctx, int(n)))
+
+    def prompt_lanes(self) -> int:
+        n = C.c_int()
+        self.check(lib.slm_hip_get_prompt_lanes(self.ctx, C.byref(n)))
+        return n.value
+
+    def lane_stats(self):
+        a, b = C.c_uint64(), C.c_uint64()
+        self.check(lib.slm_hip_prompt_lane_stats(self.ctx, C.byref(a), C.byref(b)))
+        return dict(steps=a.value, fallbacks=b.value)
 
     def last_plan(self):
         a, b = C.c_uint64(), C.c_uint64()

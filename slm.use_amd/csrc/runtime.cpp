@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -42,6 +43,7 @@ constexpr size_t BLOB = 2048;             // bytes of kernel arguments per launc
 constexpr size_t DYN_CAP = 1 << 20;       // bytes of per-step dynamic values
 constexpr size_t STAGE_CAP = 4 << 20;     // bytes of eager staging
 constexpr size_t BOUNCE_CAP = 4 << 20;    // pinned bounce buffer for reads
+constexpr int MAX_LANES = 4;              // prompt lanes (streams) a context may use
 constexpr size_t MAX_GRAPHS = 8;
 constexpr int VP_LEN_MAX = 4096;          // longest vector a fused prologue holds
 constexpr int64_t COMB_PART_MAX = 16384;  // attention partials (floats) a fused prologue combines
@@ -202,6 +204,43 @@ struct slm_hip {
     std::vector<Graph> cache;
     uint64_t clock = 0, n_launched = 0, n_captured = 0, n_eager = 0;
     uint64_t last_ops = 0, last_kernels = 0;  // of the last step the planner lowered
+
+    // Prompt lanes: consecutive prompt steps run on up to MAX_LANES streams at once, each
+    // lane writing the step's scratch (what the step writes and its flush does not keep:
+    // dead once the step is over, ops.rs:90-91) into copies of its own, and waiting for the
+    // other lanes only where a kept buffer (ring, state, cache) was last used by them.
+    struct Lane {
+        hipStream_t stream = nullptr;    // lane 0 is the context's stream and buffers
+        float* ws = nullptr;
+        size_t ws_bytes = 0;
+        float* gpart = nullptr;
+        size_t gpart_bytes = 0;
+        float* part = nullptr;
+        size_t part_bytes = 0;
+        unsigned char* dyn_dev = nullptr;
+        unsigned char* dyn_pin[2] = {nullptr, nullptr};
+        hipEvent_t dyn_ev[2] = {nullptr, nullptr};
+        int dyn_flip = 0;
+        std::map<uintptr_t, std::pair<void*, size_t>> copies;  // allocation -> (copy, bytes)
+        bool used = false;               // work queued since the lanes were entered
+    };
+    struct Touch {
+        int lane;
+        hipEvent_t ev;                   // recorded after that lane's last use of the buffer
+    };
+    std::vector<Lane> lanes;             // [0, nlanes); lanes[0] unused (the context's own)
+    int nlanes = 1, next_lane = 0;
+    bool lanes_active = false;           // lanes entered: the context's stream not joined yet
+    bool lane_launching = false;         // launch_now queues on lane_stream
+    hipStream_t lane_stream = nullptr;
+    std::vector<uintptr_t> keep;         // allocations the flush being run names
+    bool keep_valid = false;
+    std::map<uintptr_t, Touch> touch;    // kept allocation -> its last lane use
+    std::map<hipEvent_t, int> ev_refs;   // touch entries per event
+    std::vector<hipEvent_t> lane_ev_pool;
+    std::set<uintptr_t> l0_written;      // scratch lane 0 wrote in place since entering
+    std::set<uintptr_t> ln_read;         // allocations other lanes read in place since entering
+    uint64_t n_lane_steps = 0, n_lane_fallbacks = 0;
 };
 
 namespace {
@@ -372,10 +411,57 @@ hipEvent_t pool_event(slm_hip* c) {
     return e;
 }
 
+// ---- prompt lanes: ordering ----
+
+hipEvent_t lane_event(slm_hip* c) {
+    if (!c->lane_ev_pool.empty()) {
+        hipEvent_t e = c->lane_ev_pool.back();
+        c->lane_ev_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
+    return e;
+}
+
+void ev_unref(slm_hip* c, hipEvent_t e) {
+    auto it = c->ev_refs.find(e);
+    if (it == c->ev_refs.end() || --it->second > 0) return;
+    c->ev_refs.erase(it);
+    c->lane_ev_pool.push_back(e);  // (a wait already queued on it keeps what it waited for)
+}
+
+// Orders the context's stream after all the lanes' work, so that whatever the host queues or
+// waits for on it next comes after every prompt step, and leaves the lanes.
+void leave_lanes(slm_hip* c) {
+    if (!c->lanes_active) return;
+    c->lanes_active = false;
+    for (int l = 1; l < c->nlanes; l++) {
+        auto& L = c->lanes[l];
+        if (!L.used) continue;
+        L.used = false;
+        hipEvent_t e = lane_event(c);
+        if (!e || hipEventRecord(e, L.stream) != hipSuccess ||
+            hipStreamWaitEvent(c->stream, e, 0) != hipSuccess)
+            hipStreamSynchronize(L.stream);  // no event: the host waits for the lane instead
+        if (e) c->lane_ev_pool.push_back(e);
+    }
+    for (auto& t : c->touch) ev_unref(c, t.second.ev);
+    c->touch.clear();
+    c->l0_written.clear();
+    c->ln_read.clear();
+}
+
+// The context's stream, for work that is not a lane's: joined with the lanes first.
+hipStream_t mstream(slm_hip* c) {
+    leave_lanes(c);
+    return c->stream;
+}
+
 // Reads the events of the timed launches into the per-kernel statistics.
 int collect_timing(slm_hip* c) {
     if (c->timed.empty()) return SLM_OK;
-    HIPC(c, hipStreamSynchronize(c->stream));
+    HIPC(c, hipStreamSynchronize(mstream(c)));
     for (auto& t : c->timed) {
         float ms = 0.0f;
         HIPC(c, hipEventElapsedTime(&ms, t.a, t.b));
@@ -396,8 +482,8 @@ int collect_timing(slm_hip* c) {
 // Never inside a capture: a fill recorded into a graph is not replayed reliably.
 void reset_counters(slm_hip* c) {
     if (c->capturing) return;
-    hipMemsetAsync(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int), c->stream);
-    hipMemsetAsync(c->pick, 0, 16 * sizeof(float), c->stream);
+    hipMemsetAsync(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int), mstream(c));
+    hipMemsetAsync(c->pick, 0, 16 * sizeof(float), mstream(c));
 }
 
 int launch_now(slm_hip* c, const Rec& r) {
@@ -407,9 +493,10 @@ int launch_now(slm_hip* c, const Rec& r) {
     } else {
         for (uint32_t i = 0; i < r.nargs; i++) ptrs[i] = (void*)(r.blob + 8 * i);
     }
-    bool timed = c->timing && !c->capturing;
+    bool timed = c->timing && !c->capturing && !c->lane_launching;
     if (!timed) {
-        hipError_t e = hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream,
+        hipStream_t s = c->lane_launching ? c->lane_stream : mstream(c);
+        hipError_t e = hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, s,
                                              ptrs, nullptr);
         if (e != hipSuccess) {
             reset_counters(c);
@@ -428,7 +515,7 @@ int launch_now(slm_hip* c, const Rec& r) {
     Timed t{pool_event(c), pool_event(c), r.f, r.abytes};
     if (!t.a || !t.b) return fail(c, SLM_E_HIP, "hipEventCreate failed");
     hipError_t e = hipExtModuleLaunchKernel(r.f, (uint32_t)items, r.gy, r.gz, r.bx, 1, 1, r.shmem,
-                                            c->stream, ptrs, nullptr, t.a, t.b, 0);
+                                            mstream(c), ptrs, nullptr, t.a, t.b, 0);
     if (e != hipSuccess) {
         c->ev_pool.push_back(t.a);
         c->ev_pool.push_back(t.b);
@@ -453,7 +540,7 @@ int pow2_index(size_t need, int maxi) {  // smallest i with 2^i >= need
 
 void drop_graphs(slm_hip* c) {
     if (c->cache.empty()) return;
-    hipStreamSynchronize(c->stream);
+    hipStreamSynchronize(mstream(c));
     for (auto& g : c->cache)
         if (g.exec) hipGraphExecDestroy(g.exec);
     c->cache.clear();
@@ -1017,10 +1104,18 @@ int64_t nsplit_of(int64_t cols) {
     return (nsl + SLM_SPLIT - 1) / SLM_SPLIT;
 }
 
+// Where the planner stood between two ops it took: `out` kernels emitted so far, `next` the
+// next op it takes, `low` the first op not yet inside an emitted kernel (ops it holds back
+// for a later kernel: prologue ops, row chains, l2norms).
+struct PlanMark {
+    size_t out, next, low;
+};
+
 struct Planner {
     slm_hip* c;
     const std::vector<Op>& ops;
     std::vector<Rec>& out;
+    std::vector<PlanMark>* marks = nullptr;
     std::vector<VpSrc> pend;
     int part_flip = 0;
     std::vector<VpSrc> next_pend;  // what a fused kernel leaves pending (a split's fold)
@@ -1034,6 +1129,7 @@ struct Planner {
         int lds;
     };
     int64_t rrows = 0;               // the chain's token rows (0: no chain)
+    size_t rstart = 0;               // index of the op the chain started at
     size_t rnext = 0;                // index of the first op after the chain
     int64_t last_m = 0;              // tokens of the last prompt linear
     RowDesc rd{};
@@ -1310,6 +1406,7 @@ struct Planner {
             Range foot;
             if (!row_lower(o, R, &ro, &foot)) return false;
             rrows = R;
+            rstart = (size_t)(&o - ops.data());
             if (row_add(&o, ro, foot)) return true;
             row_reset();
             return false;
@@ -2050,9 +2147,26 @@ struct Planner {
         return 7;
     }
 
+    void mark(size_t i) {
+        if (!marks) return;
+        size_t low = i;
+        auto at = [&](const Op* o) { low = std::min(low, (size_t)(o - ops.data())); };
+        for (auto& v : pend)
+            if (v.op) at(v.op);
+        if (l2q) at(l2q);
+        if (l2k) at(l2k);
+        if (rrows) {
+            low = std::min(low, rstart);
+            for (const Op* o : rsrc)
+                if (o) at(o);
+        }
+        marks->push_back({out.size(), i, low});
+    }
+
     int run(bool fuse) {
         size_t i = 0;
         while (i < ops.size()) {
+            mark(i);
             const Op& o = ops[i];
             VpSrc v;
             // one-token attention: its partials wait for the next fused prologue to combine
@@ -2141,6 +2255,7 @@ struct Planner {
                     ro.y = (float*)o.p[0];
                     ro.ystride = rows;
                     rrows = m;
+                    rstart = i;
                     rnext = i + 1;
                     if (rows > 16384 || !row_add(nullptr, ro, rows_rng(o.p[0], rows, rows, m))) {
                         row_reset();
@@ -2163,12 +2278,15 @@ struct Planner {
         }
         TRY(row_flush());
         TRY(flush_pending());
-        return flush_l2();
+        TRY(flush_l2());
+        if (marks) marks->push_back({out.size(), ops.size(), ops.size()});
+        return SLM_OK;
     }
 };
 
-int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fuse) {
-    Planner p{c, ops, out, {}};
+int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fuse,
+         std::vector<PlanMark>* marks = nullptr) {
+    Planner p{c, ops, out, marks, {}};
     size_t before = out.size();
     TRY(p.run(fuse));
     if (c->plan_trace) {
@@ -2207,15 +2325,22 @@ int plan(slm_hip* c, const std::vector<Op>& ops, std::vector<Rec>& out, bool fus
 // dynamic values, recording, graphs
 // ---------------------------------------------------------------------------------------
 
+// The step's dynamic values into `dev` on stream s, through one of two pinned buffers (the
+// other may still be in flight).
+int upload_dyn_on(slm_hip* c, unsigned char* dev, unsigned char* const* pin, const hipEvent_t* ev,
+                  int* flip, hipStream_t s) {
+    if (c->dyn.empty()) return SLM_OK;
+    int k = *flip ^= 1;
+    HIPC(c, hipEventSynchronize(ev[k]));
+    std::memcpy(pin[k], c->dyn.data(), c->dyn.size());
+    HIPC(c, hipMemcpyAsync(dev, pin[k], c->dyn.size(), hipMemcpyHostToDevice, s));
+    HIPC(c, hipEventRecord(ev[k], s));
+    return SLM_OK;
+}
+
 int upload_dyn(slm_hip* c) {
     if (c->dyn.empty()) return SLM_OK;
-    int k = c->dyn_flip ^= 1;
-    HIPC(c, hipEventSynchronize(c->dyn_ev[k]));
-    std::memcpy(c->dyn_pin[k], c->dyn.data(), c->dyn.size());
-    HIPC(c, hipMemcpyAsync(c->dyn_dev, c->dyn_pin[k], c->dyn.size(), hipMemcpyHostToDevice,
-                           c->stream));
-    HIPC(c, hipEventRecord(c->dyn_ev[k], c->stream));
-    return SLM_OK;
+    return upload_dyn_on(c, c->dyn_dev, c->dyn_pin, c->dyn_ev, &c->dyn_flip, mstream(c));
 }
 
 int launch_all(slm_hip* c, const std::vector<Rec>& recs) {
@@ -2290,12 +2415,12 @@ int stage(slm_hip* c, const void* src, size_t bytes, const void** out) {
     }
     if (need > STAGE_CAP) return fail(c, SLM_E_UNSUPPORTED, "stage: %zu bytes at once", bytes);
     if (c->stage_head + need > STAGE_CAP) {
-        HIPC(c, hipStreamSynchronize(c->stream));
+        HIPC(c, hipStreamSynchronize(mstream(c)));
         c->stage_head = 0;
     }
     std::memcpy(c->stage_host + c->stage_head, src, bytes);
     HIPC(c, hipMemcpyAsync(c->stage_dev + c->stage_head, c->stage_host + c->stage_head, need,
-                           hipMemcpyHostToDevice, c->stream));
+                           hipMemcpyHostToDevice, mstream(c)));
     *out = c->stage_dev + c->stage_head;
     c->stage_head += need;
     return SLM_OK;
@@ -2409,7 +2534,7 @@ void drop_shadows(slm_hip* c, uintptr_t a, uintptr_t b) {
         if (c->recording) {
             c->free_after_step.push_back(it->second.h);
         } else {
-            if (!synced) hipStreamSynchronize(c->stream);
+            if (!synced) hipStreamSynchronize(mstream(c));
             synced = true;
             dev_free(c, it->second.h);
         }
@@ -2448,7 +2573,7 @@ int shadow_of(slm_hip* c, const float* w, size_t n, const float** out) {
     }
     int rc = launch_now(c, mk(c->k.to_half, blocks_for(n), 1, 1, 256, 0, h, w, (long long)n));
     if (rc) {
-        hipStreamSynchronize(c->stream);
+        hipStreamSynchronize(mstream(c));
         dev_free(c, h);
         return rc;
     }
@@ -2483,6 +2608,251 @@ int need_ws(slm_hip* c, size_t bytes) {
     return SLM_OK;
 }
 
+// ---- prompt lanes: running a step on one ----
+
+// The live allocation holding address a: its start and size (false: none does).
+bool alloc_at(const slm_hip* c, uintptr_t a, uintptr_t* base, size_t* bytes) {
+    auto it = c->allocs.upper_bound(a);
+    if (it == c->allocs.begin()) return false;
+    --it;
+    if (a >= it->first + it->second) return false;
+    *base = it->first;
+    *bytes = it->second;
+    return true;
+}
+
+// A lane's own internal buffer of at least `bytes` (the one it replaces may still be read by
+// the lane's queued work: retired, freed at close).
+bool lane_buf(slm_hip* c, float** p, size_t* have, size_t bytes) {
+    if (bytes <= *have) return true;
+    void* np = nullptr;
+    if (dev_alloc(c, bytes, &np) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (*p) c->retired.push_back(*p);
+    *p = (float*)np;
+    *have = bytes;
+    return true;
+}
+
+// Orders the lanes after everything queued on the context's stream so far and enters them.
+int enter_lanes(slm_hip* c) {
+    if (c->lanes_active) return SLM_OK;
+    hipEvent_t e = lane_event(c);
+    if (!e) return fail(c, SLM_E_HIP, "lanes: hipEventCreate failed");
+    hipError_t err = hipEventRecord(e, c->stream);
+    for (int l = 1; l < c->nlanes && err == hipSuccess; l++)
+        err = hipStreamWaitEvent(c->lanes[l].stream, e, 0);
+    c->lane_ev_pool.push_back(e);
+    if (err != hipSuccess) {
+        for (int l = 1; l < c->nlanes; l++) hipStreamSynchronize(c->lanes[l].stream);
+        return fail(c, SLM_E_HIP, "lanes: %s", hipGetErrorString(err));
+    }
+    c->lanes_active = true;
+    c->next_lane = 0;
+    return SLM_OK;
+}
+
+int lane_fallback(slm_hip* c) {
+    c->n_lane_fallbacks++;
+    return SLM_OK;
+}
+
+// Runs the recorded prompt step on the next lane (*handled set), or leaves it to the caller
+// with nothing queued (*handled clear) when a lane cannot take it: the step reads scratch
+// before writing it, frees or grows a buffer, holds a one-token attention or pick (the
+// context's own counters), or touches in place what another lane of this session wrote or
+// read without an event. On a lane other than 0 the step's scratch allocations are renamed
+// to the lane's copies (same sizes, same offsets) and its dynamic values, attention and
+// split partials go to the lane's buffers. Before the first kernel that may touch a kept
+// allocation the lane waits for the event after another lane's last use of it; after the
+// last kernel that may touch it the lane records one. The kernels' footprints come from the
+// planner's marks: a kernel emitted before the planner took op i holds no op from i on; every
+// op before a mark's `low` is inside a kernel emitted before that mark.
+int run_lane_step(slm_hip* c, int* handled) {
+    *handled = 0;
+    if (c->nlanes < 2 || !c->keep_valid || c->timing || c->capturing) return SLM_OK;
+    if (!c->free_after_step.empty()) return lane_fallback(c);
+    const int lane = c->lanes_active ? c->next_lane : 0;
+    const std::vector<Op>& ops = c->ops;
+    struct Use {
+        size_t first = SIZE_MAX, last = 0, bytes = 0;
+        bool written = false, read_first = false;
+    };
+    std::map<uintptr_t, Use> use;
+    const uintptr_t dyn_a = (uintptr_t)c->dyn_dev, dyn_b = dyn_a + DYN_CAP;
+    auto note = [&](const Range& r, size_t i, bool w) {
+        uintptr_t b;
+        size_t n;
+        if (r.a >= r.b || !alloc_at(c, r.a, &b, &n)) return;  // internal: tables, fp16 copies
+        Use& u = use[b];
+        u.bytes = n;
+        if (u.first == SIZE_MAX) {
+            u.first = i;
+            u.read_first = !w;
+        }
+        u.last = i;
+        u.written |= w;
+    };
+    std::vector<Range> rd, wr;
+    for (size_t i = 0; i < ops.size(); i++) {
+        const Op& o = ops[i];
+        if (o.kind == OP_ARGMAX || o.kind == OP_GROW || (o.kind == OP_ATTEND && o.n[1] == 1))
+            return lane_fallback(c);
+        if (o.dyn && ((uintptr_t)o.dyn < dyn_a || (uintptr_t)o.dyn >= dyn_b)) return lane_fallback(c);
+        rd.clear();
+        wr.clear();
+        op_ranges(o, rd, wr);
+        for (const Range& r : rd) note(r, i, false);
+        for (const Range& r : wr) note(r, i, true);
+    }
+    std::set<uintptr_t> kept(c->keep.begin(), c->keep.end());
+    std::vector<uintptr_t> scratch, deps, ronly;
+    for (auto& [b, u] : use) {
+        bool k = kept.count(b) != 0;
+        if (k)
+            deps.push_back(b);
+        else if (!u.written)
+            ronly.push_back(b);
+        else if (u.read_first || c->halves.count(b))
+            return lane_fallback(c);
+        else
+            scratch.push_back(b);
+        // written in place (kept, or scratch on lane 0) while another lane may read it
+        if ((k || lane == 0) && u.written && c->ln_read.count(b)) return lane_fallback(c);
+        // in place on a lane other than 0 while lane 0's scratch write may be in flight
+        if (lane != 0 && (k || !u.written) && c->l0_written.count(b)) return lane_fallback(c);
+    }
+
+    slm_hip::Lane* L = lane ? &c->lanes[lane] : nullptr;
+    std::vector<Op> tops;
+    if (L) {
+        std::map<uintptr_t, uintptr_t> to;  // allocation -> the lane's copy
+        for (uintptr_t b : scratch) {
+            auto& cp = L->copies[b];
+            size_t n = use[b].bytes;
+            if (!cp.first || cp.second != n) {
+                void* np = nullptr;
+                if (dev_alloc(c, n, &np) != hipSuccess) {
+                    (void)hipGetLastError();
+                    return lane_fallback(c);
+                }
+                if (cp.first) c->retired.push_back(cp.first);
+                cp = {np, n};
+            }
+            to[b] = (uintptr_t)cp.first;
+        }
+        if (!lane_buf(c, &L->ws, &L->ws_bytes, c->ws_bytes) ||
+            !lane_buf(c, &L->gpart, &L->gpart_bytes, c->gpart_bytes) ||
+            !lane_buf(c, &L->part, &L->part_bytes, c->part_bytes))
+            return lane_fallback(c);
+        tops = ops;
+        for (Op& o : tops) {
+            for (int q = 0; q < 8; q++) {
+                uintptr_t a = (uintptr_t)o.p[q], b;
+                size_t n;
+                if (!a || !alloc_at(c, a, &b, &n)) continue;
+                auto it = to.find(b);
+                if (it != to.end()) o.p[q] = (const float*)(it->second + (a - b));
+            }
+            if (o.dyn) o.dyn = L->dyn_dev + ((uintptr_t)o.dyn - dyn_a);
+        }
+    }
+
+    std::vector<Rec> recs;
+    std::vector<PlanMark> marks;
+    int rc;
+    if (L) {  // plan with the lane's partial buffers in the context's place
+        std::swap(c->ws, L->ws);
+        std::swap(c->ws_bytes, L->ws_bytes);
+        std::swap(c->gpart, L->gpart);
+        std::swap(c->gpart_bytes, L->gpart_bytes);
+        std::swap(c->part, L->part);
+        std::swap(c->part_bytes, L->part_bytes);
+        rc = plan(c, tops, recs, c->fusion_on, &marks);
+        std::swap(c->ws, L->ws);
+        std::swap(c->ws_bytes, L->ws_bytes);
+        std::swap(c->gpart, L->gpart);
+        std::swap(c->gpart_bytes, L->gpart_bytes);
+        std::swap(c->part, L->part);
+        std::swap(c->part_bytes, L->part_bytes);
+    } else {
+        rc = plan(c, ops, recs, c->fusion_on, &marks);
+    }
+    TRY(rc);
+    if (marks.empty()) return lane_fallback(c);
+
+    // where each kept allocation's waits and events go
+    std::vector<std::vector<uintptr_t>> wait_at(recs.size() + 1), rec_at(recs.size() + 1);
+    for (uintptr_t b : deps) {
+        const Use& u = use[b];
+        size_t t = 0;
+        while (t + 1 < marks.size() && marks[t + 1].next <= u.first) t++;
+        size_t w = marks[t].out;
+        t = 0;
+        while (t + 1 < marks.size() && marks[t].low <= u.last) t++;
+        size_t r = marks[t].out;
+        if (w >= r) continue;  // no kernel of this step touches it
+        wait_at[w].push_back(b);
+        rec_at[r].push_back(b);
+    }
+
+    TRY(enter_lanes(c));
+    *handled = 1;
+    hipStream_t S = L ? L->stream : c->stream;
+    if (L)
+        TRY(upload_dyn_on(c, L->dyn_dev, L->dyn_pin, L->dyn_ev, &L->dyn_flip, S));
+    else
+        TRY(upload_dyn_on(c, c->dyn_dev, c->dyn_pin, c->dyn_ev, &c->dyn_flip, S));
+    if (L) L->used = true;
+    c->lane_launching = true;
+    c->lane_stream = S;
+    std::set<hipEvent_t> waited;
+    for (size_t k = 0; k <= recs.size() && !rc; k++) {
+        if (!rec_at[k].empty()) {
+            hipEvent_t e = lane_event(c);
+            hipError_t err = e ? hipEventRecord(e, S) : hipErrorOutOfMemory;
+            if (err != hipSuccess) {
+                if (e) c->lane_ev_pool.push_back(e);
+                rc = fail(c, SLM_E_HIP, "lanes: event: %s", hipGetErrorString(err));
+                break;
+            }
+            for (uintptr_t b : rec_at[k]) {
+                auto it = c->touch.find(b);
+                if (it != c->touch.end()) ev_unref(c, it->second.ev);
+                c->touch[b] = {lane, e};
+                c->ev_refs[e]++;
+            }
+        }
+        if (k == recs.size()) break;
+        for (uintptr_t b : wait_at[k]) {
+            auto it = c->touch.find(b);
+            if (it == c->touch.end() || it->second.lane == lane) continue;
+            if (!waited.insert(it->second.ev).second) continue;
+            hipError_t err = hipStreamWaitEvent(S, it->second.ev, 0);
+            if (err != hipSuccess) {
+                rc = fail(c, SLM_E_HIP, "lanes: wait: %s", hipGetErrorString(err));
+                break;
+            }
+        }
+        if (!rc) rc = launch_now(c, recs[k]);
+    }
+    c->lane_launching = false;
+    if (rc) {  // what was queued is joined; the kept buffers' contents are the caller's problem
+        leave_lanes(c);
+        return rc;
+    }
+    for (uintptr_t b : scratch)
+        if (lane == 0) c->l0_written.insert(b);
+    for (uintptr_t b : ronly)
+        if (lane != 0) c->ln_read.insert(b);
+    c->next_lane = (lane + 1) % c->nlanes;
+    c->n_lane_steps++;
+    c->last_ops = ops.size();
+    return SLM_OK;
+}
+
 int finish_step_run(slm_hip* c);
 
 // Frees deferred buffers whose step has run (all of them, after a wait, with `wait`).
@@ -2514,10 +2884,10 @@ int finish_step(slm_hip* c) {
             slm_hip::Deferred d{nullptr, std::move(c->free_after_step)};
             c->free_after_step.clear();
             hipError_t e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
-            if (e == hipSuccess) e = hipEventRecord(d.done, c->stream);
+            if (e == hipSuccess) e = hipEventRecord(d.done, mstream(c));
             if (e != hipSuccess) {  // no event: wait here instead
                 if (d.done) hipEventDestroy(d.done);
-                hipStreamSynchronize(c->stream);
+                hipStreamSynchronize(mstream(c));
                 for (void* p : d.bufs) {
                     c->halves.erase((uintptr_t)p);
                     dev_free(c, p);
@@ -2540,13 +2910,18 @@ int finish_step_run(slm_hip* c) {
         c->tainted = false;
         return SLM_OK;
     }
-    TRY(upload_dyn(c));
     // Multi-token steps (prompt chunks) run planned but uncaptured: their kernels are long
     // enough that replaying a graph saves nothing measurable, while capturing one (for each
     // new buffer arrangement a chunk brings) costs about a millisecond.
     bool multi = false;
     for (const Op& o : c->ops)
         if (o.kind == OP_LINEAR && o.n[2] > 1) { multi = true; break; }
+    if (multi) {
+        int handled = 0;
+        TRY(run_lane_step(c, &handled));
+        if (handled) return SLM_OK;
+    }
+    TRY(upload_dyn(c));
     if (!c->graphs_on || multi) {
         std::vector<Rec> recs;
         TRY(plan(c, c->ops, recs, c->fusion_on));
@@ -2557,7 +2932,7 @@ int finish_step_run(slm_hip* c) {
         if (g.ops.size() == c->ops.size() && g.ndyn == c->dyn.size() &&
             std::memcmp(g.ops.data(), c->ops.data(), c->ops.size() * sizeof(Op)) == 0) {
             g.used = c->clock;
-            HIPC(c, hipGraphLaunch(g.exec, c->stream));
+            HIPC(c, hipGraphLaunch(g.exec, mstream(c)));
             c->n_launched++;
             return SLM_OK;
         }
@@ -2584,7 +2959,7 @@ int finish_step_run(slm_hip* c) {
     if (c->cache.size() >= MAX_GRAPHS) {
         auto old = std::min_element(c->cache.begin(), c->cache.end(),
                                     [](const Graph& a, const Graph& b) { return a.used < b.used; });
-        HIPC(c, hipStreamSynchronize(c->stream));
+        HIPC(c, hipStreamSynchronize(mstream(c)));
         hipGraphExecDestroy(old->exec);
         c->cache.erase(old);
     }
@@ -2593,23 +2968,23 @@ int finish_step_run(slm_hip* c) {
     g.ndyn = c->dyn.size();
     g.used = c->clock;
     hipGraph_t graph = nullptr;
-    HIPC(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    HIPC(c, hipStreamBeginCapture(mstream(c), hipStreamCaptureModeThreadLocal));
     c->capturing = true;
     for (auto& r : recs) {
         int rc = launch_now(c, r);
         if (rc) {
             c->capturing = false;
-            hipStreamEndCapture(c->stream, &graph);
+            hipStreamEndCapture(mstream(c), &graph);
             if (graph) hipGraphDestroy(graph);
             return rc;
         }
     }
     c->capturing = false;
-    HIPC(c, hipStreamEndCapture(c->stream, &graph));
+    HIPC(c, hipStreamEndCapture(mstream(c), &graph));
     hipError_t e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
     hipGraphDestroy(graph);
     if (e != hipSuccess) return fail(c, SLM_E_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
-    HIPC(c, hipGraphLaunch(g.exec, c->stream));
+    HIPC(c, hipGraphLaunch(g.exec, mstream(c)));
     c->n_captured++;
     c->n_launched++;
     c->cache.push_back(std::move(g));
@@ -2749,6 +3124,11 @@ int slm_hip_open(int device, slm_hip** out) {
     if (env && env[0] == '0') c->graphs_on = false;
     env = getenv("SLM_HIP_FUSION");
     if (env && env[0] == '0') c->fusion_on = false;
+    // three prompt lanes by default (a 4096-token a86 prompt at R = 4 measured 155 K tok/s on
+    // one, 194 K on two, 216 K on three, 198 K on four)
+    env = getenv("SLM_HIP_LANES");
+    int lanes = env && env[0] >= '1' && env[0] <= '0' + MAX_LANES && !env[1] ? env[0] - '0' : 3;
+    if (slm_hip_set_prompt_lanes(c, lanes) != SLM_OK) return bail(SLM_E_HIP);
 #undef OPEN_HIP
     *out = c;
     return SLM_OK;
@@ -2756,7 +3136,12 @@ int slm_hip_open(int device, slm_hip** out) {
 
 void slm_hip_close(slm_hip* c) {
     if (!c) return;
-    if (c->stream) hipStreamSynchronize(c->stream);
+    if (c->stream) {
+        leave_lanes(c);
+        hipStreamSynchronize(c->stream);
+    }
+    for (int l = 1; l < (int)c->lanes.size(); l++)
+        if (c->lanes[l].stream) hipStreamSynchronize(c->lanes[l].stream);
     for (auto& g : c->cache)
         if (g.exec) hipGraphExecDestroy(g.exec);
     auto release = [&](void* p) {  // (pooled blocks go with their slabs)
@@ -2773,6 +3158,21 @@ void slm_hip_close(slm_hip* c) {
     if (c->pick) hipFree(c->pick);
     release(c->part);
     release(c->gpart);
+    for (int l = 1; l < (int)c->lanes.size(); l++) {
+        auto& L = c->lanes[l];
+        for (auto& cp : L.copies) release(cp.second.first);
+        release(L.ws);
+        release(L.gpart);
+        release(L.part);
+        if (L.dyn_dev) hipFree(L.dyn_dev);
+        for (int i = 0; i < 2; i++) {
+            if (L.dyn_pin[i]) hipHostFree(L.dyn_pin[i]);
+            if (L.dyn_ev[i]) hipEventDestroy(L.dyn_ev[i]);
+        }
+        if (L.stream) hipStreamDestroy(L.stream);
+    }
+    for (auto& r : c->ev_refs) hipEventDestroy(r.first);
+    for (auto e : c->lane_ev_pool) hipEventDestroy(e);
     for (void* r : c->retired) release(r);
     for (void* r : c->free_after_step) release(r);
     free_deferred(c, true);
@@ -2865,20 +3265,30 @@ int slm_hip_free(slm_hip* c, float* p) {
     auto it = c->allocs.find((uintptr_t)p);
     if (it == c->allocs.end()) return fail(c, SLM_E_BOUNDS, "free: %p was not allocated here", (void*)p);
     drop_shadows(c, (uintptr_t)p, (uintptr_t)p + it->second);
+    // the prompt lanes' copies of it go with it
+    std::vector<void*> copies;
+    for (int l = 1; l < (int)c->lanes.size(); l++) {
+        auto cp = c->lanes[l].copies.find((uintptr_t)p);
+        if (cp == c->lanes[l].copies.end()) continue;
+        if (cp->second.first) copies.push_back(cp->second.first);
+        c->lanes[l].copies.erase(cp);
+    }
     if (recording(c)) {
         // (an output growing inside a step, cuda.rs:122-127) the step keeps recording: ops
         // recorded before may still name the buffer, so it is freed once the step has run
         c->allocs.erase(it);
         c->halves.erase((uintptr_t)p);  // no later call may take it as fp16 weights
         c->free_after_step.push_back(p);
+        for (void* q : copies) c->free_after_step.push_back(q);
         return SLM_OK;
     }
     TRY(taint(c));
     drop_graphs(c);
     c->allocs.erase(it);
     c->halves.erase((uintptr_t)p);
-    HIPC(c, hipStreamSynchronize(c->stream));
+    HIPC(c, hipStreamSynchronize(mstream(c)));
     dev_free(c, p);
+    for (void* q : copies) dev_free(c, q);
     return SLM_OK;
 }
 
@@ -2888,7 +3298,7 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
         if (n > nh) return fail(c, SLM_E_BOUNDS, "upload: %zu values into %zu halves", n, nh);
         if (n == 0) return SLM_OK;
         TRY(taint(c));
-        HIPC(c, hipStreamSynchronize(c->stream));
+        HIPC(c, hipStreamSynchronize(mstream(c)));
         uint16_t* b = (uint16_t*)c->bounce;
         for (size_t done = 0; done < n;) {
             size_t part = std::min(n - done, BOUNCE_CAP / 2);
@@ -2905,7 +3315,7 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
     for (auto it = c->tables.begin(); it != c->tables.end();) {  // inv_freq rewritten
         if (it->first >= (uintptr_t)dst && it->first < (uintptr_t)(dst + n)) {
             drop_graphs(c);
-            hipStreamSynchronize(c->stream);
+            hipStreamSynchronize(mstream(c));
             dev_free(c, it->second.cos);
             dev_free(c, it->second.sin);
             it = c->tables.erase(it);
@@ -2913,7 +3323,7 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
             ++it;
         }
     }
-    HIPC(c, hipStreamSynchronize(c->stream));
+    HIPC(c, hipStreamSynchronize(mstream(c)));
     HIPC(c, hipMemcpy(dst, src, n * 4, hipMemcpyHostToDevice));
     return SLM_OK;
 }
@@ -2926,13 +3336,13 @@ int slm_hip_read(slm_hip* c, float* host, const float* dev, size_t n) {
         for (size_t done = 0; done < n;) {
             size_t part = std::min(n - done, BOUNCE_CAP / 2);
             HIPC(c, hipMemcpyAsync(c->bounce, (const uint16_t*)dev + done, part * 2,
-                                   hipMemcpyDeviceToHost, c->stream));
-            HIPC(c, hipStreamSynchronize(c->stream));
+                                   hipMemcpyDeviceToHost, mstream(c)));
+            HIPC(c, hipStreamSynchronize(mstream(c)));
             const uint16_t* b = (const uint16_t*)c->bounce;
             for (size_t i = 0; i < part; i++) host[done + i] = f32_of(b[i]);
             done += part;
         }
-        if (n == 0) HIPC(c, hipStreamSynchronize(c->stream));
+        if (n == 0) HIPC(c, hipStreamSynchronize(mstream(c)));
         return check_fault(c);
     }
     NEED(c, "read", dev, n);
@@ -2940,22 +3350,31 @@ int slm_hip_read(slm_hip* c, float* host, const float* dev, size_t n) {
     size_t done = 0;
     while (done < n) {
         size_t part = std::min(n - done, BOUNCE_CAP / 4);
-        HIPC(c, hipMemcpyAsync(c->bounce, dev + done, part * 4, hipMemcpyDeviceToHost, c->stream));
-        HIPC(c, hipStreamSynchronize(c->stream));
+        HIPC(c, hipMemcpyAsync(c->bounce, dev + done, part * 4, hipMemcpyDeviceToHost, mstream(c)));
+        HIPC(c, hipStreamSynchronize(mstream(c)));
         std::memcpy(host + done, c->bounce, part * 4);
         done += part;
     }
-    if (n == 0) HIPC(c, hipStreamSynchronize(c->stream));
+    if (n == 0) HIPC(c, hipStreamSynchronize(mstream(c)));
     return check_fault(c);
 }
 
 int slm_hip_flush(slm_hip* c, const float* const* keep, size_t nkeep) {
-    (void)keep;
-    (void)nkeep;
-    if (!c) return SLM_E_INVALID;
+    if (!c || (nkeep && !keep)) return SLM_E_INVALID;
     TRY(check_fault(c));  // (work already finished; the rest is reported by a later check)
-    if (c->recording) return finish_step(c);
-    return SLM_OK;
+    if (!c->recording) return SLM_OK;
+    // what outlives the step (ops.rs:90-91): a prompt step may then run on a lane, the rest
+    // of what it writes being dead once it is over
+    c->keep.clear();
+    for (size_t i = 0; i < nkeep; i++) {
+        uintptr_t b;
+        size_t n;
+        if (keep[i] && alloc_at(c, (uintptr_t)keep[i], &b, &n)) c->keep.push_back(b);
+    }
+    c->keep_valid = true;
+    int rc = finish_step(c);
+    c->keep_valid = false;
+    return rc;
 }
 
 int slm_hip_set_spin_limit(slm_hip* c, long long polls) {
@@ -2971,6 +3390,36 @@ int slm_hip_set_graphs(slm_hip* c, int on) {
     if (c->recording) TRY(finish_step(c));
     if (!on) drop_graphs(c);
     c->graphs_on = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_set_prompt_lanes(slm_hip* c, int n) {
+    if (!c || n < 1 || n > MAX_LANES) return SLM_E_INVALID;
+    leave_lanes(c);
+    if ((int)c->lanes.size() < n) c->lanes.resize(n);
+    for (int l = 1; l < n; l++) {
+        auto& L = c->lanes[l];
+        if (!L.stream) HIPC(c, hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking));
+        for (int i = 0; i < 2; i++) {
+            if (!L.dyn_pin[i]) HIPC(c, hipHostMalloc((void**)&L.dyn_pin[i], DYN_CAP, hipHostMallocDefault));
+            if (!L.dyn_ev[i]) HIPC(c, hipEventCreateWithFlags(&L.dyn_ev[i], hipEventDisableTiming));
+        }
+        if (!L.dyn_dev) HIPC(c, hipMalloc((void**)&L.dyn_dev, DYN_CAP));
+    }
+    c->nlanes = n;
+    return SLM_OK;
+}
+
+int slm_hip_get_prompt_lanes(slm_hip* c, int* n) {
+    if (!c || !n) return SLM_E_INVALID;
+    *n = c->nlanes;
+    return SLM_OK;
+}
+
+int slm_hip_prompt_lane_stats(slm_hip* c, uint64_t* steps, uint64_t* fallbacks) {
+    if (!c || !steps || !fallbacks) return SLM_E_INVALID;
+    *steps = c->n_lane_steps;
+    *fallbacks = c->n_lane_fallbacks;
     return SLM_OK;
 }
 
@@ -3278,7 +3727,7 @@ int slm_hip_rope_table(slm_hip* c, float* cs, float* sn, const float* inv, size_
     Table& t = c->tables[(uintptr_t)inv];
     if (half && t.inv.size() != half) {  // first sight of this inv_freq buffer
         t.inv.assign(half, 0.0f);
-        HIPC(c, hipStreamSynchronize(c->stream));
+        HIPC(c, hipStreamSynchronize(mstream(c)));
         HIPC(c, hipMemcpy(t.inv.data(), inv, half * 4, hipMemcpyDeviceToHost));
         t.rows = 0;
     }
@@ -3554,7 +4003,7 @@ int slm_hip_attend_noalloc(slm_hip* c, float* y, float* scores, const float* q, 
         void* ptrs[MAX_ARGS];
         for (uint32_t i = 0; i < r.nargs; i++) ptrs[i] = (void*)(r.blob + 8 * i);
         if (r.bytes) return fail(c, SLM_E_HIP, "attend_noalloc: unexpected descriptor launch");
-        hipError_t e = hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, c->stream,
+        hipError_t e = hipModuleLaunchKernel(r.f, r.gx, r.gy, r.gz, r.bx, 1, 1, r.shmem, mstream(c),
                                              ptrs, nullptr);
         if (e != hipSuccess)
             return fail(c, SLM_E_HIP, "attend_noalloc: hipModuleLaunchKernel: %s", hipGetErrorString(e));
@@ -3566,7 +4015,7 @@ int slm_hip_attend_noalloc(slm_hip* c, float* y, float* scores, const float* q, 
 
 int slm_hip_stream(slm_hip* c, void** out) {
     if (!c || !out) return SLM_E_INVALID;
-    *out = (void*)c->stream;
+    *out = (void*)mstream(c);
     return SLM_OK;
 }
 

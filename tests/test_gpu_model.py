@@ -395,11 +395,11 @@ def test_a86_fp16_mode_reads_half_weights(pkg, hip):
 def test_dropped_sessions_give_their_memory_back(pkg, hip):
     """A server makes a session per request and drops it (serve.rs:369, main.rs:308), and a Rust
     `HipBuf` frees its buffer on drop as cuda.rs's `CudaSlice` does: 40 a86 sessions at R = 16
-    (about 538 MB of rings and state each), each fed a prompt and stepped, then freed, leave
-    the device's free memory and the context's holdings where the first such session left
-    them."""
+    (about 538 MB of rings and state each), each fed a 600-token prompt (three chunks: the
+    prompt lanes' copies of the scratch buffers too) and stepped, then freed, leave the
+    device's free memory and the context's holdings where the first such session left them."""
     g = pkg.Model(hip, model_dir("a86", 2))
-    toks = synth.tokens(40, 32000, seed=4)
+    toks = synth.tokens(600, 32000, seed=4)
     s = g.session(16)
     s.feed(toks, 256)
     s.step(1)
@@ -408,7 +408,7 @@ def test_dropped_sessions_give_their_memory_back(pkg, hip):
     for i in range(40):
         s = g.session(16)
         assert s.state_bytes() > 500e6
-        s.feed(toks[:24], 256)
+        s.feed(toks, 256)
         s.step(int(toks[i]))
         del s
     free1, _, held1 = hip.mem_info()
@@ -416,3 +416,140 @@ def test_dropped_sessions_give_their_memory_back(pkg, hip):
           f"{total / 2**30:.0f}; held {held0 / 2**20:.0f} -> {held1 / 2**20:.0f} MiB")
     assert held1 <= held0
     assert free0 - free1 < 64 << 20
+
+
+# ---------------------------------------------------------------------------------------
+# prompt lanes: consecutive prompt steps on several streams at once
+# ---------------------------------------------------------------------------------------
+
+class _Lanes:
+    """Sets the context's prompt lanes for a block and restores them after."""
+
+    def __init__(self, hip, n):
+        self.hip, self.n = hip, n
+
+    def __enter__(self):
+        self.old = self.hip.prompt_lanes()
+        self.hip.set_prompt_lanes(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        self.hip.set_prompt_lanes(self.old)
+
+
+def _prompt(g, loops, toks):
+    """main.rs:309's warm-up then the prompt, as the bench runs it."""
+    s = g.session(loops)
+    s.feed(toks[:16], 256)
+    s.logits()
+    s.feed(toks[16:], 256)
+    return s
+
+
+@pytest.mark.parametrize("lanes", [2, 3, 4])
+def test_prompt_lanes_same_bits(pkg, hip, lanes):
+    """a86 at R = 4, 16 + 2048 prompt tokens: with chunks on 2, 3 and 4 streams at once, the
+    logits and every kept buffer equal one stream's bit for bit, and so do 8 greedy steps
+    after (each joining the lanes first)."""
+    g = pkg.Model(hip, model_dir("a86", 2))
+    toks = synth.tokens(2064, 32000, seed=31)
+    with _Lanes(hip, 1):
+        a = _prompt(g, 4, toks)
+        la = a.logits()
+    with _Lanes(hip, lanes):
+        st0 = hip.lane_stats()
+        b = _prompt(g, 4, toks)
+        lb = b.logits()
+        st1 = hip.lane_stats()
+    print(f"lanes {lanes}: {st1['steps'] - st0['steps']} steps on lanes, "
+          f"{st1['fallbacks'] - st0['fallbacks']} on the context's stream")
+    assert st1["steps"] - st0["steps"] >= 7  # 8 chunks after the warm-up; the first may grow outputs
+    assert np.array_equal(la, lb)
+    _kept_equal(a, b)
+    assert a.decode_greedy(8).tolist() == b.decode_greedy(8).tolist()
+    assert np.array_equal(a.logits(), b.logits())
+
+
+def test_prompt_lanes_interleaved_sessions(pkg, hip):
+    """Two sessions fed chunk by chunk in turn (consecutive steps of different sessions: no
+    kept buffer in common) on 3 lanes leave the states one stream leaves feeding each alone."""
+    g = pkg.Model(hip, model_dir("a86", 2))
+    ta = synth.tokens(1280, 32000, seed=32)
+    tb = synth.tokens(1100, 32000, seed=33)
+    with _Lanes(hip, 1):
+        a1 = g.session(4)
+        a1.feed(ta, 256)
+        b1 = g.session(8)
+        b1.feed(tb, 256)
+        la1, lb1 = a1.logits(), b1.logits()
+    with _Lanes(hip, 3):
+        a3, b3 = g.session(4), g.session(8)
+        ia = ib = 0
+        while ia < len(ta) or ib < len(tb):
+            if ia < len(ta):
+                n = min(256, len(ta) - ia)
+                a3.advance(ta[ia:ia + n], ia + n == len(ta))
+                ia += n
+            if ib < len(tb):
+                n = min(256, len(tb) - ib)
+                b3.advance(tb[ib:ib + n], ib + n == len(tb))
+                ib += n
+        la3, lb3 = a3.logits(), b3.logits()
+    assert np.array_equal(la1, la3)
+    assert np.array_equal(lb1, lb3)
+    _kept_equal(a1, a3)
+    _kept_equal(b1, b3)
+
+
+@GROW
+def test_prompt_lanes_g86_growing_caches(pkg, hip, device_grow):
+    """g86 (global caches doubling 256 -> 1024 inside the prompt, kshift state, 4 key heads):
+    a 700-token prompt in 256- and 64-token chunks on 3 lanes equals one stream's state."""
+    g = pkg.Model(hip, model_dir("g86", 5), global_cap=256, device_grow=device_grow)
+    toks = synth.tokens(700, 32000, seed=34)
+    for chunk in (256, 64):
+        with _Lanes(hip, 1):
+            a = g.session(4)
+            a.feed(toks, chunk)
+            la = a.logits()
+        with _Lanes(hip, 3):
+            b = g.session(4)
+            b.feed(toks, chunk)
+            lb = b.logits()
+        assert np.array_equal(la, lb), chunk
+        _kept_equal(a, b)
+
+
+def test_prompt_lanes_tiny_every_layer_kind(tiny_hip, hip):
+    """The reference fixture's shape (window, linear and global layers, R = 3): 300 tokens in
+    7-token chunks (the rings wrap) on 4 lanes equal one stream's state."""
+    toks = synth.tokens(300, 97, seed=5)
+    with _Lanes(hip, 1):
+        a = tiny_hip.session(3)
+        a.feed(toks, 7)
+        la = a.logits()
+    with _Lanes(hip, 4):
+        b = tiny_hip.session(3)
+        b.feed(toks, 7)
+        lb = b.logits()
+    assert np.array_equal(la, lb)
+    _kept_equal(a, b)
+
+
+def test_prompt_lanes_fp16_rings(pkg, hip):
+    """fp16 mode (fp16 weight copies and rings), a86 at R = 16, 1040 prompt tokens on 3 lanes:
+    the same bits as one stream."""
+    g = pkg.Model(hip, model_dir("a86", 2))
+    toks = synth.tokens(1040, 32000, seed=35)
+    hip.set_fp16(True)
+    try:
+        with _Lanes(hip, 1):
+            a = _prompt(g, 16, toks)
+            la = a.logits()
+        with _Lanes(hip, 3):
+            b = _prompt(g, 16, toks)
+            lb = b.logits()
+    finally:
+        hip.set_fp16(False)
+    assert np.array_equal(la, lb)
+    _kept_equal(a, b)
