@@ -327,6 +327,8 @@ def main():
     ap.add_argument("--no-graphs", action="store_true")
     ap.add_argument("--tile-rows", type=int, default=0,
                     help="fused GEMV rows per tile (0: the planner's choice; 16, 8 or 4)")
+    ap.add_argument("--prompt-lanes", type=int, default=0,
+                    help="streams consecutive prompt chunks run on (0: the backend's default)")
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16-mode leg")
     ap.add_argument("--no-g86", action="store_true", help="skip the g86 16K-prompt leg (config C4)")
     ap.add_argument("--timed-steps", type=int, default=16,
@@ -371,7 +373,9 @@ def main():
         hip.set_graphs(False)
     if a.tile_rows:
         hip.set_tile_rows(a.tile_rows)
-    log("device:", hip.name())
+    if a.prompt_lanes:
+        hip.set_prompt_lanes(a.prompt_lanes)
+    log("device:", hip.name(), "prompt lanes:", hip.prompt_lanes())
     model = pkg.Model(hip, folder)
     per_r = {}
     head = a.loops[0]
@@ -492,7 +496,10 @@ def main():
         "prefill": {"value": h["prefill_tok_s"], "unit": "tok/s", "prompt_tokens": len(prompt),
                     "flops_per_token": h["prefill_flops_per_token"],
                     "achieved_tflops": h["prefill_tflops"], "peak_tflops": FP32_MFMA_PEAK / 1e12,
-                    "frac": h["prefill_mfma_frac"]},
+                    "frac": h["prefill_mfma_frac"], "prompt_lanes": hip.prompt_lanes(),
+                    "lanes_note": "consecutive 256-token chunks on that many streams at once, "
+                                  "each lane writing its own copies of the step's scratch; "
+                                  "model.rs's calls unchanged (the flush keep lists)"},
     }
     for r in a.loops:
         line[f"r{r}"] = per_r[r]
