@@ -1010,13 +1010,15 @@ KERNEL void __launch_bounds__(256) slm_gemm(float* __restrict__ y, float* __rest
 
 // The same GEMM with a deeper pipeline, for cols a multiple of 64 and 16-byte aligned rows:
 // tiles of BM rows x 64 tokens, 64-column slices copied straight into LDS (no registers) by
-// the four waves, GEMM_STAGES slices in flight, one barrier per slice. In LDS, row r of a
+// the four waves, GEMM_STAGES slices in flight, one barrier per slice. Two stages (80 KB of
+// LDS for 96-row tiles) let two workgroups share a CU, from concurrent prompt chunks; three
+// measured the same on one stream and 2 % slower on three. In LDS, row r of a
 // slice is 16 chunks of 16 bytes with chunk c at position c ^ (r & 15), so the MFMA operand
 // reads (sixteen rows at one chunk) fall on distinct banks; the copy puts each lane's chunk
 // there by permuting the global addresses it reads. Waves 2 x 2 over the tile, each
 // (BM / 2) x 32. The arithmetic is slm_gemm's: the same MFMA chain per slice, slices added
 // in order within the split, one split per blockIdx.z.
-#define GEMM_STAGES 3
+#define GEMM_STAGES 2
 __device__ __forceinline__ int gsw(int row, int chunk) { return row * 64 + 4 * (chunk ^ (row & 15)); }
 
 template <int N>
@@ -1228,7 +1230,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt untouched
     };
-    static_assert(GEMM_STAGES == 3, "the copy waits below count three buffers");
+    static_assert(GEMM_STAGES >= 2, "the copy waits below count GEMM_STAGES buffers");
     // (two slices of operands in registers do not fit 16 waves of 128-row tiles: those read
     // each slice after its barrier)
     constexpr bool PIPE = !(BM == 128 && WAVES == 16);
@@ -1258,16 +1260,17 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
         // compiler's waits for the LDS reads stay exact.
 #pragma unroll
         for (int p = 0; p < GEMM_STAGES; p++) issue(c_first + min(p, c_last), p);
-        // slice 0 is in (this wave's copies of slices 1 and 2 may still run), then everyone's is
-        vm_wait<2 * NDMA>();
+        // slice 0 is in (this wave's copies of the later stages may still run), then everyone's is
+        vm_wait<(GEMM_STAGES - 1) * NDMA>();
         barrier();
         Ops R0, R1;
         load_ops(0, R0);
         // step q (q + 1 < nst): slice q + 1 is in (everyone's copies) and slice q's buffer is
-        // free (everyone's reads of it were waited for before the barrier): copy slice q + 3
-        // there, read slice q + 1, run slice q, whose operands the barrier waited for
+        // free (everyone's reads of it were waited for before the barrier): copy slice
+        // q + GEMM_STAGES there, read slice q + 1, run slice q, whose operands the barrier
+        // waited for
         auto step = [&](int q, Ops& cur, Ops& nxt) {
-            vm_wait<NDMA>();
+            vm_wait<(GEMM_STAGES - 2) * NDMA>();
             barrier();
             issue(c_first + min(q + GEMM_STAGES, c_last), q % GEMM_STAGES);
             load_ops((q + 1) % GEMM_STAGES, nxt);

@@ -53,7 +53,7 @@ constexpr int64_t ATTN_CTR_MAX = 65536;   // (query tile, key head) pairs one at
 constexpr int ATTN_LDS_MAX = LDS_MAX;
 constexpr int ATTN_QG_HOST = 4;   // query tiles per workgroup of the prompt attention (ATTN_QG)
 constexpr int ATTN_DEC_LDS = SLM_SB_SEGS * (2 * 64 * 64 + 1024) * 4;  // one-token attention: 256 keys and values, queries
-constexpr int GEMM_STAGES_HOST = 3;          // slices in flight in slm_gemm2 (GEMM_STAGES)
+constexpr int GEMM_STAGES_HOST = 2;          // slices in flight in slm_gemm2 (GEMM_STAGES)
 constexpr int64_t CU_COUNT = 256;           // MI355X compute units
 
 enum OpKind : uint32_t {
