@@ -553,3 +553,39 @@ def test_prompt_lanes_fp16_rings(pkg, hip):
         hip.set_fp16(False)
     assert np.array_equal(la, lb)
     _kept_equal(a, b)
+
+
+def test_prompt_lanes_with_decode_steps_between(pkg, hip):
+    """One session decodes (one-token steps through the step graph, on the context's stream)
+    after every two prompt chunks of another (lanes 0 and 1): the lanes are joined and entered
+    again around every step, and both sessions end as they do on one stream."""
+    g = pkg.Model(hip, model_dir("a86", 2))
+    ta = synth.tokens(300, 32000, seed=36)
+    tb = synth.tokens(1300, 32000, seed=37)
+
+    steps = synth.tokens(8, 32000, seed=38)
+
+    def run(lanes):
+        with _Lanes(hip, lanes):
+            a, b = g.session(4), g.session(4)
+            a.feed(ta, 256)
+            st0 = hip.lane_stats()
+            i = k = 0
+            while i < len(tb):  # two chunks of b (lanes 0 and 1), then a step of a (a join)
+                for _ in range(2):
+                    n = min(256, len(tb) - i)
+                    if n > 0:
+                        b.advance(tb[i:i + n], i + n == len(tb))
+                        i += n
+                a.step(int(steps[k]))
+                k += 1
+            st1 = hip.lane_stats()
+            return a, b, st1["steps"] - st0["steps"], a.logits(), b.logits()
+
+    a1, b1, n1, la1, lb1 = run(1)
+    a3, b3, n3, la3, lb3 = run(3)
+    assert n1 == 0 and n3 >= 3
+    assert np.array_equal(la1, la3)
+    assert np.array_equal(lb1, lb3)
+    _kept_equal(a1, a3)
+    _kept_equal(b1, b3)
