@@ -220,6 +220,22 @@ def test_a86_chunked_ring_state_equals_step(pkg, hip, loops):
     _kept_equal(a, b)
 
 
+def test_a86_prompt_past_the_ring_chunked_equals_step(pkg, hip):
+    """Config 3's overwrite run: an 8192-token prompt at R = 4 in 256-token chunks (chunks 17
+    and on overwrite ring slots the window has left, 4352 slots) leaves the same state, bit for
+    bit, as the same prompt token by token; then 8 greedy steps agree."""
+    folder = model_dir("a86", 2)
+    g = pkg.Model(hip, folder)
+    toks = synth.tokens(8192, 32000, seed=41)
+    a, b = g.session(4), g.session(4)
+    a.feed(toks, 256)
+    b.feed(toks, 1)
+    assert np.array_equal(a.logits(), b.logits())
+    _kept_equal(a, b)
+    assert a.decode_greedy(8).tolist() == b.decode_greedy(8).tolist()
+    assert np.array_equal(a.logits(), b.logits())
+
+
 @pytest.mark.parametrize("name", ["tiny", "a86"])
 def test_fused_steps_match_per_op_kernels(pkg, hip, tiny_dir, name):
     """The planner's fused one-token kernels give the same bits as one launch per op."""
