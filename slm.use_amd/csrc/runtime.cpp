@@ -186,6 +186,7 @@ struct slm_hip {
     int dyn_flip = 0;
     unsigned char* dyn_dev = nullptr;
     float* bounce = nullptr;
+    hipEvent_t read_ev[2] = {nullptr, nullptr};  // the bounce buffer's halves (large reads)
     std::map<uintptr_t, Table> tables;
     bool graphs_on = true, fusion_on = true, plan_trace = false;
     bool fp16 = false;                   // linears with fp16 operands (slm_hip_set_fp16)
@@ -3108,6 +3109,7 @@ int slm_hip_open(int device, slm_hip** out) {
     }
     OPEN_HIP(hipMalloc((void**)&c->dyn_dev, DYN_CAP));
     OPEN_HIP(hipHostMalloc((void**)&c->bounce, BOUNCE_CAP, hipHostMallocDefault));
+    for (int i = 0; i < 2; i++) OPEN_HIP(hipEventCreateWithFlags(&c->read_ev[i], hipEventDisableTiming));
     OPEN_HIP(hipHostMalloc((void**)&c->fault_host, 64, hipHostMallocMapped));
     *c->fault_host = 0;
     OPEN_HIP(hipHostGetDevicePointer((void**)&c->fault_dev, c->fault_host, 0));
@@ -3187,6 +3189,7 @@ void slm_hip_close(slm_hip* c) {
     for (int i = 0; i < 2; i++) {
         if (c->dyn_pin[i]) hipHostFree(c->dyn_pin[i]);
         if (c->dyn_ev[i]) hipEventDestroy(c->dyn_ev[i]);
+        if (c->read_ev[i]) hipEventDestroy(c->read_ev[i]);
     }
     if (c->mod) hipModuleUnload(c->mod);
     if (c->stream) hipStreamDestroy(c->stream);
@@ -3347,15 +3350,29 @@ int slm_hip_read(slm_hip* c, float* host, const float* dev, size_t n) {
     }
     NEED(c, "read", dev, n);
     TRY(taint(c));
-    size_t done = 0;
-    while (done < n) {
-        size_t part = std::min(n - done, BOUNCE_CAP / 4);
-        HIPC(c, hipMemcpyAsync(c->bounce, dev + done, part * 4, hipMemcpyDeviceToHost, mstream(c)));
-        HIPC(c, hipStreamSynchronize(mstream(c)));
-        std::memcpy(host + done, c->bounce, part * 4);
-        done += part;
+    hipStream_t s = mstream(c);
+    if (n * 4 <= BOUNCE_CAP) {
+        HIPC(c, hipMemcpyAsync(c->bounce, dev, n * 4, hipMemcpyDeviceToHost, s));
+        HIPC(c, hipStreamSynchronize(s));
+        std::memcpy(host, c->bounce, n * 4);
+        return check_fault(c);
     }
-    if (n == 0) HIPC(c, hipStreamSynchronize(mstream(c)));
+    // larger: the two halves of the bounce buffer in turn, the copy of part k + 1 running
+    // while the host copies part k out
+    const size_t P = BOUNCE_CAP / 8;  // floats a half
+    size_t parts = (n + P - 1) / P;
+    auto issue = [&](size_t k) -> hipError_t {
+        size_t part = std::min(n - k * P, P);
+        hipError_t e = hipMemcpyAsync(c->bounce + (k & 1) * P, dev + k * P, part * 4,
+                                      hipMemcpyDeviceToHost, s);
+        return e == hipSuccess ? hipEventRecord(c->read_ev[k & 1], s) : e;
+    };
+    HIPC(c, issue(0));
+    for (size_t k = 0; k < parts; k++) {
+        if (k + 1 < parts) HIPC(c, issue(k + 1));
+        HIPC(c, hipEventSynchronize(c->read_ev[k & 1]));
+        std::memcpy(host + k * P, c->bounce + (k & 1) * P, std::min(n - k * P, P) * 4);
+    }
     return check_fault(c);
 }
 
