@@ -13,6 +13,7 @@
 #include <unistd.h>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <emmintrin.h>
 #include <limits>
@@ -330,9 +331,12 @@ class Ops {
     }
     std::vector<float> read(const Buf& b, size_t n) const {
         std::vector<float> out(n);
-        if (n > b.n) throw SlmError(SLM_E_BOUNDS, "read: past the end of a buffer");
-        ok(slm_hip_read(c_, out.data(), b.p, n), "read");
+        read_into(b, out.data(), n);
         return out;
+    }
+    void read_into(const Buf& b, float* out, size_t n) const {
+        if (n > b.n) throw SlmError(SLM_E_BOUNDS, "read: past the end of a buffer");
+        ok(slm_hip_read(c_, out, b.p, n), "read");
     }
     void flush(const std::vector<const Buf*>& keep) const {
         std::vector<const float*> ptrs;
@@ -749,6 +753,17 @@ Session* new_session(Model& M, size_t loops_in) {
     return se;
 }
 
+// A zeroed host array from calloc (large ones come as untouched zero pages).
+struct HostFloats {
+    float* p;
+    explicit HostFloats(size_t n) : p((float*)std::calloc(n ? n : 1, sizeof(float))) {
+        if (!p) throw SlmError(SLM_E_MEMORY, "out of host memory");
+    }
+    ~HostFloats() { std::free(p); }
+    HostFloats(const HostFloats&) = delete;
+    HostFloats& operator=(const HostFloats&) = delete;
+};
+
 // model.rs:383-398: doubles a global cache. By default the reference's own sequence, which a
 // Rust `impl Ops for Hip` under an unchanged model.rs issues: `read` each cache (inside the
 // advance: the backend runs what the step recorded so far), lay every head's `cap` rows out
@@ -765,12 +780,13 @@ void grow(const Model& M, Buf& k, Buf& v, size_t& cap) {
             nb = M.ops.zeros_cache(kh, nw, dh);
             M.ops.ok(slm_hip_grow_cache(M.ops.ctx(), nb.p, buf->p, kh, old, dh), "grow");
         } else {
-            std::vector<float> data = M.ops.read(*buf, kh * old * dh);
-            std::vector<float> out(kh * nw * dh, 0.0f);
+            // host buffers as Rust's vec![0f32; n] gets them (cuda.rs:161, model.rs:389):
+            // zeroed pages from calloc, touched only where written or read
+            HostFloats data(kh * old * dh), out(kh * nw * dh);
+            M.ops.read_into(*buf, data.p, kh * old * dh);
             for (size_t h = 0; h < kh; h++)
-                std::copy(data.begin() + h * old * dh, data.begin() + (h + 1) * old * dh,
-                          out.begin() + h * nw * dh);
-            nb = M.ops.upload_cache(out.data(), kh, nw, dh);
+                std::copy(data.p + h * old * dh, data.p + (h + 1) * old * dh, out.p + h * nw * dh);
+            nb = M.ops.upload_cache(out.p, kh, nw, dh);
         }
         M.ops.release(*buf);
         *buf = nb;
