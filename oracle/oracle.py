@@ -42,9 +42,10 @@ class _Cfg(C.Structure):
         ("damp", C.c_float), ("rope_base", C.c_float), ("norm_eps", C.c_float)]
 
 
-def build(quiet: bool = True) -> Path:
-    """Compiles liboracle.so with oracle/Makefile."""
-    out = subprocess.run(["make", "-C", str(HERE)], capture_output=True, text=True)
+def build(quiet: bool = True, force: bool = False) -> Path:
+    """Compiles liboracle.so with oracle/Makefile (`force`: even when it is up to date)."""
+    out = subprocess.run(["make", "-C", str(HERE)] + (["-B"] if force else []), capture_output=True,
+                         text=True)
     if out.returncode != 0:
         raise RuntimeError("oracle build failed:\n" + out.stdout + out.stderr)
     return LIB_PATH
