@@ -453,6 +453,19 @@ class _Lanes:
         self.hip.set_prompt_lanes(self.old)
 
 
+def test_prompt_lane_counts(pkg, hip):
+    """1 to 4 lanes; anything else is refused and leaves the setting as it was."""
+    n0 = hip.prompt_lanes()
+    for bad in (0, 5, -1):
+        with pytest.raises(pkg.SlmError):
+            hip.set_prompt_lanes(bad)
+        assert hip.prompt_lanes() == n0
+    for n in (1, 2, 3, 4):
+        hip.set_prompt_lanes(n)
+        assert hip.prompt_lanes() == n
+    hip.set_prompt_lanes(n0)
+
+
 def _prompt(g, loops, toks):
     """main.rs:309's warm-up then the prompt, as the bench runs it."""
     s = g.session(loops)
