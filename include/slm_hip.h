@@ -87,8 +87,14 @@ int slm_hip_grow_cache(slm_hip* ctx, float* dst, const float* src, size_t heads,
 int slm_hip_free(slm_hip* ctx, float* buf);
 /* Copies n host floats into dst (Ops::upload, ops.rs:77). */
 int slm_hip_upload(slm_hip* ctx, float* dst, const float* src, size_t n);
-/* Waits for pending work and copies n floats to the host (Ops::read, ops.rs:88-89). */
+/* Waits for pending work and copies n floats to the host (Ops::read, ops.rs:88-89). When the
+ * same range was read right after the previous replay of the one-token step graph just
+ * replayed, and nothing was queued since, the backend has already queued a copy of it into
+ * mapped host memory behind the step (read-ahead) and the read only waits for that copy's flag
+ * (the usual copy after a second, or if anything else came between). */
 int slm_hip_read(slm_hip* ctx, float* host, const float* dev, size_t n);
+/* Reads served by the read-ahead copy since the context opened. */
+int slm_hip_read_ahead_stats(slm_hip* ctx, uint64_t* reads);
 /* Ops::flush (ops.rs:90-91): called once at the end of every advance with every buffer
  * that outlives it. With step graphs on it ends the step (see slm_hip_set_graphs). */
 int slm_hip_flush(slm_hip* ctx, const float* const* keep, size_t nkeep);

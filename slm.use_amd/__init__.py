@@ -93,6 +93,7 @@ _SIGS = {
     "slm_hip_attend_noalloc": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_set_graphs": (_i, [_p, _i]),
     "slm_hip_set_prompt_lanes": (_i, [_p, _i]),
+    "slm_hip_read_ahead_stats": (_i, [_p, C.POINTER(C.c_uint64)]),
     "slm_hip_get_prompt_lanes": (_i, [_p, C.POINTER(C.c_int)]),
     "slm_hip_prompt_lane_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "slm_hip_set_fusion": (_i, [_p, _i]),
@@ -251,6 +252,11 @@ class Hip:
 
     def set_graphs(self, on: bool):
         self.check(lib.slm_hip_set_graphs(self.ctx, int(on)))
+
+    def read_ahead_stats(self) -> int:
+        n = C.c_uint64()
+        self.check(lib.slm_hip_read_ahead_stats(self.ctx, C.byref(n)))
+        return n.value
 
     def set_prompt_lanes(self, n: int):
         self.check(lib.slm_hip_set_prompt_lanes(self.ctx, int(n)))

@@ -94,6 +94,30 @@ KERNEL void slm_to_half(_Float16* __restrict__ y, const float* __restrict__ x, l
     GRID_LOOP(i, n) y[i] = (_Float16)x[i];
 }
 
+// Copies n floats of device memory into mapped host memory, then the last workgroup to finish
+// stores `seq` into the host flag: every workgroup releases its stores at system scope before
+// it counts itself on the device counter (never reset: this launch's workgroups take the
+// values base .. last), and the one that takes `last` releases at system scope again before
+// the flag, so a host that sees the flag sees all n values. No waits: every workgroup ends.
+KERNEL void __launch_bounds__(256) slm_to_host(float* __restrict__ dst, const float* __restrict__ src,
+                                               long long n, unsigned long long* ctr,
+                                               unsigned long long last, unsigned long long* flag,
+                                               unsigned long long seq) {
+    long long n4 = n >> 2;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long long)gridDim.x * 256)
+        ((f4*)dst)[i] = ((const f4*)src)[i];
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) dst[4 * n4 + threadIdx.x] = src[4 * n4 + threadIdx.x];
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long k = __hip_atomic_fetch_add(ctr, 1ull, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (k == last) {
+            __threadfence_system();
+            __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
 KERNEL void slm_add(float* __restrict__ y, const float* __restrict__ a,
                     const float* __restrict__ b, long long n) {
     GRID_LOOP(i, n) y[i] = a[i] + b[i];

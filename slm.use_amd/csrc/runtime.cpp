@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -26,6 +27,8 @@
 #include <set>
 #include <string>
 #include <vector>
+
+#include <emmintrin.h>
 
 #include "fusion.h"
 #include "scratch.h"
@@ -44,6 +47,7 @@ constexpr size_t DYN_CAP = 1 << 20;       // bytes of per-step dynamic values
 constexpr size_t STAGE_CAP = 4 << 20;     // bytes of eager staging
 constexpr size_t BOUNCE_CAP = 4 << 20;    // pinned bounce buffer for reads
 constexpr int MAX_LANES = 4;              // prompt lanes (streams) a context may use
+constexpr size_t MIRROR_CAP = 512 << 10;  // bytes a read-ahead copy may take
 constexpr size_t MAX_GRAPHS = 8;
 constexpr int VP_LEN_MAX = 4096;          // longest vector a fused prologue holds
 constexpr int64_t COMB_PART_MAX = 16384;  // attention partials (floats) a fused prologue combines
@@ -97,6 +101,9 @@ struct Graph {
     size_t ndyn = 0;
     hipGraphExec_t exec = nullptr;
     uint64_t used = 0;
+    uint64_t id = 0;
+    const float* mir_src = nullptr;  // what the host read right after the last replay (mirrored)
+    size_t mir_n = 0;
 };
 
 struct Table {  // resident cos/sin rows for one inv_freq buffer
@@ -108,6 +115,7 @@ struct Table {  // resident cos/sin rows for one inv_freq buffer
 
 struct Kernels {
     hipFunction_t to_half;                   // fp32 -> fp16 weight shadows
+    hipFunction_t to_host;                   // read-ahead copies into mapped host memory
     hipFunction_t store16, grow, grow16;     // fp16 rings; cache growth
     hipFunction_t attn_dec16[3], attn_pq16[3];  // attention over fp16 rings
     hipFunction_t copy, add, add_row, mix, silu_mul, scale_rows, shift, columns, gather,
@@ -187,6 +195,20 @@ struct slm_hip {
     unsigned char* dyn_dev = nullptr;
     float* bounce = nullptr;
     hipEvent_t read_ev[2] = {nullptr, nullptr};  // the bounce buffer's halves (large reads)
+    // Read-ahead of a one-token step's output: when the host read a range right after a
+    // replay of a step graph, later replays of that graph copy the range into mapped host
+    // memory behind the step (slm_to_host), and a read of it waits for the copy's flag instead
+    // of a copy of its own.
+    float* mir_host = nullptr;           // MIRROR_CAP bytes, then the flag (mapped, pinned)
+    float* mir_dev = nullptr;            // ... its device address
+    unsigned long long* mir_ctr = nullptr;  // slm_to_host's workgroup counter (device)
+    unsigned long long mir_total = 0, mir_seq = 0;
+    bool mir_armed = false;              // a copy of (mir_src, mir_n) queued, nothing since
+    const float* mir_src = nullptr;
+    size_t mir_n = 0;
+    uint64_t last_graph = 0;             // id of the graph just replayed, nothing since
+    uint64_t next_graph_id = 0;
+    uint64_t n_mirror_reads = 0;
     std::map<uintptr_t, Table> tables;
     bool graphs_on = true, fusion_on = true, plan_trace = false;
     bool fp16 = false;                   // linears with fp16 operands (slm_hip_set_fp16)
@@ -455,6 +477,8 @@ void leave_lanes(slm_hip* c) {
 
 // The context's stream, for work that is not a lane's: joined with the lanes first.
 hipStream_t mstream(slm_hip* c) {
+    c->mir_armed = false;  // work queued after the read-ahead copy: reads go the usual way
+    c->last_graph = 0;
     leave_lanes(c);
     return c->stream;
 }
@@ -2903,6 +2927,57 @@ int finish_step(slm_hip* c) {
     return rc;
 }
 
+// After a step graph's launch: queue the read-ahead copy the graph has learned (the range the
+// host read right after its last replay, if still inside a live allocation) and note the
+// graph, so that a read of a new range right after it can be learned.
+int after_graph(slm_hip* c, Graph& g) {
+    if (!g.id) g.id = ++c->next_graph_id;
+    bool armed = false;
+    if (g.mir_src && c->mir_host && !inside(c, g.mir_src, g.mir_n * 4)) g.mir_src = nullptr;
+    if (g.mir_src && c->mir_host) {
+        size_t n = g.mir_n;
+        uint32_t nwg = (uint32_t)std::min<size_t>((n / 4 + 255) / 256, 64);
+        if (nwg == 0) nwg = 1;
+        unsigned long long base = c->mir_total, seq = c->mir_seq + 1;
+        Rec r = mk(c->k.to_host, nwg, 1, 1, 256, 0, c->mir_dev, g.mir_src, (long long)n, c->mir_ctr,
+                   (unsigned long long)(base + nwg - 1),
+                   (unsigned long long*)((char*)c->mir_dev + MIRROR_CAP), seq);
+        TRY(launch_now(c, r));
+        c->mir_total = base + nwg;
+        c->mir_seq = seq;
+        armed = true;
+    }
+    c->mir_armed = armed;  // (set after the launches: their mstream calls clear it)
+    c->mir_src = g.mir_src;
+    c->mir_n = g.mir_n;
+    c->last_graph = g.id;
+    return SLM_OK;
+}
+
+// The host read (dev, n) right after a replay of graph `id`: later replays copy that range
+// ahead (a read of anything else makes the graph forget it).
+int learn_read(slm_hip* c, uint64_t id, const float* dev, size_t n) {
+    for (auto& g : c->cache) {
+        if (g.id != id) continue;
+        bool ok = n > 0 && n * 4 <= MIRROR_CAP && aligned16(dev);
+        g.mir_src = ok ? dev : nullptr;
+        g.mir_n = ok ? n : 0;
+        if (ok && !c->mir_host) {
+            void* h = nullptr;
+            HIPC(c, hipHostMalloc(&h, MIRROR_CAP + 64, hipHostMallocMapped));
+            std::memset(h, 0, MIRROR_CAP + 64);
+            c->mir_host = (float*)h;
+            HIPC(c, hipHostGetDevicePointer((void**)&c->mir_dev, h, 0));
+            HIPC(c, hipMalloc((void**)&c->mir_ctr, 64));
+            HIPC(c, hipMemset(c->mir_ctr, 0, 64));
+            c->mir_total = 0;
+            c->mir_seq = 0;
+        }
+        break;
+    }
+    return SLM_OK;
+}
+
 // Captures the recorded step into a graph, or finds one that matches it; with graphs
 // off, plans the step and launches it directly.
 int finish_step_run(slm_hip* c) {
@@ -2935,7 +3010,7 @@ int finish_step_run(slm_hip* c) {
             g.used = c->clock;
             HIPC(c, hipGraphLaunch(g.exec, mstream(c)));
             c->n_launched++;
-            return SLM_OK;
+            return after_graph(c, g);
         }
     }
     if (c->plan_trace) {  // what sets this step apart from a cached one of the same length
@@ -2989,7 +3064,7 @@ int finish_step_run(slm_hip* c) {
     c->n_captured++;
     c->n_launched++;
     c->cache.push_back(std::move(g));
-    return SLM_OK;
+    return after_graph(c, c->cache.back());
 }
 
 int get_fn(slm_hip* c, hipFunction_t* f, const char* name) {
@@ -3013,6 +3088,7 @@ int load_kernels(slm_hip* c) {
                {&k.rms_wave, "slm_rms_wave"},   {&k.l2norm_wave, "slm_l2norm_wave"},
                {&k.fill, "slm_fill"},           {&k.combine, "slm_attn_combine"},
                {&k.to_half, "slm_to_half"},     {&k.store16, "slm_store16"},
+               {&k.to_host, "slm_to_host"},
                {&k.grow, "slm_grow"},           {&k.grow16, "slm_grow16"},
                {&k.attn_dec16[0], "slm_attn_dec16_1"}, {&k.attn_dec16[1], "slm_attn_dec16_2"},
                {&k.attn_dec16[2], "slm_attn_dec16_4"}, {&k.attn_pq16[0], "slm_attn_pq16_1"},
@@ -3173,6 +3249,8 @@ void slm_hip_close(slm_hip* c) {
         }
         if (L.stream) hipStreamDestroy(L.stream);
     }
+    if (c->mir_host) hipHostFree(c->mir_host);
+    if (c->mir_ctr) hipFree(c->mir_ctr);
     for (auto& r : c->ev_refs) hipEventDestroy(r.first);
     for (auto e : c->lane_ev_pool) hipEventDestroy(e);
     for (void* r : c->retired) release(r);
@@ -3349,12 +3427,35 @@ int slm_hip_read(slm_hip* c, float* host, const float* dev, size_t n) {
         return check_fault(c);
     }
     NEED(c, "read", dev, n);
+    // the read-ahead copy of exactly this range, queued behind the step just replayed with
+    // nothing after it: wait for its flag (a second at most, then the usual way)
+    if (c->mir_armed && !c->recording && dev == c->mir_src && n == c->mir_n) {
+        c->mir_armed = false;
+        const unsigned long long* flag = (const unsigned long long*)((char*)c->mir_host + MIRROR_CAP);
+        auto t0 = std::chrono::steady_clock::now();
+        bool got = false;
+        for (unsigned it = 0;; it++) {
+            if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) >= c->mir_seq) {
+                got = true;
+                break;
+            }
+            if ((it & 1023) == 1023 && std::chrono::steady_clock::now() - t0 > std::chrono::seconds(1)) break;
+            _mm_pause();
+        }
+        if (got) {
+            std::memcpy(host, c->mir_host, n * 4);
+            c->n_mirror_reads++;
+            return check_fault(c);
+        }
+    }
+    uint64_t after = c->recording ? 0 : c->last_graph;  // the graph this read follows, if any
     TRY(taint(c));
     hipStream_t s = mstream(c);
     if (n * 4 <= BOUNCE_CAP) {
         HIPC(c, hipMemcpyAsync(c->bounce, dev, n * 4, hipMemcpyDeviceToHost, s));
         HIPC(c, hipStreamSynchronize(s));
         std::memcpy(host, c->bounce, n * 4);
+        if (after) TRY(learn_read(c, after, dev, n));
         return check_fault(c);
     }
     // larger: the two halves of the bounce buffer in turn, the copy of part k + 1 running
@@ -3424,6 +3525,12 @@ int slm_hip_set_prompt_lanes(slm_hip* c, int n) {
         if (!L.dyn_dev) HIPC(c, hipMalloc((void**)&L.dyn_dev, DYN_CAP));
     }
     c->nlanes = n;
+    return SLM_OK;
+}
+
+int slm_hip_read_ahead_stats(slm_hip* c, uint64_t* reads) {
+    if (!c || !reads) return SLM_E_INVALID;
+    *reads = c->n_mirror_reads;
     return SLM_OK;
 }
 

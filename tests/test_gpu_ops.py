@@ -307,6 +307,59 @@ def _step(hip, body, inv, cs, sn, fuse):
     return plan
 
 
+def test_read_ahead_of_a_step_output(hip):
+    """A replayed one-token step graph whose output the host read right after its last replay
+    copies that range into mapped host memory behind the step, and the next read of it waits
+    for the copy; a read of another range, or one after other work, takes the usual copy.
+    Every read returns what the device holds."""
+    d = 768
+    inv = hip.upload((1.0 / 10000.0 ** (np.arange(32) * 2 / 64)).astype(np.float32))
+    cs, sn = hip.alloc(32), hip.alloc(32)
+    w = hip.upload(rnd(d, d, scale=0.02))
+    x = hip.upload(rnd(d))
+    y = hip.alloc(d)
+
+    def step():
+        hip.rope_table(cs.ptr, sn.ptr, inv.ptr, 7, 1, 32)
+        hip.linear(y.ptr, w.ptr, d, d, x.ptr, 1)
+        hip.flush([y.ptr])
+
+    def eager():
+        hip.set_graphs(False)
+        try:
+            step()
+            return y.read()
+        finally:
+            hip.set_graphs(True)
+
+    want = eager()
+    r0 = hip.read_ahead_stats()
+    for _ in range(5):  # capture, a read that teaches the graph, replays copied ahead
+        step()
+        assert np.array_equal(y.read(), want)
+    r1 = hip.read_ahead_stats()
+    assert r1 - r0 >= 3, (r0, r1)
+    step()  # another range: the usual copy (and the graph learns that one)
+    assert np.array_equal(y.read(100), want[:100])
+    step()
+    assert np.array_equal(y.read(), want)
+    step()
+    assert np.array_equal(y.read(), want)
+    z = rnd(d)
+    dz = hip.upload(z)
+    step()  # other work on the output after the replay: the read sees it
+    hip.copy(y.ptr, dz.ptr, d)
+    assert np.array_equal(y.read(), z)
+    x2 = rnd(d)
+    hip.upload_into(x, x2)  # new input: each replay's copy follows the device
+    want2 = eager()
+    assert not np.array_equal(want2, want)
+    for _ in range(3):
+        step()
+        assert np.array_equal(y.read(), want2)
+    assert hip.read_ahead_stats() > r1
+
+
 FUSION_CASES = ["plain", "rms", "resid", "silu", "rope_store", "l2_decay", "combine", "side_copy",
                 "split_fold", "split_flush", "gla_l2", "rounds", "row_offset"]
 
