@@ -187,6 +187,20 @@ int slm_hip_attend_noalloc(slm_hip* ctx, float* y, float* scores, const float* q
  * or upload inside a step runs what was recorded so far and finishes the step eagerly.
  * Results are identical in every mode: the same arithmetic runs. */
 int slm_hip_set_graphs(slm_hip* ctx, int on);
+/* One-launch steps (off by default; no trait counterpart, a backend setting): with graphs on,
+ * a one-token step whose planned kernels are all fp32 fused GEMVs, one-token attentions that
+ * leave their superblock partials to the next fused GEMV and one-token GLAs runs as ONE
+ * launch of 256 workgroups (one per compute unit) that runs those kernels' work as phases in
+ * order, each phase waiting for every workgroup to finish the one before (flags in device
+ * memory, polled; values handed between phases by device-scope loads and stores); other
+ * steps replay a graph. A phase's weights, and an attention phase's older keys and values,
+ * are issued before its wait. Same kernels' arithmetic, so the same bits. Needs 256 compute
+ * units free for the launch. Off by default: on the MI355X it measured slower than the
+ * step graph (a86 at R = 4: 1625 against 1850 tok/s). */
+int slm_hip_set_step_kernel(slm_hip* ctx, int on);
+/* One-launch steps run and programs built since the context opened, and whether the device
+ * can run them (1) or every step goes through a graph (0). */
+int slm_hip_step_stats(slm_hip* ctx, uint64_t* launches, uint64_t* programs, int* available);
 /* Prompt lanes (1 to 4; no trait counterpart, a backend setting): consecutive prompt steps
  * (advances of more than one token, ended by a flush) run on up to n streams at once, so
  * that chunk c + 1 starts while chunk c still runs. What a step writes and its flush does not

@@ -92,6 +92,8 @@ _SIGS = {
     "slm_hip_attend": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_attend_noalloc": (_i, [_p, _p, _p, _p, _p, _p, C.POINTER(Attn)]),
     "slm_hip_set_graphs": (_i, [_p, _i]),
+    "slm_hip_set_step_kernel": (_i, [_p, _i]),
+    "slm_hip_step_stats": (_i, [_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_int)]),
     "slm_hip_set_prompt_lanes": (_i, [_p, _i]),
     "slm_hip_read_ahead_stats": (_i, [_p, C.POINTER(C.c_uint64)]),
     "slm_hip_get_prompt_lanes": (_i, [_p, C.POINTER(C.c_int)]),
@@ -252,6 +254,14 @@ class Hip:
 
     def set_graphs(self, on: bool):
         self.check(lib.slm_hip_set_graphs(self.ctx, int(on)))
+
+    def set_step_kernel(self, on: bool):
+        self.check(lib.slm_hip_set_step_kernel(self.ctx, int(on)))
+
+    def step_stats(self):
+        a, b, c = C.c_uint64(), C.c_uint64(), C.c_int()
+        self.check(lib.slm_hip_step_stats(self.ctx, C.byref(a), C.byref(b), C.byref(c)))
+        return dict(launches=a.value, programs=b.value, available=bool(c.value))
 
     def read_ahead_stats(self) -> int:
         n = C.c_uint64()

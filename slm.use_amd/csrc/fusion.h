@@ -150,6 +150,47 @@ typedef struct {
     float pad;
 } GlaDesc;
 
+// A one-token step in one launch (slm_step): the kernels the planner made for the step, in
+// order, as phases of a program that every workgroup of a 256-workgroup launch runs through.
+// Workgroup w stores epoch + p + 1 into flags[w] when it is done with phase p; phase p
+// begins with a wait until every flag has reached epoch + p. What a phase reads that another
+// phase of the same launch wrote is read and written past the caches that are not shared by
+// the whole device (device-scope loads and stores), so a phase sees the last one's results
+// without the cache write-back and invalidation a kernel boundary brings.
+enum {
+    PH_FG = 1,    // a fused GEMV: FgDesc (slm_fg)
+    PH_ADEC = 2,  // one-token attention writing its superblock partials: AdecArgs (slm_attn_dec_*)
+    PH_GLA1 = 3,  // one-token gated linear attention: GlaDesc (slm_gla1_*)
+};
+#define SLM_STEP_WG 256       // workgroups of a step launch
+#define SLM_STEP_THREADS 1024 // threads of each
+#define SLM_STEP_GROUP 4      // query heads per key head a step's attention phase takes
+typedef struct {
+    int32_t kind, var;  // var: the attention's dim tiles (0: 1, 1: 2, 2: 4) or the GLA's rows per lane
+    int32_t grid, gx;   // workgroups that run the phase; the attention's key heads (its grid's x)
+    int32_t arg, pad;   // byte offset of the phase's argument block from the program's start
+} StepPh;
+typedef struct {
+    const char* prog;   // [nph] StepPh, then the argument blocks (16-byte aligned)
+    unsigned* flags;    // [SLM_STEP_WG]
+    int* fault;         // a wait that gives up ORs 1 in here (host memory)
+    unsigned epoch;
+    int32_t nph, spin, pad;
+} StepArgs;
+// The one-token attention's arguments as a launch record packs them: one 8-byte slot each.
+typedef struct {
+    float* part;
+    const float* q;
+    const float* kc;
+    const float* vc;
+    const long long* dyn;
+    long long pos_imm, reach, gap, cap;
+    long long heads, key_heads, dh;  // (ints in the low half of their slots)
+    float scale, pad0;
+    float* y;
+    int* ctr;
+} AdecArgs;
+
 // A prompt row chain (m > 1 tokens): consecutive row-local element-wise ops between two
 // GEMMs run as one launch, one workgroup per token row. Each op's operands come from the
 // LDS copy of an earlier op's output row or from global memory (row r at g + r·stride;

@@ -21,7 +21,6 @@
 #include <stdint.h>
 
 #include "fusion.h"
-
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 #define KERNEL extern "C" __global__
@@ -50,6 +49,87 @@ __device__ __forceinline__ void gst(T* p, T v) {
 // A value into an fp16 ring, rounded to nearest even.
 __device__ __forceinline__ void gst16(_Float16* p, float v) {
     *(GAS _Float16*)p = (_Float16)v;
+}
+
+// Device-scope loads and stores (sc1: past the per-XCD L2 for what other workgroups of the
+// same launch read or wrote), used by the phases of a one-launch step (slm_step) for every
+// value one phase hands to another; with C false, the plain access.
+template <bool C, typename T>
+__device__ __forceinline__ T ldc(const T* p) {
+    if constexpr (C) return __hip_atomic_load((const GAS T*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *(const GAS T*)p;
+}
+template <bool C, typename T>
+__device__ __forceinline__ void stc(T* p, T v) {
+    if constexpr (C) __hip_atomic_store((GAS T*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *(GAS T*)p = v;
+}
+
+// A bounded wait of a fused kernel that gave up: lane 0 ORs 1 into the fault word (host
+// memory), which the runtime reports at the next read or flush. The kernel goes on, so a
+// mistake cannot hang the GPU; its results are then not valid.
+__device__ __forceinline__ void wait_gave_up(int* fault, int lane) {
+    if (fault && lane == 0) __hip_atomic_fetch_or(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The wait at the start of a phase of slm_step: until every workgroup's flag has reached
+// `target` (workgroup w stores epoch + p + 1 into flags[w] once it is done with phase p),
+// polled by one wave with device-scope loads; no wait when `flags` is null (the first
+// phase). Gives up after `spin` polls and returns true then (the fault word set).
+struct StepWait {
+    const unsigned* flags;
+    unsigned target;
+    int spin;
+    int* fault;
+};
+__device__ __forceinline__ bool step_wait(const StepWait& w, int lane) {
+    if (!w.flags) return false;
+    // two polls in flight: each check waits only for the older one
+    constexpr int NJ = SLM_STEP_WG / 64;
+    auto poll = [&](unsigned (&f)[NJ]) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            f[j] = __hip_atomic_load(w.flags + 64 * j + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto done = [&](const unsigned (&f)[NJ]) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) ok = ok && (int)(f[j] - w.target) >= 0;
+        return __all(ok) != 0;
+    };
+    unsigned fa[NJ], fb[NJ];
+    int it = 0;
+    if (w.spin > 0) poll(fa);
+    for (; it < w.spin; it += 2) {
+        poll(fb);
+        if (done(fa)) break;
+        poll(fa);
+        if (done(fb)) break;
+    }
+    // (later loads stay after the polls: the compiler may not lift them above this fence, and
+    // the hardware issues them only once the loop has seen the flags)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    bool gave_up = it >= w.spin;
+    if (gave_up) wait_gave_up(w.fault, lane);
+    return gave_up;
+}
+
+// A workgroup barrier that orders LDS only (what memory loads are in flight stay in flight).
+__device__ __forceinline__ void lds_bar() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The wait of a step phase whose body runs on every wave of the workgroup: wave 0 polls, the
+// workgroup learns the outcome at an LDS barrier (`gave` in LDS). True: the wait gave up.
+__device__ __forceinline__ bool step_wait_wg(const StepWait& w, int* gave, int tid) {
+    if ((tid >> 6) == 0) {
+        bool g = step_wait(w, tid & 63);
+        if (tid == 0) *gave = g;
+    }
+    lds_bar();
+    return *gave != 0;
 }
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
@@ -2245,23 +2325,25 @@ ATTN_PQ(slm_attn_pq16_4, 4, true)
 // With KH the rings hold fp16 values (fp16 mode's caches): each lane loads its four halves of
 // a chunk into registers and writes them, widened exactly, where the copy would have put the
 // floats; everything after the staging is the fp32 kernel's.
-template <int DT, bool KH = false>
-__device__ void attn_dec_body(float* __restrict__ part, const float* __restrict__ q,
+template <int DT, bool KH = false, bool STEP = false>
+__device__ __forceinline__ bool attn_dec_body(float* __restrict__ part, const float* __restrict__ q,
                               const float* __restrict__ kc, const float* __restrict__ vc,
                               const long long* __restrict__ dyn, long long pos_imm,
                               long long reach, long long gap, long long cap, int heads,
                               int key_heads, int dh, float scale, float* __restrict__ y,
-                              int* __restrict__ ctr) {
+                              int* __restrict__ ctr, int bx, int by, int ny, int tid,
+                                              const StepWait* sw = nullptr, int* gave = nullptr) {
+    static_assert(!(STEP && KH), "a step phase reads fp32 rings");
     static_assert(DT >= 1 && DT <= 4, "one-token attention: head size at most 64");
     constexpr int DP = 16 * DT;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     long long pos = dyn_or(dyn, pos_imm);
-    int lane = threadIdx.x & 63;
-    int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    int group = heads / key_heads, kvh = blockIdx.x;
+    int lane = tid & 63;
+    int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int group = heads / key_heads, kvh = bx;
     int nch = dh >> 2;  // 16-byte chunks per row
     long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
-    long long sb = first / SLM_SB_KEYS + blockIdx.y;
+    long long sb = first / SLM_SB_KEYS + by;
     long long seg_lo = (sb * SLM_SB_SEGS + wave) * 64;
     constexpr unsigned ES = KH ? 2u : 4u;  // bytes per ring element
     const char* kb = (const char*)kc + (long long)kvh * cap * dh * ES;
@@ -2273,59 +2355,125 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
     // chunks per instruction (a lane past the end copies the last chunk into unused LDS)
     int nqc = (group * dh) >> 2;
     const float* qg = q + (long long)kvh * group * dh;
-    for (int k = 0; k < (nqc + 63) / 64; k++) {
-        int ch = min(64 * k + lane, nqc - 1);
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(qg + 4 * ch),
-                                         (__attribute__((address_space(3))) void*)(qt + 256 * k), 16, 0, 0);
-    }
+    auto copy_q = [&]() {
+        for (int k = 0; k < (nqc + 63) / 64; k++) {
+            int ch = min(64 * k + lane, nqc - 1);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(qg + 4 * ch),
+                                             (__attribute__((address_space(3))) void*)(qt + 256 * k), 16, 0, STEP ? 16 : 0);
+        }
+    };
+    if (!STEP) copy_q();
     // keys, then values: instruction k covers keys 4k .. 4k+3; lane L takes key 4k + L/16 and
     // puts chunk (L % 16) ^ (key & 15) of its row at position L % 16 (a chunk at or past dh
     // copies the row's last one: it is never read). Key 4k + g is ring slot (seg_lo + 4k + g)
     // mod cap; with cap >= 64 each step of four keys wraps at most once, and a key head's
     // ring is under 4 GB, so byte offsets are 32-bit (the host checks both).
+    // (the offsets are worked out again for the values: sixteen registers fewer held)
     unsigned rowb = (unsigned)dh * ES, wrapb = (unsigned)cap * rowb;
     unsigned slot = (unsigned)(seg_lo % cap) + (unsigned)(lane >> 4);
     if (slot >= (unsigned)cap) slot -= (unsigned)cap;
-    unsigned roff = slot * rowb;
-    unsigned off[16];
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
+    const unsigned roff0 = slot * rowb;
+    auto off_of = [&](int k, unsigned roff) {
         int key = 4 * k + (lane >> 4);
-        off[k] = roff + 4u * ES * (unsigned)min((lane & 15) ^ (key & 15), nch - 1);
-        roff += 4 * rowb;
-        if (roff >= wrapb) roff -= wrapb;
-    }
+        return roff + 4u * ES * (unsigned)min((lane & 15) ^ (key & 15), nch - 1);
+    };
     h4 hk[KH ? 16 : 1], hv[KH ? 16 : 1];
     if constexpr (KH) {  // four halves per lane per instruction, into registers
+        unsigned roff = roff0;
 #pragma unroll
-        for (int k = 0; k < 16; k++) hk[k] = __builtin_nontemporal_load((const GAS h4*)(kb + off[k]));
+        for (int k = 0; k < 16; k++) {
+            hk[k] = __builtin_nontemporal_load((const GAS h4*)(kb + off_of(k, roff)));
+            roff += 4 * rowb;
+            if (roff >= wrapb) roff -= wrapb;
+        }
+        roff = roff0;
 #pragma unroll
-        for (int k = 0; k < 16; k++) hv[k] = __builtin_nontemporal_load((const GAS h4*)(vb + off[k]));
+        for (int k = 0; k < 16; k++) {
+            hv[k] = __builtin_nontemporal_load((const GAS h4*)(vb + off_of(k, roff)));
+            roff += 4 * rowb;
+            if (roff >= wrapb) roff -= wrapb;
+        }
     } else {
         // (non-temporal: the keys and values are read once per token, and should not push
         // this kernel's code and the partials out of L2)
+        unsigned roff = roff0;
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off[k]),
+        for (int k = 0; k < 16; k++) {
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off_of(k, roff)),
                                              (__attribute__((address_space(3))) void*)(kt + 256 * k), 16, 0, 2);
+            roff += 4 * rowb;
+            if (roff >= wrapb) roff -= wrapb;
+        }
+        roff = roff0;
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off[k]),
+        for (int k = 0; k < 16; k++) {
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off_of(k, roff)),
                                              (__attribute__((address_space(3))) void*)(vt + 256 * k), 16, 0, 2);
+            roff += 4 * rowb;
+            if (roff >= wrapb) roff -= wrapb;
+        }
     }
-    vm_wait<16>();  // the queries and keys are in (the values may still be on their way)
+    if constexpr (STEP) {
+        // As a step phase the copies above went out before the wait for the QKV phase: the
+        // ring held everything but the newest key and value then. After the wait, the queries
+        // and that one slot (copied again, device scope, over its first copy: a wave's copies
+        // land in order) — in the wave whose segment holds the position.
+        if (step_wait_wg(*sw, gave, tid)) return false;
+        copy_q();
+        long long kidx = pos - seg_lo;
+        if (kidx >= 0 && kidx < 64 && (int)(kidx & 3) == (lane >> 4)) {
+            int k = (int)(kidx >> 2);
+            unsigned r = roff0 + (unsigned)k * 4u * rowb;
+            if (r >= wrapb) r -= wrapb;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(kb + off_of(k, r)),
+                                             (__attribute__((address_space(3))) void*)(kt + 256 * k), 16, 0, 18);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(vb + off_of(k, r)),
+                                             (__attribute__((address_space(3))) void*)(vt + 256 * k), 16, 0, 18);
+        }
+        vm_wait<0>();
+    } else {
+        vm_wait<16>();  // the queries and keys are in (the values may still be on their way)
+    }
     asm volatile("" ::: "memory");
     if constexpr (KH) {  // the keys, widened, where the copies put fp32 rows
 #pragma unroll
         for (int k = 0; k < 16; k++) *(f4*)(kt + 256 * k + 4 * lane) = wide4(hk[k]);
     }
-    // this lane's key: dims 16t + 4g .. +3 as kr[t][g]
+    // this lane's key: dims 16t + 4g .. +3 as kr[t][g], in registers before anything is
+    // written over the keys (the p tile and the fold slots below take their first rows). As
+    // a step phase (fewer registers: a quarter of the CU's each), the scores of every query
+    // column (at most SLM_STEP_GROUP) instead, one dim tile of the key at a time: each
+    // column's chain runs over t, e, g in the same order.
     int j = lane;
-    f4 kr[DT][4];
+    f4 kr[STEP ? 1 : DT][4];
+    float sc[SLM_STEP_GROUP];
+    if constexpr (STEP) {
 #pragma unroll
-    for (int t = 0; t < DT; t++)
+        for (int c = 0; c < SLM_STEP_GROUP; c++) sc[c] = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 4; g++) kr[t][g] = *(const f4*)(kt + 4 * (16 * j + ((4 * t + g) ^ (j & 15))));
+        for (int t = 0; t < DT; t++) {
+            f4 kt4[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) kt4[g] = *(const f4*)(kt + 4 * (16 * j + ((4 * t + g) ^ (j & 15))));
+#pragma unroll
+            for (int c = 0; c < SLM_STEP_GROUP; c++) {
+                if (c >= group) break;
+                f4 qv[4];
+#pragma unroll
+                for (int g = 0; g < 4; g++) qv[g] = *(const f4*)(qt + c * dh + min(16 * t + 4 * g, dh - 4));
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+                        if (16 * t + 4 * g < dh) sc[c] = fmaf(kt4[g][e], qv[g][e], sc[c]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) kr[t][g] = *(const f4*)(kt + 4 * (16 * j + ((4 * t + g) ^ (j & 15))));
+    }
     long long kp = seg_lo + j;
     float* pt = kt;             // p of the current tile [16], over the keys once read
     float* fs = kt + 64;        // fold slots [group][DP + 2]
@@ -2338,19 +2486,25 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
     bool vwait = true;
     for (int c = 0; c < group; c++) {
         Col col = column(c, 0, pos, 1, reach, gap, group, 16 / group, kvh);
-        f4 qv[DT][4];  // the same for every lane (LDS broadcast)
-#pragma unroll
-        for (int t = 0; t < DT; t++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) qv[t][g] = *(const f4*)(qt + c * dh + min(16 * t + 4 * g, dh - 4));
         float s = 0.0f;
+        if constexpr (STEP) {
+            s = sc[0];
 #pragma unroll
-        for (int t = 0; t < DT; t++)
+            for (int q = 1; q < SLM_STEP_GROUP; q++)
+                if (c == q) s = sc[q];
+        } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++)
+            for (int t = 0; t < DT; t++) {
+                f4 qv[4];  // the query's dims of tile t (the same for every lane: LDS broadcast)
 #pragma unroll
-                for (int g = 0; g < 4; g++)
-                    if (16 * t + 4 * g < dh) s = fmaf(kr[t][g][e], qv[t][g][e], s);
+                for (int g = 0; g < 4; g++) qv[g] = *(const f4*)(qt + c * dh + min(16 * t + 4 * g, dh - 4));
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+                        if (16 * t + 4 * g < dh) s = fmaf(kr[t][g][e], qv[g][e], s);
+            }
+        }
         bool ok = kp >= col.lo && kp < col.hi;
         float sv = ok ? s * scale : NEG_INF;
         float tm = sv;  // tile maxima
@@ -2414,7 +2568,7 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
     }
     __syncthreads();
     // fold the four segments in order, one (column, dim) per thread
-    for (int t = threadIdx.x; t < group * DP; t += 64 * SLM_SB_SEGS) {
+    for (int t = tid; t < group * DP; t += 64 * SLM_SB_SEGS) {
         int cc = t / DP, dd = t % DP;
         if (dd >= dh) continue;
         float FM = NEG_INF, FL = 0.0f, FO = 0.0f;
@@ -2424,8 +2578,8 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
             fold(FM, FL, FO, F[0], F[1], F[2 + dd]);
         }
         int head = kvh * group + cc;
-        float* P = part + ((long long)blockIdx.y * heads + head) * (long long)(DP + 2);
-        if (ctr) {  // written through to where every workgroup's loads see it
+        float* P = part + ((long long)by * heads + head) * (long long)(DP + 2);
+        if (ctr || STEP) {  // written through to where every workgroup's loads see it
             if (dd == 0) {
                 __hip_atomic_store(P, FM, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(P + 1, FL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2439,43 +2593,43 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
             P[2 + dd] = FO;
         }
     }
-    if (!ctr) return;
+    if (!ctr) return true;
     // the last workgroup of this key head combines the superblocks (slm_attn_combine's
     // expressions) from a copy of every partial in LDS, read in one pass
     __builtin_amdgcn_s_waitcnt(0);
     __shared__ int last;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int* cp = ctr + blockIdx.x;
+    if (tid == 0) {
+        int* cp = ctr + bx;
         int before = __hip_atomic_fetch_add(cp, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = before == (int)gridDim.y - 1;
+        last = before == ny - 1;
         if (last) __hip_atomic_store(cp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!last) return;
+    if (!last) return true;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // the key head's slots are group·(DP + 2) contiguous floats per superblock; thread f of a
     // pass takes float f mod 2^sh of slot f / 2^sh (2^sh: that count rounded up to a power of 2)
-    int nsb = (int)gridDim.y, sr = group * (DP + 2);
+    int nsb = ny, sr = group * (DP + 2);
     int sh = 32 - __clz(sr - 1);
     int nf = nsb << sh;
     for (int b = 0; b < nf; b += 8 * 64 * SLM_SB_SEGS) {
         float v[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            int f = b + threadIdx.x + u * 64 * SLM_SB_SEGS;
+            int f = b + tid + u * 64 * SLM_SB_SEGS;
             int z = min(f >> sh, nsb - 1), e = min(f & ((1 << sh) - 1), sr - 1);
             v[u] = part[((long long)z * heads + kvh * group) * (DP + 2) + e];
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            int f = b + threadIdx.x + u * 64 * SLM_SB_SEGS;
+            int f = b + tid + u * 64 * SLM_SB_SEGS;
             int z = f >> sh, e = f & ((1 << sh) - 1);
             if (z < nsb && e < sr) lds[z * sr + e] = v[u];
         }
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < group * DP; t += 64 * SLM_SB_SEGS) {
+    for (int t = tid; t < group * DP; t += 64 * SLM_SB_SEGS) {
         int cc = t / DP, dd = t % DP;
         if (dd >= dh) continue;
         const float* P = lds + cc * (DP + 2);
@@ -2512,6 +2666,7 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
         }
         y[(long long)(kvh * group + cc) * dh + dd] = L > 0.0f ? O / L : 0.0f;
     }
+    return true;
 }
 
 #define ATTN_DEC(NAME, DT, KH)                                                           \
@@ -2521,7 +2676,8 @@ __device__ void attn_dec_body(float* __restrict__ part, const float* __restrict_
         long long cap, int heads, int key_heads, int dh, float scale, float* y,          \
         int* ctr) {                                                                      \
         attn_dec_body<DT, KH>(part, q, kc, vc, dyn, pos_imm, reach, gap, cap, heads,      \
-                              key_heads, dh, scale, y, ctr);                             \
+                              key_heads, dh, scale, y, ctr, blockIdx.x, blockIdx.y,      \
+                              gridDim.y, threadIdx.x);                                   \
     }
 ATTN_DEC(slm_attn_dec_1, 1, false)
 ATTN_DEC(slm_attn_dec_2, 2, false)
@@ -2611,13 +2767,6 @@ KERNEL void slm_probe_mfma(float* out, const float* a, const float* b) {
 // ---------------------------------------------------------------------------------------
 // fused decode kernels (one token), driven by the descriptors of fusion.h
 // ---------------------------------------------------------------------------------------
-
-// A bounded wait of a fused kernel that gave up: lane 0 ORs 1 into the fault word (host
-// memory), which the runtime reports at the next read or flush. The kernel goes on, so a
-// mistake cannot hang the GPU; its results are then not valid.
-__device__ __forceinline__ void wait_gave_up(int* fault, int lane) {
-    if (fault && lane == 0) __hip_atomic_fetch_or(fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
 
 // The prologue waves' own barrier: a counter in LDS that each of the `nw` waves bumps once
 // per barrier, then waits for (the GEMV waves meanwhile wait for their weights, not for
@@ -3090,8 +3239,7 @@ struct KDw {
         return (long long)(unsigned)(*this)[q] | ((long long)(*this)[q + 1] << 32);
     }
 };
-__device__ __forceinline__ KDw kdw_load(int base, int lane) {
-    const int* k = (const int*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
+__device__ __forceinline__ KDw kdw_load(const int* k, int base, int lane) {
     return KDw{gld(k + base + lane), gld(k + base + 64 + lane)};
 }
 
@@ -3175,6 +3323,7 @@ __device__ __forceinline__ void fg_load(const FgLane& p, f4 (&wa)[SLM_KS]) {
 // finds M (the largest m of the superblocks that saw a key) from the (m, l) pairs, lane z
 // holds superblock z's weight w_z = e^(m_z − M) and l_z·w_z, lane d sums dim d in
 // superblock order; x[64h + d] = O / L (0 when no superblock saw a key). nsb ≤ 64.
+template <bool C>
 __device__ __forceinline__ void fg_comb_wave(const float* part, float* x, int heads, int dp,
                                              int nsb, int h, int lane, float* gout) {
     int sr = heads * (dp + 2);
@@ -3215,7 +3364,7 @@ __device__ __forceinline__ void fg_comb_wave(const float* part, float* x, int he
     }
     float v = L > 0.0f ? O / L : 0.0f;
     x[64 * h + lane] = v;
-    if (gout) gout[64 * h + lane] = v;
+    if (gout) stc<C>(gout + 64 * h + lane, v);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
 }
 
@@ -3260,7 +3409,7 @@ __device__ __forceinline__ unsigned long long pick_key(float v, int row) {
 // workgroup to count itself in writes the pick out and clears the key and the counter for
 // the next launch. (The release of the count orders the maximum before it; the acquire of
 // the last count sees every workgroup's.)
-__device__ void fg_pick_finish(const FgSeg& g, unsigned long long best, int lane) {
+__device__ void fg_pick_finish(const FgSeg& g, unsigned long long best, int lane, int nwg) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         unsigned lo = __shfl_xor((unsigned)best, off), hi = __shfl_xor((unsigned)(best >> 32), off);
@@ -3272,7 +3421,7 @@ __device__ void fg_pick_finish(const FgSeg& g, unsigned long long best, int lane
     int* ctr = (int*)g.o3 + 2;
     if (best) __hip_atomic_fetch_max(key, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (before != (int)gridDim.x - 1) return;
+    if (before != nwg - 1) return;
     unsigned long long k = __hip_atomic_load(key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     long long r = k ? (long long)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)) : 0;
     gst((long long*)g.o1, r);
@@ -3282,28 +3431,17 @@ __device__ void fg_pick_finish(const FgSeg& g, unsigned long long best, int lane
 }
 
 // The fused GEMV, fp32 (slm_fg), fp16 mode (slm_fgh) and fp16 mode with fp16 weights
-// (slm_fghw): one kernel text, expanded three times.
-#define FG_NAME slm_fg
-#define FG_H false
-#define FG_W false
+// (slm_fghw): one body, fg_run, whose descriptor is the kernel's only argument.
 #include "fg_body.inc"
-#undef FG_NAME
-#undef FG_H
-#undef FG_W
-#define FG_NAME slm_fgh
-#define FG_H true
-#define FG_W false
-#include "fg_body.inc"
-#undef FG_NAME
-#undef FG_H
-#undef FG_W
-#define FG_NAME slm_fghw
-#define FG_H true
-#define FG_W true
-#include "fg_body.inc"
-#undef FG_NAME
-#undef FG_H
-#undef FG_W
+#define FG_KERNEL(NAME, H, W)                                                                   \
+    KERNEL void __launch_bounds__(1024) NAME(const FgDesc dk) {                                 \
+        fg_run<H, W, false>(dk, (const int*)(const void*)__builtin_amdgcn_kernarg_segment_ptr(), \
+                            blockIdx.x, gridDim.x, StepWait{nullptr, 0, 0, nullptr},            \
+                            threadIdx.x);                                                       \
+    }
+FG_KERNEL(slm_fg, false, false)
+FG_KERNEL(slm_fgh, true, false)
+FG_KERNEL(slm_fghw, true, true)
 
 // The splits of a linear added in order: y[c] = ((P0[c] + P1[c]) + P2[c]) + ...
 KERNEL void slm_fold(float* __restrict__ y, const float* __restrict__ part, long long n, int nsplit) {
@@ -3421,7 +3559,7 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     long long r = blockIdx.x;
     int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    KDw hd = kdw_load(0, lane);
+    KDw hd = kdw_load((const int*)(const void*)__builtin_amdgcn_kernarg_segment_ptr(), 0, lane);
     f4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (tid < ND4) dv = ((const f4*)(const void*)__builtin_amdgcn_kernarg_segment_ptr())[tid];
     int nops = hd[0], npf = hd[1];
@@ -3610,10 +3748,11 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
 // gla_body, same expressions). When `l2`, q and k are first l2-normalised per head
 // (model.rs:465-467, the expressions of slm_l2norm); when `fuse`, the head RMSNorm and the
 // SiLU gate of model.rs:483-484 follow, in the expressions of slm_rms and slm_silu_mul.
-template <int RPL>
-__device__ void gla1_body(const GlaDesc& g) {
+template <int RPL, bool STEP = false>
+__device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int nt,
+                                          const StepWait* sw = nullptr, int* gave = nullptr) {
     extern __shared__ __attribute__((aligned(16))) float lds[];  // [dh + 4] rms, [dh] q, [dh] k, 4 norms
-    int h = blockIdx.x, tid = threadIdx.x, dh = g.dh;
+    int dh = g.dh;
     int b = tid >> 4, j = tid & 15;
     bool live = b < dh;
     float* Sh = g.s + (long long)h * dh * dh;
@@ -3624,12 +3763,15 @@ __device__ void gla1_body(const GlaDesc& g) {
         int a = j * RPL + rr;
         st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
     }
+    // (as a step phase, the state, from earlier steps, is read before the wait for the
+    // phase that made q, k, v and the decay)
+    if (STEP && step_wait_wg(*sw, gave, tid)) return false;
     float* lq = lds + dh + 4;
     float* lk = lq + dh;
     float* nr = lk + dh;
-    for (int c = tid; c < dh; c += blockDim.x) {
-        lq[c] = g.q[at + c];
-        lk[c] = g.k[at + c];
+    for (int c = tid; c < dh; c += nt) {
+        lq[c] = ldc<STEP>(g.q + at + c);
+        lk[c] = ldc<STEP>(g.k + at + c);
     }
     __syncthreads();
     if (g.l2) {
@@ -3644,8 +3786,8 @@ __device__ void gla1_body(const GlaDesc& g) {
         if (c < dh) {
             aq = lq[c] * rq;
             ak = lk[c] * rk;
-            g.qn[at + c] = aq;
-            g.kn[at + c] = ak;
+            stc<STEP>(g.qn + at + c, aq);
+            stc<STEP>(g.kn + at + c, ak);
         }
         __syncthreads();
         if (c < dh) {
@@ -3654,8 +3796,8 @@ __device__ void gla1_body(const GlaDesc& g) {
         }
         __syncthreads();
     }
-    float dc = 1.0f / (1.0f + expf(g.decay[h] + g.bias[h]));
-    float vb = live ? g.v[at + b] : 0.0f;
+    float dc = 1.0f / (1.0f + expf(ldc<STEP>(g.decay + h) + g.bias[h]));
+    float vb = live ? ldc<STEP>(g.v + at + b) : 0.0f;
     float part = live ? gla_rows<RPL>(st, lk, lq, dc, vb, j, dh) : 0.0f;
     float t2 = gla_colsum(part);
 #pragma unroll
@@ -3663,8 +3805,8 @@ __device__ void gla1_body(const GlaDesc& g) {
         int a = j * RPL + rr;
         if (live && a < dh) Sh[(long long)a * dh + b] = st[rr];
     }
-    if (live && j == 0) g.y[at + b] = t2;
-    if (!g.fuse) return;
+    if (live && j == 0) stc<STEP>(g.y + at + b, t2);
+    if (!g.fuse) return true;
     if (live && j == 0) lds[b] = t2;
     __syncthreads();
     if (tid < 16) {
@@ -3674,14 +3816,87 @@ __device__ void gla1_body(const GlaDesc& g) {
     __syncthreads();
     if (live && j == 0) {
         float y2 = lds[b] * lds[dh] * g.hn[b];
-        g.y2[at + b] = y2;
-        float gt = g.gate[at + b];
-        g.out[at + b] = y2 * gt / (1.0f + expf(-gt));
+        stc<STEP>(g.y2 + at + b, y2);
+        float gt = ldc<STEP>(g.gate + at + b);
+        stc<STEP>(g.out + at + b, y2 * gt / (1.0f + expf(-gt)));
     }
+    return true;
 }
 
 #define GLA1(R)                                                                   \
-    KERNEL void __launch_bounds__(1024) slm_gla1_##R(const GlaDesc g) { gla1_body<R>(g); }
+    KERNEL void __launch_bounds__(1024) slm_gla1_##R(const GlaDesc g) { gla1_body<R>(g, blockIdx.x, threadIdx.x, blockDim.x); }
 GLA1(1)
 GLA1(2)
 GLA1(4)
+
+// ---------------------------------------------------------------------------------------
+// one one-token step in one launch
+// ---------------------------------------------------------------------------------------
+
+// Every workgroup runs the step's phases in order: the kernels the planner made for the step
+// (fused GEMVs, one-token attentions that leave their superblock partials to the next fused
+// GEMV, one-token GLAs), each as the workgroups of its own grid would have run it, waiting
+// before it until every workgroup is done with the previous phase (StepWait). Workgroups past
+// a phase's grid pass it at once. A wait that gives up ends the workgroup (the others' waits
+// then give up in turn), so a mistake cannot hang the GPU. The launch needs every workgroup
+// resident at once: 256 workgroups of 1024 threads, one per compute unit. One kernel per head
+// size class (V: the attention's 16-dim tiles and the GLA's rows per lane, 1, 2 or 4), so
+// that each holds only the code its phases run.
+// The kernel argument, read again where it is used: nothing of it stays in registers across
+// a phase (the fused GEMV needs nearly every scalar register).
+__device__ __forceinline__ const StepArgs* step_args() {
+    const StepArgs* p = (const StepArgs*)(const void*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return p;
+}
+template <int V>
+__device__ __forceinline__ void step_run() {
+    __shared__ int gave;
+    for (int p = 0;; p++) {
+        // The thread and workgroup indices, taken afresh each phase: the compiler cannot
+        // lift what a phase works out from them out of the loop, where it would hold
+        // registers through every other phase.
+        int tid = threadIdx.x, bid = blockIdx.x;
+        asm volatile("" : "+v"(tid), "+s"(bid));
+        int lane = tid & 63, wave = tid >> 6;
+        const StepArgs& a = *step_args();
+        if (p >= a.nph) break;
+        const StepPh* ph = (const StepPh*)a.prog;
+        int kind = uni(ph[p].kind), grid = uni(ph[p].grid), gx = uni(ph[p].gx);
+        const char* arg = a.prog + uni(ph[p].arg);
+        StepWait sw{p > 0 ? a.flags : nullptr, a.epoch + (unsigned)p, a.spin, a.fault};
+        if (bid < grid) {
+            if (kind == PH_FG) {
+                if (!fg_run<false, false, true>(*(const FgDesc*)arg, (const int*)arg, bid, grid, sw, tid)) return;
+            } else if (kind == PH_ADEC) {
+                // one (key head, superblock) a workgroup on waves 0..3, as the kernel; it waits
+                // for the previous phase once its old keys and values are on their way
+                const AdecArgs& A = *(const AdecArgs*)arg;
+                if (wave < SLM_SB_SEGS) {
+                    if (!attn_dec_body<V, false, true>(A.part, A.q, A.kc, A.vc, A.dyn, A.pos_imm, A.reach,
+                                                       A.gap, A.cap, (int)A.heads, (int)A.key_heads,
+                                                       (int)A.dh, A.scale, nullptr, nullptr, bid % gx,
+                                                       bid / gx, grid / gx, tid, &sw, &gave))
+                        return;
+                } else {  // the body's barriers: the wait's, then its own
+                    lds_bar();
+                    if (gave) return;
+                    __syncthreads();
+                }
+            } else {
+                if (!gla1_body<V, true>(*(const GlaDesc*)arg, bid, tid, SLM_STEP_THREADS, &sw, &gave)) return;
+            }
+        }
+        // this workgroup's stores are complete before its flag moves
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_setprio(0);  // (a fused GEMV's prologue waves raised theirs)
+        __syncthreads();
+        if (tid == 0) {
+            const StepArgs& e = *step_args();
+            __hip_atomic_store(e.flags + bid, e.epoch + (unsigned)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+KERNEL void __launch_bounds__(SLM_STEP_THREADS) slm_step_1(const StepArgs) { step_run<1>(); }
+KERNEL void __launch_bounds__(SLM_STEP_THREADS) slm_step_2(const StepArgs) { step_run<2>(); }
+KERNEL void __launch_bounds__(SLM_STEP_THREADS) slm_step_4(const StepArgs) { step_run<4>(); }

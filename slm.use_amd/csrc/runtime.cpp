@@ -100,6 +100,11 @@ struct Graph {
     std::vector<Op> ops;
     size_t ndyn = 0;
     hipGraphExec_t exec = nullptr;
+    // or, for a one-launch step (slm_step_*): its program in device memory
+    char* prog = nullptr;
+    int nph = 0, step_var = 0;
+    uint32_t step_shmem = 0;
+    double step_abytes = 0.0;
     uint64_t used = 0;
     uint64_t id = 0;
     const float* mir_src = nullptr;  // what the host read right after the last replay (mirrored)
@@ -137,6 +142,7 @@ struct Kernels {
     hipFunction_t gemm2k_32, gemm2k_16;      // 32- and 16-row tiles, two slice groups (fp32)
     hipFunction_t gemm2_48;                  // 48-row tiles, four waves of three row blocks
     hipFunction_t gemm2hk_16, gemm2hwk_16, gemm2h_48, gemm2hw_48;  // the same in fp16 mode
+    hipFunction_t step[3];                   // one-launch one-token steps, head size classes 16, 32, 64
 };
 
 }  // namespace
@@ -227,6 +233,16 @@ struct slm_hip {
     std::vector<Graph> cache;
     uint64_t clock = 0, n_launched = 0, n_captured = 0, n_eager = 0;
     uint64_t last_ops = 0, last_kernels = 0;  // of the last step the planner lowered
+    // One-launch steps: a one-token step whose kernels can all be phases of slm_step_* (fused
+    // GEMVs, one-token attentions whose partials the next fused GEMV combines, one-token GLAs)
+    // runs as one launch of SLM_STEP_WG workgroups over a program of those kernels' arguments,
+    // each phase waiting on the flags the workgroups raise as they finish the one before.
+    bool step_on = false;                // slm_hip_set_step_kernel (measured slower than graphs)
+    bool step_ok = false;                // the device has a compute unit for every workgroup
+    unsigned* step_flags = nullptr;      // [SLM_STEP_WG] (device)
+    unsigned step_epoch = 0;             // flags reach epoch + phases by the end of a launch
+    int step_static_lds = 0;             // bytes of static LDS of the step kernels
+    uint64_t n_step = 0, n_step_plans = 0;
 
     // Prompt lanes: consecutive prompt steps run on up to MAX_LANES streams at once, each
     // lane writing the step's scratch (what the step writes and its flush does not keep:
@@ -563,11 +579,15 @@ int pow2_index(size_t need, int maxi) {  // smallest i with 2^i >= need
     return i;
 }
 
+void dev_free(slm_hip* c, void* p);
+
 void drop_graphs(slm_hip* c) {
     if (c->cache.empty()) return;
     hipStreamSynchronize(mstream(c));
-    for (auto& g : c->cache)
+    for (auto& g : c->cache) {
         if (g.exec) hipGraphExecDestroy(g.exec);
+        if (g.prog) dev_free(c, g.prog);
+    }
     c->cache.clear();
 }
 
@@ -2978,6 +2998,117 @@ int learn_read(slm_hip* c, uint64_t id, const float* dev, size_t n) {
     return SLM_OK;
 }
 
+// The program of a one-launch step (slm_step_*) for a planned one-token step, into g: a
+// phase per launch record, each launch's arguments copied as they are. Leaves g.prog null
+// when some launch cannot be a phase: a kernel other than the fp32 fused GEMV, the one-token
+// attention that leaves its partials to the next fused GEMV (no counters) and the one-token
+// GLA; fp16 rings; head size classes that differ; more workgroups or LDS than a step has.
+int build_step(slm_hip* c, const std::vector<Rec>& recs, Graph& g) {
+    static_assert(sizeof(AdecArgs) == 15 * 8, "the attention's argument slots");
+    static_assert(sizeof(StepPh) == 24, "phase table layout");
+    g.prog = nullptr;
+    if (!c->step_on || !c->step_ok || recs.empty()) return SLM_OK;
+    const Kernels& k = c->k;
+    std::vector<StepPh> ph;
+    std::vector<std::pair<const unsigned char*, size_t>> args;
+    int var = -1;
+    uint32_t lds = 0;
+    double ab = 0.0;
+    auto same_var = [&](int v) {
+        if (var >= 0 && var != v) return false;
+        var = v;
+        return true;
+    };
+    for (const Rec& r : recs) {
+        StepPh p{};
+        p.gx = (int32_t)r.gx;
+        p.grid = (int32_t)(r.gx * r.gy * r.gz);
+        if (r.gy != 1 && r.f != k.attn_dec[0] && r.f != k.attn_dec[1] && r.f != k.attn_dec[2]) return SLM_OK;
+        if (p.grid < 1 || p.grid > SLM_STEP_WG || r.bx > SLM_STEP_THREADS || r.gz != 1) return SLM_OK;
+        if (r.f == k.fg) {
+            FgDesc d;
+            if (r.bytes != sizeof d) return SLM_OK;
+            std::memcpy(&d, r.blob, sizeof d);
+            if (d.f16) return SLM_OK;
+            for (int q = 0; q < d.nseg; q++)
+                if (d.seg[q].ring16) return SLM_OK;
+            if (64 * (d.W + SLM_FG_EPI_WAVES) != (int)r.bx) return SLM_OK;
+            p.kind = PH_FG;
+        } else if (r.f == k.attn_dec[0] || r.f == k.attn_dec[1] || r.f == k.attn_dec[2]) {
+            if (r.bytes || r.nargs != 15 || r.bx != 64 * SLM_SB_SEGS) return SLM_OK;
+            AdecArgs a;
+            std::memcpy(&a, r.blob, sizeof a);
+            if (a.ctr || a.y) return SLM_OK;  // (it combines itself: not a phase)
+            if (a.key_heads < 1 || a.heads % a.key_heads || a.heads / a.key_heads > SLM_STEP_GROUP) return SLM_OK;
+            p.kind = PH_ADEC;
+            if (!same_var(r.f == k.attn_dec[0] ? 0 : r.f == k.attn_dec[1] ? 1 : 2)) return SLM_OK;
+        } else if (r.f == k.gla1[0] || r.f == k.gla1[1] || r.f == k.gla1[2]) {
+            if (r.bytes != sizeof(GlaDesc)) return SLM_OK;
+            p.kind = PH_GLA1;
+            if (!same_var(r.f == k.gla1[0] ? 0 : r.f == k.gla1[1] ? 1 : 2)) return SLM_OK;
+        } else {
+            return SLM_OK;
+        }
+        lds = std::max(lds, r.shmem);
+        ab += r.abytes;
+        ph.push_back(p);
+        args.push_back({r.blob, r.bytes ? (size_t)r.bytes : (size_t)8 * r.nargs});
+    }
+    if (var < 0) var = 0;  // (GEMVs only: any of the kernels)
+    if ((int)lds + c->step_static_lds > LDS_MAX) return SLM_OK;
+    int nb = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k.step[var], SLM_STEP_THREADS, lds) != hipSuccess ||
+        nb < 1)
+        return SLM_OK;
+    // [phase table][argument blocks, 16-byte aligned]
+    size_t at = (ph.size() * sizeof(StepPh) + 15) & ~(size_t)15;
+    for (size_t i = 0; i < ph.size(); i++) {
+        ph[i].arg = (int32_t)at;
+        at = (at + args[i].second + 15) & ~(size_t)15;
+    }
+    if (at > (size_t)INT_MAX) return SLM_OK;
+    // (a fused GEMV reads its segment table as 128 dwords, past the descriptor's end: zeros
+    // after the last block keep those reads inside the buffer)
+    at += 512;
+    std::vector<unsigned char> host(at, 0);
+    std::memcpy(host.data(), ph.data(), ph.size() * sizeof(StepPh));
+    for (size_t i = 0; i < ph.size(); i++) std::memcpy(host.data() + ph[i].arg, args[i].first, args[i].second);
+    void* dev = nullptr;
+    hipError_t e = dev_alloc(c, at, &dev);
+    if (e != hipSuccess) return fail(c, SLM_E_MEMORY, "step program of %zu bytes: %s", at, hipGetErrorString(e));
+    e = hipMemcpyAsync(dev, host.data(), at, hipMemcpyHostToDevice, mstream(c));
+    if (e == hipSuccess) e = hipStreamSynchronize(mstream(c));
+    if (e != hipSuccess) {
+        dev_free(c, dev);
+        return fail(c, SLM_E_HIP, "step program upload: %s", hipGetErrorString(e));
+    }
+    g.prog = (char*)dev;
+    g.nph = (int)ph.size();
+    g.step_var = var;
+    g.step_shmem = lds;
+    g.step_abytes = ab;
+    c->n_step_plans++;
+    return SLM_OK;
+}
+
+int launch_step(slm_hip* c, const Graph& g) {
+    StepArgs a{};
+    a.prog = g.prog;
+    a.flags = c->step_flags;
+    a.fault = c->fault_dev;
+    a.epoch = c->step_epoch;
+    a.nph = g.nph;
+    // (a poll of the flags takes a memory round trip: a sixteenth of the LDS polls' limit
+    // gives up after about as long)
+    a.spin = c->spin > 0 ? std::max(1, c->spin >> 4) : 0;
+    Rec r = mk_desc(c->k.step[g.step_var], SLM_STEP_WG, SLM_STEP_THREADS, g.step_shmem, a);
+    r.abytes = g.step_abytes;
+    TRY(launch_now(c, r));
+    c->step_epoch += (unsigned)g.nph;
+    c->n_step++;
+    return SLM_OK;
+}
+
 // Captures the recorded step into a graph, or finds one that matches it; with graphs
 // off, plans the step and launches it directly.
 int finish_step_run(slm_hip* c) {
@@ -2998,6 +3129,8 @@ int finish_step_run(slm_hip* c) {
         if (handled) return SLM_OK;
     }
     TRY(upload_dyn(c));
+    // with graphs on, a one-token step runs as one launch where its kernels allow, else as a graph
+    bool step = !multi && c->graphs_on && c->step_on && c->step_ok;
     if (!c->graphs_on || multi) {
         std::vector<Rec> recs;
         TRY(plan(c, c->ops, recs, c->fusion_on));
@@ -3008,7 +3141,8 @@ int finish_step_run(slm_hip* c) {
         if (g.ops.size() == c->ops.size() && g.ndyn == c->dyn.size() &&
             std::memcmp(g.ops.data(), c->ops.data(), c->ops.size() * sizeof(Op)) == 0) {
             g.used = c->clock;
-            HIPC(c, hipGraphLaunch(g.exec, mstream(c)));
+            if (g.prog) TRY(launch_step(c, g));
+            else HIPC(c, hipGraphLaunch(g.exec, mstream(c)));
             c->n_launched++;
             return after_graph(c, g);
         }
@@ -3036,13 +3170,24 @@ int finish_step_run(slm_hip* c) {
         auto old = std::min_element(c->cache.begin(), c->cache.end(),
                                     [](const Graph& a, const Graph& b) { return a.used < b.used; });
         HIPC(c, hipStreamSynchronize(mstream(c)));
-        hipGraphExecDestroy(old->exec);
+        if (old->exec) hipGraphExecDestroy(old->exec);
+        if (old->prog) dev_free(c, old->prog);
         c->cache.erase(old);
     }
     Graph g;
     g.ops = c->ops;
     g.ndyn = c->dyn.size();
     g.used = c->clock;
+    if (step) {
+        TRY(build_step(c, recs, g));
+        if (g.prog) {
+            c->cache.push_back(std::move(g));
+            Graph& n = c->cache.back();
+            TRY(launch_step(c, n));
+            c->n_launched++;
+            return after_graph(c, n);
+        }
+    }
     hipGraph_t graph = nullptr;
     HIPC(c, hipStreamBeginCapture(mstream(c), hipStreamCaptureModeThreadLocal));
     c->capturing = true;
@@ -3127,7 +3272,9 @@ int load_kernels(slm_hip* c) {
                {&k.gemm2hw[2], "slm_gemm2hw_96"}, {&k.gemm2hw[3], "slm_gemm2hw_128"},
                {&k.gemm2hsw[0], "slm_gemm2hsw_32"}, {&k.gemm2hsw[1], "slm_gemm2hsw_64"},
                {&k.gemm2hsw[2], "slm_gemm2hsw_96"}, {&k.gemm2hsw[3], "slm_gemm2hsw_128"},
-               {&k.gemm2hrw, "slm_gemm2hrw_64"},  {&k.gemm2hnw, "slm_gemm2hnw_64"}};
+               {&k.gemm2hrw, "slm_gemm2hrw_64"},  {&k.gemm2hnw, "slm_gemm2hnw_64"},
+               {&k.step[0], "slm_step_1"},        {&k.step[1], "slm_step_2"},
+               {&k.step[2], "slm_step_4"}};
     for (auto& f : fns) {
         TRY(get_fn(c, f.f, f.n));
         c->fname[*f.f] = f.n;
@@ -3195,6 +3342,15 @@ int slm_hip_open(int device, slm_hip** out) {
     OPEN_HIP(hipMemset(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int)));
     OPEN_HIP(hipMalloc((void**)&c->pick, 16 * sizeof(float)));
     OPEN_HIP(hipMemset(c->pick, 0, 16 * sizeof(float)));
+    OPEN_HIP(hipMalloc((void**)&c->step_flags, SLM_STEP_WG * sizeof(unsigned)));
+    OPEN_HIP(hipMemset(c->step_flags, 0, SLM_STEP_WG * sizeof(unsigned)));
+    {  // a step launch needs all its workgroups resident: one per compute unit
+        int lds = 0;
+        OPEN_HIP(hipFuncGetAttribute(&lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, c->k.step[2]));
+        c->step_static_lds = lds;
+        c->step_ok = prop.multiProcessorCount >= SLM_STEP_WG;
+    }
+
     c->dyn.reserve(DYN_CAP);
     c->ops.reserve(4096);
     c->plan_trace = getenv("SLM_HIP_PLAN_TRACE") != nullptr;
@@ -3225,6 +3381,8 @@ void slm_hip_close(slm_hip* c) {
     auto release = [&](void* p) {  // (pooled blocks go with their slabs)
         if (p && !c->pooled.count((uintptr_t)p)) hipFree(p);
     };
+    for (auto& g : c->cache) release(g.prog);
+    if (c->step_flags) hipFree(c->step_flags);
     for (auto& t : c->tables) {
         release(t.second.cos);
         release(t.second.sin);
@@ -3508,6 +3666,22 @@ int slm_hip_set_graphs(slm_hip* c, int on) {
     if (c->recording) TRY(finish_step(c));
     if (!on) drop_graphs(c);
     c->graphs_on = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_set_step_kernel(slm_hip* c, int on) {
+    if (!c) return SLM_E_INVALID;
+    if (c->recording) TRY(finish_step(c));
+    if (c->step_on != (on != 0)) drop_graphs(c);
+    c->step_on = on != 0;
+    return SLM_OK;
+}
+
+int slm_hip_step_stats(slm_hip* c, uint64_t* launches, uint64_t* programs, int* available) {
+    if (!c) return SLM_E_INVALID;
+    if (launches) *launches = c->n_step;
+    if (programs) *programs = c->n_step_plans;
+    if (available) *available = c->step_ok ? 1 : 0;
     return SLM_OK;
 }
 
