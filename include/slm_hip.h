@@ -218,13 +218,19 @@ int slm_hip_get_prompt_lanes(slm_hip* ctx, int* n);
 int slm_hip_prompt_lane_stats(slm_hip* ctx, uint64_t* steps, uint64_t* fallbacks);
 /* fp16 mode (off by default), the analogue of the reference's --fp16 (mlx.rs:19-23,
  * main.rs:421-423, where it selects Float16 for every MLX buffer): from this call on, every
- * linear rounds both operands to fp16 (to nearest even) at fp16 MFMAs and sums in fp32;
- * attention, GLA, norms and states stay fp32. A linear then needs a multiple of 64 columns
- * and 16-byte aligned weights and input (else SLM_E_UNSUPPORTED). Weights stay as uploaded
- * (fp32, ops.rs:77); the first linear that reads a weight buffer in this mode keeps an fp16
- * copy of it (the halves the mode rounds it to, so the same bits), which later linears read
- * instead: half the weight bytes, as mlx.rs:61-63 uploads every buffer in its dtype. The copy
- * is dropped when the buffer is freed, uploaded into or written by an operation. */
+ * buffer holds fp16 values, as mlx.rs's Float16 arrays do. An upload rounds to fp16 (to
+ * nearest even; mlx.rs:61-63), and every operation rounds what it writes — activations,
+ * GLA states, norms' outputs, attention outputs — at mlx.rs's rounding points (a product or
+ * sum of two arrays, a scalar factor turned into the dtype, RMSNorm's fp32 quotient before
+ * its weight, mlx.rs:178-185; rope angles in fp32, mlx.rs:203-208); reductions (a linear's
+ * chain, a norm's dot, attention's softmax, the GLA's column sums) sum in fp32. Linears round
+ * both operands to fp16 at fp16 MFMAs; a linear then needs a multiple of 64 columns and
+ * 16-byte aligned weights and input (else SLM_E_UNSUPPORTED). Caches from
+ * slm_hip_alloc_cache hold halves. Set it before the model uploads its weights, as the
+ * reference fixes the dtype when it creates the backend (mlx.rs:19-23): weights uploaded
+ * before keep their fp32 values, which the linears then round themselves. The first linear
+ * that reads a weight buffer keeps an fp16 copy of it (half the weight bytes, the same bits),
+ * dropped when the buffer is freed, uploaded into or written by an operation. */
 int slm_hip_set_fp16(slm_hip* ctx, int on);
 /* Whether fp16 mode is on. */
 int slm_hip_get_fp16(slm_hip* ctx, int* on);

@@ -147,7 +147,7 @@ typedef struct {
     float* kn;
     int32_t heads, dh, fuse, l2;
     float eps;
-    float pad;
+    int32_t r16;     // fp16 mode: every value written rounded to fp16
 } GlaDesc;
 
 // A one-token step in one launch (slm_step): the kernels the planner made for the step, in
@@ -234,7 +234,7 @@ typedef struct {  // a global operand row copied into LDS before the first op
     int32_t n, lds;  // floats (a multiple of 4, 16-byte aligned rows), LDS offset
 } RowPf;
 typedef struct {
-    int32_t nops, npf, pad1, pad2;
+    int32_t nops, npf, r16, pad2;    // r16: fp16 mode (each op's output rounded to fp16)
     RowPf pf[SLM_ROW_PF];
     RowOp op[SLM_ROW_OPS];
 } RowDesc;

@@ -155,6 +155,52 @@ __device__ __forceinline__ f4 block16hw(h4 a, f4 b, f4 c) {
 // Four fp16 weights widened to fp32 (exactly): what block16h rounds back to the same halves.
 __device__ __forceinline__ f4 wide4(h4 v) { return f4{(float)v.x, (float)v.y, (float)v.z, (float)v.w}; }
 
+// fp16 mode's values (mlx.rs:19-23, 53-67: every buffer Float16): each operation's result is
+// rounded to fp16 (to nearest even) as it is written, at the points where mlx.rs's fp16
+// arrays round: a product or sum of two arrays, a scalar turned into the dtype
+// (mlx.rs:25-27), the norm's fp32 quotient before its weight (mlx.rs:178-185). Sums inside a
+// reduction (a linear's chain, a norm's dot, attention, the GLA's column sums) stay fp32.
+// Kernels that run in both modes read the mode word slm_h16 (set by the host); those that
+// run only in fp16 mode, or take a descriptor, decide it at compile time or from a field.
+__constant__ int slm_h16;
+// (the fp32 value goes through an opaque register first: otherwise the compiler may turn
+// (half)(a·b) into one v_fma_mixlo_f16, a single rounding of the exact product, in some
+// kernels and not in others, and the same expression would differ by an fp16 step)
+__device__ __forceinline__ float r16(float v) {
+    asm("" : "+v"(v));
+    return (float)(_Float16)v;
+}
+template <bool H>
+__device__ __forceinline__ float h16(float v) { return H ? r16(v) : v; }
+// The element-wise expressions of both modes (fp32: cpu.rs's; fp16: mlx.rs's roundings).
+template <bool H>
+__device__ __forceinline__ float e_add(float a, float b) { return h16<H>(a + b); }
+template <bool H>
+__device__ __forceinline__ float e_mix(float a, float b, float t) {  // mlx.rs:165-169
+    return H ? r16(a + r16(r16(b - a) * r16(t))) : a + t * (b - a);
+}
+template <bool H>
+__device__ __forceinline__ float e_scale(float a, float f) {  // mlx.rs:157-163
+    return H ? r16(a * r16(f)) : a * f;
+}
+template <bool H>
+__device__ __forceinline__ float e_silu(float g, float u) {  // mlx.rs:188-192: g·sigmoid(g), then ·u
+    if (H) return r16(r16(g * r16(1.0f / (1.0f + expf(-g)))) * u);
+    return u * g / (1.0f + expf(-g));
+}
+template <bool H>
+__device__ __forceinline__ float e_rms(float a, float r, float w) {  // mlx.rs:178-185
+    return H ? r16(r16(a * r) * w) : a * r * w;
+}
+template <bool H>  // rope's two halves (mlx.rs:227-230): a·c − b·s, a·s + b·c
+__device__ __forceinline__ float e_rope_l(float a, float b, float c, float s) {
+    return H ? r16(r16(a * c) - r16(b * s)) : a * c - b * s;
+}
+template <bool H>
+__device__ __forceinline__ float e_rope_r(float a, float b, float c, float s) {
+    return H ? r16(r16(a * s) + r16(b * c)) : a * s + b * c;
+}
+
 // ---------------------------------------------------------------------------------------
 // element-wise operations (src/cpu.rs:66-185, 209-268, 331-350)
 // ---------------------------------------------------------------------------------------
@@ -200,23 +246,27 @@ KERNEL void __launch_bounds__(256) slm_to_host(float* __restrict__ dst, const fl
 
 KERNEL void slm_add(float* __restrict__ y, const float* __restrict__ a,
                     const float* __restrict__ b, long long n) {
-    GRID_LOOP(i, n) y[i] = a[i] + b[i];
+    if (slm_h16) GRID_LOOP(i, n) y[i] = e_add<true>(a[i], b[i]);
+    else GRID_LOOP(i, n) y[i] = a[i] + b[i];
 }
 
 KERNEL void slm_add_row(float* __restrict__ y, const float* __restrict__ x,
                         const float* __restrict__ row, long long n, long long d) {
-    GRID_LOOP(i, n) y[i] = x[i] + row[i % d];
+    if (slm_h16) GRID_LOOP(i, n) y[i] = e_add<true>(x[i], row[i % d]);
+    else GRID_LOOP(i, n) y[i] = x[i] + row[i % d];
 }
 
 KERNEL void slm_mix(float* __restrict__ y, const float* __restrict__ a,
                     const float* __restrict__ b, long long n, float t) {
-    GRID_LOOP(i, n) y[i] = a[i] + t * (b[i] - a[i]);
+    if (slm_h16) GRID_LOOP(i, n) y[i] = e_mix<true>(a[i], b[i], t);
+    else GRID_LOOP(i, n) y[i] = a[i] + t * (b[i] - a[i]);
 }
 
 // y = silu(g)·u = u·g / (1 + e^-g), cpu.rs:209-215.
 KERNEL void slm_silu_mul(float* __restrict__ y, const float* __restrict__ g,
                          const float* __restrict__ u, long long n) {
-    GRID_LOOP(i, n) {
+    if (slm_h16) GRID_LOOP(i, n) y[i] = e_silu<true>(g[i], u[i]);
+    else GRID_LOOP(i, n) {
         float v = g[i];
         y[i] = u[i] * v / (1.0f + expf(-v));
     }
@@ -225,7 +275,8 @@ KERNEL void slm_silu_mul(float* __restrict__ y, const float* __restrict__ g,
 // y[i] = f[i]·x[i] with rows of d; one factor `f0` when `f` is null.
 KERNEL void slm_scale_rows(float* __restrict__ y, const float* __restrict__ x,
                            const float* __restrict__ f, float f0, long long n, long long d) {
-    GRID_LOOP(i, n) y[i] = x[i] * (f ? f[i / d] : f0);
+    if (slm_h16) GRID_LOOP(i, n) y[i] = e_scale<true>(x[i], f ? f[i / d] : f0);
+    else GRID_LOOP(i, n) y[i] = x[i] * (f ? f[i / d] : f0);
 }
 
 KERNEL void slm_shift(float* __restrict__ y, const float* __restrict__ first,
@@ -328,8 +379,13 @@ KERNEL void slm_rope(float* __restrict__ y, const float* __restrict__ x,
         long long at = (row * heads + h) * dh;
         float c = cs[row * half + i], s = sn[row * half + i];
         float a = x[at + i], b = x[at + half + i];
-        y[at + i] = a * c - b * s;
-        y[at + half + i] = a * s + b * c;
+        if (slm_h16) {
+            y[at + i] = e_rope_l<true>(a, b, c, s);
+            y[at + half + i] = e_rope_r<true>(a, b, c, s);
+        } else {
+            y[at + i] = a * c - b * s;
+            y[at + half + i] = a * s + b * c;
+        }
     }
 }
 
@@ -395,7 +451,10 @@ __device__ void norm_body(float* __restrict__ y, const float* __restrict__ x,
     float d = dot16_self(in, size, l);
     float r = MODE == 0 ? 1.0f / sqrtf(d / (float)size + eps) : 1.0f / fmaxf(sqrtf(d), 1e-12f);
     float* out = y + (g0 + grp) * size;
-    for (int j = l; j < size; j += 16) out[j] = MODE == 0 ? in[j] * r * w[j] : in[j] * r;
+    if (slm_h16)
+        for (int j = l; j < size; j += 16) out[j] = MODE == 0 ? e_rms<true>(in[j], r, w[j]) : r16(in[j] * r);
+    else
+        for (int j = l; j < size; j += 16) out[j] = MODE == 0 ? in[j] * r * w[j] : in[j] * r;
 }
 
 // Wide groups (size a multiple of 4, at most 4096, vectors 16-byte aligned): one wave per
@@ -419,15 +478,16 @@ __device__ void norm_wave_body(float* __restrict__ y, const float* __restrict__ 
     float d = dot16_wave(row, size, lane);
     float r = MODE == 0 ? 1.0f / sqrtf(d / (float)size + eps) : 1.0f / fmaxf(sqrtf(d), 1e-12f);
     f4* out = (f4*)(y + grp * size);
+    bool h = slm_h16;
     for (int c = lane; c < n4; c += 64) {
         f4 v = ((const f4*)row)[c], o;
         if (MODE == 0) {
             f4 wv = ((const f4*)w)[c];
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = v[e] * r * wv[e];
+            for (int e = 0; e < 4; e++) o[e] = h ? e_rms<true>(v[e], r, wv[e]) : v[e] * r * wv[e];
         } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = v[e] * r;
+            for (int e = 0; e < 4; e++) o[e] = h ? r16(v[e] * r) : v[e] * r;
         }
         out[c] = o;
     }
@@ -494,7 +554,18 @@ __device__ __forceinline__ float gla_colsum0(float p) {
 }
 
 // One lane's rows for one token: st = d·st + k·v, and the lane's sum of q·st in order.
-template <int RPL>
+// One state element's update for one token, st·d + k·v (fp16 mode: mlx.rs:321's state.multiply,
+// ki.multiply and add, each rounded); and the decay factor sigmoid(−(raw + bias)) (mlx.rs:313).
+template <bool H>
+__device__ __forceinline__ float gla_upd(float dc, float s, float k, float v) {
+    return H ? r16(r16(dc * s) + r16(k * v)) : dc * s + k * v;
+}
+template <bool H>
+__device__ __forceinline__ float gla_decay(float raw, float bias) {
+    return H ? r16(1.0f / (1.0f + expf(r16(raw + bias)))) : 1.0f / (1.0f + expf(raw + bias));
+}
+
+template <int RPL, bool H = false>
 __device__ __forceinline__ float gla_rows(float (&st)[RPL], const float* kk, const float* qq,
                                           float dc, float vb, int j, int dh) {
     float part = 0.0f;
@@ -502,7 +573,7 @@ __device__ __forceinline__ float gla_rows(float (&st)[RPL], const float* kk, con
 #pragma unroll
         for (int rr = 0; rr < RPL; rr++) {
             int a = j * RPL + rr;
-            st[rr] = dc * st[rr] + kk[a] * vb;
+            st[rr] = gla_upd<H>(dc, st[rr], kk[a], vb);
             part = part + qq[a] * st[rr];
         }
     } else {
@@ -510,7 +581,7 @@ __device__ __forceinline__ float gla_rows(float (&st)[RPL], const float* kk, con
         for (int rr = 0; rr < RPL; rr++) {
             int a = j * RPL + rr;
             if (a < dh) {
-                st[rr] = dc * st[rr] + kk[a] * vb;
+                st[rr] = gla_upd<H>(dc, st[rr], kk[a], vb);
                 part = part + qq[a] * st[rr];
             }
         }
@@ -519,7 +590,7 @@ __device__ __forceinline__ float gla_rows(float (&st)[RPL], const float* kk, con
 }
 
 // gla_rows when every lane's RPL rows are inside the head: the rows' k and q read as float4s.
-template <int RPL>
+template <int RPL, bool H = false>
 __device__ __forceinline__ float gla_rows_full(float (&st)[RPL], const float* kk, const float* qq,
                                                float dc, float vb, int j) {
     float kv[RPL], qv[RPL];
@@ -543,7 +614,7 @@ __device__ __forceinline__ float gla_rows_full(float (&st)[RPL], const float* kk
     float part = 0.0f;
 #pragma unroll
     for (int rr = 0; rr < RPL; rr++) {
-        st[rr] = dc * st[rr] + kv[rr] * vb;
+        st[rr] = gla_upd<H>(dc, st[rr], kv[rr], vb);
         part = part + qv[rr] * st[rr];
     }
     return part;
@@ -570,7 +641,7 @@ __device__ __forceinline__ float gla_step(float (&st)[RPL], const GlaOps<RPL>& o
 // The prompt kernel: grid (heads, groups of SLM_GLA_COLS columns), one wave a workgroup (so a
 // CU's LDS serves one wave's reads); each workgroup stages q and k of its head and v of its
 // columns for SLM_GLA_T tokens at a time in LDS.
-template <int RPL>
+template <int RPL, bool H>
 __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                          const float* __restrict__ q, const float* __restrict__ k,
                          const float* __restrict__ v, const float* __restrict__ decay,
@@ -662,7 +733,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
         const float* rows = lds + buf * bufl;
         float* dcs = lds + buf * bufl + SLM_GLA_T * rowl;
         __builtin_amdgcn_s_waitcnt(0);  // this thread's copies of the group are in
-        if (tid < nt_tok) dcs[tid] = 1.0f / (1.0f + expf(dnext + bh));
+        if (tid < nt_tok) dcs[tid] = gla_decay<H>(dnext, bh);
         // every thread's copies and decays are in, and every thread is done with the group
         // before (whose buffer the next copies overwrite)
         __syncthreads();
@@ -736,7 +807,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                 if (t < SLM_GLA_T) {
                     const GlaOps<RPL>& o = ops[t & 3];
 #pragma unroll
-                    for (int rr = 0; rr < RPL; rr++) sn[rr] = dg[t] * st[rr] + o.k[rr] * o.v;
+                    for (int rr = 0; rr < RPL; rr++) sn[rr] = gla_upd<H>(dg[t], st[rr], o.k[rr], o.v);
                 }
                 if (t > 0) {
                     const GlaOps<RPL>& o = ops[(t - 1) & 3];
@@ -751,7 +822,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                 __builtin_amdgcn_sched_barrier(0);
                 if (t > 0 && (t & 7) == 0) {
 #pragma unroll
-                    for (int u = 0; u < 8; u++) part[u] = gla_colsum0(part[u]);
+                    for (int u = 0; u < 8; u++) part[u] = h16<H>(gla_colsum0(part[u]));
                     if (t == SLM_GLA_T) {
 #pragma unroll
                         for (int u = 0; u < 8; u++) pend[u] = part[u];
@@ -771,7 +842,7 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
                     const float* row = rows + (t0 + u) * rowl;
-                    part[u] = gla_rows_full<RPL>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j);
+                    part[u] = gla_rows_full<RPL, H>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j);
                 }
             } else {
 #pragma unroll
@@ -779,12 +850,12 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
                     part[u] = 0.0f;
                     if (u < nu && live) {
                         const float* row = rows + (t0 + u) * rowl;
-                        part[u] = gla_rows<RPL>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j, dh);
+                        part[u] = gla_rows<RPL, H>(st, row + dh, row, dcs[t0 + u], row[2 * dh + (b - c0)], j, dh);
                     }
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) part[u] = gla_colsum0(part[u]);
+            for (int u = 0; u < 8; u++) part[u] = h16<H>(gla_colsum0(part[u]));
             if (live && j == 0)
 #pragma unroll
                 for (int u = 0; u < 8; u++)
@@ -799,13 +870,15 @@ __device__ void gla_body(float* __restrict__ y, float* __restrict__ S,
     }
 }
 
-#define GLA(R)                                                                          \
+// (slm_glah_*: fp16 mode's)
+#define GLA_K(NAME, R, H)                                                              \
     KERNEL void __launch_bounds__(16 * SLM_GLA_COLS)                                    \
-        slm_gla_##R(float* y, float* S, const float* q, const float* k, const float* v, \
-                    const float* decay, const float* bias, int m, int heads, int dh,    \
-                    int vec) {                                                          \
-        gla_body<R>(y, S, q, k, v, decay, bias, m, heads, dh, vec);                     \
+        NAME(float* y, float* S, const float* q, const float* k, const float* v,        \
+             const float* decay, const float* bias, int m, int heads, int dh,           \
+             int vec) {                                                                 \
+        gla_body<R, H>(y, S, q, k, v, decay, bias, m, heads, dh, vec);                  \
     }
+#define GLA(R) GLA_K(slm_gla_##R, R, false) GLA_K(slm_glah_##R, R, true)
 GLA(1)
 GLA(2)
 GLA(4)
@@ -923,7 +996,7 @@ __device__ void linear_small_body(float* __restrict__ y, const float* __restrict
             for (int s = s0 + 1; s < s1; s++) q = q + part[s * 256 + t];
             tot = s0 == 0 ? q : tot + q;
         }
-        if (r0 + rr < rows && tt < m) y[(long long)tt * rows + r0 + rr] = tot;
+        if (r0 + rr < rows && tt < m) y[(long long)tt * rows + r0 + rr] = h16<H>(tot);
     }
 }
 
@@ -1437,7 +1510,11 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
 #pragma unroll
             for (int v = 0; v < NV; v++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = sp[u][v][r];
+                for (int r = 0; r < 4; r++) {
+                    // (fp16 mode: the linear's output rounded; a split's partials are not)
+                    float o = sp[u][v][r];
+                    so[(wt + 16 * v + i) * (BM + 1) + wr + 16 * u + 4 * g + r] = H && gridDim.z == 1 ? r16(o) : o;
+                }
     }
     __syncthreads();
     if constexpr (ROPE == 2) {
@@ -1455,7 +1532,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
             y[t * rows + r0 + lane] = v;
             if (region < 2) {
                 float dd = dot16_wave(sr, 64, lane);
-                v = v * (1.0f / fmaxf(sqrtf(dd), 1e-12f));
+                v = h16<H>(v * (1.0f / fmaxf(sqrtf(dd), 1e-12f)));
             }
             dst[t * ep.d + head * 64 + lane] = v;
         }
@@ -1480,7 +1557,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
                 int i = j & 31;
                 float c = ep.cs[t * 32 + i], sn = ep.sn[t * 32 + i];
                 float a = sr[i], b = sr[32 + i];
-                v = j < 32 ? a * c - b * sn : a * sn + b * c;
+                v = j < 32 ? e_rope_l<H>(a, b, c, sn) : e_rope_r<H>(a, b, c, sn);
             }
             dst[t * ep.d + head * 64 + j] = v;
             if (region > 0) {
@@ -1497,7 +1574,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
             int tok = e / HB, j = e % HB;
             if (t0 + tok < m && r0h + j < half) {
                 float gt = so[tok * (BM + 1) + j], up = so[tok * (BM + 1) + HB + j];
-                y[(t0 + tok) * half + r0h + j] = up * gt / (1.0f + expf(-gt));
+                y[(t0 + tok) * half + r0h + j] = e_silu<H>(gt, up);
             }
         }
         return;
@@ -1924,7 +2001,8 @@ __device__ void attn_part_body(float* __restrict__ part, const float* __restrict
                     O = O + oz[v] * w;
                 }
         }
-        y[(c2.qidx * heads + c2.head) * (long long)dh + dd] = L > 0.0f ? O / L : 0.0f;
+        float ov = L > 0.0f ? O / L : 0.0f;
+        y[(c2.qidx * heads + c2.head) * (long long)dh + dd] = slm_h16 ? r16(ov) : ov;
     }
 }
 
@@ -2664,7 +2742,8 @@ __device__ __forceinline__ bool attn_dec_body(float* __restrict__ part, const fl
                     O = O + oz[u] * w;
                 }
         }
-        y[(long long)(kvh * group + cc) * dh + dd] = L > 0.0f ? O / L : 0.0f;
+        float ov = L > 0.0f ? O / L : 0.0f;
+        y[(long long)(kvh * group + cc) * dh + dd] = slm_h16 ? r16(ov) : ov;
     }
     return true;
 }
@@ -2749,7 +2828,8 @@ KERNEL void __launch_bounds__(256) slm_attn_combine(float* __restrict__ y, const
                 }
             }
         }
-        if (dd < dh) y[rw * dh + dd] = L > 0.0f ? O / L : 0.0f;
+        float ov = L > 0.0f ? O / L : 0.0f;
+        if (dd < dh) y[rw * dh + dd] = slm_h16 ? r16(ov) : ov;
     }
 }
 
@@ -2837,17 +2917,18 @@ __device__ float dot16_wave(const float* in, int size, int lane) {
 // The prologue's element-wise ops, one loop per kind so each compiles to its own
 // straight-line code (the expressions of the per-op kernels). Every lane reads all its
 // float4s of a 1024-element chunk before it writes any.
-template <int KIND>
+// (H: fp16 mode's roundings, the e_* expressions)
+template <int KIND, bool H = false>
 __device__ __forceinline__ float vp_elem(float a, float b, float f, float r) {
     if (KIND == VP_COPY) return a;
-    if (KIND == VP_ADD) return a + b;
-    if (KIND == VP_MIX) return a + f * (b - a);
-    if (KIND == VP_SCALE) return a * f;
-    if (KIND == VP_RMS) return a * r * b;  // b: the rms weight
-    return b * a / (1.0f + expf(-a));      // VP_SILU: g = a, u = b
+    if (KIND == VP_ADD) return e_add<H>(a, b);
+    if (KIND == VP_MIX) return e_mix<H>(a, b, f);
+    if (KIND == VP_SCALE) return e_scale<H>(a, f);
+    if (KIND == VP_RMS) return e_rms<H>(a, r, b);  // b: the rms weight
+    return e_silu<H>(a, b);                        // VP_SILU: g = a, u = b
 }
 
-template <int KIND>
+template <int KIND, bool H>
 __device__ __forceinline__ void vp_map4(const f4* a, const f4* b, f4* out, int n4, float f,
                                         float r, int tid, int nt) {
     for (int c0 = tid; c0 < n4; c0 += 4 * nt) {
@@ -2864,13 +2945,13 @@ __device__ __forceinline__ void vp_map4(const f4* a, const f4* b, f4* out, int n
             if (c >= n4) break;
             f4 v;
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[e] = vp_elem<KIND>(A[j][e], B[j][e], f, r);
+            for (int e = 0; e < 4; e++) v[e] = vp_elem<KIND, H>(A[j][e], B[j][e], f, r);
             out[c] = v;
         }
     }
 }
 
-template <int KIND>
+template <int KIND, bool H>
 __device__ __forceinline__ void vp_map1(const float* a, const float* b, float* out, int n,
                                         float f, float r, int tid, int nt) {
     for (int c0 = tid; c0 < n; c0 += 4 * nt) {
@@ -2885,20 +2966,21 @@ __device__ __forceinline__ void vp_map1(const float* a, const float* b, float* o
         for (int j = 0; j < 4; j++) {
             int c = c0 + nt * j;
             if (c >= n) break;
-            out[c] = vp_elem<KIND>(A[j], B[j], f, r);
+            out[c] = vp_elem<KIND, H>(A[j], B[j], f, r);
         }
     }
 }
 
-template <int KIND>
+template <int KIND, bool H>
 __device__ __forceinline__ void vp_map(const float* a, const float* b, float* out, int n,
                                        bool v4, float f, float r, int tid, int nt) {
-    if (v4) vp_map4<KIND>((const f4*)a, (const f4*)b, (f4*)out, n >> 2, f, r, tid, nt);
-    else vp_map1<KIND>(a, b, out, n, f, r, tid, nt);
+    if (v4) vp_map4<KIND, H>((const f4*)a, (const f4*)b, (f4*)out, n >> 2, f, r, tid, nt);
+    else vp_map1<KIND, H>(a, b, out, n, f, r, tid, nt);
 }
 
 // slm_fold in LDS: out[c] = ((P0[c] + P1[c]) + P2[c]) + ..., parts [nsplit][n]; all the
 // splits of a float4 are read before the sums.
+template <bool H>
 __device__ __forceinline__ void vp_fold(const float* part, float* out, int n, int nsplit,
                                         bool v4, int tid, int nt) {
     constexpr int ZMAX = 8;
@@ -2920,6 +3002,8 @@ __device__ __forceinline__ void vp_fold(const float* part, float* out, int n, in
 #pragma unroll
                 for (int z = 1; z < ZMAX; z++)
                     if (z < nsplit) v = v + P[j][z];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = h16<H>(v[e]);
                 ((f4*)out)[c] = v;
             }
         }
@@ -2928,7 +3012,7 @@ __device__ __forceinline__ void vp_fold(const float* part, float* out, int n, in
     for (int c = tid; c < n; c += nt) {
         float v = part[c];
         for (int z = 1; z < nsplit; z++) v = v + part[z * n + c];
-        out[c] = v;
+        out[c] = h16<H>(v);
     }
 }
 
@@ -2959,7 +3043,7 @@ __device__ void vp_comb_w(const float* part, float2* wl, int heads, int dp, int 
 
 // Then DW dims per thread: L = Σ l_z·w_z and O = Σ o_z·w_z in superblock order,
 // out = O / L (0 when no superblock saw a key).
-template <int DW>
+template <int DW, bool H>
 __device__ void vp_comb_o(const float* part, const float2* wl, float* out, int heads, int dh,
                           int dp, int nsb, int tid, int nt) {
     int nq = dh / DW, sr = heads * (dp + 2);
@@ -2997,7 +3081,7 @@ __device__ void vp_comb_o(const float* part, const float2* wl, float* out, int h
                 }
         }
 #pragma unroll
-        for (int e = 0; e < DW; e++) out[h * dh + d0 + e] = L > 0.0f ? O[e] / L : 0.0f;
+        for (int e = 0; e < DW; e++) out[h * dh + d0 + e] = h16<H>(L > 0.0f ? O[e] / L : 0.0f);
     }
 }
 
@@ -3040,7 +3124,7 @@ __device__ __forceinline__ VpOp vp_load(const VpOp& src) {
 // whose vectors hold at most one float4 per thread (thread tid owns float4 tid, as in
 // vp_map4), so each thread reads its operands once, computes the expressions of vp_elem /
 // vp_fold / rms and writes once.
-template <int NSPLIT>
+template <int NSPLIT, bool H>
 __device__ __forceinline__ f4 vp_fold4(const f4* p, int n4, int c) {
     f4 P[NSPLIT];
 #pragma unroll
@@ -3048,6 +3132,8 @@ __device__ __forceinline__ f4 vp_fold4(const f4* p, int n4, int c) {
     f4 v = P[0];
 #pragma unroll
     for (int z = 1; z < NSPLIT; z++) v = v + P[z];
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = h16<H>(v[e]);
     return v;
 }
 
@@ -3070,7 +3156,7 @@ __device__ __forceinline__ VpFast vp_fast_load(const VpOp& src) {
     return o;
 }
 
-template <int KIND>
+template <int KIND, bool H>
 __device__ __forceinline__ void vp_fast(const VpFast& o, float* lds, float f, int tid) {
     if (o.out < 0) return;  // a copy whose source slot is written out as it is
     int n4 = o.n4, c = tid;
@@ -3084,7 +3170,7 @@ __device__ __forceinline__ void vp_fast(const VpFast& o, float* lds, float f, in
         if (c < n4) {
             f4 a = A[c], w = B[c], v;
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[e] = a[e] * r * w[e];
+            for (int e = 0; e < 4; e++) v[e] = e_rms<H>(a[e], r, w[e]);
             O[c] = v;
         }
         return;
@@ -3093,25 +3179,25 @@ __device__ __forceinline__ void vp_fast(const VpFast& o, float* lds, float f, in
     if (KIND == VP_FOLD) {
         const f4* P = (const f4*)(lds + o.w);
         switch (o.nsb) {
-            case 1: O[c] = vp_fold4<1>(P, n4, c); return;
-            case 2: O[c] = vp_fold4<2>(P, n4, c); return;
-            case 3: O[c] = vp_fold4<3>(P, n4, c); return;
-            case 4: O[c] = vp_fold4<4>(P, n4, c); return;
-            case 5: O[c] = vp_fold4<5>(P, n4, c); return;
-            case 6: O[c] = vp_fold4<6>(P, n4, c); return;
-            case 7: O[c] = vp_fold4<7>(P, n4, c); return;
-            default: O[c] = vp_fold4<8>(P, n4, c); return;
+            case 1: O[c] = vp_fold4<1, H>(P, n4, c); return;
+            case 2: O[c] = vp_fold4<2, H>(P, n4, c); return;
+            case 3: O[c] = vp_fold4<3, H>(P, n4, c); return;
+            case 4: O[c] = vp_fold4<4, H>(P, n4, c); return;
+            case 5: O[c] = vp_fold4<5, H>(P, n4, c); return;
+            case 6: O[c] = vp_fold4<6, H>(P, n4, c); return;
+            case 7: O[c] = vp_fold4<7, H>(P, n4, c); return;
+            default: O[c] = vp_fold4<8, H>(P, n4, c); return;
         }
     }
     f4 a = A[c], b = KIND == VP_COPY || KIND == VP_SCALE ? a : B[c], v;
 #pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = vp_elem<KIND>(a[e], b[e], f, 0.0f);
+    for (int e = 0; e < 4; e++) v[e] = vp_elem<KIND, H>(a[e], b[e], f, 0.0f);
     O[c] = v;
 }
 
 // A prologue of compile-time kinds K... (every op on the float4 path), run by the prologue
 // waves with `sync` (their barrier) before an op that reads what other threads wrote.
-template <int... K>
+template <bool H, int... K>
 struct VpSeq {
     template <typename Sync>
     __device__ __forceinline__ static void run(const VpOp* vp, float* lds, const float* sfac,
@@ -3127,35 +3213,36 @@ struct VpSeq {
         if (k > 0 && (o.sync || KIND == VP_RMS)) sync();
         float f = o.f;
         if (KIND == VP_SCALE && vp[k].dyn) f = sfac[k];
-        vp_fast<KIND>(o, lds, f, tid);
+        vp_fast<KIND, H>(o, lds, f, tid);
     }
 };
 
 // The prologue through its straight-line code when its signature is one of these; false
 // when it is not (the caller then runs the general loop).
-template <typename Sync>
+template <bool H, typename Sync>
 __device__ __forceinline__ bool vp_seq(int sig, const VpOp* vp, float* lds, const float* sfac,
                                        Sync& sync, int tid, bool first) {
     switch (sig) {
         case SLM_SIG1(VP_RMS):
-            VpSeq<VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+            VpSeq<H, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
         case SLM_SIG3(VP_FOLD, VP_ADD, VP_RMS):
-            VpSeq<VP_FOLD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+            VpSeq<H, VP_FOLD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
         case SLM_SIG5(VP_FOLD, VP_ADD, VP_ADD, VP_ADD, VP_RMS):
-            VpSeq<VP_FOLD, VP_ADD, VP_ADD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+            VpSeq<H, VP_FOLD, VP_ADD, VP_ADD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
         case SLM_SIG3(VP_ADD, VP_ADD, VP_RMS):
-            VpSeq<VP_ADD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+            VpSeq<H, VP_ADD, VP_ADD, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
         case SLM_SIG3(VP_FOLD, VP_ADD, VP_COPY):
-            VpSeq<VP_FOLD, VP_ADD, VP_COPY>::run(vp, lds, sfac, sync, tid, first); return true;
+            VpSeq<H, VP_FOLD, VP_ADD, VP_COPY>::run(vp, lds, sfac, sync, tid, first); return true;
         case SLM_SIG4(VP_FOLD, VP_ADD, VP_COPY, VP_RMS):
-            VpSeq<VP_FOLD, VP_ADD, VP_COPY, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+            VpSeq<H, VP_FOLD, VP_ADD, VP_COPY, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
         case SLM_SIG5(VP_COPY, VP_COPY, VP_COPY, VP_COPY, VP_RMS):
-            VpSeq<VP_COPY, VP_COPY, VP_COPY, VP_COPY, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
+            VpSeq<H, VP_COPY, VP_COPY, VP_COPY, VP_COPY, VP_RMS>::run(vp, lds, sfac, sync, tid, first); return true;
         default:
             return false;
     }
 }
 
+template <bool H>
 __device__ void vp_run(const VpOp& o, float* lds, float f, int tid, int nt) {
     if (o.out < 0) return;  // a copy whose source slot is written out as it is
     int n = o.n;
@@ -3164,22 +3251,22 @@ __device__ void vp_run(const VpOp& o, float* lds, float f, int tid, int nt) {
     float* out = lds + o.out;
     bool v4 = vp_v4(o);
     switch (o.kind) {
-        case VP_COPY: vp_map<VP_COPY>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
-        case VP_ADD: vp_map<VP_ADD>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
-        case VP_MIX: vp_map<VP_MIX>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
-        case VP_SCALE: vp_map<VP_SCALE>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
-        case VP_SILU: vp_map<VP_SILU>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
-        case VP_FOLD: vp_fold(lds + o.w, out, n, o.nsb, v4, tid, nt); break;
+        case VP_COPY: vp_map<VP_COPY, H>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_ADD: vp_map<VP_ADD, H>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_MIX: vp_map<VP_MIX, H>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_SCALE: vp_map<VP_SCALE, H>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_SILU: vp_map<VP_SILU, H>(a, b, out, n, v4, f, 0.0f, tid, nt); break;
+        case VP_FOLD: vp_fold<H>(lds + o.w, out, n, o.nsb, v4, tid, nt); break;
         case VP_COMB:  // the second pass (the caller ran vp_comb_w and a barrier)
-            if (o.dh % 4 == 0) vp_comb_o<4>(lds + o.w, (const float2*)(lds + o.in1), out, o.heads, o.dh, o.dp, o.nsb, tid, nt);
-            else vp_comb_o<1>(lds + o.w, (const float2*)(lds + o.in1), out, o.heads, o.dh, o.dp, o.nsb, tid, nt);
+            if (o.dh % 4 == 0) vp_comb_o<4, H>(lds + o.w, (const float2*)(lds + o.in1), out, o.heads, o.dh, o.dp, o.nsb, tid, nt);
+            else vp_comb_o<1, H>(lds + o.w, (const float2*)(lds + o.in1), out, o.heads, o.dh, o.dp, o.nsb, tid, nt);
             break;
         case VP_RMS: {  // rms (cpu.rs:187-207) of one group: out = a·r·w
             // (only the waves that own elements of the group sum it, each the same sum)
             if (64 * (tid >> 6) >= (v4 ? n >> 2 : n)) break;
             float dsum = dot16_wave(a, n, tid & 63);
             float r = 1.0f / sqrtf(dsum / (float)n + o.f);
-            vp_map<VP_RMS>(a, b, out, n, v4, f, r, tid, nt);
+            vp_map<VP_RMS, H>(a, b, out, n, v4, f, r, tid, nt);
             break;
         }
         default: break;
@@ -3323,7 +3410,7 @@ __device__ __forceinline__ void fg_load(const FgLane& p, f4 (&wa)[SLM_KS]) {
 // finds M (the largest m of the superblocks that saw a key) from the (m, l) pairs, lane z
 // holds superblock z's weight w_z = e^(m_z − M) and l_z·w_z, lane d sums dim d in
 // superblock order; x[64h + d] = O / L (0 when no superblock saw a key). nsb ≤ 64.
-template <bool C>
+template <bool C, bool H>
 __device__ __forceinline__ void fg_comb_wave(const float* part, float* x, int heads, int dp,
                                              int nsb, int h, int lane, float* gout) {
     int sr = heads * (dp + 2);
@@ -3362,7 +3449,7 @@ __device__ __forceinline__ void fg_comb_wave(const float* part, float* x, int he
             }
         }
     }
-    float v = L > 0.0f ? O / L : 0.0f;
+    float v = h16<H>(L > 0.0f ? O / L : 0.0f);
     x[64 * h + lane] = v;
     if (gout) stc<C>(gout + 64 * h + lane, v);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
@@ -3445,10 +3532,11 @@ FG_KERNEL(slm_fghw, true, true)
 
 // The splits of a linear added in order: y[c] = ((P0[c] + P1[c]) + P2[c]) + ...
 KERNEL void slm_fold(float* __restrict__ y, const float* __restrict__ part, long long n, int nsplit) {
+    bool h = slm_h16;  // (the linear's output: rounded in fp16 mode)
     GRID_LOOP(c, n) {
         float v = part[c];
         for (int z = 1; z < nsplit; z++) v = v + part[z * n + c];
-        y[c] = v;
+        y[c] = h ? r16(v) : v;
     }
 }
 
@@ -3480,17 +3568,18 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+// (h: fp16 mode's roundings, the e_* expressions)
 template <int KIND>
-__device__ __forceinline__ float row_ew(float a, float b, float f) {
+__device__ __forceinline__ float row_ew(float a, float b, float f, bool h) {
     if (KIND == R_COPY) return a;
-    if (KIND == R_ADD) return a + b;
-    if (KIND == R_MIX) return a + f * (b - a);
-    return b * a / (1.0f + expf(-a));  // R_SILU: a = gate, b = up
+    if (KIND == R_ADD) return h ? e_add<true>(a, b) : e_add<false>(a, b);
+    if (KIND == R_MIX) return h ? e_mix<true>(a, b, f) : e_mix<false>(a, b, f);
+    return h ? e_silu<true>(a, b) : e_silu<false>(a, b);  // R_SILU: a = gate, b = up
 }
 // out = f(a, b) element by element
 template <int KIND>
 __device__ __forceinline__ void row_elementwise(const RowOp& o, float* lds, float* yr, long long r,
-                                                int tid) {
+                                                int tid, bool h) {
     int n = o.n;
     bool two = KIND != R_COPY;
     if (o.vec) {
@@ -3510,7 +3599,7 @@ __device__ __forceinline__ void row_elementwise(const RowOp& o, float* lds, floa
                 if (i < n) {
                     f4 v;
 #pragma unroll
-                    for (int e = 0; e < 4; e++) v[e] = row_ew<KIND>(av[u][e], two ? bv[u][e] : 0.0f, o.f0);
+                    for (int e = 0; e < 4; e++) v[e] = row_ew<KIND>(av[u][e], two ? bv[u][e] : 0.0f, o.f0, h);
                     row_put4(lds, o, yr, i, v);
                 }
             }
@@ -3519,7 +3608,7 @@ __device__ __forceinline__ void row_elementwise(const RowOp& o, float* lds, floa
     }
     for (int i = tid; i < n; i += 256)
         row_put(lds, o, yr, i, row_ew<KIND>(row_in(lds, o.la, o.a, r, i),
-                                              two ? row_in(lds, o.lb, o.b, r, i) : 0.0f, o.f0));
+                                              two ? row_in(lds, o.lb, o.b, r, i) : 0.0f, o.f0, h));
 }
 // An op read from the descriptor in LDS, its fields made wave-uniform (they are).
 __device__ __forceinline__ const float* uni_ptr(const float* p) {
@@ -3563,6 +3652,7 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
     f4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (tid < ND4) dv = ((const f4*)(const void*)__builtin_amdgcn_kernarg_segment_ptr())[tid];
     int nops = hd[0], npf = hd[1];
+    bool h16r = hd[2] != 0;  // fp16 mode: every op's output rounded (RowDesc::r16)
 #pragma unroll
     for (int e = 0; e < SLM_ROW_PF; e++) {
         if (e >= npf) break;
@@ -3601,13 +3691,13 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
         int kind = o.kind, n = o.n;
         float* yr = o.y ? o.y + r * o.ystride : nullptr;
         if (kind == R_COPY) {
-            row_elementwise<R_COPY>(o, lds, yr, r, tid);
+            row_elementwise<R_COPY>(o, lds, yr, r, tid, h16r);
         } else if (kind == R_ADD) {
-            row_elementwise<R_ADD>(o, lds, yr, r, tid);
+            row_elementwise<R_ADD>(o, lds, yr, r, tid, h16r);
         } else if (kind == R_MIX) {
-            row_elementwise<R_MIX>(o, lds, yr, r, tid);
+            row_elementwise<R_MIX>(o, lds, yr, r, tid, h16r);
         } else if (kind == R_SILU) {
-            row_elementwise<R_SILU>(o, lds, yr, r, tid);
+            row_elementwise<R_SILU>(o, lds, yr, r, tid, h16r);
         } else if (kind == R_ROPE) {
             int heads = o.i0, dh = o.i1, half = dh / 2;
             if (o.vec) {  // four consecutive i of one head per thread
@@ -3619,8 +3709,8 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
                     f4 v0, v1;
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        v0[e] = a[e] * c[e] - b[e] * sn[e];
-                        v1[e] = a[e] * sn[e] + b[e] * c[e];
+                        v0[e] = h16r ? e_rope_l<true>(a[e], b[e], c[e], sn[e]) : e_rope_l<false>(a[e], b[e], c[e], sn[e]);
+                        v1[e] = h16r ? e_rope_r<true>(a[e], b[e], c[e], sn[e]) : e_rope_r<false>(a[e], b[e], c[e], sn[e]);
                     }
                     row_put4(lds, o, yr, at + i, v0);
                     row_put4(lds, o, yr, at + half + i, v1);
@@ -3630,8 +3720,8 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
                     int h = t / half, i = t % half, at = h * dh;
                     float c = row_in(lds, o.lc, o.c, r, i), sn = row_in(lds, o.ld, o.d, r, i);
                     float a = row_in(lds, o.la, o.a, r, at + i), b = row_in(lds, o.la, o.a, r, at + half + i);
-                    row_put(lds, o, yr, at + i, a * c - b * sn);
-                    row_put(lds, o, yr, at + half + i, a * sn + b * c);
+                    row_put(lds, o, yr, at + i, h16r ? e_rope_l<true>(a, b, c, sn) : e_rope_l<false>(a, b, c, sn));
+                    row_put(lds, o, yr, at + half + i, h16r ? e_rope_r<true>(a, b, c, sn) : e_rope_r<false>(a, b, c, sn));
                 }
             }
         } else if (kind == R_STORE) {
@@ -3690,12 +3780,16 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
                         f4 v = *(const f4*)(in + j), w, out;
                         if (kind == R_RMS) w = row_in4(lds, o.lb, o.b, 0, j);
 #pragma unroll
-                        for (int e = 0; e < 4; e++) out[e] = kind == R_RMS ? v[e] * rr * w[e] : v[e] * rr;
+                        for (int e = 0; e < 4; e++)
+                            out[e] = kind == R_RMS ? (h16r ? e_rms<true>(v[e], rr, w[e]) : v[e] * rr * w[e])
+                                                   : (h16r ? r16(v[e] * rr) : v[e] * rr);
                         row_put4(lds, o, yr, grp * size + j, out);
                     }
                 } else {
                     for (int j = lane; j < size; j += 64) {
-                        float v = kind == R_RMS ? in[j] * rr * row_in(lds, o.lb, o.b, 0, j) : in[j] * rr;
+                        float v = kind == R_RMS ? (h16r ? e_rms<true>(in[j], rr, row_in(lds, o.lb, o.b, 0, j))
+                                                        : in[j] * rr * row_in(lds, o.lb, o.b, 0, j))
+                                                : (h16r ? r16(in[j] * rr) : in[j] * rr);
                         row_put(lds, o, yr, grp * size + j, v);
                     }
                 }
@@ -3710,6 +3804,9 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
                         if (z < o.i0)
 #pragma unroll
                             for (int e = 0; e < 4; e++) v[e] = v[e] + fpre[z][e];
+                    if (h16r)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[e] = r16(v[e]);
                     row_put4(lds, o, yr, i, v);
                 }
             } else if (o.vec) {
@@ -3729,6 +3826,9 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
 #pragma unroll
                                 for (int e = 0; e < 4; e++) v[e] = v[e] + w[u][e];
                     }
+                    if (h16r)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[e] = r16(v[e]);
                     row_put4(lds, o, yr, i, v);
                 }
             } else {
@@ -3736,7 +3836,7 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
                     const float* pp = o.a.g + r * o.a.stride + i;
                     float v = pp[0];
                     for (int z = 1; z < o.i0; z++) v = v + pp[z * o.q0];
-                    row_put(lds, o, yr, i, v);
+                    row_put(lds, o, yr, i, h16r ? r16(v) : v);
                 }
             }
         }
@@ -3786,6 +3886,10 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
         if (c < dh) {
             aq = lq[c] * rq;
             ak = lk[c] * rk;
+            if (g.r16) {
+                aq = r16(aq);
+                ak = r16(ak);
+            }
             stc<STEP>(g.qn + at + c, aq);
             stc<STEP>(g.kn + at + c, ak);
         }
@@ -3796,10 +3900,12 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
         }
         __syncthreads();
     }
-    float dc = 1.0f / (1.0f + expf(ldc<STEP>(g.decay + h) + g.bias[h]));
+    bool hm = g.r16 != 0;
+    float dc = hm ? gla_decay<true>(ldc<STEP>(g.decay + h), g.bias[h]) : gla_decay<false>(ldc<STEP>(g.decay + h), g.bias[h]);
     float vb = live ? ldc<STEP>(g.v + at + b) : 0.0f;
-    float part = live ? gla_rows<RPL>(st, lk, lq, dc, vb, j, dh) : 0.0f;
+    float part = !live ? 0.0f : hm ? gla_rows<RPL, true>(st, lk, lq, dc, vb, j, dh) : gla_rows<RPL, false>(st, lk, lq, dc, vb, j, dh);
     float t2 = gla_colsum(part);
+    if (hm) t2 = r16(t2);
 #pragma unroll
     for (int rr = 0; rr < RPL; rr++) {
         int a = j * RPL + rr;
@@ -3815,10 +3921,10 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
     }
     __syncthreads();
     if (live && j == 0) {
-        float y2 = lds[b] * lds[dh] * g.hn[b];
+        float y2 = hm ? e_rms<true>(lds[b], lds[dh], g.hn[b]) : lds[b] * lds[dh] * g.hn[b];
         stc<STEP>(g.y2 + at + b, y2);
         float gt = ldc<STEP>(g.gate + at + b);
-        stc<STEP>(g.out + at + b, y2 * gt / (1.0f + expf(-gt)));
+        stc<STEP>(g.out + at + b, hm ? e_silu<true>(gt, y2) : y2 * gt / (1.0f + expf(-gt)));
     }
     return true;
 }

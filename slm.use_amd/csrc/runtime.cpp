@@ -112,6 +112,7 @@ struct Graph {
 };
 
 struct Table {  // resident cos/sin rows for one inv_freq buffer
+    bool h16 = false;  // built in fp16 mode: the rows hold fp16 values
     std::vector<float> inv;
     float* cos = nullptr;
     float* sin = nullptr;
@@ -131,6 +132,7 @@ struct Kernels {
     hipFunction_t lin_small_hw, fghw, gemm2hw[4], gemm2hsw[4], gemm2hrw, gemm2hnw;
     hipFunction_t lin_small[2], lin_big[2];  // [vec]
     hipFunction_t gla[5], gla1[3];           // rows per lane 1, 2, 4, .. (16 lanes per column)
+    hipFunction_t glah[5];                   // the prompt GLA in fp16 mode
     hipFunction_t attn[5];                   // dim tiles 1, 2, 4, 8, 16
     hipFunction_t attn_dec[3];               // one-token attention, dim tiles 1, 2, 4
     hipFunction_t argmax;                    // greedy pick on the device
@@ -217,7 +219,8 @@ struct slm_hip {
     uint64_t n_mirror_reads = 0;
     std::map<uintptr_t, Table> tables;
     bool graphs_on = true, fusion_on = true, plan_trace = false;
-    bool fp16 = false;                   // linears with fp16 operands (slm_hip_set_fp16)
+    bool fp16 = false;                   // fp16 mode (slm_hip_set_fp16)
+    int* h16_dev = nullptr;              // the code object's mode word slm_h16 (device)
     int fg_rpt = 0;                      // fused GEMV rows per tile: 0 = the planner's choice
     bool timing = false, capturing = false;
     std::vector<Timed> timed;             // launches whose events are not read yet
@@ -371,6 +374,9 @@ float f32_of(uint16_t h) {
     std::memcpy(&f, &u, 4);
     return f;
 }
+
+// fp16 mode's rounding of a host value (to nearest even), as an fp32 value.
+float round16(float f) { return f32_of(f16_of(f)); }
 
 // The fp16 allocation that starts at p: its element count (0 if p starts none).
 size_t half_count(const slm_hip* c, const void* p) {
@@ -845,7 +851,7 @@ int lower_one(slm_hip* c, const Op& o, std::vector<Rec>& out) {
             int i = pow2_index((n[2] + 15) / 16, 4);
             uint32_t shmem = (uint32_t)(2 * SLM_GLA_T * (2 * n[2] + SLM_GLA_COLS + 1) * 4);  // two token groups
             int vec = (n[2] % 4 == 0 && aligned16(p[2]) && aligned16(p[3]) && aligned16(p[4])) ? 4 : 1;
-            out.push_back(mk(k.gla[i], (uint32_t)n[1], (uint32_t)((n[2] + SLM_GLA_COLS - 1) / SLM_GLA_COLS), 1,
+            out.push_back(mk(c->fp16 ? k.glah[i] : k.gla[i], (uint32_t)n[1], (uint32_t)((n[2] + SLM_GLA_COLS - 1) / SLM_GLA_COLS), 1,
                              16 * SLM_GLA_COLS, shmem,
                              p[0], p[1], p[2], p[3], p[4], p[5], p[6], (int)n[0], (int)n[1],
                              (int)n[2], vec));
@@ -1435,6 +1441,7 @@ struct Planner {
             for (int q = 0; q < rd.nops; q++)
                 if (rd.op[q].y && rd.op[q].kind != R_STORE && dead_after(ops, rnext, rwr[q]))
                     rd.op[q].y = nullptr;
+            rd.r16 = c->fp16 ? 1 : 0;
             Rec r = mk_desc(c->k.rows, (uint32_t)rrows, 256, (uint32_t)(rlds * 4), rd);
             out.push_back(r);
         }
@@ -1986,6 +1993,7 @@ struct Planner {
         if (dh * 16 > 1024) return 0;  // a head per workgroup, sixteen lanes per column
         GlaDesc d;
         std::memset(&d, 0, sizeof d);
+        d.r16 = c->fp16 ? 1 : 0;
         d.y = (float*)g.p[0];
         d.s = (float*)g.p[1];
         d.q = g.p[2];
@@ -3253,6 +3261,8 @@ int load_kernels(slm_hip* c) {
                {&k.lin_big[0], "slm_linear_big_s"},     {&k.lin_big[1], "slm_linear_big_v"},
                {&k.gla[0], "slm_gla_1"},   {&k.gla[1], "slm_gla_2"},   {&k.gla[2], "slm_gla_4"},
                {&k.gla[3], "slm_gla_8"},   {&k.gla[4], "slm_gla_16"},
+               {&k.glah[0], "slm_glah_1"}, {&k.glah[1], "slm_glah_2"}, {&k.glah[2], "slm_glah_4"},
+               {&k.glah[3], "slm_glah_8"}, {&k.glah[4], "slm_glah_16"},
                {&k.gla1[0], "slm_gla1_1"}, {&k.gla1[1], "slm_gla1_2"}, {&k.gla1[2], "slm_gla1_4"},
                {&k.attn[0], "slm_attn_part_1"}, {&k.attn[1], "slm_attn_part_2"},
                {&k.attn[2], "slm_attn_part_4"}, {&k.attn[3], "slm_attn_part_8"},
@@ -3342,6 +3352,13 @@ int slm_hip_open(int device, slm_hip** out) {
     OPEN_HIP(hipMemset(c->attn_ctr, 0, ATTN_CTR_MAX * sizeof(int)));
     OPEN_HIP(hipMalloc((void**)&c->pick, 16 * sizeof(float)));
     OPEN_HIP(hipMemset(c->pick, 0, 16 * sizeof(float)));
+    {  // fp16 mode's word in the code object, zero: fp32 mode
+        size_t bytes = 0;
+        OPEN_HIP(hipModuleGetGlobal((hipDeviceptr_t*)&c->h16_dev, &bytes, c->mod, "slm_h16"));
+        if (bytes != sizeof(int)) return bail(fail(c, SLM_E_HIP, "slm_h16: %zu bytes", bytes));
+        int zero = 0;
+        OPEN_HIP(hipMemcpy(c->h16_dev, &zero, sizeof zero, hipMemcpyHostToDevice));
+    }
     OPEN_HIP(hipMalloc((void**)&c->step_flags, SLM_STEP_WG * sizeof(unsigned)));
     OPEN_HIP(hipMemset(c->step_flags, 0, SLM_STEP_WG * sizeof(unsigned)));
     {  // a step launch needs all its workgroups resident: one per compute unit
@@ -3563,7 +3580,18 @@ int slm_hip_upload(slm_hip* c, float* dst, const float* src, size_t n) {
         }
     }
     HIPC(c, hipStreamSynchronize(mstream(c)));
-    HIPC(c, hipMemcpy(dst, src, n * 4, hipMemcpyHostToDevice));
+    if (!c->fp16) {
+        HIPC(c, hipMemcpy(dst, src, n * 4, hipMemcpyHostToDevice));
+        return SLM_OK;
+    }
+    // fp16 mode: the values rounded to fp16 as they go up (mlx.rs:61-63 uploads every buffer
+    // in its dtype), through the bounce buffer
+    for (size_t done = 0; done < n;) {
+        size_t part = std::min(n - done, BOUNCE_CAP / 4);
+        for (size_t i = 0; i < part; i++) c->bounce[i] = round16(src[done + i]);
+        HIPC(c, hipMemcpy(dst + done, c->bounce, part * 4, hipMemcpyHostToDevice));
+        done += part;
+    }
     return SLM_OK;
 }
 
@@ -3724,6 +3752,19 @@ int slm_hip_prompt_lane_stats(slm_hip* c, uint64_t* steps, uint64_t* fallbacks) 
 int slm_hip_set_fp16(slm_hip* c, int on) {
     if (!c) return SLM_E_INVALID;
     if (c->recording) TRY(finish_step(c));
+    if (c->fp16 == (on != 0)) return SLM_OK;
+    // planned steps and resident rope tables belong to one mode; the kernels that run in both
+    // read the mode word
+    leave_lanes(c);
+    drop_graphs(c);
+    HIPC(c, hipStreamSynchronize(c->stream));
+    for (auto& t : c->tables) {
+        dev_free(c, t.second.cos);
+        dev_free(c, t.second.sin);
+    }
+    c->tables.clear();
+    int v = on != 0;
+    HIPC(c, hipMemcpy(c->h16_dev, &v, sizeof v, hipMemcpyHostToDevice));
     c->fp16 = on != 0;
     return SLM_OK;
 }
@@ -4024,6 +4065,7 @@ int slm_hip_rope_table(slm_hip* c, float* cs, float* sn, const float* inv, size_
     if (c->recording) TRY(finish_step(c));
     Table& t = c->tables[(uintptr_t)inv];
     if (half && t.inv.size() != half) {  // first sight of this inv_freq buffer
+        t.h16 = c->fp16;
         t.inv.assign(half, 0.0f);
         HIPC(c, hipStreamSynchronize(mstream(c)));
         HIPC(c, hipMemcpy(t.inv.data(), inv, half * 4, hipMemcpyDeviceToHost));
@@ -4033,12 +4075,14 @@ int slm_hip_rope_table(slm_hip* c, float* cs, float* sn, const float* inv, size_
         size_t rows = std::max<size_t>({pos + m, t.rows * 2, 8192});
         // cpu.rs:228-236: angle (pos + i) as f32 times inv[j], then libm cos/sin
         std::vector<float> hc(rows * half), hs(rows * half);
+        // (fp16 mode: the angles in fp32 from the fp16 inv_freq, cos and sin rounded to fp16,
+        // mlx.rs:203-208)
         for (size_t p = 0; p < rows; p++) {
             float fp = (float)p;
             for (size_t j = 0; j < half; j++) {
                 float a = fp * t.inv[j];
-                hc[p * half + j] = cosf(a);
-                hs[p * half + j] = sinf(a);
+                hc[p * half + j] = t.h16 ? round16(cosf(a)) : cosf(a);
+                hs[p * half + j] = t.h16 ? round16(sinf(a)) : sinf(a);
             }
         }
         TRY(internal_realloc(c, (void**)&t.cos, rows * half * 4));
@@ -4252,7 +4296,7 @@ int attend_op(slm_hip* c, float* y, const float* q, const float* k, const float*
     o.n[7] = (int64_t)dh;
     o.n[8] = (int64_t)nsb;
     o.n[9] = hk ? 1 : 0;
-    o.f[0] = a->scale;
+    o.f[0] = c->fp16 ? round16(a->scale) : a->scale;  // (fp16 mode: the dtype's scalar, mlx.rs:344)
     if (hk && m > 1 && (int64_t)((qtiles + ATTN_QG_HOST - 1) / ATTN_QG_HOST) * (int64_t)kh * (int64_t)nsb > (int64_t)INT_MAX)
         return fail(c, SLM_E_UNSUPPORTED, "attend: fp16 rings: %zu query tiles", qtiles);
     return SLM_OK;

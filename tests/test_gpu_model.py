@@ -360,6 +360,40 @@ def test_c5_fp16_against_fp32_oracle(pkg, hip):
         hip.set_fp16(False)
 
 
+def test_a86_fp16_mode_keeps_fp16_values(pkg, hip):
+    """fp16 mode as mlx.rs keeps its Float16 arrays (mlx.rs:19-23, 53-67): with the model loaded
+    in the mode, after a 300-token prompt (chunks of 256 + 44) and 4 steps at R = 4 every
+    buffer the session keeps (rings, GLA states, the residual and loop states) and the logits
+    hold fp16 values; chunked == token by token bitwise; within 2e-2 of the fp32 oracle."""
+    folder = model_dir("a86", 2)
+    toks = synth.tokens(304, 32000, seed=41)
+    c = O.Model(folder)
+    cs = c.session(4)
+    cs.feed(toks[:300], 256)
+    hip.set_fp16(True)
+    try:
+        g = pkg.Model(hip, folder)
+        a, b = g.session(4), g.session(4)
+        a.feed(toks[:300], 256)
+        b.feed(toks[:300], 1)
+        assert np.array_equal(a.logits(), b.logits())
+        _kept_equal(a, b)
+        worst = rel(a.logits(), cs.logits())
+        for t in toks[300:]:
+            a.step(int(t))
+            cs.step(int(t))
+            worst = max(worst, rel(a.logits(), cs.logits()))
+        kept = a.kept()
+        for i, x in enumerate(kept):
+            assert np.array_equal(x, x.astype(np.float16).astype(np.float32)), i
+        lg = a.logits()
+        assert np.array_equal(lg, lg.astype(np.float16).astype(np.float32))
+        print(f"fp16 values: {len(kept)} kept buffers; rel vs fp32 oracle {worst:.3g}")
+        assert worst < 2e-2
+    finally:
+        hip.set_fp16(False)
+
+
 def test_a86_fp16_mode_reads_half_weights(pkg, hip):
     """fp16 mode through the unchanged trait: the model uploads fp32 weights (ops.rs:77, as
     model.rs does), and the backend's linears read fp16 copies of them (half the bytes) with

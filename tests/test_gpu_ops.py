@@ -800,20 +800,29 @@ def _row_chain(hip, case, m, fp16):
 
 
 # ---------------------------------------------------------------------------------------
-# fp16 mode: linears round their operands to fp16 at fp16 MFMAs and sum in fp32
+# fp16 mode: linears round their operands to fp16 at fp16 MFMAs, sum in fp32 and round the
+# result to fp16; every operation's result is rounded to fp16 (mlx.rs's Float16 arrays)
 # ---------------------------------------------------------------------------------------
+
+def _is_f16(a):
+    a = np.asarray(a, np.float32)
+    return np.array_equal(a, a.astype(np.float16).astype(np.float32))
+
 
 @pytest.mark.parametrize("rows,cols", [(768, 768), (2304, 768), (768, 3072), (40, 128)])
 def test_linear_fp16(hip, rows, cols):
     """Every m (the small-m GEMV and the GEMM) against float64 sums of the fp16-rounded
-    operands (their products are exact in fp32, so only the fp32 sums differ), and the same
-    bits for a row whatever m is."""
+    operands (their products are exact in fp32, so only the fp32 sums differ) rounded to fp16:
+    the result holds fp16 values, each the fp16 rounding of the float64 sum except where the
+    fp32 sum falls on the other side of a rounding boundary (then one fp16 step, or for sums
+    near zero the fp32 sum's own error, away); and the same bits for a row whatever m is."""
     w = rnd(rows, cols, scale=0.05)
     x = rnd(256, cols)
     dw, dx = hip.upload(w), hip.upload(x)
     w16 = w.astype(np.float16).astype(np.float64)
     x16 = x.astype(np.float16).astype(np.float64)
     want = x16 @ w16.T
+    want16 = want.astype(np.float16).astype(np.float32)
     hip.set_fp16(True)
     try:
         got = {}
@@ -821,8 +830,11 @@ def test_linear_fp16(hip, rows, cols):
             dy = hip.alloc(m * rows)
             hip.linear(dy.ptr, dw.ptr, rows, cols, dx.ptr, m)
             got[m] = dy.read().reshape(m, rows)
-            err = np.abs(got[m] - want[:m]).max() / np.abs(want[:m]).max()
-            assert err < 1e-5, (m, err)
+            assert _is_f16(got[m]), m
+            step = np.spacing(np.abs(want16[:m]).astype(np.float16)).astype(np.float32)
+            tol = step + 1e-6 * np.abs(want).max()  # (fp32 summation error, absolute)
+            assert np.all(np.abs(got[m] - want16[:m]) <= tol), m
+            assert np.mean(got[m] == want16[:m]) > 0.99, m
         for m in (1, 5, 37):
             assert np.array_equal(got[m], got[256][:m]), m
         # fp16 rounding is visible: the fp32 path gives other values
@@ -840,6 +852,81 @@ def test_linear_fp16_rejects_ragged_columns(hip):
     try:
         with pytest.raises(Exception):
             hip.linear(dy.ptr, dw.ptr, 16, 40, dx.ptr, 1)
+    finally:
+        hip.set_fp16(False)
+
+
+def test_fp16_mode_values(hip):
+    """fp16 mode keeps every buffer's values in fp16, as mlx.rs's Float16 arrays (mlx.rs:19-23,
+    53-67): an upload rounds (mlx.rs:61-63); add, add_row, mix, scale_rows and rope give
+    mlx.rs's rounding points over fp32 arithmetic bit for bit (each fp16 array operation is the
+    fp32 one rounded to nearest even: numpy below); rms rounds its fp32 quotient before the
+    weight (mlx.rs:178-185); rms, l2norm, silu_mul and the GLA give fp16 values within fp16
+    roundings of float64, the GLA's state too."""
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)  # noqa: E731
+    n, heads, dh, m = 1536, 12, 64, 3
+    a, b = rnd(n), rnd(n)
+    hip.set_fp16(True)
+    try:
+        da, db = hip.upload(a), hip.upload(b)
+        a16, b16 = da.read(), db.read()
+        assert np.array_equal(a16, f16(a)) and np.array_equal(b16, f16(b))
+        y = hip.alloc(n)
+        hip.add(y.ptr, da.ptr, db.ptr, n)
+        assert np.array_equal(y.read(), f16(a16 + b16))
+        hip.add_row(y.ptr, da.ptr, db.ptr, 2, n // 2)
+        assert np.array_equal(y.read(), f16(a16 + np.tile(b16[:n // 2], 2)))
+        t = np.float32(0.3)
+        hip.mix(y.ptr, da.ptr, db.ptr, n, float(t))
+        assert np.array_equal(y.read(), f16(a16 + f16(f16(b16 - a16) * f16(t))))
+        f = np.array([1.7, -0.25], np.float32)
+        hip.scale_rows(y.ptr, da.ptr, f, n // 2)
+        assert np.array_equal(y.read(), f16(a16 * np.repeat(f16(f), n // 2)))
+        # rope over one token of 12 heads, cos / sin rows as fp16 values
+        half = dh // 2
+        c16, s16 = f16(rnd(half)), f16(rnd(half))
+        dc, ds = hip.upload(c16), hip.upload(s16)
+        x = f16(rnd(heads, dh))
+        dx, yr = hip.upload(x), hip.alloc(heads * dh)
+        hip.rope(yr.ptr, dx.ptr, dc.ptr, ds.ptr, 1, heads, dh)
+        lo, hi = x[:, :half], x[:, half:]
+        want = np.concatenate([f16(f16(lo * c16) - f16(hi * s16)), f16(f16(lo * s16) + f16(hi * c16))], 1)
+        assert np.array_equal(yr.read().reshape(heads, dh), want)
+        # rms, l2norm, silu_mul: fp16 values, within fp16 roundings of float64
+        w = f16(rnd(dh))
+        dw, yn = hip.upload(w), hip.alloc(heads * dh)
+        hip.rms(yn.ptr, dx.ptr, dw.ptr, heads, dh, 1e-6)
+        x64 = x.astype(np.float64)
+        r = 1.0 / np.sqrt((x64 * x64).mean(1, keepdims=True) + 1e-6)
+        got = yn.read().reshape(heads, dh)
+        assert _is_f16(got)
+        assert np.allclose(got, x64 * r * w, rtol=2e-3, atol=1e-6)
+        hip.l2norm(yn.ptr, dx.ptr, heads, dh)
+        got = yn.read().reshape(heads, dh)
+        assert _is_f16(got)
+        assert np.allclose(got, x64 / np.sqrt((x64 * x64).sum(1, keepdims=True)), rtol=1e-3, atol=1e-6)
+        hip.silu_mul(y.ptr, da.ptr, db.ptr, n)
+        g64, u64 = a16.astype(np.float64), b16.astype(np.float64)
+        assert _is_f16(y.read())
+        assert np.allclose(y.read(), g64 / (1 + np.exp(-g64)) * u64, rtol=3e-3, atol=1e-6)
+        # the GLA over m tokens: output and state in fp16
+        q, k, v = f16(rnd(m, heads, dh, scale=0.2)), f16(rnd(m, heads, dh, scale=0.2)), f16(rnd(m, heads, dh))
+        dec, bias = f16(rnd(m, heads)), f16(rnd(heads))
+        s0 = f16(rnd(heads, dh, dh, scale=0.1))
+        S = hip.upload(s0)
+        yg = hip.alloc(m * heads * dh)
+        hip.gla(yg.ptr, S.ptr, hip.upload(q).ptr, hip.upload(k).ptr, hip.upload(v).ptr,
+                hip.upload(dec).ptr, hip.upload(bias).ptr, m, heads, dh)
+        st = s0.astype(np.float64)
+        want = np.zeros((m, heads, dh))
+        for i in range(m):
+            dd = 1.0 / (1.0 + np.exp(dec[i] + bias))
+            st = st * dd[:, None, None] + k[i][:, :, None] * v[i][:, None, :]
+            want[i] = np.einsum("hd,hde->he", q[i], st)
+        gy, gs = yg.read().reshape(m, heads, dh), S.read().reshape(heads, dh, dh)
+        assert _is_f16(gy) and _is_f16(gs)
+        assert np.abs(gs - st).max() <= 4e-3 * np.abs(st).max()
+        assert np.abs(gy - want).max() <= 8e-3 * np.abs(want).max()
     finally:
         hip.set_fp16(False)
 
