@@ -269,10 +269,10 @@ def g86_leg(pkg, hip, synth, device_grow=False):
 
 
 def fp16_leg(pkg, hip, folder, a, prompt, fl):
-    """The same workload in fp16 mode (the --fp16 analogue, slm_hip_set_fp16): the model uploads
-    fp32 weights through the trait as model.rs does; the backend's linears read fp16 copies of
-    them (half the bytes) with fp16 operands at fp16 MFMAs and fp32 sums; attention, GLA,
-    norms and states fp32."""
+    """The same workload in fp16 mode (the --fp16 analogue, slm_hip_set_fp16, set before the
+    model loads as mlx.rs fixes its dtype): every buffer holds fp16 values — uploads round,
+    every operation rounds what it writes at mlx.rs's rounding points; the linears read fp16
+    copies of the weights (half the bytes) at fp16 MFMAs with fp32 sums; the rings hold halves."""
     hip.set_fp16(True)
     model = pkg.Model(hip, folder)
     s16 = model.session(a.loops)
@@ -305,11 +305,12 @@ def fp16_leg(pkg, hip, folder, a, prompt, fl):
             "us_per_launch_by_kernel": {n: round(v["us"] / max(v["launches"], 1), 2) for n, v in kern.items()},
             "rings": "fp16 (slm_hip_alloc_cache in fp16 mode): K/V bytes halved",
             "prefill_tflops": round(fl / fill16_s / 1e12, 2),
-            "path": "the trait's calls unchanged: fp32 uploads, then slm_hip_set_fp16(1)",
-            "note": "linears read fp16 copies of the fp32 weights the backend makes on first use, "
-                    "operands at v_mfma_f32_16x16x16f16 (fp32 sums); attention, GLA, norms and "
-                    "states fp32; the bits of fp16 mode over the fp32 weights; checked at 2e-2 vs "
-                    "the fp32 oracle (config C5)"}
+            "path": "the trait's calls unchanged: slm_hip_set_fp16(1), then the model's fp32 uploads",
+            "note": "every buffer holds fp16 values (uploads and every op's output rounded, "
+                    "mlx.rs:19-23, 53-67); linears read fp16 copies of the weights the backend "
+                    "makes on first use, operands at v_mfma_f32_16x16x16f16 (fp32 sums); "
+                    "checked at 2e-2 vs the fp32 oracle (config C5), chunked == token by token "
+                    "bitwise"}
     log(f"fp16 mode: prefill {fp16['prefill_tok_s']} tok/s, decode {fp16['decode_tok_s']} tok/s")
     return fp16
 
@@ -434,8 +435,7 @@ def main():
         f"{bpl / 1e6:.2f} MB/launch, {gemv_bw / 1e9:.0f} GB/s")
     share = {n: round(v["us"] / max(a.timed_steps, 1), 1) for n, v in kern.items()}
 
-    # the same workload in fp16 mode (the --fp16 analogue: linears with fp16 operands at
-    # fp16 MFMAs, fp32 sums; attention, GLA, norms and states fp32)
+    # the same workload in fp16 mode (the --fp16 analogue: every buffer's values in fp16)
     fp16 = None
     if not a.no_fp16:
         fp16 = fp16_leg(pkg, hip, folder, argparse.Namespace(loops=head, warmup=a.warmup, steps=a.steps,
