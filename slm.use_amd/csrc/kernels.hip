@@ -1255,7 +1255,7 @@ __device__ void gemm2_body(float* __restrict__ y, float* __restrict__ part,
     constexpr int NTH = 64 * WAVES * KG;                        // threads
     extern __shared__ __attribute__((aligned(16))) float lds[];  // [KG][GEMM_STAGES][w: BM x 64 | x: 64 x 64]
     int tid = threadIdx.x, lane = tid & 63;
-    int kg = __builtin_amdgcn_readfirstlane((tid >> 6) / WAVES), wave = (tid >> 6) % WAVES;
+    int kg = __builtin_amdgcn_readfirstlane((tid >> 6) / WAVES), wave = __builtin_amdgcn_readfirstlane((tid >> 6) % WAVES);
     int i = lane & 15, g = lane >> 4;
     // waves: RG groups of the rows times (64 / 16NV) groups of tokens
     int wr = (wave % RG) * (BM / RG), wt = (wave / RG) * 16 * NV;
@@ -3647,7 +3647,7 @@ KERNEL void __launch_bounds__(256) slm_rows(const RowDesc dk) {
     static_assert(O0 + (int)(sizeof(RowOp) / 4) <= 128, "the first op in the registers' dwords");
     extern __shared__ __attribute__((aligned(16))) float lds[];
     long long r = blockIdx.x;
-    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     KDw hd = kdw_load((const int*)(const void*)__builtin_amdgcn_kernarg_segment_ptr(), 0, lane);
     f4 dv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (tid < ND4) dv = ((const f4*)(const void*)__builtin_amdgcn_kernarg_segment_ptr())[tid];
