@@ -97,6 +97,9 @@ typedef struct {
     int32_t epi, rpt, ring16;  // ring16 (ROPE): the rings hold fp16 values
     int32_t d, dh;          // ROPE: part width, head size
     int32_t cs_lds, sn_lds; // ROPE: LDS offsets of the cos / sin row
+    // ceil(2^32 / tiles) and ceil(2^32 / half) (0 where the divisor is 0 or 1): the kernel's
+    // n / d is the high word of n · m, exact while n · d < 2^32
+    uint32_t mtiles, mhalf;
     float* o1;
     float* o2;
     float* o3;

@@ -3277,30 +3277,39 @@ struct FgUnit {
     int seg, tile, split;
 };
 
+// n / d through m = ceil(2^32 / d) (the planner's FgSeg::mtiles, mhalf): the high word of n·m,
+// exact while n·d < 2^32 (indices here stay far below); d = 1 gives n.
+__device__ __forceinline__ int mdiv(int n, int d, unsigned m) {
+    return d == 1 ? n : (int)__umulhi((unsigned)n, m);
+}
+
 __device__ __forceinline__ FgUnit fg_unit(const FgDesc& d, int u) {
     int k = 0;
     for (int q = 1; q < d.nseg; q++)
         if (u >= d.seg[q].unit_first) k = q;
     const FgSeg& s = d.seg[k];
     int local = u - s.unit_first;
-    return FgUnit{k, local % s.tiles, local / s.tiles};
+    int split = mdiv(local, s.tiles, s.mtiles);
+    return FgUnit{k, local - split * s.tiles, split};
 }
 
 // Row of lane row i (0..15) of tile t of a matrix of `rows` rows in tiles of rpt rows (16, 12,
 // 8 or 4; lane rows past rpt hold none: `rows` is returned, one past the last). In the first
 // pair_rows rows lane rows i and i + rpt/2 hold a (row, row + half) pair.
-__device__ __forceinline__ long long fg_row_of(int rpt, int pair_rows, int half, int rows, int t, int i) {
+__device__ __forceinline__ long long fg_row_of(int rpt, int pair_rows, int half, unsigned mhalf, int rows,
+                                               int t, int i) {
     if (i >= rpt) return rows;
     int hp = rpt >> 1;
     if (t * rpt < pair_rows) {
         bool second = i >= hp;
         int P = t * hp + (second ? i - hp : i);
-        return (long long)(P / half) * 2 * half + P % half + (second ? half : 0);
+        int q = mdiv(P, half, mhalf);
+        return (long long)q * 2 * half + (P - q * half) + (second ? half : 0);
     }
     return (long long)t * rpt + i;
 }
 __device__ __forceinline__ long long fg_row(const FgSeg& s, int t, int i) {
-    return fg_row_of(s.rpt, s.pair_rows, s.half, s.rows, t, i);
+    return fg_row_of(s.rpt, s.pair_rows, s.half, s.mhalf, s.rows, t, i);
 }
 
 // Sixteen zero bytes: what a lane past the end of a weight matrix loads.
@@ -3341,6 +3350,7 @@ __device__ __forceinline__ FgLane fg_lane_k(const KDw& hd, const KDw& sd, int u,
     constexpr int SWT = (int)(offsetof(FgSeg, w) / 4), SR = (int)(offsetof(FgSeg, rows) / 4);
     constexpr int SP = (int)(offsetof(FgSeg, pair_rows) / 4), SH = (int)(offsetof(FgSeg, half) / 4);
     constexpr int SRT = (int)(offsetof(FgSeg, rpt) / 4);
+    constexpr int SMT = (int)(offsetof(FgSeg, mtiles) / 4), SMH = (int)(offsetof(FgSeg, mhalf) / 4);
     static_assert(sizeof(FgSeg) % 4 == 0 && SLM_SEG_MAX * sizeof(FgSeg) <= 512, "segment table layout");
     FgLane p{slm_zero16, 0, 0};
     if (u >= hd[HU]) return p;
@@ -3349,7 +3359,7 @@ __device__ __forceinline__ FgLane fg_lane_k(const KDw& hd, const KDw& sd, int u,
     for (int q = 1; q < SLM_SEG_MAX; q++)
         if (q < nseg && u >= sd[q * SW + SF]) k = q;
     int local = u - sd[k * SW + SF], tiles = sd[k * SW + ST];
-    int tile = local % tiles, split = local / tiles;
+    int split = mdiv(local, tiles, (unsigned)sd[k * SW + SMT]), tile = local - split * tiles;
     int sl = split * SLM_SPLIT + wave;
     int cols = hd[HC];
     int kblocks = (cols + 15) >> 4;
@@ -3357,7 +3367,8 @@ __device__ __forceinline__ FgLane fg_lane_k(const KDw& hd, const KDw& sd, int u,
     p.kb0 = sl * SLM_KS;
     p.nkb = min(SLM_KS, kblocks - p.kb0);
     int rows = sd[k * SW + SR];
-    long long row = fg_row_of(sd[k * SW + SRT], sd[k * SW + SP], sd[k * SW + SH], rows, tile, i);
+    long long row = fg_row_of(sd[k * SW + SRT], sd[k * SW + SP], sd[k * SW + SH], (unsigned)sd[k * SW + SMH], rows,
+                              tile, i);
     if (row < rows) {
         const float* w = (const float*)sd.q64(k * SW + SWT);
         if constexpr (W16) p.base = (const float*)((const _Float16*)w + row * cols + 4 * g);

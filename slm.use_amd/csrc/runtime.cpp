@@ -1957,7 +1957,12 @@ struct Planner {
         d.fold_off = d.lds_vp + SLM_FG_MISC;
         int total = d.fold_off + 4 * W * 16;
         if (total * 4 > LDS_MAX) return nofuse(i, "LDS");
-        for (int k = 0; k < nseg; k++) d.seg[k] = seg[k];
+        auto magic = [](int32_t v) { return v > 1 ? (uint32_t)(((1ull << 32) + (uint64_t)v - 1) / (uint64_t)v) : 0u; };
+        for (int k = 0; k < nseg; k++) {
+            d.seg[k] = seg[k];
+            d.seg[k].mtiles = magic(seg[k].tiles);
+            d.seg[k].mhalf = magic(seg[k].half);
+        }
         int threads = 64 * (W + SLM_FG_EPI_WAVES);
         uint32_t grid = (uint32_t)std::min(units, FG_GRID_MAX);
         hipFunction_t fk = L.n[4] ? c->k.fghw : d.f16 ? c->k.fgh : c->k.fg;
