@@ -3868,29 +3868,58 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
     bool live = b < dh;
     float* Sh = g.s + (long long)h * dh * dh;
     long long at = (long long)h * dh;
+    // A launch of its own loads the step's q, k, v and decay first and the state (dh x dh a
+    // head) after them, so that the state streams in while the norms run: its barriers only
+    // order LDS (lds_bar), so none of them waits for the state or for a store. As a step
+    // phase, the state, from earlier steps, is read before the wait for the phase that made
+    // q, k, v and the decay, and those after it. (nt ≥ dh: one element of q and k a thread.)
+    // (every lane loads, from a clamped index where it has nothing to load, and drops the
+    // value after: the loads are then a fixed sequence, so the wait for q and k does not wait
+    // for the state behind them)
+    float q0 = 0.0f, k0 = 0.0f, vb = 0.0f, draw = 0.0f, bias = g.bias[h];
+    int tq = min(tid, dh - 1), bq = min(b, dh - 1);
+    if (!STEP) {
+        q0 = gld(g.q + at + tq);
+        k0 = gld(g.k + at + tq);
+        vb = gld(g.v + at + bq);
+        draw = gld(g.decay + h);
+        asm volatile("" : : : "memory");  // (issued before the state's loads)
+    }
     float st[RPL];
 #pragma unroll
     for (int rr = 0; rr < RPL; rr++) {
-        int a = j * RPL + rr;
-        st[rr] = (live && a < dh) ? Sh[(long long)a * dh + b] : 0.0f;
+        int a = min(j * RPL + rr, dh - 1);
+        st[rr] = Sh[(long long)a * dh + bq];
     }
-    // (as a step phase, the state, from earlier steps, is read before the wait for the
-    // phase that made q, k, v and the decay)
-    if (STEP && step_wait_wg(*sw, gave, tid)) return false;
+    if (STEP) {
+        if (step_wait_wg(*sw, gave, tid)) return false;
+        q0 = ldc<STEP>(g.q + at + tq);
+        k0 = ldc<STEP>(g.k + at + tq);
+        vb = ldc<STEP>(g.v + at + bq);
+        draw = ldc<STEP>(g.decay + h);
+    }
+    if (!live) vb = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPL; rr++)
+        if (!live || j * RPL + rr >= dh) st[rr] = 0.0f;
+    auto bar = [] {
+        if (STEP) __syncthreads();
+        else lds_bar();
+    };
     float* lq = lds + dh + 4;
     float* lk = lq + dh;
     float* nr = lk + dh;
-    for (int c = tid; c < dh; c += nt) {
-        lq[c] = ldc<STEP>(g.q + at + c);
-        lk[c] = ldc<STEP>(g.k + at + c);
+    if (tid < dh) {
+        lq[tid] = q0;
+        lk[tid] = k0;
     }
-    __syncthreads();
+    bar();
     if (g.l2) {
         if (tid < 32) {
             float d = dot16_self(tid < 16 ? lq : lk, dh, tid & 15);
             if ((tid & 15) == 0) nr[tid >> 4] = 1.0f / fmaxf(sqrtf(d), 1e-12f);
         }
-        __syncthreads();
+        bar();
         float rq = nr[0], rk = nr[1];
         float aq = 0.0f, ak = 0.0f;
         int c = tid;
@@ -3904,16 +3933,15 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
             stc<STEP>(g.qn + at + c, aq);
             stc<STEP>(g.kn + at + c, ak);
         }
-        __syncthreads();
+        bar();
         if (c < dh) {
             lq[c] = aq;
             lk[c] = ak;
         }
-        __syncthreads();
+        bar();
     }
     bool hm = g.r16 != 0;
-    float dc = hm ? gla_decay<true>(ldc<STEP>(g.decay + h), g.bias[h]) : gla_decay<false>(ldc<STEP>(g.decay + h), g.bias[h]);
-    float vb = live ? ldc<STEP>(g.v + at + b) : 0.0f;
+    float dc = hm ? gla_decay<true>(draw, bias) : gla_decay<false>(draw, bias);
     float part = !live ? 0.0f : hm ? gla_rows<RPL, true>(st, lk, lq, dc, vb, j, dh) : gla_rows<RPL, false>(st, lk, lq, dc, vb, j, dh);
     float t2 = gla_colsum(part);
     if (hm) t2 = r16(t2);
@@ -3925,12 +3953,12 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
     if (live && j == 0) stc<STEP>(g.y + at + b, t2);
     if (!g.fuse) return true;
     if (live && j == 0) lds[b] = t2;
-    __syncthreads();
+    bar();
     if (tid < 16) {
         float d = dot16_self(lds, dh, tid);
         if (tid == 0) lds[dh] = 1.0f / sqrtf(d / (float)dh + g.eps);
     }
-    __syncthreads();
+    bar();
     if (live && j == 0) {
         float y2 = hm ? e_rms<true>(lds[b], lds[dh], g.hn[b]) : lds[b] * lds[dh] * g.hn[b];
         stc<STEP>(g.y2 + at + b, y2);
