@@ -3878,11 +3878,14 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
     // for the state behind them)
     float q0 = 0.0f, k0 = 0.0f, vb = 0.0f, draw = 0.0f, bias = g.bias[h];
     int tq = min(tid, dh - 1), bq = min(b, dh - 1);
+    // (and, when fused, the gate and the head norm's weight, used last)
+    float gt = 0.0f, hnw = g.fuse ? g.hn[bq] : 0.0f;
     if (!STEP) {
         q0 = gld(g.q + at + tq);
         k0 = gld(g.k + at + tq);
         vb = gld(g.v + at + bq);
         draw = gld(g.decay + h);
+        if (g.fuse) gt = gld(g.gate + at + bq);
         asm volatile("" : : : "memory");  // (issued before the state's loads)
     }
     float st[RPL];
@@ -3897,6 +3900,7 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
         k0 = ldc<STEP>(g.k + at + tq);
         vb = ldc<STEP>(g.v + at + bq);
         draw = ldc<STEP>(g.decay + h);
+        if (g.fuse) gt = ldc<STEP>(g.gate + at + bq);
     }
     if (!live) vb = 0.0f;
 #pragma unroll
@@ -3960,9 +3964,8 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
     }
     bar();
     if (live && j == 0) {
-        float y2 = hm ? e_rms<true>(lds[b], lds[dh], g.hn[b]) : lds[b] * lds[dh] * g.hn[b];
+        float y2 = hm ? e_rms<true>(lds[b], lds[dh], hnw) : lds[b] * lds[dh] * hnw;
         stc<STEP>(g.y2 + at + b, y2);
-        float gt = ldc<STEP>(g.gate + at + b);
         stc<STEP>(g.out + at + b, hm ? e_silu<true>(gt, y2) : y2 * gt / (1.0f + expf(-gt)));
     }
     return true;
