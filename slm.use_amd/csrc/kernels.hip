@@ -3888,11 +3888,23 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
         if (g.fuse) gt = gld(g.gate + at + bq);
         asm volatile("" : : : "memory");  // (issued before the state's loads)
     }
+    // The state: where dh = 64 (RPL = 4, 1024 threads), thread t loads elements t, t + 1024, ...
+    // (whole rows a wave, one memory line per 32 lanes) and the values reach their lanes
+    // through LDS (row a at a·65: lanes of one column read distinct banks); otherwise each
+    // lane loads its own rows of its column.
+    constexpr bool ST64 = RPL == 4;
+    bool staged = ST64 && dh == 64 && nt == 1024;
+    float* ls = lds + 4 * dh + 16;
     float st[RPL];
+    if (staged) {
 #pragma unroll
-    for (int rr = 0; rr < RPL; rr++) {
-        int a = min(j * RPL + rr, dh - 1);
-        st[rr] = Sh[(long long)a * dh + bq];
+        for (int q = 0; q < RPL; q++) st[q] = Sh[tid + q * 1024];
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < RPL; rr++) {
+            int a = min(j * RPL + rr, dh - 1);
+            st[rr] = Sh[(long long)a * dh + bq];
+        }
     }
     if (STEP) {
         if (step_wait_wg(*sw, gave, tid)) return false;
@@ -3903,9 +3915,11 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
         if (g.fuse) gt = ldc<STEP>(g.gate + at + bq);
     }
     if (!live) vb = 0.0f;
+    if (!staged) {
 #pragma unroll
-    for (int rr = 0; rr < RPL; rr++)
-        if (!live || j * RPL + rr >= dh) st[rr] = 0.0f;
+        for (int rr = 0; rr < RPL; rr++)
+            if (!live || j * RPL + rr >= dh) st[rr] = 0.0f;
+    }
     auto bar = [] {
         if (STEP) __syncthreads();
         else lds_bar();
@@ -3944,20 +3958,42 @@ __device__ __forceinline__ bool gla1_body(const GlaDesc& g, int h, int tid, int 
         }
         bar();
     }
+    if (staged) {  // (every lane of dh = 64 is live, with all its rows)
+#pragma unroll
+        for (int q = 0; q < RPL; q++) {
+            int e = tid + q * 1024;
+            ls[(e >> 6) * 65 + (e & 63)] = st[q];
+        }
+        bar();
+#pragma unroll
+        for (int rr = 0; rr < RPL; rr++) st[rr] = ls[(j * RPL + rr) * 65 + b];
+    }
     bool hm = g.r16 != 0;
     float dc = hm ? gla_decay<true>(draw, bias) : gla_decay<false>(draw, bias);
     float part = !live ? 0.0f : hm ? gla_rows<RPL, true>(st, lk, lq, dc, vb, j, dh) : gla_rows<RPL, false>(st, lk, lq, dc, vb, j, dh);
     float t2 = gla_colsum(part);
     if (hm) t2 = r16(t2);
+    if (staged) {  // back through LDS (each lane's own slots), then whole rows a wave
 #pragma unroll
-    for (int rr = 0; rr < RPL; rr++) {
-        int a = j * RPL + rr;
-        if (live && a < dh) Sh[(long long)a * dh + b] = st[rr];
+        for (int rr = 0; rr < RPL; rr++) ls[(j * RPL + rr) * 65 + b] = st[rr];
+    } else {
+#pragma unroll
+        for (int rr = 0; rr < RPL; rr++) {
+            int a = j * RPL + rr;
+            if (live && a < dh) Sh[(long long)a * dh + b] = st[rr];
+        }
     }
     if (live && j == 0) stc<STEP>(g.y + at + b, t2);
-    if (!g.fuse) return true;
-    if (live && j == 0) lds[b] = t2;
+    if (g.fuse && live && j == 0) lds[b] = t2;
     bar();
+    if (staged) {
+#pragma unroll
+        for (int q = 0; q < RPL; q++) {
+            int e = tid + q * 1024;
+            Sh[e] = ls[(e >> 6) * 65 + (e & 63)];
+        }
+    }
+    if (!g.fuse) return true;
     if (tid < 16) {
         float d = dot16_self(lds, dh, tid);
         if (tid == 0) lds[dh] = 1.0f / sqrtf(d / (float)dh + g.eps);

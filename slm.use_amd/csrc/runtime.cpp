@@ -2059,8 +2059,10 @@ struct Planner {
             }
         }
         int ri = pow2_index((dh + 15) / 16, 2);
+        // (dh = 64: the state staged in LDS, 64 rows of 65)
+        size_t stage = dh == 64 ? 64 * 65 : 0;
         out.push_back(mk_desc(c->k.gla1[ri], (uint32_t)heads, (uint32_t)((dh * 16 + 63) / 64 * 64),
-                              (uint32_t)((4 * dh + 16) * 4), d));
+                              (uint32_t)((4 * dh + 16 + stage) * 4), d));
         return used;
     }
 
