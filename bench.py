@@ -341,7 +341,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print(f"bench.py runs on one GPU: --gpus {a.gpus} (WORLD_SIZE {world}) is not "
-              "supported; the token loop has no multi-GPU path in this build", file=sys.stderr)
+              "supported; the token loop has no multi-GPU path here", file=sys.stderr)
         sys.exit(2)
 
     pkg = package()

@@ -1,6 +1,6 @@
 // ORACLE — test infrastructure only. Nothing in the product links, loads or calls this
-// file; only tests/, the smoke check and bench.py's CPU-baseline leg do, and only as the
-// checker or the timed CPU baseline.
+// file; only tests/, the smoke check and bench.py's CPU-baseline leg do, and only as what
+// the GPU results are compared against or as the timed CPU baseline.
 //
 // A CPU restatement of the reference's CPU backend and model, op for op and in the same
 // arithmetic order, so that it computes what the reference computes bit for bit:

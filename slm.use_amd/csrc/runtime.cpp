@@ -3334,7 +3334,7 @@ int slm_hip_open(int device, slm_hip** out) {
     snprintf(c->name, sizeof c->name, "hip (%s, %s)", prop.name[0] ? prop.name : "AMD GPU",
              prop.gcnArchName);
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
-        return bail(fail(c, SLM_E_UNSUPPORTED, "device %d is %s; this build is for gfx950",
+        return bail(fail(c, SLM_E_UNSUPPORTED, "device %d is %s; the library is built for gfx950",
                          device, prop.gcnArchName));
     OPEN_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     OPEN_HIP(slm_scratch_address((void**)&c->scratch));  // this device current (hipSetDevice above)
