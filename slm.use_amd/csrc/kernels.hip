@@ -3426,18 +3426,16 @@ __device__ __forceinline__ void fg_comb_wave(const float* part, float* x, int he
                                              int nsb, int h, int lane, float* gout) {
     int sr = heads * (dp + 2);
     const float* P = part + h * (dp + 2);
-    float M = NEG_INF;
-    for (int z0 = 0; z0 < nsb; z0 += 8) {
-        float2 ml[8];
+    // M: lane z holds superblock z's (m, l); the largest m with l > 0 across the wave (a
+    // maximum, so its order does not matter: NaNs drop out, and -inf starts it as a pass over
+    // the superblocks in order does)
+    float2 me = lane < nsb ? *(const float2*)(P + lane * sr) : float2{NEG_INF, 0.0f};
+    float M = me.y > 0.0f ? me.x : NEG_INF;
 #pragma unroll
-        for (int u = 0; u < 8; u++) ml[u] = *(const float2*)(P + min(z0 + u, nsb - 1) * sr);
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (z0 + u < nsb && ml[u].y > 0.0f) M = fmaxf(M, ml[u].x);
-    }
+    for (int d = 32; d >= 1; d >>= 1) M = fmaxf(M, __shfl_xor(M, d));
+    M = fmaxf(NEG_INF, M);
     float wz = -1.0f, lwz = 0.0f;
     if (lane < nsb) {
-        float2 me = *(const float2*)(P + lane * sr);
         float w = expf(me.x - M);
         if (me.y > 0.0f) {
             wz = w;
