@@ -2415,14 +2415,27 @@ __device__ __forceinline__ bool attn_dec_body(float* __restrict__ part, const fl
     static_assert(DT >= 1 && DT <= 4, "one-token attention: head size at most 64");
     constexpr int DP = 16 * DT;
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    long long pos = dyn_or(dyn, pos_imm);
     int lane = tid & 63;
     int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int group = heads / key_heads, kvh = bx;
     int nch = dh >> 2;  // 16-byte chunks per row
-    long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
-    long long sb = first / SLM_SB_KEYS + by;
-    long long seg_lo = (sb * SLM_SB_SEGS + wave) * 64;
+    // Ring order, for a ring of exactly ny superblocks (cap = 256·ny, not as a step phase):
+    // workgroup y takes ring slots 256y .. 256y + 255, which hold the one superblock
+    // sb ≡ y (mod ny) of the span's ny consecutive ones, so its copies need no position and
+    // go out before the position is read; its partial goes to that superblock's place zb in
+    // position order. Otherwise workgroup y takes superblock y of the span.
+    const bool ring = !STEP && cap == (long long)ny * SLM_SB_KEYS;
+    long long pos = 0, sb = 0, seg_lo = 0;
+    int zb = by;
+    auto at_pos = [&]() {
+        pos = dyn_or(dyn, pos_imm);
+        long long first = (reach - 1 > pos) ? 0 : pos - (reach - 1);
+        long long fsb = first / SLM_SB_KEYS;
+        if (ring) zb = (int)((by + ny - fsb % ny) % ny);
+        sb = fsb + zb;
+        seg_lo = (sb * SLM_SB_SEGS + wave) * 64;
+    };
+    if (!ring) at_pos();
     constexpr unsigned ES = KH ? 2u : 4u;  // bytes per ring element
     const char* kb = (const char*)kc + (long long)kvh * cap * dh * ES;
     const char* vb = (const char*)vc + (long long)kvh * cap * dh * ES;
@@ -2448,8 +2461,9 @@ __device__ __forceinline__ bool attn_dec_body(float* __restrict__ part, const fl
     // ring is under 4 GB, so byte offsets are 32-bit (the host checks both).
     // (the offsets are worked out again for the values: sixteen registers fewer held)
     unsigned rowb = (unsigned)dh * ES, wrapb = (unsigned)cap * rowb;
-    unsigned slot = (unsigned)(seg_lo % cap) + (unsigned)(lane >> 4);
-    if (slot >= (unsigned)cap) slot -= (unsigned)cap;
+    unsigned slot = ring ? (unsigned)(by * SLM_SB_KEYS + wave * 64) + (unsigned)(lane >> 4)
+                         : (unsigned)(seg_lo % cap) + (unsigned)(lane >> 4);
+    if (slot >= (unsigned)cap) slot -= (unsigned)cap;  // (never in ring order)
     const unsigned roff0 = slot * rowb;
     auto off_of = [&](int k, unsigned roff) {
         int key = 4 * k + (lane >> 4);
@@ -2490,6 +2504,10 @@ __device__ __forceinline__ bool attn_dec_body(float* __restrict__ part, const fl
             roff += 4 * rowb;
             if (roff >= wrapb) roff -= wrapb;
         }
+    }
+    if (ring) {
+        asm volatile("" ::: "memory");  // (the position is read after the copies are out)
+        at_pos();
     }
     if constexpr (STEP) {
         // As a step phase the copies above went out before the wait for the QKV phase: the
@@ -2656,7 +2674,7 @@ __device__ __forceinline__ bool attn_dec_body(float* __restrict__ part, const fl
             fold(FM, FL, FO, F[0], F[1], F[2 + dd]);
         }
         int head = kvh * group + cc;
-        float* P = part + ((long long)by * heads + head) * (long long)(DP + 2);
+        float* P = part + ((long long)zb * heads + head) * (long long)(DP + 2);
         if (ctr || STEP) {  // written through to where every workgroup's loads see it
             if (dd == 0) {
                 __hip_atomic_store(P, FM, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -266,6 +266,13 @@ ATTN_CASES = [
     dict(pos=400, m=4, reach=300, gap=0, cap=512, heads=4, key_heads=2, dh=48),
     dict(pos=90, m=2, reach=64, gap=0, cap=100, heads=2, key_heads=1, dh=4),
     dict(pos=9000, m=2, reach=O.USIZE_MAX, gap=0, cap=9100, heads=16, key_heads=1, dh=64),
+    # rings of exactly the one-token kernel's superblock count (cap = 256 x slots): its
+    # workgroups copy ring slots before they read the position. Wrapped; the oldest key on a
+    # superblock boundary at 4607 (one slot holds no key); grouped heads; a global span
+    dict(pos=5000, m=3, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
+    dict(pos=4605, m=3, reach=4096, gap=0, cap=4352, heads=12, key_heads=12, dh=64),
+    dict(pos=2000, m=2, reach=512, gap=0, cap=768, heads=4, key_heads=2, dh=32),
+    dict(pos=700, m=2, reach=O.USIZE_MAX, gap=0, cap=768, heads=4, key_heads=1, dh=64),
 ]
 
 
